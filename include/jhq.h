@@ -1,0 +1,173 @@
+/*
+ * jhq.h — C-ABI of the MI355X-native JHQ IVF engine (libjhq_amd.so).
+ *
+ * Drop-in boundary for the reference's JHQ search path.  Each entry point names
+ * the reference interface it replaces (paths relative to the lrlorry/JHQ_GPU
+ * checkout; canonical version jhq_v14_streaming_add, abbreviated v14/).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only; no C++ or torch types cross the boundary.
+ *   - Every call returns JHQ_OK (0) or an error code; jhq_last_error() gives
+ *     a thread-local message.  Nothing calls exit() (the reference's
+ *     CUDA_CHECK/CUBLAS_CHECK exit the process, common/cuda_utils.cuh:7-25).
+ *   - Host-pointer calls copy inputs in and outputs out before returning.
+ *     Calls with a `_device` suffix or a `jhq_k_` prefix take device pointers
+ *     and a HIP stream passed as void* (NULL = the index's own stream for
+ *     index calls, the null stream for jhq_k_ calls); they are asynchronous
+ *     with respect to the host unless stated otherwise.
+ *   - An index is not thread-safe: one call at a time per index (the
+ *     reference's search() mutates its workspace the same way,
+ *     v14/jhq_gpu_index.cuh:73).
+ *
+ * Results
+ *   ids are int32 positions in add() input order (0-based, counted across
+ *   add() calls); dists are the reference's composite estimate
+ *   ||q - x_hat||^2 + ||q||^2 (v14/search.cu:240 with v14/encode.cu:85).
+ *   Rows are sorted ascending by (dist, id); unfilled slots are (+inf, -1)
+ *   (v14/search.cu:284-286).
+ */
+#ifndef JHQ_H
+#define JHQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    JHQ_OK = 0,
+    JHQ_EINVAL = 1,  /* bad argument     (reference: std::invalid_argument) */
+    JHQ_ESTATE = 2,  /* wrong call order (reference: std::runtime_error)    */
+    JHQ_EDEVICE = 3, /* HIP runtime / kernel launch failure                 */
+    JHQ_ENOMEM = 4   /* device or host allocation failure                   */
+};
+
+typedef struct jhq_index jhq_index;
+
+/* JHQGpuIndex::Params (v14/jhq_gpu_index.cuh:16-36), same fields, same
+ * defaults (jhq_params_default). */
+typedef struct {
+    int   M;          /* subspaces; d % M == 0                        */
+    int   B;          /* primary bits per subspace; B % (d/M) == 0, <=8 */
+    int   Br;         /* residual bits per dimension: 4 or 8           */
+    float alpha;      /* short-list factor: ck = max(k, ceil(alpha*k)) */
+    int   nlist;      /* IVF lists                                     */
+    int   nprobe;     /* lists probed per query (clamped to nlist)     */
+    int   ivf_iters;  /* Lloyd iterations of the coarse k-means        */
+    int   batch_size; /* queries per search batch                      */
+    int   seed;       /* JL rotation seed                              */
+    int   add_batch;  /* rows rotated/encoded per add() step           */
+} jhq_params;
+
+/* Fills the reference defaults: M=96 B=8 Br=4 alpha=4 nlist=1024 nprobe=8
+ * ivf_iters=8 batch_size=256 seed=42 add_batch=65536. */
+void jhq_params_default(jhq_params* p);
+
+/* JHQGpuIndex::JHQGpuIndex(int d, Params) — v14/jhq_gpu_index.cu:103-131.
+ * Validates the parameters exactly like the reference and builds the JL
+ * rotation (cpu/jl_transform.cpp:25-56) on the host. */
+int jhq_create(int d, const jhq_params* p, jhq_index** out);
+
+/* JHQGpuIndex::~JHQGpuIndex — v14/jhq_gpu_index.cu:133-163. NULL is a no-op. */
+int jhq_destroy(jhq_index* idx);
+
+/* JHQGpuIndex::train(const float* h_x, int n_train) —
+ * v14/jhq_gpu_index.cu:333-364.  x is host [n_train x d] row-major. */
+int jhq_train(jhq_index* idx, const float* x, int64_t n_train);
+
+/* JHQGpuIndex::add(const float* h_x, int n) — v14/jhq_gpu_index.cu:417-532.
+ * x is host [n x d].  Like the reference, one add() call per index;
+ * a second call fails with JHQ_ESTATE. */
+int jhq_add(jhq_index* idx, const float* x, int64_t n);
+
+/* JHQGpuIndex::search(h_q, nq, k, h_dists, h_labels) —
+ * v14/jhq_gpu_index.cu:535-552 -> search_gpu, v14/search.cu:388-445.
+ * q host [nq x d]; dists/ids host [nq x k]. */
+int jhq_search(jhq_index* idx, const float* q, int64_t nq, int k,
+               float* dists, int32_t* ids);
+
+/* Same pipeline with queries and results already in device memory
+ * (the reference's graph body v14/search.cu:315-386 without the host
+ * copies around it).  Returns after the work is enqueued on `stream`. */
+int jhq_search_device(jhq_index* idx, const float* d_q, int64_t nq, int k,
+                      float* d_dists, int32_t* d_ids, void* stream);
+
+/* JHQGpuIndex::ntotal() / dim() — v14/jhq_gpu_index.cuh:46-47 */
+int64_t jhq_ntotal(const jhq_index* idx);
+int     jhq_dim(const jhq_index* idx);
+
+/* Params.nprobe is fixed at construction in the reference; changing it
+ * recaptures the search graph (v14/search.cu:411-418).  This setter does the
+ * same for an existing index (clamped to nlist). */
+int jhq_set_nprobe(jhq_index* idx, int nprobe);
+
+/* Thread-local message of the last failed call on this thread. */
+const char* jhq_last_error(void);
+
+/* ---- introspection (copies to host; used by parity tests and tools) ---- */
+
+/* Derived sizes: Ds, K1D, bits_per_dim, Kr, bpv (v14/jhq_gpu_index.cu:123-128). */
+int jhq_get_dims(const jhq_index* idx, int* Ds, int* K1D, int* bpd, int* Kr, int* bpv);
+
+/* Trained state: sigma, c1d[K1D], res_c1d[Kr], P[d*d] (row-major Pi(j,k),
+ * i.e. the transpose of JLTransform::pi_data()), centroids[nlist*d],
+ * cent_norms[nlist].  Any pointer may be NULL. */
+int jhq_get_codebooks(const jhq_index* idx, float* sigma, float* c1d,
+                      float* res_c1d, float* P, float* centroids,
+                      float* cent_norms);
+
+/* List storage in stored-position order (the reference's list_* arrays,
+ * v14/jhq_gpu_index.cuh:67-71): offsets[nlist+1], ids[ntotal],
+ * codes[ntotal*M] (row-major primary codes, untransposed), res[ntotal*bpv],
+ * corr[ntotal].  Any pointer may be NULL. */
+int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids,
+                  uint8_t* codes, uint8_t* res, float* corr);
+
+/* Search that also returns, per query, the probed list ids [nq x nprobe]
+ * (ascending (score, list)) and the merged top-ck short list
+ * [nq x ck] as stored positions and primary distances ((dist, pos)
+ * ascending; unfilled = -1 / +inf).  ck = max(k, ceil(alpha*k)). */
+int jhq_search_debug(jhq_index* idx, const float* q, int64_t nq, int k,
+                     float* dists, int32_t* ids, int32_t* probes,
+                     int32_t* topck_pos, float* topck_dist);
+
+/* Per-step device timing (hipEvents around each step, the reference's
+ * step list of jhq_v13_step_timing/search.cu:424-491).  When enabled,
+ * every search batch records events; jhq_get_timing returns accumulated
+ * milliseconds per step and the number of batches:
+ *   ms[0] rotate  ms[1] centroid scores  ms[2] select probes
+ *   ms[3] scan + top-ck  ms[4] merge + refine + final top-k */
+int jhq_set_timing(jhq_index* idx, int enable);
+int jhq_get_timing(const jhq_index* idx, double* ms, int n_ms, int64_t* batches);
+
+/* ---- kernel-granular entry points (device pointers) ---- */
+
+/* Rotation Y = X * Pi^T as an fmaf chain over k ascending; P row-major
+ * Pi(j,k).  Replaces the cuBLAS Sgemm of v14/jhq_gpu_index.cu:444-448 and
+ * v14/search.cu:338-339. */
+int jhq_k_rotate(const float* d_P, const float* d_x, int64_t n, int d,
+                 float* d_y, void* stream);
+
+/* launch_primary_encode — v14/encode.cuh:7-12, kernel v14/encode.cu:20-41. */
+int jhq_k_primary_encode(const float* d_y, uint8_t* d_codes, const float* d_c1d,
+                         int64_t n, int d, int M, int Ds, int K1D,
+                         int bits_per_dim, void* stream);
+
+/* launch_residual_encode — v14/encode.cuh:14-22, kernel v14/encode.cu:43-86. */
+int jhq_k_residual_encode(const float* d_y, const uint8_t* d_primary,
+                          uint8_t* d_res_codes, float* d_corrections,
+                          const float* d_c1d, const float* d_res_c1d,
+                          int64_t n, int d, int M, int Ds, int K1D, int Kr,
+                          int Br, int bpv, int bits_per_dim, void* stream);
+
+/* assign_on_gpu + assign_from_dots_kernel — v14/jhq_gpu_index.cu:367-393,
+ * 23-40: argmin_c ||c||^2 - 2<c,y>, ties to the lowest c. */
+int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent,
+                 const float* d_cent_norms, int nlist, int32_t* d_assign,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JHQ_H */

@@ -1,0 +1,733 @@
+// jhq_capi.hip — C-ABI of the JHQ IVF engine: index object, train / add /
+// search orchestration over the HIP kernels in kernels.hip.
+//
+// Mirrors JHQGpuIndex (lrlorry/JHQ_GPU jhq_v14_streaming_add/jhq_gpu_index.cu)
+// and search_gpu (jhq_v14_streaming_add/search.cu:388-445); every entry point
+// of include/jhq.h cites the reference interface it replaces.
+#include "../../include/jhq.h"
+#include "host_train.h"
+#include "kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define JHQ_HIP(expr)                                                                  \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return fail(e_ == hipErrorOutOfMemory ? JHQ_ENOMEM : JHQ_EDEVICE,          \
+                        std::string(#expr) + ": " + hipGetErrorString(e_));            \
+    } while (0)
+
+#define JHQ_TRY(expr)            \
+    do {                         \
+        int rc_ = (expr);        \
+        if (rc_ != JHQ_OK) return rc_; \
+    } while (0)
+
+// Owning device buffer.
+template <class T>
+struct DBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    DBuf() = default;
+    DBuf(const DBuf&) = delete;
+    DBuf& operator=(const DBuf&) = delete;
+    ~DBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    int alloc(size_t count) {
+        release();
+        if (count == 0) count = 1;
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&p), count * sizeof(T));
+        if (e != hipSuccess) {
+            p = nullptr;
+            return fail(JHQ_ENOMEM, "hipMalloc of " + std::to_string(count * sizeof(T)) +
+                                        " bytes: " + hipGetErrorString(e));
+        }
+        n = count;
+        return JHQ_OK;
+    }
+    int ensure(size_t count) { return count <= n && p ? JHQ_OK : alloc(count); }
+    int upload(const T* h, size_t count) {
+        JHQ_TRY(alloc(count));
+        JHQ_HIP(hipMemcpy(p, h, count * sizeof(T), hipMemcpyHostToDevice));
+        return JHQ_OK;
+    }
+};
+
+constexpr int kSteps = 5;
+
+}  // namespace
+
+struct jhq_index {
+    // parameters (v14/jhq_gpu_index.cuh:50-54)
+    int d = 0, M = 0, B = 0, Br = 0, Ds = 0, K1D = 0, bpd = 0, Kr = 0, bpv = 0;
+    int nlist = 0, nprobe = 0, ivf_iters = 0, batch_size = 0, seed = 0, add_batch = 0;
+    float alpha = 0.f;
+    int64_t ntotal = 0;
+    bool trained = false;
+    bool added = false;
+    int num_cu = 256;
+
+    float sigma = 1.f;
+    std::vector<float> Pi_cm;  // JLTransform::pi_data() (column-major)
+    std::vector<float> P_rm;   // row-major Pi(j,k)
+    std::vector<float> c1d, res_c1d, cent, cent_norms;
+    std::vector<int32_t> list_off_h, list_padoff_h;
+    std::vector<int64_t> top_groups_prefix;  // prefix sums of list group counts, descending
+
+    hipStream_t stream = nullptr;
+    DBuf<float> dP, dc1d, dres_c1d, dcent, dnorms;
+    DBuf<int32_t> dlist_off, dlist_padoff, dlist_ids;
+    DBuf<uint8_t> dcodes_t, dres;
+    DBuf<float> dcorr;
+
+    // search workspace (v14/search.cuh:24-46)
+    DBuf<float> wq, wqrot, wscores, wout_d;
+    DBuf<int32_t> wprobes, wgofs, wout_i;
+    DBuf<unsigned long long> wpartial, wtopck;
+    float* h_q = nullptr;  // pinned staging
+    float* h_d = nullptr;
+    int32_t* h_i = nullptr;
+    size_t h_q_n = 0, h_d_n = 0, h_i_n = 0;
+
+    bool timing = false;
+    hipEvent_t ev[kSteps + 1] = {};
+    double tms[kSteps] = {};
+    int64_t tbatches = 0;
+
+    ~jhq_index() {
+        if (h_q) (void)hipHostFree(h_q);
+        if (h_d) (void)hipHostFree(h_d);
+        if (h_i) (void)hipHostFree(h_i);
+        for (auto& e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    int ensure_stream() {
+        if (stream) return JHQ_OK;
+        int ndev = 0;
+        if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+            return fail(JHQ_EDEVICE, "no HIP device available");
+        int dev = 0;
+        JHQ_HIP(hipGetDevice(&dev));
+        hipDeviceProp_t prop;
+        JHQ_HIP(hipGetDeviceProperties(&prop, dev));
+        num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+        JHQ_HIP(hipStreamCreate(&stream));
+        return JHQ_OK;
+    }
+};
+
+namespace {
+
+int ceil_ck(float alpha, int k) {
+    const int c = static_cast<int>(std::ceil(alpha * static_cast<float>(k)));
+    return std::max(k, c);
+}
+
+// Host pinned buffer growth.
+template <class T>
+int ensure_pinned(T*& p, size_t& cap, size_t n) {
+    if (p && cap >= n) return JHQ_OK;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+    JHQ_HIP(hipHostMalloc(reinterpret_cast<void**>(&p), std::max<size_t>(n, 1) * sizeof(T),
+                          hipHostMallocDefault));
+    cap = n;
+    return JHQ_OK;
+}
+
+// assign rows of d_y (device, [n x d]) to the nearest of the index's centroids.
+int assign_rows(jhq_index* ix, const float* d_y, int64_t n, int32_t* d_assign,
+                DBuf<unsigned long long>& keys) {
+    JHQ_TRY(keys.ensure(static_cast<size_t>(n)));
+    JHQ_HIP(jhq::fill_u64(keys.p, n, ~0ull, ix->stream));
+    JHQ_HIP(jhq::gemm_nt_argmin(d_y, ix->d, ix->dcent.p, ix->d, n, ix->nlist, ix->d, ix->dnorms.p,
+                                keys.p, ix->stream));
+    JHQ_HIP(jhq::keys_to_assign(keys.p, n, d_assign, ix->stream));
+    return JHQ_OK;
+}
+
+void compute_norms(jhq_index* ix) {
+    ix->cent_norms.assign(ix->nlist, 0.f);
+    for (int c = 0; c < ix->nlist; c++) {
+        double s = 0.0;
+        const float* cc = ix->cent.data() + static_cast<int64_t>(c) * ix->d;
+        for (int j = 0; j < ix->d; j++) s += static_cast<double>(cc[j]) * static_cast<double>(cc[j]);
+        ix->cent_norms[c] = static_cast<float>(s);
+    }
+}
+
+int upload_centroids(jhq_index* ix) {
+    compute_norms(ix);
+    JHQ_TRY(ix->dcent.upload(ix->cent.data(), ix->cent.size()));
+    JHQ_TRY(ix->dnorms.upload(ix->cent_norms.data(), ix->cent_norms.size()));
+    return JHQ_OK;
+}
+
+// v14/jhq_gpu_index.cu:228-299 — coarse k-means in rotated space.
+int train_ivf(jhq_index* ix, const float* h_y, const float* d_y, int64_t n) {
+    const int d = ix->d, nlist = ix->nlist;
+    ix->cent.assign(static_cast<size_t>(nlist) * d, 0.f);
+    for (int c = 0; c < nlist; c++) {
+        const int64_t src = static_cast<int64_t>(c) * n / nlist;
+        std::memcpy(ix->cent.data() + static_cast<int64_t>(c) * d, h_y + src * d,
+                    static_cast<size_t>(d) * sizeof(float));
+    }
+    DBuf<int32_t> dasg;
+    DBuf<unsigned long long> keys;
+    JHQ_TRY(dasg.alloc(static_cast<size_t>(n)));
+    std::vector<int32_t> asg(static_cast<size_t>(n));
+    std::vector<double> sums(static_cast<size_t>(nlist) * d);
+    std::vector<int64_t> counts(nlist);
+    for (int iter = 0; iter < ix->ivf_iters; iter++) {
+        JHQ_TRY(upload_centroids(ix));
+        JHQ_TRY(assign_rows(ix, d_y, n, dasg.p, keys));
+        JHQ_HIP(hipMemcpyAsync(asg.data(), dasg.p, static_cast<size_t>(n) * sizeof(int32_t),
+                               hipMemcpyDeviceToHost, ix->stream));
+        JHQ_HIP(hipStreamSynchronize(ix->stream));
+        std::fill(sums.begin(), sums.end(), 0.0);
+        std::fill(counts.begin(), counts.end(), 0);
+        for (int64_t i = 0; i < n; i++) {
+            const int c = asg[i];
+            counts[c]++;
+            double* sc = sums.data() + static_cast<int64_t>(c) * d;
+            const float* yi = h_y + i * d;
+            for (int j = 0; j < d; j++) sc[j] += yi[j];
+        }
+        for (int c = 0; c < nlist; c++) {
+            float* cc = ix->cent.data() + static_cast<int64_t>(c) * d;
+            if (counts[c] == 0) {
+                const int64_t src = (static_cast<int64_t>(c) * 1103515245 +
+                                     static_cast<int64_t>(iter) * 12345) % n;
+                std::memcpy(cc, h_y + src * d, static_cast<size_t>(d) * sizeof(float));
+                continue;
+            }
+            const double inv = 1.0 / static_cast<double>(counts[c]);
+            const double* sc = sums.data() + static_cast<int64_t>(c) * d;
+            for (int j = 0; j < d; j++) cc[j] = static_cast<float>(sc[j] * inv);
+        }
+    }
+    return upload_centroids(ix);
+}
+
+int ensure_workspace(jhq_index* ix, int ck, int k, int P, int S) {
+    const size_t B = static_cast<size_t>(ix->batch_size);
+    JHQ_TRY(ix->wq.ensure(B * ix->d));
+    JHQ_TRY(ix->wqrot.ensure(B * ix->d));
+    JHQ_TRY(ix->wscores.ensure(B * ix->nlist));
+    JHQ_TRY(ix->wprobes.ensure(B * P));
+    JHQ_TRY(ix->wgofs.ensure(B * (P + 1)));
+    JHQ_TRY(ix->wpartial.ensure(B * S * ck));
+    JHQ_TRY(ix->wtopck.ensure(B * ck));
+    JHQ_TRY(ix->wout_d.ensure(B * k));
+    JHQ_TRY(ix->wout_i.ensure(B * k));
+    return JHQ_OK;
+}
+
+struct BatchPlan {
+    int ck, P;
+    jhq::ScanShape sh;
+};
+
+int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
+    bp->ck = ceil_ck(ix->alpha, k);
+    bp->P = std::min(ix->nprobe, ix->nlist);
+    const int64_t maxg = ix->top_groups_prefix[bp->P];
+    if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, static_cast<int>(maxg), Bq, ix->num_cu,
+                        &bp->sh))
+        return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) +
+                                    ": the byte LUT (M*1 KiB) does not fit in LDS");
+    return ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.S);
+}
+
+// One batch of Bq queries at d_q (device) through the whole pipeline
+// (the graph body of v14/search.cu:315-386).
+int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& bp, float* d_out,
+              int32_t* d_ids, bool want_topck, hipStream_t s) {
+    const int d = ix->d;
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
+    JHQ_HIP(jhq::gemm_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, ix->wqrot.p, d, true, s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
+    JHQ_HIP(jhq::gemm_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
+                               ix->wscores.p, ix->nlist, true, s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
+    JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dlist_padoff.p,
+                               ix->wprobes.p, ix->wgofs.p, s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
+    JHQ_HIP(jhq::scan_topck(ix->wqrot.p, Bq, d, ix->M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p,
+                            ix->wprobes.p, ix->wgofs.p, bp.P, ix->dlist_off.p,
+                            ix->dlist_padoff.p, ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p,
+                            s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[4], s));
+    JHQ_HIP(jhq::refine_topk(ix->wpartial.p, Bq, bp.sh.S, bp.ck, k, ix->wqrot.p, d,
+                             ix->dres_c1d.p, ix->Kr, ix->Br, ix->bpv, ix->dres.p, ix->dcorr.p,
+                             ix->dlist_ids.p, d_out, d_ids, want_topck ? ix->wtopck.p : nullptr,
+                             s));
+    if (ix->timing) {
+        JHQ_HIP(hipEventRecord(ix->ev[5], s));
+        JHQ_HIP(hipEventSynchronize(ix->ev[5]));
+        for (int i = 0; i < kSteps; i++) {
+            float ms = 0.f;
+            JHQ_HIP(hipEventElapsedTime(&ms, ix->ev[i], ix->ev[i + 1]));
+            ix->tms[i] += ms;
+        }
+        ix->tbatches++;
+    }
+    return JHQ_OK;
+}
+
+int check_searchable(jhq_index* ix, int64_t nq, int k) {
+    if (!ix) return fail(JHQ_EINVAL, "null index");
+    if (ix->ntotal == 0) return fail(JHQ_ESTATE, "index is empty");
+    if (nq < 0) return fail(JHQ_EINVAL, "nq must be >= 0");
+    if (k <= 0) return fail(JHQ_EINVAL, "k must be positive");
+    return JHQ_OK;
+}
+
+int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, int32_t* ids,
+                int32_t* probes, int32_t* topck_pos, float* topck_dist) {
+    JHQ_TRY(check_searchable(ix, nq, k));
+    if (nq == 0) return JHQ_OK;
+    const int d = ix->d;
+    const int Bmax = ix->batch_size;
+    BatchPlan bp;
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp));
+    JHQ_TRY(ensure_pinned(ix->h_q, ix->h_q_n, static_cast<size_t>(Bmax) * d));
+    JHQ_TRY(ensure_pinned(ix->h_d, ix->h_d_n, static_cast<size_t>(Bmax) * k));
+    JHQ_TRY(ensure_pinned(ix->h_i, ix->h_i_n, static_cast<size_t>(Bmax) * k));
+    std::vector<unsigned long long> tk;
+    for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
+        const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
+        std::memcpy(ix->h_q, q + q0 * d, static_cast<size_t>(Bq) * d * sizeof(float));
+        JHQ_HIP(hipMemcpyAsync(ix->wq.p, ix->h_q, static_cast<size_t>(Bq) * d * sizeof(float),
+                               hipMemcpyHostToDevice, ix->stream));
+        const bool dbg = (probes || topck_pos || topck_dist);
+        JHQ_TRY(run_batch(ix, ix->wq.p, Bq, k, bp, ix->wout_d.p, ix->wout_i.p, dbg, ix->stream));
+        JHQ_HIP(hipMemcpyAsync(ix->h_d, ix->wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
+                               hipMemcpyDeviceToHost, ix->stream));
+        JHQ_HIP(hipMemcpyAsync(ix->h_i, ix->wout_i.p, static_cast<size_t>(Bq) * k * sizeof(int32_t),
+                               hipMemcpyDeviceToHost, ix->stream));
+        JHQ_HIP(hipStreamSynchronize(ix->stream));
+        std::memcpy(dists + q0 * k, ix->h_d, static_cast<size_t>(Bq) * k * sizeof(float));
+        std::memcpy(ids + q0 * k, ix->h_i, static_cast<size_t>(Bq) * k * sizeof(int32_t));
+        if (probes) {
+            JHQ_HIP(hipMemcpy(probes + q0 * bp.P, ix->wprobes.p,
+                              static_cast<size_t>(Bq) * bp.P * sizeof(int32_t),
+                              hipMemcpyDeviceToHost));
+        }
+        if (topck_pos || topck_dist) {
+            tk.resize(static_cast<size_t>(Bq) * bp.ck);
+            JHQ_HIP(hipMemcpy(tk.data(), ix->wtopck.p, tk.size() * sizeof(unsigned long long),
+                              hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < tk.size(); i++) {
+                const unsigned long long kk = tk[i];
+                const bool empty = (kk == ~0ull);
+                const uint32_t hi = static_cast<uint32_t>(kk >> 32);
+                uint32_t bits = hi & 0x7fffffffu;
+                float f;
+                std::memcpy(&f, &bits, 4);
+                if (topck_pos) topck_pos[q0 * bp.ck + i] = empty ? -1 : static_cast<int32_t>(kk & 0xffffffffull);
+                if (topck_dist) topck_dist[q0 * bp.ck + i] = empty ? INFINITY : f;
+            }
+        }
+    }
+    return JHQ_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* jhq_last_error(void) { return g_err.c_str(); }
+
+void jhq_params_default(jhq_params* p) {
+    if (!p) return;
+    p->M = 96;
+    p->B = 8;
+    p->Br = 4;
+    p->alpha = 4.0f;
+    p->nlist = 1024;
+    p->nprobe = 8;
+    p->ivf_iters = 8;
+    p->batch_size = 256;
+    p->seed = 42;
+    p->add_batch = 65536;
+}
+
+int jhq_create(int d, const jhq_params* p, jhq_index** out) {
+    if (!out) return fail(JHQ_EINVAL, "out must not be NULL");
+    *out = nullptr;
+    if (!p) return fail(JHQ_EINVAL, "params must not be NULL");
+    // v14/jhq_gpu_index.cu:110-121, same checks, same order
+    if (d <= 0) return fail(JHQ_EINVAL, "d must be positive");
+    if (p->M <= 0) return fail(JHQ_EINVAL, "M must be positive");
+    if (d % p->M != 0) return fail(JHQ_EINVAL, "d must be divisible by M");
+    if (p->B % (d / p->M) != 0) return fail(JHQ_EINVAL, "B must be divisible by Ds = d/M");
+    if (p->B > 8) return fail(JHQ_EINVAL, "B must be <= 8");
+    if (p->Br != 4 && p->Br != 8) return fail(JHQ_EINVAL, "Br must be 4 or 8");
+    if (p->nlist <= 0) return fail(JHQ_EINVAL, "nlist must be positive");
+    if (p->nprobe <= 0) return fail(JHQ_EINVAL, "nprobe must be positive");
+    if (p->ivf_iters <= 0) return fail(JHQ_EINVAL, "ivf_iters must be positive");
+    if (p->batch_size <= 0) return fail(JHQ_EINVAL, "batch_size must be positive");
+    if (p->add_batch <= 0) return fail(JHQ_EINVAL, "add_batch must be positive");
+    if (!(p->alpha > 0.0f)) return fail(JHQ_EINVAL, "alpha must be positive");
+    if (p->B <= 0) return fail(JHQ_EINVAL, "B must be positive");
+
+    jhq_index* ix = new (std::nothrow) jhq_index();
+    if (!ix) return fail(JHQ_ENOMEM, "host allocation failed");
+    ix->d = d;
+    ix->M = p->M;
+    ix->B = p->B;
+    ix->Br = p->Br;
+    ix->nlist = p->nlist;
+    ix->nprobe = std::min(p->nprobe, p->nlist);
+    ix->ivf_iters = p->ivf_iters;
+    ix->batch_size = p->batch_size;
+    ix->seed = p->seed;
+    ix->add_batch = p->add_batch;
+    ix->alpha = p->alpha;
+    ix->Ds = d / p->M;
+    ix->bpd = p->B / ix->Ds;
+    ix->K1D = 1 << ix->bpd;
+    ix->Kr = 1 << p->Br;
+    ix->bpv = (d * p->Br + 7) / 8;
+    // JLTransform jl_(d, seed): the rotation is built with the index.
+    ix->Pi_cm = jhq::build_rotation(d, p->seed);
+    ix->P_rm.resize(static_cast<size_t>(d) * d);
+    for (int j = 0; j < d; j++)
+        for (int k = 0; k < d; k++)
+            ix->P_rm[static_cast<size_t>(j) * d + k] = ix->Pi_cm[static_cast<size_t>(k) * d + j];
+    *out = ix;
+    return JHQ_OK;
+}
+
+int jhq_destroy(jhq_index* idx) {
+    delete idx;
+    return JHQ_OK;
+}
+
+int64_t jhq_ntotal(const jhq_index* idx) { return idx ? idx->ntotal : 0; }
+int jhq_dim(const jhq_index* idx) { return idx ? idx->d : 0; }
+
+int jhq_set_nprobe(jhq_index* idx, int nprobe) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (nprobe <= 0) return fail(JHQ_EINVAL, "nprobe must be positive");
+    idx->nprobe = std::min(nprobe, idx->nlist);
+    return JHQ_OK;
+}
+
+int jhq_get_dims(const jhq_index* idx, int* Ds, int* K1D, int* bpd, int* Kr, int* bpv) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (Ds) *Ds = idx->Ds;
+    if (K1D) *K1D = idx->K1D;
+    if (bpd) *bpd = idx->bpd;
+    if (Kr) *Kr = idx->Kr;
+    if (bpv) *bpv = idx->bpv;
+    return JHQ_OK;
+}
+
+// v14/jhq_gpu_index.cu:333-364
+int jhq_train(jhq_index* ix, const float* x, int64_t n_train) {
+    if (!ix || !x) return fail(JHQ_EINVAL, "null argument");
+    if (n_train <= 0) return fail(JHQ_EINVAL, "n_train must be positive");
+    if (n_train < ix->nlist)
+        return fail(JHQ_EINVAL, "n_train must be >= nlist");
+    if (n_train * static_cast<int64_t>(ix->d) > INT32_MAX)
+        return fail(JHQ_EINVAL, "n_train * d must fit in int (the reference's residual k-means size)");
+    if (ix->added) return fail(JHQ_ESTATE, "train() after add() is not supported");
+    JHQ_TRY(ix->ensure_stream());
+    const int d = ix->d, M = ix->M;
+    ix->sigma = jhq::estimate_sigma(x, n_train, d);
+    ix->c1d = jhq::lloyd_max_c1d(ix->sigma, ix->K1D);
+    JHQ_TRY(ix->dP.upload(ix->P_rm.data(), ix->P_rm.size()));
+    JHQ_TRY(ix->dc1d.upload(ix->c1d.data(), ix->c1d.size()));
+
+    DBuf<float> dx, dy;
+    DBuf<uint8_t> dcodes;
+    JHQ_TRY(dx.upload(x, static_cast<size_t>(n_train) * d));
+    JHQ_TRY(dy.alloc(static_cast<size_t>(n_train) * d));
+    JHQ_TRY(dcodes.alloc(static_cast<size_t>(n_train) * M));
+    JHQ_HIP(jhq::gemm_nt_store(dx.p, d, ix->dP.p, d, n_train, d, d, dy.p, d, false, ix->stream));
+    JHQ_HIP(jhq::encode(dy.p, n_train, d, M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr, ix->Br,
+                        ix->bpv, nullptr, dcodes.p, nullptr, nullptr, 1, ix->stream));
+    dx.release();
+    std::vector<float> h_y(static_cast<size_t>(n_train) * d);
+    std::vector<uint8_t> h_codes(static_cast<size_t>(n_train) * M);
+    JHQ_HIP(hipMemcpyAsync(h_y.data(), dy.p, h_y.size() * sizeof(float), hipMemcpyDeviceToHost,
+                           ix->stream));
+    JHQ_HIP(hipMemcpyAsync(h_codes.data(), dcodes.p, h_codes.size(), hipMemcpyDeviceToHost,
+                           ix->stream));
+    JHQ_HIP(hipStreamSynchronize(ix->stream));
+
+    JHQ_TRY(train_ivf(ix, h_y.data(), dy.p, n_train));
+
+    // v14/jhq_gpu_index.cu:302-330 — residual scalars over all training dims
+    {
+        std::vector<float> resid(static_cast<size_t>(n_train) * d);
+        const int kmask = ix->K1D - 1;
+        for (int64_t i = 0; i < n_train; i++) {
+            const uint8_t* code = h_codes.data() + i * M;
+            const float* yi = h_y.data() + i * d;
+            float* ri = resid.data() + i * d;
+            for (int m = 0; m < M; m++)
+                for (int k = 0; k < ix->Ds; k++)
+                    ri[m * ix->Ds + k] =
+                        yi[m * ix->Ds + k] - ix->c1d[(code[m] >> (k * ix->bpd)) & kmask];
+        }
+        ix->res_c1d = jhq::train_1d_kmeans(resid.data(), static_cast<int64_t>(resid.size()), ix->Kr);
+    }
+    // Kr may shrink only for tiny training sets (train_1d_kmeans clamps Kr to n)
+    std::vector<float> rc(ix->Kr, ix->res_c1d.empty() ? 0.f : ix->res_c1d.back());
+    std::copy(ix->res_c1d.begin(), ix->res_c1d.end(), rc.begin());
+    ix->res_c1d = rc;
+    JHQ_TRY(ix->dres_c1d.upload(ix->res_c1d.data(), ix->res_c1d.size()));
+    ix->trained = true;
+    return JHQ_OK;
+}
+
+// v14/jhq_gpu_index.cu:417-532
+int jhq_add(jhq_index* ix, const float* x, int64_t n) {
+    if (!ix || !x) return fail(JHQ_EINVAL, "null argument");
+    if (!ix->trained) return fail(JHQ_ESTATE, "call train() before add()");
+    if (ix->added) return fail(JHQ_ESTATE, "only one add() call is supported");
+    if (n <= 0) return fail(JHQ_EINVAL, "n must be positive");
+    if (n > INT32_MAX) return fail(JHQ_EINVAL, "n exceeds int32 ids");
+    JHQ_TRY(ix->ensure_stream());
+    const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
+    hipStream_t s = ix->stream;
+
+    DBuf<uint8_t> dpc, drc;
+    DBuf<float> dco;
+    DBuf<int32_t> dasg;
+    JHQ_TRY(dpc.alloc(static_cast<size_t>(n) * M));
+    JHQ_TRY(drc.alloc(static_cast<size_t>(n) * bpv));
+    JHQ_TRY(dco.alloc(static_cast<size_t>(n)));
+    JHQ_TRY(dasg.alloc(static_cast<size_t>(n)));
+    {
+        const int64_t AB = std::min<int64_t>(ix->add_batch, n);
+        DBuf<float> dxb, dyb;
+        DBuf<unsigned long long> keys;
+        JHQ_TRY(dxb.alloc(static_cast<size_t>(AB) * d));
+        JHQ_TRY(dyb.alloc(static_cast<size_t>(AB) * d));
+        for (int64_t start = 0; start < n; start += AB) {
+            const int64_t nb = std::min(AB, n - start);
+            JHQ_HIP(hipMemcpyAsync(dxb.p, x + start * d, static_cast<size_t>(nb) * d * sizeof(float),
+                                   hipMemcpyHostToDevice, s));
+            JHQ_HIP(jhq::gemm_nt_store(dxb.p, d, ix->dP.p, d, nb, d, d, dyb.p, d, false, s));
+            JHQ_HIP(jhq::encode(dyb.p, nb, d, M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr,
+                                ix->Br, bpv, ix->dres_c1d.p, dpc.p + start * M,
+                                drc.p + start * bpv, dco.p + start, 3, s));
+            JHQ_TRY(assign_rows(ix, dyb.p, nb, dasg.p + start, keys));
+            JHQ_HIP(hipStreamSynchronize(s));
+        }
+    }
+    // stable counting sort by list (the reference's thrust::sort_by_key,
+    // v14/jhq_gpu_index.cu:468-486)
+    std::vector<int32_t> asg(static_cast<size_t>(n));
+    JHQ_HIP(hipMemcpy(asg.data(), dasg.p, asg.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+    std::vector<int32_t> off(nlist + 1, 0), padoff(nlist + 1, 0);
+    for (int64_t i = 0; i < n; i++) {
+        const int a = asg[i];
+        if (a < 0 || a >= nlist) return fail(JHQ_EDEVICE, "invalid IVF assignment");
+        off[a + 1]++;
+    }
+    std::vector<int64_t> groups(nlist);
+    for (int c = 0; c < nlist; c++) {
+        const int cnt = off[c + 1];
+        const int npad = (cnt + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+        groups[c] = npad / jhq::kGroup;
+        off[c + 1] = off[c] + cnt;
+        padoff[c + 1] = padoff[c] + npad;
+    }
+    std::vector<int32_t> order(static_cast<size_t>(n)), slist(static_cast<size_t>(n));
+    {
+        std::vector<int32_t> fill(off.begin(), off.end() - 1);
+        for (int64_t i = 0; i < n; i++) {
+            const int a = asg[i];
+            const int32_t pos = fill[a]++;
+            order[pos] = static_cast<int32_t>(i);
+            slist[pos] = a;
+        }
+    }
+    DBuf<int32_t> dorder, dslist;
+    JHQ_TRY(dorder.upload(order.data(), order.size()));
+    JHQ_TRY(dslist.upload(slist.data(), slist.size()));
+    JHQ_TRY(ix->dlist_off.upload(off.data(), off.size()));
+    JHQ_TRY(ix->dlist_padoff.upload(padoff.data(), padoff.size()));
+    JHQ_TRY(ix->dlist_ids.alloc(static_cast<size_t>(n)));
+    JHQ_TRY(ix->dcodes_t.alloc(static_cast<size_t>(padoff[nlist]) * M + 16));
+    JHQ_TRY(ix->dres.alloc(static_cast<size_t>(n) * bpv));
+    JHQ_TRY(ix->dcorr.alloc(static_cast<size_t>(n)));
+    JHQ_HIP(hipMemsetAsync(ix->dcodes_t.p, 0, ix->dcodes_t.n, s));
+    JHQ_HIP(jhq::scatter_lists(dorder.p, dslist.p, n, 0, ix->dlist_off.p, ix->dlist_padoff.p,
+                               dpc.p, drc.p, dco.p, M, bpv, ix->dlist_ids.p, ix->dcodes_t.p,
+                               ix->dres.p, ix->dcorr.p, s));
+    JHQ_HIP(hipStreamSynchronize(s));
+    ix->list_off_h = off;
+    ix->list_padoff_h = padoff;
+    std::sort(groups.begin(), groups.end(), [](int64_t a, int64_t b) { return a > b; });
+    ix->top_groups_prefix.assign(nlist + 1, 0);
+    for (int c = 0; c < nlist; c++) ix->top_groups_prefix[c + 1] = ix->top_groups_prefix[c] + groups[c];
+    ix->ntotal = n;
+    ix->added = true;
+    return JHQ_OK;
+}
+
+int jhq_search(jhq_index* idx, const float* q, int64_t nq, int k, float* dists, int32_t* ids) {
+    if (!q || !dists || !ids) return fail(JHQ_EINVAL, "null argument");
+    return search_host(idx, q, nq, k, dists, ids, nullptr, nullptr, nullptr);
+}
+
+int jhq_search_debug(jhq_index* idx, const float* q, int64_t nq, int k, float* dists,
+                     int32_t* ids, int32_t* probes, int32_t* topck_pos, float* topck_dist) {
+    if (!q || !dists || !ids) return fail(JHQ_EINVAL, "null argument");
+    return search_host(idx, q, nq, k, dists, ids, probes, topck_pos, topck_dist);
+}
+
+int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float* d_dists,
+                      int32_t* d_ids, void* stream) {
+    JHQ_TRY(check_searchable(ix, nq, k));
+    if (!d_q || !d_dists || !d_ids) return fail(JHQ_EINVAL, "null argument");
+    if (nq == 0) return JHQ_OK;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ix->stream;
+    BatchPlan bp;
+    JHQ_TRY(plan_batch(ix, ix->batch_size, k, &bp));
+    for (int64_t q0 = 0; q0 < nq; q0 += ix->batch_size) {
+        const int Bq = static_cast<int>(std::min<int64_t>(ix->batch_size, nq - q0));
+        JHQ_TRY(run_batch(ix, d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k, d_ids + q0 * k, false,
+                          s));
+    }
+    return JHQ_OK;
+}
+
+int jhq_get_codebooks(const jhq_index* idx, float* sigma, float* c1d, float* res_c1d, float* P,
+                      float* centroids, float* cent_norms) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (sigma) *sigma = idx->sigma;
+    if (P) std::memcpy(P, idx->P_rm.data(), idx->P_rm.size() * sizeof(float));
+    if ((c1d || res_c1d || centroids || cent_norms) && !idx->trained)
+        return fail(JHQ_ESTATE, "index is not trained");
+    if (c1d) std::memcpy(c1d, idx->c1d.data(), idx->c1d.size() * sizeof(float));
+    if (res_c1d) std::memcpy(res_c1d, idx->res_c1d.data(), idx->res_c1d.size() * sizeof(float));
+    if (centroids) std::memcpy(centroids, idx->cent.data(), idx->cent.size() * sizeof(float));
+    if (cent_norms) std::memcpy(cent_norms, idx->cent_norms.data(), idx->cent_norms.size() * sizeof(float));
+    return JHQ_OK;
+}
+
+int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids, uint8_t* codes,
+                  uint8_t* res, float* corr) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (!idx->added) return fail(JHQ_ESTATE, "index is empty");
+    const int64_t n = idx->ntotal;
+    const int M = idx->M, nlist = idx->nlist;
+    if (offsets) std::memcpy(offsets, idx->list_off_h.data(), (nlist + 1) * sizeof(int32_t));
+    if (ids) JHQ_HIP(hipMemcpy(ids, idx->dlist_ids.p, n * sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (res) JHQ_HIP(hipMemcpy(res, idx->dres.p, static_cast<size_t>(n) * idx->bpv, hipMemcpyDeviceToHost));
+    if (corr) JHQ_HIP(hipMemcpy(corr, idx->dcorr.p, n * sizeof(float), hipMemcpyDeviceToHost));
+    if (codes) {
+        std::vector<uint8_t> t(idx->dcodes_t.n);
+        JHQ_HIP(hipMemcpy(t.data(), idx->dcodes_t.p, t.size(), hipMemcpyDeviceToHost));
+        for (int l = 0; l < nlist; l++) {
+            const int64_t pad0 = idx->list_padoff_h[l];
+            const int64_t npad = idx->list_padoff_h[l + 1] - pad0;
+            const int64_t o = idx->list_off_h[l];
+            const int64_t nl = idx->list_off_h[l + 1] - o;
+            for (int64_t i = 0; i < nl; i++)
+                for (int m = 0; m < M; m++)
+                    codes[(o + i) * M + m] = t[pad0 * M + m * npad + i];
+        }
+    }
+    return JHQ_OK;
+}
+
+int jhq_set_timing(jhq_index* idx, int enable) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    JHQ_TRY(idx->ensure_stream());
+    if (enable && !idx->ev[0])
+        for (auto& e : idx->ev) JHQ_HIP(hipEventCreate(&e));
+    idx->timing = enable != 0;
+    for (double& t : idx->tms) t = 0.0;
+    idx->tbatches = 0;
+    return JHQ_OK;
+}
+
+int jhq_get_timing(const jhq_index* idx, double* ms, int n_ms, int64_t* batches) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    for (int i = 0; i < n_ms && i < kSteps; i++) ms[i] = idx->tms[i];
+    if (batches) *batches = idx->tbatches;
+    return JHQ_OK;
+}
+
+int jhq_k_rotate(const float* d_P, const float* d_x, int64_t n, int d, float* d_y, void* stream) {
+    if (!d_P || !d_x || !d_y || n < 0 || d <= 0) return fail(JHQ_EINVAL, "bad argument");
+    JHQ_HIP(jhq::gemm_nt_store(d_x, d, d_P, d, n, d, d, d_y, d, n < 1024,
+                               static_cast<hipStream_t>(stream)));
+    return JHQ_OK;
+}
+
+int jhq_k_primary_encode(const float* d_y, uint8_t* d_codes, const float* d_c1d, int64_t n, int d,
+                         int M, int Ds, int K1D, int bits_per_dim, void* stream) {
+    if (!d_y || !d_codes || !d_c1d || n < 0 || M <= 0 || Ds * M != d || (1 << bits_per_dim) != K1D)
+        return fail(JHQ_EINVAL, "bad argument");
+    JHQ_HIP(jhq::encode(d_y, n, d, M, Ds, K1D, bits_per_dim, d_c1d, 1, 4, 1, nullptr, d_codes,
+                        nullptr, nullptr, 1, static_cast<hipStream_t>(stream)));
+    return JHQ_OK;
+}
+
+int jhq_k_residual_encode(const float* d_y, const uint8_t* d_primary, uint8_t* d_res_codes,
+                          float* d_corrections, const float* d_c1d, const float* d_res_c1d,
+                          int64_t n, int d, int M, int Ds, int K1D, int Kr, int Br, int bpv,
+                          int bits_per_dim, void* stream) {
+    if (!d_y || !d_primary || !d_res_codes || !d_corrections || !d_c1d || !d_res_c1d || n < 0 ||
+        M <= 0 || Ds * M != d || (1 << bits_per_dim) != K1D || (Br != 4 && Br != 8) ||
+        bpv != (d * Br + 7) / 8 || Kr <= 0 || Kr > (1 << Br))
+        return fail(JHQ_EINVAL, "bad argument");
+    JHQ_HIP(jhq::encode(d_y, n, d, M, Ds, K1D, bits_per_dim, d_c1d, Kr, Br, bpv, d_res_c1d,
+                        const_cast<uint8_t*>(d_primary), d_res_codes, d_corrections, 2,
+                        static_cast<hipStream_t>(stream)));
+    return JHQ_OK;
+}
+
+int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent, const float* d_cent_norms,
+                 int nlist, int32_t* d_assign, void* stream) {
+    if (!d_y || !d_cent || !d_cent_norms || !d_assign || n < 0 || d <= 0 || nlist <= 0)
+        return fail(JHQ_EINVAL, "bad argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    unsigned long long* keys = nullptr;
+    JHQ_HIP(hipMallocAsync(reinterpret_cast<void**>(&keys), std::max<int64_t>(n, 1) * 8, s));
+    hipError_t e = jhq::fill_u64(keys, n, ~0ull, s);
+    if (e == hipSuccess) e = jhq::gemm_nt_argmin(d_y, d, d_cent, d, n, nlist, d, d_cent_norms, keys, s);
+    if (e == hipSuccess) e = jhq::keys_to_assign(keys, n, d_assign, s);
+    (void)hipFreeAsync(keys, s);
+    if (e != hipSuccess) return fail(JHQ_EDEVICE, std::string("assign: ") + hipGetErrorString(e));
+    return JHQ_OK;
+}
+
+}  // extern "C"

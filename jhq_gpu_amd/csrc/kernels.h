@@ -1,0 +1,80 @@
+// kernels.h — launchers of the HIP kernels (gfx950).  Internal C++ interface
+// between the C-ABI layer (jhq_capi.hip) and the kernels (kernels.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace jhq {
+
+// LDS available to one workgroup on gfx950.
+constexpr int kLdsBytes = 160 * 1024;
+// Candidates per padded group of the per-list code-major layout.
+constexpr int kGroup = 16;
+
+// C[i][j] = sum_k A[i][k] * Bm[j][k] as an fmaf chain, k ascending from 0.
+//   store : C[i*ldc + j] = acc
+//   score : C[i*ldc + j] = fmaf(-2, acc, norms[j])     (= norms[j] - 2 acc)
+//   argmin: keys[i] = min over j of (ord(fmaf(-2, acc, norms[j])) << 32 | j)
+//           (keys must be pre-filled with ~0)
+hipError_t gemm_nt_store(const float* A, int64_t lda, const float* Bm, int64_t ldb,
+                         int64_t n, int m, int d, float* C, int64_t ldc,
+                         bool small_rows, hipStream_t s);
+hipError_t gemm_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb,
+                         int64_t n, int m, int d, const float* norms, float* C,
+                         int64_t ldc, bool small_rows, hipStream_t s);
+hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t ldb,
+                          int64_t n, int m, int d, const float* norms,
+                          unsigned long long* keys, hipStream_t s);
+hipError_t fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
+hipError_t keys_to_assign(const unsigned long long* keys, int64_t n, int32_t* assign,
+                          hipStream_t s);
+
+// Primary / residual encode.  mode bit 0: compute and write primary codes from
+// y; mode bit 1: residual codes + corrections (primary digits from y when bit 0
+// is set, else read from `codes`).
+hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int bpd,
+                  const float* c1d, int Kr, int Br, int bpv, const float* res_c1d,
+                  uint8_t* codes, uint8_t* res, float* corr, int mode, hipStream_t s);
+
+// Scatter per-vector data into list storage.  For stored position s:
+// id = order[s], list = slist[s]; ids_out[s] = id + id_base; res/corr copied;
+// primary codes written to the code-major padded block of the list.
+hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n,
+                         int64_t id_base, const int32_t* list_off,
+                         const int32_t* list_padoff, const uint8_t* pc,
+                         const uint8_t* rc, const float* co, int M, int bpv,
+                         int32_t* ids_out, uint8_t* codes_t, uint8_t* res_out,
+                         float* corr_out, hipStream_t s);
+
+// Per query: top-P lists by (score, list) from scores[b][nlist]; writes
+// probes[b][P] (ascending) and gofs[b][P+1] (prefix of padded group counts).
+hipError_t select_probes(const float* scores, int B, int nlist, int P,
+                         const int32_t* list_padoff, int32_t* probes,
+                         int32_t* gofs, hipStream_t s);
+
+struct ScanShape {
+    int S;      // workgroups per query
+    int cap;    // candidate slots per workgroup (multiple of kGroup)
+    int lds;    // dynamic LDS bytes
+};
+// LDS plan of the scan kernel; returns false if M does not fit.
+bool scan_plan(int M, int d, int P, int ck, int max_groups_per_query, int B, int target_wg,
+               ScanShape* out);
+
+// IVF ADC scan + exact per-workgroup top-ck; partial[b][s][ck] keys
+// (ord(dist) << 32 | pos), unfilled = ~0.
+hipError_t scan_topck(const float* q_rot, int B, int d, int M, int Ds, int K1D, int bpd,
+                      const float* c1d, const int32_t* probes, const int32_t* gofs, int P,
+                      const int32_t* list_off, const int32_t* list_padoff,
+                      const uint8_t* codes_t, int ck, const ScanShape& sh,
+                      unsigned long long* partial, hipStream_t s);
+
+// Per query: merge S partial top-ck lists, residual refine, final top-k.
+// If topck_dbg != nullptr it receives the merged short list [B][ck] keys.
+hipError_t refine_topk(const unsigned long long* partial, int B, int S, int ck, int k,
+                       const float* q_rot, int d, const float* res_c1d, int Kr, int Br,
+                       int bpv, const uint8_t* list_res, const float* list_corr,
+                       const int32_t* list_ids, float* out_d, int32_t* out_i,
+                       unsigned long long* topck_dbg, hipStream_t s);
+
+}  // namespace jhq

@@ -1,0 +1,69 @@
+"""Kernel-granular parity through the C-ABI (jhq_k_* entry points) against the
+CPU oracle: rotation, primary/residual encode and IVF assignment must be
+bit-exact, including ragged shapes and exact ties."""
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+import jhq_gpu_amd as jg
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("n,d", [(1, 8), (37, 64), (300, 100), (1000, 128), (129, 1024)])
+def test_rotate_bit_exact(gpu, n, d):
+    import torch
+    rng = np.random.default_rng(n * 7 + d)
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    P = po.rotation_rowmajor(d, 42) if d <= 256 else rng.standard_normal((d, d)).astype(np.float32)
+    y = torch.empty((n, d), dtype=torch.float32, device=gpu)
+    jg.k_rotate(_t(P, gpu), _t(x, gpu), y)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), po.rotate(P, x).view(np.uint32))
+
+
+@pytest.mark.parametrize("d,M,B,Br,Kr", [(64, 8, 8, 4, 16), (100, 25, 8, 4, 16), (32, 32, 8, 8, 256),
+                                          (48, 12, 4, 4, 16), (33, 33, 2, 4, 7), (1024, 128, 8, 4, 16)])
+def test_encode_bit_exact(gpu, d, M, B, Br, Kr):
+    import torch
+    rng = np.random.default_rng(d * 31 + M)
+    n = 777
+    y = (rng.standard_normal((n, d)) * 0.05).astype(np.float32)
+    y[0, :] = 0.0  # exact midpoint (0) for K1D=2 → upper codeword
+    Ds = d // M
+    K1D = 1 << (B // Ds)
+    c1d = po.lloyd_max_c1d(0.05, K1D)
+    res_c1d = np.sort(rng.standard_normal(Kr).astype(np.float32) * 0.02)
+    codes = torch.empty((n, M), dtype=torch.uint8, device=gpu)
+    jg.k_primary_encode(_t(y, gpu), codes, _t(c1d, gpu), M)
+    torch.cuda.synchronize()
+    oc = po.primary_encode(y, M, c1d)
+    assert np.array_equal(codes.cpu().numpy(), oc)
+    bpv = (d * Br + 7) // 8
+    res = torch.empty((n, bpv), dtype=torch.uint8, device=gpu)
+    corr = torch.empty((n,), dtype=torch.float32, device=gpu)
+    jg.k_residual_encode(_t(y, gpu), codes, res, corr, _t(c1d, gpu), _t(res_c1d, gpu), M, Br)
+    torch.cuda.synchronize()
+    ores, ocorr = po.residual_encode(y, oc, M, c1d, res_c1d, Br)
+    assert np.array_equal(res.cpu().numpy(), ores)
+    assert np.array_equal(corr.cpu().numpy().view(np.uint32), ocorr.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,d,nlist", [(1000, 64, 16), (513, 100, 300), (64, 1024, 4096)])
+def test_assign_bit_exact_with_ties(gpu, n, d, nlist):
+    import torch
+    rng = np.random.default_rng(n + d + nlist)
+    y = rng.standard_normal((n, d)).astype(np.float32)
+    cent = rng.standard_normal((nlist, d)).astype(np.float32)
+    cent[nlist // 2] = cent[nlist // 3]  # duplicate centroid: ties go to the lower id
+    norms = po.cent_norms(cent)
+    a = torch.empty((n,), dtype=torch.int32, device=gpu)
+    jg.k_assign(_t(y, gpu), _t(cent, gpu), _t(norms, gpu), a)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), po.assign(y, cent, norms))

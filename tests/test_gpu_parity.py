@@ -1,0 +1,164 @@
+"""GPU parity: the HIP product against the CPU oracle on identical seeded inputs.
+
+Bar: codebooks, rotation, codes, list layout, probe
+lists and the top-ck short list are bit-exact; final ids are exact wherever
+neighbouring distances differ by more than 1e-5 relative; final distances
+agree within 1e-4 relative (the tolerance asserted below).
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+from datagen import queries_and_base
+
+import jhq_gpu_amd as jg
+
+pytestmark = pytest.mark.gpu
+
+DIST_RTOL = 1e-4
+TIE_RTOL = 1e-5
+
+# (name, d, M, B, Br, nlist, nprobe, alpha, n, nq, k, batch)
+CASES = [
+    ("ds8_k1d2", 64, 8, 8, 4, 16, 4, 4.0, 3000, 70, 10, 32),
+    ("ds4_k1d4_d100", 100, 25, 8, 4, 8, 3, 4.0, 2000, 40, 10, 16),
+    ("ds1_k1d256_br8", 32, 32, 8, 8, 8, 2, 2.0, 1500, 33, 5, 64),
+    ("b4_ds4_k1d2", 48, 12, 4, 4, 8, 8, 3.0, 1200, 20, 7, 8),
+    ("flat_nlist1", 64, 16, 8, 4, 1, 1, 4.0, 2500, 25, 10, 1),
+    ("d1024_m128", 1024, 128, 8, 4, 32, 6, 4.0, 2000, 20, 10, 64),
+]
+IDS = [c[0] for c in CASES]
+
+_BUILT = {}
+
+
+def _build(case):
+    name, d, M, B, Br, nlist, nprobe, alpha, n, nq, k, batch = case
+    if name in _BUILT:
+        return _BUILT[name]
+    base, q = queries_and_base(n, nq, d, max(4, nlist * 2), seed=zlib.crc32(name.encode()) % 10000)
+    p = jg.Params(M=M, B=B, Br=Br, alpha=alpha, nlist=nlist, nprobe=nprobe, ivf_iters=4,
+                  batch_size=batch, seed=42)
+    g = jg.JHQGpuIndex(d, p)
+    o = po.OracleIndex(d, M=M, B=B, Br=Br, alpha=alpha, nlist=nlist, nprobe=nprobe, ivf_iters=4,
+                       seed=42)
+    ntrain = min(n, 1000) if nlist > 1 else n
+    g.train(base[:ntrain])
+    o.train(base[:ntrain])
+    g.add(base)
+    o.add(base)
+    _BUILT[name] = (g, o, base, q, k)
+    return _BUILT[name]
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_codebooks_bit_exact(gpu, case):
+    g, o, *_ = _build(case)
+    cb = g.codebooks()
+    assert np.array_equal(_bits(cb["P"]), _bits(o.P))
+    assert np.float32(cb["sigma"]) == o.sigma
+    assert np.array_equal(_bits(cb["c1d"]), _bits(o.c1d))
+    assert np.array_equal(_bits(cb["centroids"]), _bits(o.cent))
+    assert np.array_equal(_bits(cb["cent_norms"]), _bits(o.cent_norms))
+    assert np.array_equal(_bits(cb["res_c1d"]), _bits(o.res_c1d))
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_lists_bit_exact(gpu, case):
+    g, o, *_ = _build(case)
+    L = g.lists()
+    assert np.array_equal(L["offsets"], o.list_offsets)
+    assert np.array_equal(L["ids"], o.list_ids)
+    assert np.array_equal(L["codes"], o.list_codes)
+    assert np.array_equal(L["res"], o.list_res)
+    assert np.array_equal(_bits(L["corr"]), _bits(o.list_corr))
+
+
+def _check_final(gd, gi, od, oi):
+    fin = np.isfinite(od)
+    assert np.array_equal(np.isfinite(gd), fin)
+    assert np.array_equal(gi[~fin], oi[~fin])
+    rel = np.abs(gd[fin].astype(np.float64) - od[fin]) / np.maximum(np.abs(od[fin]), 1e-30)
+    assert rel.max(initial=0.0) <= DIST_RTOL, rel.max()
+    tie = po.near_tie_mask(np.where(fin, od, np.float32(3e38)), TIE_RTOL)
+    mism = (gi != oi) & ~tie
+    assert not mism.any(), np.argwhere(mism)[:5]
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_search_parity(gpu, case):
+    g, o, base, q, k = _build(case)
+    gr = g.search_debug(q, k)
+    orr = o.search(q, k, debug=True)
+    assert np.array_equal(gr["probes"], orr["probes"])
+    assert np.array_equal(gr["topck_pos"], orr["topck_pos"])
+    assert np.array_equal(_bits(gr["topck_dist"]), _bits(orr["topck_dist"]))
+    _check_final(gr["dists"], gr["ids"], orr["dists"], orr["ids"])
+    # the plain API returns the same rows as the debug path
+    d2, i2 = g.search(q, k)
+    assert np.array_equal(i2, gr["ids"])
+    assert np.array_equal(_bits(d2), _bits(gr["dists"]))
+
+
+@pytest.mark.parametrize("case", CASES[:2], ids=IDS[:2])
+def test_search_device_matches_host(gpu, case):
+    import torch
+    g, o, base, q, k = _build(case)
+    d1, i1 = g.search(q, k)
+    qt = torch.from_numpy(q).to(gpu)
+    od = torch.empty((q.shape[0], k), dtype=torch.float32, device=gpu)
+    oi = torch.empty((q.shape[0], k), dtype=torch.int32, device=gpu)
+    g.search_device(qt, k, od, oi, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(oi.cpu().numpy(), i1)
+    assert np.array_equal(_bits(od.cpu().numpy()), _bits(d1))
+
+
+def test_k_larger_than_candidates(gpu):
+    """Unfilled slots are (+inf, -1) like v14/search.cu:284-286."""
+    g, o, base, q, _ = _build(CASES[3])
+    k = 64
+    gd, gi = g.search(q, k)
+    od, oi = o.search(q, k)
+    _check_final(gd, gi, od, oi)
+
+
+def test_nprobe_sweep_matches_oracle(gpu):
+    g, o, base, q, k = _build(CASES[0])
+    for nprobe in (1, 7, 16, 40):
+        g.set_nprobe(nprobe)
+        o.nprobe = min(nprobe, o.nlist)
+        gr = g.search_debug(q, k)
+        orr = o.search(q, k, debug=True)
+        assert np.array_equal(gr["probes"], orr["probes"])
+        assert np.array_equal(gr["topck_pos"], orr["topck_pos"])
+        _check_final(gr["dists"], gr["ids"], orr["dists"], orr["ids"])
+    g.set_nprobe(CASES[0][6])
+    o.nprobe = CASES[0][6]
+
+
+def test_call_order_errors(gpu):
+    p = jg.Params(M=8, nlist=4, nprobe=2)
+    g = jg.JHQGpuIndex(16, p)
+    x = np.random.default_rng(1).standard_normal((100, 16)).astype(np.float32)
+    with pytest.raises(RuntimeError, match="train"):
+        g.add(x)
+    with pytest.raises(RuntimeError, match="empty"):
+        g.search(x[:2], 3)
+    with pytest.raises(ValueError, match="nlist"):
+        g.train(x[:3])
+    g.train(x)
+    g.add(x)
+    with pytest.raises(RuntimeError, match="one add"):
+        g.add(x)
+    with pytest.raises(ValueError):
+        g.search(x[:2], 0)
+    d, i = g.search(x[:0], 3)
+    assert d.shape == (0, 3)
