@@ -27,7 +27,8 @@ _LIB_PATH = os.path.join(_HERE, "libjhq_amd.so")
 _lib = None
 
 JHQ_OK, JHQ_EINVAL, JHQ_ESTATE, JHQ_EDEVICE, JHQ_ENOMEM = 0, 1, 2, 3, 4
-STEP_NAMES = ("rotate", "centroid_scores", "select_probes", "scan_topck", "refine_topk")
+STEP_NAMES = ("rotate", "centroid_scores", "select_probes", "byte_lut", "scan_topck",
+              "refine_topk")
 
 
 class JHQError(RuntimeError):
@@ -85,6 +86,7 @@ _SIGS = {
     "jhq_ntotal": (_I64, [_VP]),
     "jhq_dim": (_I, [_VP]),
     "jhq_set_nprobe": (_I, [_VP, _I]),
+    "jhq_set_alpha": (_I, [_VP, ctypes.c_float]),
     "jhq_last_error": (ctypes.c_char_p, []),
     "jhq_get_dims": (_I, [_VP] + [ctypes.POINTER(_I)] * 5),
     "jhq_get_codebooks": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP]),
@@ -207,6 +209,10 @@ class JHQGpuIndex:
         _check(lib().jhq_set_nprobe(self._h, int(nprobe)))
         self._p.nprobe = min(int(nprobe), self._p.nlist)
 
+    def set_alpha(self, alpha):
+        _check(lib().jhq_set_alpha(self._h, float(alpha)))
+        self._p.alpha = float(alpha)
+
     def search_device(self, q, k, out_dists, out_ids, stream=None):
         """q, out_dists, out_ids: torch device tensors (or int addresses)."""
         nq = int(q.shape[0])
@@ -240,10 +246,15 @@ class JHQGpuIndex:
         return dict(sigma=float(sigma[0]), c1d=c1d, res_c1d=rc, P=P, centroids=cent,
                     cent_norms=norms)
 
-    def lists(self):
+    def lists(self, include_payload=True):
+        """List storage in stored-position order; offsets only when
+        include_payload is False."""
         dm = self.dims()
         n = self.ntotal
         off = np.empty(self._p.nlist + 1, np.int32)
+        if not include_payload:
+            _check(lib().jhq_get_lists(self._h, _ptr(off), None, None, None, None))
+            return dict(offsets=off)
         ids = np.empty(n, np.int32)
         codes = np.empty((n, self._p.M), np.uint8)
         res = np.empty((n, dm["bpv"]), np.uint8)

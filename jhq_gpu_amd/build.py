@@ -22,7 +22,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]
-CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off"]
+CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-pthread"]
 
 
 def _run(cmd):
@@ -57,7 +57,7 @@ def build_engine(verbose=False):
     if failed:
         raise RuntimeError("HIP engine compilation failed")
     tmp = LIB + ".tmp"
-    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp,
+    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-pthread", "-o", tmp,
           os.path.join(BUILD, "kernels.o"), os.path.join(BUILD, "jhq_capi.o"),
           os.path.join(BUILD, "host_train.o")])
     os.replace(tmp, LIB)

@@ -6,6 +6,7 @@
 #include <cstring>
 #include <limits>
 #include <random>
+#include <thread>
 
 namespace jhq {
 
@@ -117,14 +118,42 @@ std::vector<float> train_1d_kmeans(const float* vals, int64_t n, int Kr, int max
     std::vector<float> c(quant);
     std::vector<double> sum(Kr);
     std::vector<int64_t> cnt(Kr);
+    // Assignment is a pure function of (value, codewords): computed in
+    // parallel.  The per-cluster double sums stay one sequential pass in index
+    // order, so every rounding matches the reference loop.
+    std::vector<uint8_t> a8(Kr <= 256 ? static_cast<size_t>(n) : 0);
+    std::vector<int32_t> a32(Kr <= 256 ? 0 : static_cast<size_t>(n));
+    unsigned nth = std::thread::hardware_concurrency();
+    nth = std::max(1u, std::min(nth, 16u));
+    if (n < (int64_t)1 << 16) nth = 1;
     for (int iter = 0; iter < max_iter; iter++) {
         std::fill(sum.begin(), sum.end(), 0.0);
         std::fill(cnt.begin(), cnt.end(), 0);
-        for (int64_t i = 0; i < n; i++) {
-            const float v = vals[i];
-            const int lo = nearest_sorted(c.data(), Kr, v);
-            sum[lo] += v;
-            cnt[lo]++;
+        auto work = [&](int64_t i0, int64_t i1) {
+            for (int64_t i = i0; i < i1; i++) {
+                const int lo = nearest_sorted(c.data(), Kr, vals[i]);
+                if (Kr <= 256) a8[i] = static_cast<uint8_t>(lo);
+                else a32[i] = lo;
+            }
+        };
+        if (nth == 1) {
+            work(0, n);
+        } else {
+            std::vector<std::thread> th;
+            for (unsigned t = 0; t < nth; t++)
+                th.emplace_back(work, n * t / nth, n * (t + 1) / nth);
+            for (auto& t : th) t.join();
+        }
+        if (Kr <= 256) {
+            for (int64_t i = 0; i < n; i++) {
+                sum[a8[i]] += vals[i];
+                cnt[a8[i]]++;
+            }
+        } else {
+            for (int64_t i = 0; i < n; i++) {
+                sum[a32[i]] += vals[i];
+                cnt[a32[i]]++;
+            }
         }
         bool changed = false;
         for (int i = 0; i < Kr; i++) {

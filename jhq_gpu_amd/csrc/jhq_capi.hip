@@ -75,7 +75,7 @@ struct DBuf {
     }
 };
 
-constexpr int kSteps = 5;
+constexpr int kSteps = 6;
 
 }  // namespace
 
@@ -103,8 +103,8 @@ struct jhq_index {
     DBuf<float> dcorr;
 
     // search workspace (v14/search.cuh:24-46)
-    DBuf<float> wq, wqrot, wscores, wout_d;
-    DBuf<int32_t> wprobes, wgofs, wout_i;
+    DBuf<float> wq, wqrot, wscores, wlut, wout_d;
+    DBuf<int32_t> wprobes, wgofs, wqtot, wout_i;
     DBuf<unsigned long long> wpartial, wtopck;
     float* h_q = nullptr;  // pinned staging
     float* h_d = nullptr;
@@ -234,14 +234,16 @@ int train_ivf(jhq_index* ix, const float* h_y, const float* d_y, int64_t n) {
     return upload_centroids(ix);
 }
 
-int ensure_workspace(jhq_index* ix, int ck, int k, int P, int S) {
+int ensure_workspace(jhq_index* ix, int ck, int k, int P, int max_chunks) {
     const size_t B = static_cast<size_t>(ix->batch_size);
     JHQ_TRY(ix->wq.ensure(B * ix->d));
     JHQ_TRY(ix->wqrot.ensure(B * ix->d));
     JHQ_TRY(ix->wscores.ensure(B * ix->nlist));
+    JHQ_TRY(ix->wlut.ensure(B * ix->M * 256));
     JHQ_TRY(ix->wprobes.ensure(B * P));
     JHQ_TRY(ix->wgofs.ensure(B * (P + 1)));
-    JHQ_TRY(ix->wpartial.ensure(B * S * ck));
+    JHQ_TRY(ix->wqtot.ensure(B));
+    JHQ_TRY(ix->wpartial.ensure(static_cast<size_t>(max_chunks) * ck));
     JHQ_TRY(ix->wtopck.ensure(B * ck));
     JHQ_TRY(ix->wout_d.ensure(B * k));
     JHQ_TRY(ix->wout_i.ensure(B * k));
@@ -261,7 +263,7 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
                         &bp->sh))
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) +
                                     ": the byte LUT (M*1 KiB) does not fit in LDS");
-    return ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.S);
+    return ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.max_chunks);
 }
 
 // One batch of Bq queries at d_q (device) through the whole pipeline
@@ -276,20 +278,22 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
                                ix->wscores.p, ix->nlist, true, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dlist_padoff.p,
-                               ix->wprobes.p, ix->wgofs.p, s));
+                               ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
-    JHQ_HIP(jhq::scan_topck(ix->wqrot.p, Bq, d, ix->M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p,
-                            ix->wprobes.p, ix->wgofs.p, bp.P, ix->dlist_off.p,
-                            ix->dlist_padoff.p, ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p,
-                            s));
+    JHQ_HIP(jhq::build_lut(ix->wqrot.p, Bq, d, ix->M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p,
+                           ix->wlut.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[4], s));
-    JHQ_HIP(jhq::refine_topk(ix->wpartial.p, Bq, bp.sh.S, bp.ck, k, ix->wqrot.p, d,
+    JHQ_HIP(jhq::scan_topck(ix->wlut.p, Bq, ix->M, ix->wprobes.p, ix->wgofs.p, ix->wqtot.p,
+                            bp.P, ix->dlist_off.p, ix->dlist_padoff.p, ix->dcodes_t.p, bp.ck,
+                            bp.sh, ix->wpartial.p, s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[5], s));
+    JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k, ix->wqrot.p, d,
                              ix->dres_c1d.p, ix->Kr, ix->Br, ix->bpv, ix->dres.p, ix->dcorr.p,
                              ix->dlist_ids.p, d_out, d_ids, want_topck ? ix->wtopck.p : nullptr,
                              s));
     if (ix->timing) {
-        JHQ_HIP(hipEventRecord(ix->ev[5], s));
-        JHQ_HIP(hipEventSynchronize(ix->ev[5]));
+        JHQ_HIP(hipEventRecord(ix->ev[6], s));
+        JHQ_HIP(hipEventSynchronize(ix->ev[6]));
         for (int i = 0; i < kSteps; i++) {
             float ms = 0.f;
             JHQ_HIP(hipEventElapsedTime(&ms, ix->ev[i], ix->ev[i + 1]));
@@ -440,6 +444,13 @@ int jhq_set_nprobe(jhq_index* idx, int nprobe) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (nprobe <= 0) return fail(JHQ_EINVAL, "nprobe must be positive");
     idx->nprobe = std::min(nprobe, idx->nlist);
+    return JHQ_OK;
+}
+
+int jhq_set_alpha(jhq_index* idx, float alpha) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (!(alpha > 0.0f)) return fail(JHQ_EINVAL, "alpha must be positive");
+    idx->alpha = alpha;
     return JHQ_OK;
 }
 

@@ -47,34 +47,39 @@ hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n,
                          float* corr_out, hipStream_t s);
 
 // Per query: top-P lists by (score, list) from scores[b][nlist]; writes
-// probes[b][P] (ascending) and gofs[b][P+1] (prefix of padded group counts).
+// probes[b][P] (ascending), gofs[b][P+1] (prefix of padded group counts) and
+// qtot[b] (= gofs[b][P]).
 hipError_t select_probes(const float* scores, int B, int nlist, int P,
-                         const int32_t* list_padoff, int32_t* probes,
-                         int32_t* gofs, hipStream_t s);
+                         const int32_t* list_padoff, int32_t* probes, int32_t* gofs,
+                         int32_t* qtot, hipStream_t s);
 
 struct ScanShape {
-    int S;      // workgroups per query
-    int cap;    // candidate slots per workgroup (multiple of kGroup)
-    int lds;    // dynamic LDS bytes
+    int G;           // persistent scan workgroups
+    int cap;         // candidate slots per chunk (multiple of kGroup)
+    int lds;         // dynamic LDS bytes of the scan kernel
+    int max_chunks;  // upper bound on chunks per batch (partial buffer rows)
 };
-// LDS plan of the scan kernel; returns false if M does not fit.
+// LDS plan of the scan kernel; returns false if the byte LUT does not fit.
 bool scan_plan(int M, int d, int P, int ck, int max_groups_per_query, int B, int target_wg,
                ScanShape* out);
 
-// IVF ADC scan + exact per-workgroup top-ck; partial[b][s][ck] keys
-// (ord(dist) << 32 | pos), unfilled = ~0.
-hipError_t scan_topck(const float* q_rot, int B, int d, int M, int Ds, int K1D, int bpd,
-                      const float* c1d, const int32_t* probes, const int32_t* gofs, int P,
-                      const int32_t* list_off, const int32_t* list_padoff,
-                      const uint8_t* codes_t, int ck, const ScanShape& sh,
-                      unsigned long long* partial, hipStream_t s);
+// Byte LUT lut[b][m][256] for a query batch (v14/search.cu:65-91).
+hipError_t build_lut(const float* q_rot, int B, int d, int M, int Ds, int K1D, int bpd,
+                     const float* c1d, float* lut, hipStream_t s);
 
-// Per query: merge S partial top-ck lists, residual refine, final top-k.
+// IVF ADC scan + exact per-chunk top-ck; partial[chunk][ck] keys
+// (ord(dist) << 32 | pos), unfilled = ~0.
+hipError_t scan_topck(const float* glut, int B, int M, const int32_t* probes, const int32_t* gofs,
+                      const int32_t* qtot, int P, const int32_t* list_off,
+                      const int32_t* list_padoff, const uint8_t* codes_t, int ck,
+                      const ScanShape& sh, unsigned long long* partial, hipStream_t s);
+
+// Per query: merge its chunk lists, residual refine, final top-k.
 // If topck_dbg != nullptr it receives the merged short list [B][ck] keys.
-hipError_t refine_topk(const unsigned long long* partial, int B, int S, int ck, int k,
-                       const float* q_rot, int d, const float* res_c1d, int Kr, int Br,
-                       int bpv, const uint8_t* list_res, const float* list_corr,
-                       const int32_t* list_ids, float* out_d, int32_t* out_i,
-                       unsigned long long* topck_dbg, hipStream_t s);
+hipError_t refine_topk(const unsigned long long* partial, const int32_t* qtot, int B,
+                       const ScanShape& sh, int ck, int k, const float* q_rot, int d,
+                       const float* res_c1d, int Kr, int Br, int bpv, const uint8_t* list_res,
+                       const float* list_corr, const int32_t* list_ids, float* out_d,
+                       int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s);
 
 }  // namespace jhq

@@ -28,6 +28,10 @@ CASES = [
     ("b4_ds4_k1d2", 48, 12, 4, 4, 8, 8, 3.0, 1200, 20, 7, 8),
     ("flat_nlist1", 64, 16, 8, 4, 1, 1, 4.0, 2500, 25, 10, 1),
     ("d1024_m128", 1024, 128, 8, 4, 32, 6, 4.0, 2000, 20, 10, 64),
+    # one query per batch split into ~250 chunks: multi-round streaming merge
+    ("flat_many_chunks", 32, 8, 8, 4, 1, 1, 4.0, 20000, 6, 10, 1),
+    # k=100 with alpha=4: ck=400 short list
+    ("k100_ck400", 64, 16, 8, 4, 8, 4, 4.0, 6000, 12, 100, 16),
 ]
 IDS = [c[0] for c in CASES]
 
@@ -128,6 +132,19 @@ def test_k_larger_than_candidates(gpu):
     gd, gi = g.search(q, k)
     od, oi = o.search(q, k)
     _check_final(gd, gi, od, oi)
+
+
+def test_alpha_sweep_matches_oracle(gpu):
+    g, o, base, q, k = _build(CASES[0])
+    for alpha in (1.0, 2.5, 10.0):
+        g.set_alpha(alpha)
+        o.alpha = np.float32(alpha)
+        gr = g.search_debug(q, k)
+        orr = o.search(q, k, debug=True)
+        assert np.array_equal(gr["topck_pos"], orr["topck_pos"])
+        _check_final(gr["dists"], gr["ids"], orr["dists"], orr["ids"])
+    g.set_alpha(CASES[0][7])
+    o.alpha = np.float32(CASES[0][7])
 
 
 def test_nprobe_sweep_matches_oracle(gpu):
