@@ -49,6 +49,10 @@ def parse():
                     help="short-list factors swept (ck = max(k, ceil(alpha*k)))")
     ap.add_argument("--scale", type=float, default=1.0, help="fraction of N (debug only)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--profile-batches", type=int, default=0,
+                    help="profiling mode: build the index, run this many search batches at the "
+                         "first --nprobe/--alpha plus one 256 MiB device copy (the counter "
+                         "calibration kernel), print per-step times and exit")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0x4A48510002)
     return ap.parse_args()
@@ -121,10 +125,12 @@ def main():
     hb = base.cpu().numpy()
     hq = q.cpu().numpy()
 
-    t0 = time.time()
-    gt = ground_truth(torch, base, q, K)
-    torch.cuda.synchronize()
-    log(f"ground truth {time.time() - t0:.1f}s")
+    gt = None
+    if args.profile_batches <= 0:
+        t0 = time.time()
+        gt = ground_truth(torch, base, q, K)
+        torch.cuda.synchronize()
+        log(f"ground truth {time.time() - t0:.1f}s")
 
     p = jg.Params(M=M, B=B, Br=Br, alpha=alphas[0], nlist=NLIST, nprobe=nprobes[0],
                   ivf_iters=8, batch_size=BATCH, seed=42)
@@ -142,6 +148,10 @@ def main():
     log(f"add {t_add:.1f}s")
     del base
     torch.cuda.empty_cache()
+
+    if args.profile_batches > 0:
+        profile_mode(torch, dev, ix, q, K, BATCH, nprobes[0], alphas[0], args.profile_batches)
+        return
 
     out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
@@ -259,6 +269,42 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def profile_mode(torch, dev, ix, q, k, batch, nprobe, alpha, nbatches):
+    """A short, fixed workload for rocprofv3 counter runs: `nbatches` search
+    batches over distinct queries, then one plain device-to-device copy of
+    256 MiB whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters."""
+    ix.set_nprobe(nprobe)
+    ix.set_alpha(alpha)
+    out_d = torch.empty((batch, k), dtype=torch.float32, device=dev)
+    out_i = torch.empty((batch, k), dtype=torch.int32, device=dev)
+    nq = q.shape[0]
+    ix.set_timing(True)
+    for s in range(nbatches):
+        q0 = (s * batch) % max(1, nq - batch + 1)
+        ix.search_device(q[q0:q0 + batch], k, out_d, out_i)
+    torch.cuda.synchronize()
+    tm, nb = ix.timing()
+    ix.set_timing(False)
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    # algorithmic scan bytes of the profiled batches
+    L = ix.lists(include_payload=False)
+    sizes = np.diff(L["offsets"]).astype(np.int64)
+    qs = [q[(s * batch) % max(1, nq - batch + 1):][:batch] for s in range(nbatches)]
+    tot = 0
+    for qq in qs:
+        dbg = ix.search_debug(qq.cpu().numpy(), k)
+        tot += int(sizes[dbg["probes"]].sum()) * ix.params.M
+    print(json.dumps({"profile_batches": nbatches, "nprobe": nprobe, "alpha": alpha,
+                      "scan_bytes_per_launch": tot / nbatches,
+                      "step_us_per_batch": {k2: round(v * 1000.0 / nb, 2) for k2, v in tm.items()},
+                      "copy_bytes": 256 << 20}), flush=True)
 
 
 def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds):

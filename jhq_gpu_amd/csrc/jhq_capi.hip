@@ -75,7 +75,7 @@ struct DBuf {
     }
 };
 
-constexpr int kSteps = 6;
+constexpr int kSteps = 5;
 
 }  // namespace
 
@@ -94,7 +94,6 @@ struct jhq_index {
     std::vector<float> P_rm;   // row-major Pi(j,k)
     std::vector<float> c1d, res_c1d, cent, cent_norms;
     std::vector<int32_t> list_off_h, list_padoff_h;
-    std::vector<int64_t> top_groups_prefix;  // prefix sums of list group counts, descending
 
     hipStream_t stream = nullptr;
     DBuf<float> dP, dc1d, dres_c1d, dcent, dnorms;
@@ -103,7 +102,7 @@ struct jhq_index {
     DBuf<float> dcorr;
 
     // search workspace (v14/search.cuh:24-46)
-    DBuf<float> wq, wqrot, wscores, wlut, wout_d;
+    DBuf<float> wq, wqrot, wscores, wout_d;
     DBuf<int32_t> wprobes, wgofs, wqtot, wout_i;
     DBuf<unsigned long long> wpartial, wtopck;
     float* h_q = nullptr;  // pinned staging
@@ -234,16 +233,15 @@ int train_ivf(jhq_index* ix, const float* h_y, const float* d_y, int64_t n) {
     return upload_centroids(ix);
 }
 
-int ensure_workspace(jhq_index* ix, int ck, int k, int P, int max_chunks) {
+int ensure_workspace(jhq_index* ix, int ck, int k, int P, int max_segments) {
     const size_t B = static_cast<size_t>(ix->batch_size);
     JHQ_TRY(ix->wq.ensure(B * ix->d));
     JHQ_TRY(ix->wqrot.ensure(B * ix->d));
     JHQ_TRY(ix->wscores.ensure(B * ix->nlist));
-    JHQ_TRY(ix->wlut.ensure(B * ix->M * 256));
     JHQ_TRY(ix->wprobes.ensure(B * P));
     JHQ_TRY(ix->wgofs.ensure(B * (P + 1)));
     JHQ_TRY(ix->wqtot.ensure(B));
-    JHQ_TRY(ix->wpartial.ensure(static_cast<size_t>(max_chunks) * ck));
+    JHQ_TRY(ix->wpartial.ensure(static_cast<size_t>(max_segments) * ck));
     JHQ_TRY(ix->wtopck.ensure(B * ck));
     JHQ_TRY(ix->wout_d.ensure(B * k));
     JHQ_TRY(ix->wout_i.ensure(B * k));
@@ -258,12 +256,11 @@ struct BatchPlan {
 int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
-    const int64_t maxg = ix->top_groups_prefix[bp->P];
-    if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, static_cast<int>(maxg), Bq, ix->num_cu,
-                        &bp->sh))
-        return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) +
-                                    ": the byte LUT (M*1 KiB) does not fit in LDS");
-    return ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.max_chunks);
+    if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh))
+        return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
+                                    ", batch=" + std::to_string(Bq) +
+                                    ": the byte LUT and selection buffers do not fit in LDS");
+    return ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.max_segments);
 }
 
 // One batch of Bq queries at d_q (device) through the whole pipeline
@@ -280,20 +277,17 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
     JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dlist_padoff.p,
                                ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
-    JHQ_HIP(jhq::build_lut(ix->wqrot.p, Bq, d, ix->M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p,
-                           ix->wlut.p, s));
+    JHQ_HIP(jhq::scan_topck(ix->wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
+                            ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dlist_off.p,
+                            ix->dlist_padoff.p, ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[4], s));
-    JHQ_HIP(jhq::scan_topck(ix->wlut.p, Bq, ix->M, ix->wprobes.p, ix->wgofs.p, ix->wqtot.p,
-                            bp.P, ix->dlist_off.p, ix->dlist_padoff.p, ix->dcodes_t.p, bp.ck,
-                            bp.sh, ix->wpartial.p, s));
-    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[5], s));
     JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k, ix->wqrot.p, d,
                              ix->dres_c1d.p, ix->Kr, ix->Br, ix->bpv, ix->dres.p, ix->dcorr.p,
                              ix->dlist_ids.p, d_out, d_ids, want_topck ? ix->wtopck.p : nullptr,
                              s));
     if (ix->timing) {
-        JHQ_HIP(hipEventRecord(ix->ev[6], s));
-        JHQ_HIP(hipEventSynchronize(ix->ev[6]));
+        JHQ_HIP(hipEventRecord(ix->ev[kSteps], s));
+        JHQ_HIP(hipEventSynchronize(ix->ev[kSteps]));
         for (int i = 0; i < kSteps; i++) {
             float ms = 0.f;
             JHQ_HIP(hipEventElapsedTime(&ms, ix->ev[i], ix->ev[i + 1]));
@@ -569,11 +563,9 @@ int jhq_add(jhq_index* ix, const float* x, int64_t n) {
         if (a < 0 || a >= nlist) return fail(JHQ_EDEVICE, "invalid IVF assignment");
         off[a + 1]++;
     }
-    std::vector<int64_t> groups(nlist);
     for (int c = 0; c < nlist; c++) {
         const int cnt = off[c + 1];
         const int npad = (cnt + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
-        groups[c] = npad / jhq::kGroup;
         off[c + 1] = off[c] + cnt;
         padoff[c + 1] = padoff[c] + npad;
     }
@@ -603,9 +595,6 @@ int jhq_add(jhq_index* ix, const float* x, int64_t n) {
     JHQ_HIP(hipStreamSynchronize(s));
     ix->list_off_h = off;
     ix->list_padoff_h = padoff;
-    std::sort(groups.begin(), groups.end(), [](int64_t a, int64_t b) { return a > b; });
-    ix->top_groups_prefix.assign(nlist + 1, 0);
-    for (int c = 0; c < nlist; c++) ix->top_groups_prefix[c + 1] = ix->top_groups_prefix[c] + groups[c];
     ix->ntotal = n;
     ix->added = true;
     return JHQ_OK;

@@ -46,35 +46,32 @@ hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n,
                          int32_t* ids_out, uint8_t* codes_t, uint8_t* res_out,
                          float* corr_out, hipStream_t s);
 
-// Per query: top-P lists by (score, list) from scores[b][nlist]; writes
-// probes[b][P] (ascending), gofs[b][P+1] (prefix of padded group counts) and
-// qtot[b] (= gofs[b][P]).
+// Per query: exact top-P lists by (score, list) from scores[b][nlist];
+// writes probes[b][P] (ascending), gofs[b][P+1] (prefix of padded group
+// counts) and qtot[b] (= gofs[b][P]).
 hipError_t select_probes(const float* scores, int B, int nlist, int P,
                          const int32_t* list_padoff, int32_t* probes, int32_t* gofs,
                          int32_t* qtot, hipStream_t s);
 
 struct ScanShape {
-    int G;           // persistent scan workgroups
-    int cap;         // candidate slots per chunk (multiple of kGroup)
-    int lds;         // dynamic LDS bytes of the scan kernel
-    int max_chunks;  // upper bound on chunks per batch (partial buffer rows)
+    int G;             // persistent scan workgroups
+    int lds;           // dynamic LDS bytes of the scan kernel
+    int max_segments;  // upper bound on top-ck lists per batch (partial rows)
 };
-// LDS plan of the scan kernel; returns false if the byte LUT does not fit.
-bool scan_plan(int M, int d, int P, int ck, int max_groups_per_query, int B, int target_wg,
-               ScanShape* out);
+// LDS plan of the scan kernel; returns false if the byte LUT and the
+// selection buffers do not fit.
+bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out);
 
-// Byte LUT lut[b][m][256] for a query batch (v14/search.cu:65-91).
-hipError_t build_lut(const float* q_rot, int B, int d, int M, int Ds, int K1D, int bpd,
-                     const float* c1d, float* lut, hipStream_t s);
-
-// IVF ADC scan + exact per-chunk top-ck; partial[chunk][ck] keys
+// IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from
+// q_rot (v14/search.cu:65-195); partial[segment][ck] keys
 // (ord(dist) << 32 | pos), unfilled = ~0.
-hipError_t scan_topck(const float* glut, int B, int M, const int32_t* probes, const int32_t* gofs,
+hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d,
+                      int B, int M, const int32_t* probes, const int32_t* gofs,
                       const int32_t* qtot, int P, const int32_t* list_off,
                       const int32_t* list_padoff, const uint8_t* codes_t, int ck,
                       const ScanShape& sh, unsigned long long* partial, hipStream_t s);
 
-// Per query: merge its chunk lists, residual refine, final top-k.
+// Per query: merge its segment lists, residual refine, final top-k.
 // If topck_dbg != nullptr it receives the merged short list [B][ck] keys.
 hipError_t refine_topk(const unsigned long long* partial, const int32_t* qtot, int B,
                        const ScanShape& sh, int ck, int k, const float* q_rot, int d,

@@ -117,7 +117,7 @@ __device__ __forceinline__ void wave_hist_add(uint32_t* hist, int bin) {
 // value, so the window narrows 256x per pass whatever the bit patterns.  Returns the rule: v selected iff v < lo, or
 // lo <= v < lo+len and (done, or v wins the tie-break among equal values).
 template <int NT, class GetV>
-__device__ SelResult sel_threshold(GetV getv, int n, uint32_t k, SelState* st) {
+__device__ __forceinline__ SelResult sel_threshold(GetV getv, int n, uint32_t k, SelState* st) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid == 0) { st->vmin = ~0u; st->vmax = 0u; }
     __syncthreads();
@@ -207,7 +207,7 @@ __device__ SelResult sel_threshold(GetV getv, int n, uint32_t k, SelState* st) {
 // Ballot compaction of pred(i) over i < n into out[], counter st->cnt
 // (zeroed here).  Returns the count.
 template <int NT, class Pred>
-__device__ int sel_compact(Pred pred, int n, int* out, int cap, SelState* st) {
+__device__ __forceinline__ int sel_compact(Pred pred, int n, int* out, int cap, SelState* st) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid == 0) st->cnt = 0;
     __syncthreads();
@@ -232,7 +232,7 @@ __device__ int sel_compact(Pred pred, int n, int* out, int cap, SelState* st) {
 // elements whose value is not ~0u.  gett is evaluated only for elements tied
 // at the threshold value and for the k selected elements.
 template <int NT, class GetV, class GetT>
-__device__ int block_topk(GetV getv, GetT gett, int n, int k, int* idx, unsigned long long* tmp,
+__device__ __forceinline__ int block_topk(GetV getv, GetT gett, int n, int k, int* idx, unsigned long long* tmp,
                           unsigned long long* keys, SelState* st,
                           unsigned long long* sub = nullptr) {
 #ifdef JHQ_PHASE_TIMING
@@ -728,128 +728,335 @@ hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n, 
     return hipGetLastError();
 }
 
+
 // ---------------------------------------------------------------------------
-// Probe selection: exact top-P of (score, list) per query, read straight
-// from the score rows (no nlist-sized LDS array, so any nlist works).
+// Streaming exact top-k.
+//
+// The candidates of one selection arrive in rounds: in each round every
+// thread of the workgroup supplies up to 4 (value, tag) pairs (value ~0u =
+// no candidate).  The exact top-k by (value, tag) ascending is kept as a short
+// list of survivors in LDS:
+//   - bound: in the first round a bound is derived from the round itself.
+//     Each wave finds the c-th smallest of its values (c = ceil(k / waves))
+//     by c rounds of wave-min; the largest of these is >= at least k values,
+//     so no candidate above it can be in the top k.  Later the bound is the
+//     k-th smallest survivor after each prune.
+//   - survivors (value <= bound) are appended with one ballot per wave;
+//   - when the survivor list passes half its capacity it is pruned to the
+//     exact top-k (rank selection for short lists, radix selection else);
+//   - if a round overflows the list, the round's values (kept in rbuf) and
+//     the survivors from before the round are selected together.
+// Every step is exact: a candidate is dropped only when k kept candidates
+// precede it in (value, tag) order.
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ void rank_select(const unsigned long long* in, int n, int k,
+                                            unsigned long long* out) {
+    // Key i's rank = number of keys smaller than it; keys are distinct except
+    // for the ~0 padding, which ranks after every key that is written
+    // (k <= number of real keys).  tpk lanes share one key, each counting over
+    // a contiguous slice of the keys, then add their counts with xor shuffles.
+    int tpk = 1;
+    while (tpk < 64 && tpk * 2 * n <= NT) tpk *= 2;
+    const int part = threadIdx.x & (tpk - 1);
+    const int j0 = (int)((int64_t)n * part / tpk), j1 = (int)((int64_t)n * (part + 1) / tpk);
+    for (int base = 0; base < n; base += NT / tpk) {
+        const int i = base + (int)threadIdx.x / tpk;
+        const unsigned long long ki = i < n ? in[i] : ~0ull;
+        int r = 0;
+#pragma unroll 8
+        for (int j = j0; j < j1; j++) r += (in[j] < ki) ? 1 : 0;
+        for (int off = tpk >> 1; off > 0; off >>= 1) r += __shfl_xor(r, off);
+        if (part == 0 && i < n && r < k) out[r] = ki;
+    }
+    __syncthreads();
+}
+
+// Exact top-k of n keys in LDS (n >= k, the first k are real) into out[0..k).
+template <int NT>
+__device__ __forceinline__ void select_keys(const unsigned long long* in, int n, int k, unsigned long long* out,
+                            int* idx, unsigned long long* tmp, SelState* st) {
+    if ((int64_t)n * n <= (int64_t)NT * 512) {
+        rank_select<NT>(in, n, k, out);
+    } else {
+        block_topk<NT>([&](int i) { return (uint32_t)(in[i] >> 32); },
+                       [&](int i) { return (uint32_t)(in[i] & 0xffffffffull); }, n, k, idx, tmp,
+                       out, st);
+    }
+}
+
+// Values each wave contributes to the first-round bound.
+__host__ __device__ constexpr int est_per_wave(int k, int nw) {
+    return ((k + nw - 1) / nw) * 2 < ((k + nw - 1) / nw) + 8 ? ((k + nw - 1) / nw) * 2
+                                                               : ((k + nw - 1) / nw) + 8;
+}
+
+struct StreamSel {
+    uint32_t* rbuf;             // [NT*4] values of the current round
+    unsigned long long* skeys;  // [scap] survivors
+    unsigned long long* kout;   // [k]
+    unsigned long long* ktmp;   // [k]
+    int* kidx;                  // [k]
+    uint32_t* wstat;            // [NT/64 * est_per_wave(k)] per-wave smallest values
+    int* ctl;                   // [4]: survivor count, bound, bound valid, estimate
+    SelState* st;
+    int scap;
+};
+
+template <int NT>
+__device__ __forceinline__ void stream_begin(const StreamSel& S) {
+    if (threadIdx.x == 0) {
+        S.ctl[0] = 0;
+        S.ctl[1] = (int)~0u;
+        S.ctl[2] = 0;
+    }
+}
+
+// One round.  o[j] / tg[j]: this thread's values and tags; tag_of(s) returns
+// the tag of round slot s (= thread*4 + j) for the overflow path.
+template <int NT, class TagOf>
+__device__ __forceinline__ void stream_round(const StreamSel& S, int k, const uint32_t (&o)[4],
+                             const uint32_t (&tg)[4], TagOf tag_of,
+                             unsigned long long* stats = nullptr) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int sn_before = S.ctl[0];
+    const uint32_t Tcur = (uint32_t)S.ctl[1];
+    const bool est = S.ctl[2] == 0;
+    *(uint4*)(S.rbuf + tid * 4) = make_uint4(o[0], o[1], o[2], o[3]);
+    if (est) {
+        // each wave contributes its c smallest values; the bound is the k-th
+        // smallest of the pooled values (>= k values are <= it)
+        const int c = est_per_wave(k, NW);
+        uint32_t t0 = o[0], t1 = o[1], t2 = o[2], t3 = o[3];
+        for (int it = 0; it < c; it++) {
+            const uint32_t lm = min(min(t0, t1), min(t2, t3));
+            uint32_t m = lm;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) m = min(m, (uint32_t)__shfl_xor((int)m, off));
+            if (lane == 0) S.wstat[wv * c + it] = m;
+            if (m == ~0u) continue;
+            const unsigned long long bal = __ballot(lm == m);
+            if (lane == __ffsll((long long)bal) - 1) {
+                if (t0 == m) t0 = ~0u;
+                else if (t1 == m) t1 = ~0u;
+                else if (t2 == m) t2 = ~0u;
+                else t3 = ~0u;
+            }
+        }
+        if (tid == 0) S.ctl[3] = (int)~0u;
+    }
+    __syncthreads();
+    uint32_t T = Tcur;
+    if (est) {
+        const int c = est_per_wave(k, NW);
+        const int npool = NW * c;
+        for (int i = tid; i < npool; i += NT) {
+            const uint32_t v = S.wstat[i];
+            if (v == ~0u) continue;
+            int lt = 0, le = 0;
+            for (int j = 0; j < npool; j++) {
+                const uint32_t u = S.wstat[j];
+                lt += (u < v) ? 1 : 0;
+                le += (u <= v) ? 1 : 0;
+            }
+            if (lt < k && k <= le) S.ctl[3] = (int)v;  // the k-th smallest (all writers agree)
+        }
+        __syncthreads();
+        T = min(T, (uint32_t)S.ctl[3]);
+    }
+    // append survivors: one atomic per wave
+    bool p[4];
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        p[j] = (o[j] != ~0u) && (o[j] <= T);
+        cnt += p[j] ? 1 : 0;
+    }
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+    }
+    int wbase = 0;
+    if (lane == 63 && incl) wbase = atomicAdd(&S.ctl[0], incl);
+    wbase = __shfl(wbase, 63);
+    int at = wbase + incl - cnt;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (p[j]) {
+            if (at < S.scap) S.skeys[at] = ((unsigned long long)o[j] << 32) | tg[j];
+            at++;
+        }
+    }
+    if (tid == 0 && est && T != ~0u) {
+        S.ctl[1] = (int)T;
+        S.ctl[2] = 1;
+    }
+    __syncthreads();
+    const int n_after = S.ctl[0];
+#ifdef JHQ_PHASE_TIMING
+    const unsigned long long st0 = wall_clock64();
+    if (stats && threadIdx.x == 0) {
+        stats[0] += (n_after > S.scap) ? 1 : 0;
+        stats[1] += (n_after <= S.scap && n_after > k && 2 * n_after >= S.scap) ? 1 : 0;
+        stats[2] += (unsigned long long)n_after;
+    }
+#endif
+    if (n_after > S.scap) {
+        // overflow: survivors from before this round plus this round's values
+        const int kk = min(k, n_after);
+        const int nb = sn_before;
+        block_topk<NT>(
+            [&](int i) -> uint32_t {
+                if (i < nb) return (uint32_t)(S.skeys[i] >> 32);
+                const uint32_t v = S.rbuf[i - nb];
+                return v <= T ? v : ~0u;
+            },
+            [&](int i) -> uint32_t {
+                if (i < nb) return (uint32_t)(S.skeys[i] & 0xffffffffull);
+                return tag_of(i - nb);
+            },
+            nb + NT * 4, kk, S.kidx, S.ktmp, S.kout, S.st);
+        for (int i = tid; i < kk; i += NT) S.skeys[i] = S.kout[i];
+        if (tid == 0) {
+            S.ctl[0] = kk;
+            if (kk == k) {
+                S.ctl[1] = (int)(uint32_t)(S.kout[kk - 1] >> 32);
+                S.ctl[2] = 1;
+            }
+        }
+        __syncthreads();
+    } else if (n_after > k && 2 * n_after >= S.scap) {
+        select_keys<NT>(S.skeys, n_after, k, S.kout, S.kidx, S.ktmp, S.st);
+        for (int i = tid; i < k; i += NT) S.skeys[i] = S.kout[i];
+        if (tid == 0) {
+            S.ctl[0] = k;
+            S.ctl[1] = (int)min((uint32_t)S.ctl[1], (uint32_t)(S.kout[k - 1] >> 32));
+            S.ctl[2] = 1;
+        }
+        __syncthreads();
+    }
+#ifdef JHQ_PHASE_TIMING
+    if (stats && threadIdx.x == 0) stats[3] += wall_clock64() - st0;
+#endif
+}
+
+// Finishes a selection: out = S.kout[0..kk) sorted ascending; returns kk.
+template <int NT>
+__device__ __forceinline__ int stream_end(const StreamSel& S, int k) {
+    const int n = S.ctl[0];
+    const int kk = min(k, n);
+    if (kk > 0) select_keys<NT>(S.skeys, n, kk, S.kout, S.kidx, S.ktmp, S.st);
+    return kk;
+}
+
+static int stream_scap(int k) { return 4 * k < 512 ? 512 : (4 * k + 63) / 64 * 64; }
+
+
+__host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+// LDS bytes of a StreamSel (rounded to 16 so that what follows stays aligned).
+static size_t stream_lds_bytes(int NT, int k) {
+    return align16((size_t)NT * 4 * 4 + (size_t)stream_scap(k) * 8 + (size_t)k * (8 + 8 + 4) +
+                   (size_t)(NT / 64) * est_per_wave(k, NT / 64) * 4 + 16 + sizeof(SelState));
+}
+
+// Carves a StreamSel out of LDS at p (16-byte aligned); returns the next
+// 16-byte aligned address.
+template <int NT>
+__device__ unsigned char* stream_carve(unsigned char* p, int k, StreamSel* S) {
+    S->scap = (4 * k < 512 ? 512 : (4 * k + 63) / 64 * 64);
+    S->rbuf = (uint32_t*)p;
+    S->skeys = (unsigned long long*)(S->rbuf + NT * 4);
+    S->kout = S->skeys + S->scap;
+    S->ktmp = S->kout + k;
+    S->kidx = (int*)(S->ktmp + k);
+    S->wstat = (uint32_t*)(S->kidx + k);
+    S->ctl = (int*)(S->wstat + (NT / 64) * est_per_wave(k, NT / 64));
+    S->st = (SelState*)(S->ctl + 4);
+    const size_t used = (size_t)((unsigned char*)(S->st + 1) - p);
+    return p + align16(used);
+}
+
+// ---------------------------------------------------------------------------
+// Probe selection: exact top-P of (score, list) per query, streamed from the
+// score row (no nlist-sized LDS array, so any nlist works).  One workgroup
+// per query; writes probes[b][P] ascending, gofs[b][P+1] (prefix of the
+// probed lists' padded group counts) and qtot[b] = gofs[b][P].
 // ---------------------------------------------------------------------------
 template <int NT>
 __global__ void __launch_bounds__(NT)
 select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                      const int32_t* __restrict__ list_padoff, int32_t* __restrict__ probes,
-                     int32_t* __restrict__ gofs, int32_t* __restrict__ qtot, bool in_lds) {
+                     int32_t* __restrict__ gofs, int32_t* __restrict__ qtot) {
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned long long* tmp = (unsigned long long*)smem;
-    unsigned long long* sk = tmp + P;
-    int* scratch = (int*)(sk + P);
-    SelState* st = (SelState*)(scratch + P);
-    uint32_t* keys = (uint32_t*)(st + 1);
-    const int b = blockIdx.x;
+    StreamSel S;
+    int* gcnt = (int*)stream_carve<NT>(smem, P, &S);
+    const int b = blockIdx.x, tid = threadIdx.x;
     const float* row = scores + (int64_t)b * nlist;
-    JHQ_PHASE_DECL
-    if (in_lds) {
-        for (int i = threadIdx.x; i < nlist; i += NT) keys[i] = f2ord(row[i]);
-        __syncthreads();
-        JHQ_PHASE(0);
-        block_topk<NT>([&](int i) { return keys[i]; }, [&](int i) { return (uint32_t)i; }, nlist,
-                       P, scratch, tmp, sk, st);
-    } else {
-        block_topk<NT>([&](int i) { return f2ord(row[i]); }, [&](int i) { return (uint32_t)i; },
-                       nlist, P, scratch, tmp, sk, st);
-    }
-    JHQ_PHASE(1);
-    for (int r = threadIdx.x; r < P; r += NT) probes[(int64_t)b * P + r] = (int)(uint32_t)sk[r];
-    // group counts of the probed lists, gathered in parallel into scratch[]
-    for (int r = threadIdx.x; r < P; r += NT) {
-        const int l = (int)(uint32_t)sk[r];
-        scratch[r] = (list_padoff[l + 1] - list_padoff[l]) / kGroup;
-    }
+    stream_begin<NT>(S);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        int32_t* g = gofs + (int64_t)b * (P + 1);
-        g[0] = 0;
-        for (int r = 0; r < P; r++) {
-            acc += scratch[r];
-            g[r + 1] = acc;
+    const int rounds = (nlist + NT * 4 - 1) / (NT * 4);
+    for (int r = 0; r < rounds; r++) {
+        const int i0 = r * NT * 4 + tid * 4;
+        uint32_t o[4], tg[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j;
+            o[j] = i < nlist ? f2ord(row[i]) : ~0u;
+            tg[j] = (uint32_t)i;
         }
-        qtot[b] = acc;
+        stream_round<NT>(S, P, o, tg, [&](int s) { return (uint32_t)(r * NT * 4 + s); });
     }
-    JHQ_PHASE(2);
-    JHQ_PHASE_FLUSH(1);
-}
-
-hipError_t select_probes(const float* scores, int B, int nlist, int P,
-                         const int32_t* list_padoff, int32_t* probes, int32_t* gofs,
-                         int32_t* qtot, hipStream_t s) {
-    constexpr int NT = 256;
-    size_t lds = (size_t)P * (8 + 8 + 4) + sizeof(SelState);
-    const bool in_lds = lds + (size_t)nlist * 4 <= 64 * 1024;
-    if (in_lds) lds += (size_t)nlist * 4;
-    hipLaunchKernelGGL(select_probes_kernel<NT>, dim3(B), dim3(NT), lds, s, scores, nlist, P,
-                       list_padoff, probes, gofs, qtot, in_lds);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// Byte LUT (v14/search.cu:65-91): lut[b][m][v] = sum_k (q[m*Ds+k] - c1d[digit_k(v)])^2
-// accumulated with fma in k order.  One workgroup per (m, b), one thread per v.
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256)
-byte_lut_kernel(const float* __restrict__ q_rot, int d, int M, int Ds, int K1D, int bpd,
-                const float* __restrict__ c1d, float* __restrict__ lut) {
-    __shared__ float sq[8];
-    __shared__ float sc[256];
-    const int m = blockIdx.x, b = blockIdx.y, v = threadIdx.x;
-    if (v < Ds) sq[v] = q_rot[(int64_t)b * d + m * Ds + v];
-    if (v < K1D) sc[v] = c1d[v];
+    const int kk = stream_end<NT>(S, P);
+    for (int i = tid; i < P; i += NT) {
+        const int l = i < kk ? (int)(uint32_t)(S.kout[i] & 0xffffffffull) : 0;
+        probes[(int64_t)b * P + i] = l;
+        gcnt[i] = i < kk ? (list_padoff[l + 1] - list_padoff[l]) / kGroup : 0;
+    }
     __syncthreads();
-    float s = 0.0f;
-    for (int k = 0; k < Ds; k++) {
-        const float df = sq[k] - sc[(v >> (k * bpd)) & (K1D - 1)];
-        s = fmaf(df, df, s);
+    // prefix of the group counts (P is small: one wave)
+    if (tid < 64) {
+        int carry = 0;
+        int32_t* g = gofs + (int64_t)b * (P + 1);
+        if (tid == 0) g[0] = 0;
+        for (int base = 0; base < P; base += 64) {
+            const int i = base + tid;
+            const int v = i < P ? gcnt[i] : 0;
+            int incl = v;
+            for (int off = 1; off < 64; off <<= 1) {
+                const int t = __shfl_up(incl, off);
+                if (tid >= off) incl += t;
+            }
+            if (i < P) g[i + 1] = carry + incl;
+            carry += __shfl(incl, 63);
+        }
+        if (tid == 0) qtot[b] = carry;
     }
-    lut[((int64_t)b * M + m) * 256 + v] = s;
-}
-
-hipError_t build_lut(const float* q_rot, int B, int d, int M, int Ds, int K1D, int bpd,
-                     const float* c1d, float* lut, hipStream_t s) {
-    if (Ds > 8 || K1D > 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(byte_lut_kernel, dim3(M, B), dim3(256), 0, s, q_rot, d, M, Ds, K1D, bpd,
-                       c1d, lut);
-    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Chunk plan shared by the scan and merge kernels.  Each query's padded
-// candidate groups are cut into chunks of CHg groups, CHg chosen so that the
-// batch makes about one chunk per scan workgroup but never more than the
-// LDS distance buffer holds.  cpre[b] = first chunk of query b (cpre[B] total).
+// Work plan of one search batch, computed identically by the scan and the
+// refine kernels.  The batch's padded candidate groups are laid end to end in
+// query order; workgroup w of G owns groups [w*T/G, (w+1)*T/G).  The groups of
+// one query inside one workgroup's range form a segment, which yields one
+// top-ck list.  qpre[b] = first group of query b (qpre[B] = T); spre[b] =
+// first segment of query b (spre[B] <= G + B - 1).
 // ---------------------------------------------------------------------------
-template <int NT>
-__device__ int chunk_plan(const int32_t* __restrict__ qtot, int B, int capg, int G, int* cpre) {
-    // cpre needs B + 2 ints.  Totals gathered in parallel and block-reduced;
-    // per-query chunk counts prefix-summed over per-thread segments.
-    __shared__ int wsum[NT / 64];
-    __shared__ int tot_sh;
+__device__ __forceinline__ int wg_of_group(int64_t x, int64_t T, int G) {
+    return (int)(((x + 1) * G - 1) / T);
+}
+
+// Exclusive prefix over B values f(b) into out[0..B] (out[B] = total).
+template <int NT, class F>
+__device__ void block_exclusive_scan(F f, int B, int* out, int* wsum) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if (tid == 0) tot_sh = 0;
-    __syncthreads();
-    int loc = 0;
-    for (int b = tid; b < B; b += NT) {
-        const int t = qtot[b];
-        cpre[b] = t;
-        loc += t;
-    }
-    for (int off = 32; off > 0; off >>= 1) loc += __shfl_xor(loc, off);
-    if (lane == 0 && loc) atomicAdd(&tot_sh, loc);
-    __syncthreads();
-    int chg = (tot_sh + G - 1) / G;
-    if (chg < 4) chg = 4;
-    if (chg > capg) chg = capg;
     const int per = (B + NT - 1) / NT;
-    const int s0 = tid * per, s1 = (s0 + per) < B ? (s0 + per) : B;
+    const int s0 = min(B, tid * per), s1 = min(B, s0 + per);
     int seg = 0;
-    for (int b = s0; b < s1; b++) seg += (cpre[b] + chg - 1) / chg;
+    for (int b = s0; b < s1; b++) seg += f(b);
     int inc = seg;
     for (int off = 1; off < 64; off <<= 1) {
         const int t = __shfl_up(inc, off);
@@ -861,183 +1068,260 @@ __device__ int chunk_plan(const int32_t* __restrict__ qtot, int B, int capg, int
     for (int j = 0; j < w; j++) base += wsum[j];
     int acc = base + inc - seg;
     for (int b = s0; b < s1; b++) {
-        const int nch = (cpre[b] + chg - 1) / chg;
-        cpre[b] = acc;
-        acc += nch;
+        const int v = f(b);
+        out[b] = acc;
+        acc += v;
     }
-    if (tid == NT - 1) {
-        cpre[B] = acc;
-        cpre[B + 1] = chg;
-    }
+    if (tid == NT - 1) out[B] = acc;
     __syncthreads();
-    return cpre[B + 1];
+}
+
+// Returns the number of workgroups that take part: min(G, T), so that every
+// participating workgroup owns at least one group.
+template <int NT>
+__device__ int work_plan(const int32_t* __restrict__ qtot, int B, int Gmax, int* qpre, int* spre,
+                         int* wsum) {
+    block_exclusive_scan<NT>([&](int b) { return (int)qtot[b]; }, B, qpre, wsum);
+    const int64_t T = qpre[B];
+    const int G = (int)min<int64_t>(Gmax, T);
+    block_exclusive_scan<NT>(
+        [&](int b) {
+            const int64_t a = qpre[b], e = qpre[b + 1];
+            if (e <= a) return 0;
+            return wg_of_group(e - 1, T, G) - wg_of_group(a, T, G) + 1;
+        },
+        B, spre, wsum);
+    return G;
 }
 
 // ---------------------------------------------------------------------------
-// IVF ADC scan + exact top-ck.  A persistent grid: workgroup w takes the
-// contiguous chunk range [w*TC/G, (w+1)*TC/G), so consecutive chunks mostly
-// belong to one query and its byte LUT is loaded into LDS once.
+// Byte LUT of one query in LDS (v14/search.cu:65-91):
+//   lut[m][v] = sum_k (q[m*Ds+k] - c1d[digit_k(v)])^2, one fma per k, k
+// ascending.  A group of NT/M threads shares subspace m with q[m*Ds..] in
+// registers.  For 1-bit digits and Ds = 8 the 16 entries that share the low
+// 4 bits share the first 4 steps of their fma chain, so each thread finishes
+// one low-nibble prefix and expands the high nibble as a binary tree (34
+// fmas for 16 entries instead of 128); every entry is still the same chain.
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, int K1D, int bpd,
+                                              const float* sc1d, float* lut) {
+    const int tpm = NT / M > 0 ? NT / M : 1;
+    const int part = threadIdx.x % tpm;
+    const int kmask = K1D - 1;
+    for (int m = threadIdx.x / tpm; m < M; m += NT / tpm) {
+        float qv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) qv[k] = k < Ds ? sq[m * Ds + k] : 0.0f;
+        float* lm = lut + m * 256;
+        if (K1D == 2 && Ds == 8) {
+            const float c0 = sc1d[0], c1 = sc1d[1];
+            for (int p = part; p < 16; p += tpm) {
+                float s4 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float df = qv[k] - (((p >> k) & 1) ? c1 : c0);
+                    s4 = fmaf(df, df, s4);
+                }
+                float t[16];
+                t[0] = s4;
+#pragma unroll
+                for (int L = 0; L < 4; L++) {
+                    const float d0 = qv[4 + L] - c0, d1 = qv[4 + L] - c1;
+#pragma unroll
+                    for (int i = (1 << L) - 1; i >= 0; i--) {
+                        const float base = t[i];
+                        t[i | (1 << L)] = fmaf(d1, d1, base);
+                        t[i] = fmaf(d0, d0, base);
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < 16; h++) lm[p + 16 * h] = t[h];
+            }
+        } else {
+            for (int v = part; v < 256; v += tpm) {
+                float sacc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    if (k < Ds) {
+                        const float df = qv[k] - sc1d[(v >> (k * bpd)) & kmask];
+                        sacc = fmaf(df, df, sacc);
+                    }
+                }
+                lm[v] = sacc;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// IVF ADC scan + exact top-ck per segment (v14/search.cu:105-195 with the
+// exact selection of jhq_v3_ivf/search.cu:189-225).
+//   - persistent grid, one workgroup per CU, each owning an equal share of
+//     the batch's candidate groups (work_plan);
+//   - the query's byte LUT lut[m][v] (v14/search.cu:65-91) is built straight
+//     into LDS from q_rot;
 //   - each thread takes 4 consecutive candidates of one list: per subspace m
-//     one 32-bit coalesced load gives their 4 code bytes (16 loads kept in
-//     flight), 4 LDS gathers accumulate dist in m order;
-//   - all chunk distances stay in LDS; one radix select + rank sort yields
-//     the chunk's exact top-ck by (dist, pos) -> partial[chunk][ck].
+//     one 32-bit coalesced load gives their 4 code bytes (SU loads kept in
+//     flight), 4 LDS gathers accumulate dist in m order (v14/search.cu:146-151);
+//   - the segment's exact top-ck by (dist, stored position) is kept by the
+//     streaming selection above -> partial[segment][ck] keys
+//     (ord(dist) << 32 | pos), unfilled = ~0.
 // ---------------------------------------------------------------------------
 template <int NT, int SU>
 __global__ void __launch_bounds__(NT)
-scan_topck_kernel(const float* __restrict__ glut, int M, const int32_t* __restrict__ probes,
+scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
+                  const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                   const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
                   const int32_t* __restrict__ list_off, const int32_t* __restrict__ list_padoff,
-                  const uint8_t* __restrict__ codes_t, int ck, int cap, int max_chunks,
+                  const uint8_t* __restrict__ codes_t, int ck,
                   unsigned long long* __restrict__ partial) {
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;
-    uint32_t* dbuf = (uint32_t*)(lut + (size_t)M * 256);
-    unsigned long long* tmpk = (unsigned long long*)(dbuf + cap);  // cap % 64 == 0
-    unsigned long long* topk = tmpk + ck;
-    int32_t* sg = (int32_t*)(topk + ck);
-    int32_t* sprobe = sg + (P + 1);
-    int* scratch = (int*)(sprobe + P);
-    int* cpre = scratch + ck;
-    int32_t* spad0 = cpre + B + 2;  // per probe: padded start, padded size,
+    StreamSel S;
+    int* qpre = (int*)stream_carve<NT>(smem + (size_t)M * 256 * 4, ck, &S);
+    int* spre = qpre + B + 1;
+    int32_t* sg = spre + B + 1;     // per probe: group prefix [P+1],
+    int32_t* spad0 = sg + P + 1;    // padded start, padded size,
     int32_t* snpad = spad0 + P;     // list size, stored-position start
     int32_t* snl = snpad + P;
     int32_t* soff = snl + P;
-    SelState* st = (SelState*)(soff + P);
+    float* sc1d = (float*)(soff + P);
+    int* wsum = (int*)(sc1d + K1D);
 
-    const int tid = threadIdx.x, G = gridDim.x;
-    const int capg = cap / kGroup;
+    const int tid = threadIdx.x, w = blockIdx.x;
     JHQ_PHASE_DECL
-    const int chg = chunk_plan<NT>(qtot, B, capg, G, cpre);
+    for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
+    const int64_t T = qpre[B];
     JHQ_PHASE(0);
-    const int TC = cpre[B] < max_chunks ? cpre[B] : max_chunks;
-    const int c_begin = (int)((int64_t)TC * blockIdx.x / G);
-    const int c_end = (int)((int64_t)TC * (blockIdx.x + 1) / G);
-    int cur_b = -1;
-    for (int c = c_begin; c < c_end; c++) {
-        // query of chunk c: last b with cpre[b] <= c
+    if (w >= G) return;
+    const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
+    // first query whose groups reach x0
+    int b;
+    {
         int lo = 0, hi = B - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (cpre[mid] <= c) lo = mid;
+            if (qpre[mid] <= x0) lo = mid;
             else hi = mid - 1;
         }
-        const int b = lo;
-        if (b != cur_b) {
-            __syncthreads();
-            for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
-            for (int i = tid; i < P; i += NT) {
-                const int l = probes[(int64_t)b * P + i];
-                sprobe[i] = l;
-                const int p0 = list_padoff[l], o0 = list_off[l];
-                spad0[i] = p0;
-                snpad[i] = list_padoff[l + 1] - p0;
-                soff[i] = o0;
-                snl[i] = list_off[l + 1] - o0;
-            }
-            const uint4* src = (const uint4*)(glut + (int64_t)b * M * 256);
-            uint4* dst = (uint4*)lut;
-            for (int i = tid; i < M * 64; i += NT) dst[i] = src[i];
-            cur_b = b;
+        b = lo;
+    }
+    for (; b < B && qpre[b] < x1; b++) {
+        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
+        if (qb1 <= qb0) continue;
+        const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
+        const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
+        __syncthreads();
+        // probe metadata and the query's rotated vector (staged in rbuf)
+        for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
+        for (int i = tid; i < P; i += NT) {
+            const int l = probes[(int64_t)b * P + i];
+            const int p0 = list_padoff[l], o0 = list_off[l];
+            spad0[i] = p0;
+            snpad[i] = list_padoff[l + 1] - p0;
+            soff[i] = o0;
+            snl[i] = list_off[l + 1] - o0;
         }
-        if (tid == 0) st->aux = 0;
+        float* sq = (float*)S.rbuf;
+        for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
+        stream_begin<NT>(S);
+        __syncthreads();
+        // byte LUT: lut[m][v] = sum_k (q[m*Ds+k] - c1d[digit_k(v)])^2, fma in k order
+        build_lut_lds<NT>(sq, M, Ds, K1D, bpd, sc1d, lut);
         __syncthreads();
         JHQ_PHASE(1);
-        const int T = sg[P];
-        const int g0 = (c - cpre[b]) * chg;
-        const int g1 = (g0 + chg) < T ? (g0 + chg) : T;
-        unsigned long long* outp = partial + (int64_t)c * ck;
 
-        const int nq4 = (g1 - g0) * 4;
-        int nvalid = 0;
-        for (int qd = tid; qd < nq4; qd += NT) {
-            const int gq = g0 * 4 + qd;
-            const int g = gq >> 2, sub = gq & 3;
+        const int nq4 = (gB - gA) * 4;
+        const int rounds = (nq4 + NT - 1) / NT;
+        auto probe_of = [&](int g) {
             int plo = 0, phi = P - 1;  // last p with sg[p] <= g
             while (plo < phi) {
                 const int mid = (plo + phi + 1) >> 1;
                 if (sg[mid] <= g) plo = mid;
                 else phi = mid - 1;
             }
-            const int gi = g - sg[plo];
-            const int pad0 = spad0[plo];
-            const int npad = snpad[plo];
-            const int nl = snl[plo];
-            const int c0 = gi * kGroup + sub * 4;
-            const uint8_t* base = codes_t + (int64_t)pad0 * M + c0;
-            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-            // software pipeline: the next SU subspaces' code words are in
-            // flight while the current SU are gathered from the LUT
-            const int M16 = M & ~(SU - 1);
-            uint32_t w[SU], wn[SU];
-            if (M16 > 0) {
-#pragma unroll
-                for (int u = 0; u < SU; u++) w[u] = *(const uint32_t*)(base + (int64_t)u * npad);
-            }
-            for (int m = 0; m < M16; m += SU) {
-                if (m + SU < M16) {
-#pragma unroll
-                    for (int u = 0; u < SU; u++)
-                        wn[u] = *(const uint32_t*)(base + (int64_t)(m + SU + u) * npad);
-                }
-#pragma unroll
-                for (int u = 0; u < SU; u++) {
-                    const float* lm = lut + (m + u) * 256;
-                    a0 += lm[w[u] & 0xffu];
-                    a1 += lm[(w[u] >> 8) & 0xffu];
-                    a2 += lm[(w[u] >> 16) & 0xffu];
-                    a3 += lm[w[u] >> 24];
-                }
-#pragma unroll
-                for (int u = 0; u < SU; u++) w[u] = wn[u];
-            }
-            for (int m = M16; m < M; m++) {
-                const uint32_t ww = *(const uint32_t*)(base + (int64_t)m * npad);
-                const float* lm = lut + m * 256;
-                a0 += lm[ww & 0xffu];
-                a1 += lm[(ww >> 8) & 0xffu];
-                a2 += lm[(ww >> 16) & 0xffu];
-                a3 += lm[ww >> 24];
-            }
-            uint32_t* db = dbuf + qd * 4;
-            db[0] = (c0 + 0 < nl) ? f2ord(a0) : ~0u;
-            db[1] = (c0 + 1 < nl) ? f2ord(a1) : ~0u;
-            db[2] = (c0 + 2 < nl) ? f2ord(a2) : ~0u;
-            db[3] = (c0 + 3 < nl) ? f2ord(a3) : ~0u;
-            const int left = nl - c0;
-            nvalid += left >= 4 ? 4 : (left > 0 ? left : 0);
-        }
-        for (int off = 32; off > 0; off >>= 1) nvalid += __shfl_xor(nvalid, off);
-        if ((tid & 63) == 0) atomicAdd(&st->aux, nvalid);
-        __syncthreads();
-        const int nv = st->aux;
-        const int ksel = nv < ck ? nv : ck;
-        const int nslot = nq4 * 4;
-        JHQ_PHASE(2);
-
-        auto pos_of = [&](int i) -> uint32_t {
-            const int gq = g0 * 4 + (i >> 2);
-            const int g = gq >> 2;
-            int plo = 0, phi = P - 1;
-            while (plo < phi) {
-                const int mid = (plo + phi + 1) >> 1;
-                if (sg[mid] <= g) plo = mid;
-                else phi = mid - 1;
-            }
-            const int cand = (g - sg[plo]) * kGroup + (gq & 3) * 4 + (i & 3);
-            return (uint32_t)(soff[plo] + cand);
+            return plo;
         };
-        if (ksel > 0)
+        for (int r = 0; r < rounds; r++) {
+            const int qd = r * NT + tid;
+            uint32_t o[4] = {~0u, ~0u, ~0u, ~0u}, tg[4] = {0u, 0u, 0u, 0u};
+            if (qd < nq4) {
+                const int gq = gA * 4 + qd;
+                const int g = gq >> 2, sub = gq & 3;
+                const int plo = probe_of(g);
+                const int npad = snpad[plo], nl = snl[plo];
+                const int c0 = (g - sg[plo]) * kGroup + sub * 4;
+                const uint8_t* base = codes_t + (int64_t)spad0[plo] * M + c0;
+                float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+                // the next SU subspaces' code words are in flight while the
+                // current SU are gathered from the LUT
+                const int MS = M - M % SU;
+                uint32_t wc[SU], wn[SU];
+                if (MS > 0) {
+#pragma unroll
+                    for (int u = 0; u < SU; u++) wc[u] = *(const uint32_t*)(base + (int64_t)u * npad);
+                }
+                for (int m = 0; m < MS; m += SU) {
+                    if (m + SU < MS) {
+#pragma unroll
+                        for (int u = 0; u < SU; u++)
+                            wn[u] = *(const uint32_t*)(base + (int64_t)(m + SU + u) * npad);
+                    }
+#pragma unroll
+                    for (int u = 0; u < SU; u++) {
+                        const float* lm = lut + (m + u) * 256;
+                        a0 += lm[wc[u] & 0xffu];
+                        a1 += lm[(wc[u] >> 8) & 0xffu];
+                        a2 += lm[(wc[u] >> 16) & 0xffu];
+                        a3 += lm[wc[u] >> 24];
+                    }
+#pragma unroll
+                    for (int u = 0; u < SU; u++) wc[u] = wn[u];
+                }
+                for (int m = MS; m < M; m++) {
+                    const uint32_t ww = *(const uint32_t*)(base + (int64_t)m * npad);
+                    const float* lm = lut + m * 256;
+                    a0 += lm[ww & 0xffu];
+                    a1 += lm[(ww >> 8) & 0xffu];
+                    a2 += lm[(ww >> 16) & 0xffu];
+                    a3 += lm[ww >> 24];
+                }
+                const uint32_t p0 = (uint32_t)(soff[plo] + c0);
+                o[0] = (c0 + 0 < nl) ? f2ord(a0) : ~0u;
+                o[1] = (c0 + 1 < nl) ? f2ord(a1) : ~0u;
+                o[2] = (c0 + 2 < nl) ? f2ord(a2) : ~0u;
+                o[3] = (c0 + 3 < nl) ? f2ord(a3) : ~0u;
+                tg[0] = p0;
+                tg[1] = p0 + 1u;
+                tg[2] = p0 + 2u;
+                tg[3] = p0 + 3u;
+            }
 #ifdef JHQ_PHASE_TIMING
-            block_topk<NT>([&](int i) { return dbuf[i]; }, pos_of, nslot, ksel, scratch, tmpk, topk,
-                           st, ph_acc + 6);
-#else
-            block_topk<NT>([&](int i) { return dbuf[i]; }, pos_of, nslot, ksel, scratch, tmpk, topk,
-                           st);
+            __syncthreads();  // attribute the wait for the slowest wave to the scan
 #endif
+            JHQ_PHASE(2);
+            stream_round<NT>(
+                S, ck, o, tg,
+                [&](int s) -> uint32_t {
+                    const int gq = gA * 4 + r * NT + (s >> 2);
+                    const int g = gq >> 2;
+                    const int plo = probe_of(g);
+                    return (uint32_t)(soff[plo] + (g - sg[plo]) * kGroup + (gq & 3) * 4 + (s & 3));
+                },
+#ifdef JHQ_PHASE_TIMING
+                ph_acc + 4
+#else
+                nullptr
+#endif
+            );
+            JHQ_PHASE(3);
+        }
+        const int kk = stream_end<NT>(S, ck);
+        unsigned long long* outp = partial + (int64_t)seg * ck;
+        for (int i = tid; i < ck; i += NT) outp[i] = i < kk ? S.kout[i] : ~0ull;
         JHQ_PHASE(3);
-        for (int r = tid; r < ck; r += NT) outp[r] = (r < ksel) ? topk[r] : ~0ull;
-        JHQ_PHASE(4);
     }
     JHQ_PHASE_FLUSH(0);
 }
@@ -1054,114 +1338,110 @@ static int allow_max_lds(const void* kernel) {
     return dyn;
 }
 
-bool scan_plan(int M, int d, int P, int ck, int max_groups_per_query, int B, int target_wg,
-               ScanShape* out) {
-    (void)d;
-    const int fixed = M * 256 * 4 + 2 * ck * 8 + (P + 1) * 4 + 5 * P * 4 + ck * 4 + (B + 2) * 4 +
-                      (int)sizeof(SelState) + 64;
-    const int avail = kLdsBytes - 2048 /* static LDS of the kernel */ - fixed;
-    if (avail < 1024 * 4) return false;
-    int cap = avail / 4;
-    if (cap > 16384) cap = 16384;
-    cap = (cap / 64) * 64;
-    const int capg = cap / kGroup;
+constexpr int kScanNT = JHQ_SCAN_NT;
+constexpr int kRefineNT = 512;
+constexpr int kProbeNT = 512;
+
+bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out) {
+    const size_t lds = (size_t)M * 256 * 4 + stream_lds_bytes(kScanNT, ck) +
+                       (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 + (size_t)K1D * 4 +
+                       (kScanNT / 64) * 4 + 64;
+    if (lds > (size_t)kLdsBytes - 1024) return false;
+    if ((size_t)d * 4 > (size_t)kScanNT * 16) return false;  // q staged in the round buffer
     out->G = target_wg;
-    out->cap = cap;
-    out->lds = fixed + cap * 4;
-    // chunks: at most ceil(total/CHg) + B with CHg >= min(capg, ceil(total/G))
-    const int64_t per_q_capped = (max_groups_per_query + capg - 1) / capg;
-    int64_t mc = (int64_t)B * (per_q_capped + 1);
-    if (mc < (int64_t)target_wg + B) mc = (int64_t)target_wg + B;
-    out->max_chunks = (int)mc;
+    out->lds = (int)lds;
+    out->max_segments = target_wg + B;
     return true;
 }
 
-hipError_t scan_topck(const float* glut, int B, int M, const int32_t* probes, const int32_t* gofs,
+hipError_t select_probes(const float* scores, int B, int nlist, int P,
+                         const int32_t* list_padoff, int32_t* probes, int32_t* gofs,
+                         int32_t* qtot, hipStream_t s) {
+    const size_t lds = stream_lds_bytes(kProbeNT, P) + (size_t)P * 4 + 16;
+    static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<kProbeNT>);
+    if ((int)lds > max_dyn) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(select_probes_kernel<kProbeNT>, dim3(B), dim3(kProbeNT), lds, s, scores,
+                       nlist, P, list_padoff, probes, gofs, qtot);
+    return hipGetLastError();
+}
+
+hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d,
+                      int B, int M, const int32_t* probes, const int32_t* gofs,
                       const int32_t* qtot, int P, const int32_t* list_off,
                       const int32_t* list_padoff, const uint8_t* codes_t, int ck,
                       const ScanShape& sh, unsigned long long* partial, hipStream_t s) {
-    constexpr int NT = JHQ_SCAN_NT, SU = JHQ_SCAN_SU;
+    constexpr int NT = kScanNT, SU = JHQ_SCAN_SU;
     static const int max_dyn = allow_max_lds((const void*)scan_topck_kernel<NT, SU>);
-    if (sh.lds > max_dyn) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((scan_topck_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, glut, M, probes,
-                       gofs, qtot, B, P, list_off, list_padoff, codes_t, ck, sh.cap,
-                       sh.max_chunks, partial);
+    if (sh.lds > max_dyn || Ds > 8 || K1D > 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((scan_topck_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d, Ds,
+                       K1D, bpd, c1d, M, probes, gofs, qtot, B, P, list_off, list_padoff, codes_t,
+                       ck, partial);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Merge + residual refine + final top-k, one workgroup per query.
-// The residual distance of a candidate is summed by 16 lanes over 16
-// contiguous dimension ranges, then added across the lanes in a fixed tree.
+// Merge + residual refine + final top-k, one workgroup per query
+// (v14/search.cu:198-291 with the exact selection of jhq_v3_ivf).
+// The query's segment lists are merged by the streaming selection; the
+// residual distance of a candidate is summed by 16 lanes over 16 contiguous
+// dimension ranges, then added across the lanes in a fixed xor tree.
 // ---------------------------------------------------------------------------
 template <int NT>
 __global__ void __launch_bounds__(NT)
 refine_topk_kernel(const unsigned long long* __restrict__ partial,
-                   const int32_t* __restrict__ qtot, int B, int cap, int G, int max_chunks, int mc,
-                   int ck, int k, const float* __restrict__ q_rot, int d,
-                   const float* __restrict__ res_c1d, int Kr, int Br, int bpv,
-                   const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
-                   const int32_t* __restrict__ list_ids, float* __restrict__ out_d,
-                   int32_t* __restrict__ out_i, unsigned long long* __restrict__ topck_dbg) {
+                   const int32_t* __restrict__ qtot, int B, int Gmax, int ck, int k,
+                   const float* __restrict__ q_rot, int d, const float* __restrict__ res_c1d,
+                   int Kr, int Br, int bpv, const uint8_t* __restrict__ list_res,
+                   const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
+                   float* __restrict__ out_d, int32_t* __restrict__ out_i,
+                   unsigned long long* __restrict__ topck_dbg) {
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned long long* keys = (unsigned long long*)smem;  // [ck + mc]
-    unsigned long long* tmpk = keys + ck + mc;             // [ck]
-    unsigned long long* topk = tmpk + ck;                  // [ck]
+    StreamSel S;
+    unsigned char* p = stream_carve<NT>(smem, ck, &S);
+    unsigned long long* fkeys = (unsigned long long*)p;  // [ck] final-candidate keys
+    int* qpre = (int*)(fkeys + ck);
+    int* spre = qpre + B + 1;
+    int* cpos = spre + B + 1;
+    float* cprim = (float*)(cpos + ck);
+    int* wsum = (int*)(cprim + ck);
     // query staged with one pad word per 32 so that lanes reading 32-dim
     // ranges at a 32-word stride hit distinct banks
-    float* sq = (float*)(topk + ck);
-    int* scratch = (int*)(sq + d + d / 32 + 1);
-    float* cprim = (float*)(scratch + ck);
-    int* cpos = (int*)(cprim + ck);
-    float* ccomp = (float*)(cpos + ck);
-    int* cid = (int*)(ccomp + ck);
-    int* cpre = cid + ck;
-    SelState* st = (SelState*)(cpre + B + 2);
+    float* sq = (float*)(wsum + NT / 64);
     __shared__ float rc[256];
 
     const int b = blockIdx.x, tid = threadIdx.x;
     JHQ_PHASE_DECL
-    chunk_plan<NT>(qtot, B, cap / kGroup, G, cpre);
-    JHQ_PHASE(0);
+    work_plan<NT>(qtot, B, Gmax, qpre, spre, wsum);
     for (int i = tid; i < d; i += NT) sq[i + (i >> 5)] = q_rot[(int64_t)b * d + i];
     for (int i = tid; i < Kr; i += NT) rc[i] = res_c1d[i];
-    const int cb = cpre[b] < max_chunks ? cpre[b] : max_chunks;
-    const int ce = cpre[b + 1] < max_chunks ? cpre[b + 1] : max_chunks;
-    const int per_round = mc / ck > 0 ? mc / ck : 1;
+    const int s0 = spre[b], s1 = spre[b + 1];
+    stream_begin<NT>(S);
+    __syncthreads();
+    JHQ_PHASE(0);
 
-    // streaming merge of the query's chunk lists into the exact top-ck
-    int cur = 0;
-    for (int c0 = cb; c0 < ce; c0 += per_round) {
-        const int c1 = (c0 + per_round) < ce ? (c0 + per_round) : ce;
-        const int m = (c1 - c0) * ck;
-        if (tid == 0) st->aux = 0;
-        __syncthreads();
-        int nv = 0;
-        for (int i = tid; i < m; i += NT) {
-            const unsigned long long kk = partial[(int64_t)c0 * ck + i];
-            keys[cur + i] = kk;
-            nv += (kk != ~0ull) ? 1 : 0;
+    // merge the query's segment lists: 4 keys per thread per round
+    const int nkeys = (s1 - s0) * ck;
+    const unsigned long long* src = partial + (int64_t)s0 * ck;
+    const int rounds = (nkeys + NT * 4 - 1) / (NT * 4);
+    for (int r = 0; r < rounds; r++) {
+        uint32_t o[4], tg[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = r * NT * 4 + threadIdx.x * 4 + j;
+            const unsigned long long kk = i < nkeys ? src[i] : ~0ull;
+            o[j] = (uint32_t)(kk >> 32);
+            tg[j] = (uint32_t)(kk & 0xffffffffull);
         }
-        for (int off = 32; off > 0; off >>= 1) nv += __shfl_xor(nv, off);
-        if ((tid & 63) == 0 && nv) atomicAdd(&st->aux, nv);
-        __syncthreads();
-        const int n = cur + m;
-        const int nvalid = cur + st->aux;
-        const int kk = nvalid < ck ? nvalid : ck;
-        if (kk > 0) {
-            block_topk<NT>([&](int i) { return (uint32_t)(keys[i] >> 32); },
-                           [&](int i) { return (uint32_t)(keys[i] & 0xffffffffull); }, n, kk,
-                           scratch, tmpk, topk, st);
-            for (int r = tid; r < kk; r += NT) keys[r] = topk[r];
-        }
-        cur = kk;
-        __syncthreads();
+        stream_round<NT>(S, ck, o, tg, [&](int s) {
+            const int i = r * NT * 4 + s;
+            return (uint32_t)(src[i] & 0xffffffffull);
+        });
     }
-    const int ksel = cur;
+    const int ksel = stream_end<NT>(S, ck);
     JHQ_PHASE(1);
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
-            const unsigned long long kk = keys[r];
+            const unsigned long long kk = S.kout[r];
             cprim[r] = ord2f((uint32_t)(kk >> 32));
             cpos[r] = (int)(uint32_t)(kk & 0xffffffffull);
             if (topck_dbg) topck_dbg[(int64_t)b * ck + r] = kk;
@@ -1175,7 +1455,6 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     // range of dimensions, then a fixed xor tree adds the 16 partial sums.
     const int grp = tid >> 4, l16 = tid & 15;
     constexpr int NG = NT / 16;
-    // vector path: each lane's range is whole 16-byte chunks of the code row
     const int dpc = (Br == 4) ? 32 : 16;  // dimensions per 16-byte chunk
     const bool vec = (bpv % 16) == 0 && (d % dpc) == 0;
     int chk = (d + 15) / 16;
@@ -1247,22 +1526,19 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
         sres = sres + __shfl_xor(sres, 2);
         sres = sres + __shfl_xor(sres, 1);
         if (valid && l16 == 0) {
-            ccomp[c] = (cprim[c] + sres) + list_corr[pos];
-            cid[c] = list_ids[pos];
+            const float comp = (cprim[c] + sres) + list_corr[pos];
+            fkeys[c] = ((unsigned long long)f2ord(comp) << 32) | (uint32_t)list_ids[pos];
         }
     }
     __syncthreads();
-
     JHQ_PHASE(2);
+
     // final top-k by (dist, id)
     const int kf = ksel < k ? ksel : k;
-    if (kf > 0) {
-        block_topk<NT>([&](int i) { return f2ord(ccomp[i]); }, [&](int i) { return (uint32_t)cid[i]; },
-                       ksel, kf, scratch, tmpk, topk, st);
-    }
+    if (kf > 0) select_keys<NT>(fkeys, ksel, kf, S.kout, S.kidx, S.ktmp, S.st);
     for (int r = tid; r < k; r += NT) {
         if (r < kf) {
-            const unsigned long long kk = topk[r];
+            const unsigned long long kk = S.kout[r];
             out_d[(int64_t)b * k + r] = ord2f((uint32_t)(kk >> 32));
             out_i[(int64_t)b * k + r] = (int32_t)(uint32_t)(kk & 0xffffffffull);
         } else {
@@ -1279,16 +1555,15 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* qtot, i
                        const float* res_c1d, int Kr, int Br, int bpv, const uint8_t* list_res,
                        const float* list_corr, const int32_t* list_ids, float* out_d,
                        int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s) {
-    constexpr int NT = 512;
-    if (k > ck || ck > 4 * NT) return hipErrorInvalidValue;
-    const int mc = 4096;
-    const size_t lds = (size_t)(3 * ck + mc) * 8 + (size_t)(d + d / 32 + 1) * 4 +
-                       (size_t)ck * 4 * 5 + (size_t)(B + 2) * 4 + sizeof(SelState) + 64;
+    constexpr int NT = kRefineNT;
+    if (k > ck) return hipErrorInvalidValue;
+    const size_t lds = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)(2 * (B + 1)) * 4 +
+                       (size_t)ck * 4 * 2 + (NT / 64) * 4 + (size_t)(d + d / 32 + 1) * 4 + 16;
     static const int max_dyn = allow_max_lds((const void*)refine_topk_kernel<NT>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, qtot, B, sh.cap,
-                       sh.G, sh.max_chunks, mc, ck, k, q_rot, d, res_c1d, Kr, Br, bpv, list_res,
-                       list_corr, list_ids, out_d, out_i, topck_dbg);
+    hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, qtot, B, sh.G,
+                       ck, k, q_rot, d, res_c1d, Kr, Br, bpv, list_res, list_corr, list_ids, out_d,
+                       out_i, topck_dbg);
     return hipGetLastError();
 }
 
