@@ -129,12 +129,13 @@ int jhq_get_codebooks(const jhq_index* idx, float* sigma, float* c1d,
 int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids,
                   uint8_t* codes, uint8_t* res, float* corr);
 
-/* Search that also returns, per query, the probed list ids [nq x nprobe]
- * (ascending (score, list)) and the merged top-ck short list
- * [nq x ck] as stored positions and primary distances ((dist, pos)
- * ascending; unfilled = -1 / +inf).  ck = max(k, ceil(alpha*k)). */
+/* Search that also returns, per query, the rotated query [nq x d] (the
+ * fp32 MFMA product the pipeline used), the probed list ids [nq x nprobe]
+ * (ascending (score, list)) and the merged top-ck short list [nq x ck] as
+ * stored positions and primary distances ((dist, pos) ascending; unfilled =
+ * -1 / +inf).  ck = max(k, ceil(alpha*k)).  Any debug pointer may be NULL. */
 int jhq_search_debug(jhq_index* idx, const float* q, int64_t nq, int k,
-                     float* dists, int32_t* ids, int32_t* probes,
+                     float* dists, int32_t* ids, float* q_rot, int32_t* probes,
                      int32_t* topck_pos, float* topck_dist);
 
 /* Per-step device timing (hipEvents around each step, the reference's

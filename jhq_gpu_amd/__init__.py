@@ -90,7 +90,7 @@ _SIGS = {
     "jhq_get_dims": (_I, [_VP] + [ctypes.POINTER(_I)] * 5),
     "jhq_get_codebooks": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "jhq_get_lists": (_I, [_VP, _VP, _VP, _VP, _VP, _VP]),
-    "jhq_search_debug": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP, _VP, _VP]),
+    "jhq_search_debug": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP, _VP, _VP, _VP]),
     "jhq_set_timing": (_I, [_VP, _I]),
     "jhq_get_timing": (_I, [_VP, _VP, _I, ctypes.POINTER(_I64)]),
     "jhq_k_rotate": (_I, [_VP, _VP, _I64, _I, _VP, _VP]),
@@ -269,12 +269,14 @@ class JHQGpuIndex:
         ck = max(k, int(np.ceil(np.float32(self._p.alpha) * np.float32(k))))
         dists = np.empty((nq, k), np.float32)
         ids = np.empty((nq, k), np.int32)
+        q_rot = np.empty((nq, self._d), np.float32)
         probes = np.empty((nq, P), np.int32)
         tpos = np.empty((nq, ck), np.int32)
         tdist = np.empty((nq, ck), np.float32)
         _check(lib().jhq_search_debug(self._h, _ptr(q), nq, int(k), _ptr(dists), _ptr(ids),
-                                      _ptr(probes), _ptr(tpos), _ptr(tdist)))
-        return dict(dists=dists, ids=ids, probes=probes, topck_pos=tpos, topck_dist=tdist)
+                                      _ptr(q_rot), _ptr(probes), _ptr(tpos), _ptr(tdist)))
+        return dict(dists=dists, ids=ids, q_rot=q_rot, probes=probes, topck_pos=tpos,
+                    topck_dist=tdist)
 
     def set_timing(self, enable=True):
         _check(lib().jhq_set_timing(self._h, 1 if enable else 0))

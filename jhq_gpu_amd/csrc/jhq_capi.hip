@@ -269,10 +269,10 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
               int32_t* d_ids, bool want_topck, hipStream_t s) {
     const int d = ix->d;
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
-    JHQ_HIP(jhq::gemm_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, ix->wqrot.p, d, true, s));
+    JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, ix->wqrot.p, d, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
-    JHQ_HIP(jhq::gemm_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
-                               ix->wscores.p, ix->nlist, true, s));
+    JHQ_HIP(jhq::mfma_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
+                               ix->wscores.p, ix->nlist, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dlist_padoff.p,
                                ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, s));
@@ -307,7 +307,7 @@ int check_searchable(jhq_index* ix, int64_t nq, int k) {
 }
 
 int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, int32_t* ids,
-                int32_t* probes, int32_t* topck_pos, float* topck_dist) {
+                float* q_rot, int32_t* probes, int32_t* topck_pos, float* topck_dist) {
     JHQ_TRY(check_searchable(ix, nq, k));
     if (nq == 0) return JHQ_OK;
     const int d = ix->d;
@@ -323,7 +323,7 @@ int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, 
         std::memcpy(ix->h_q, q + q0 * d, static_cast<size_t>(Bq) * d * sizeof(float));
         JHQ_HIP(hipMemcpyAsync(ix->wq.p, ix->h_q, static_cast<size_t>(Bq) * d * sizeof(float),
                                hipMemcpyHostToDevice, ix->stream));
-        const bool dbg = (probes || topck_pos || topck_dist);
+        const bool dbg = (q_rot || probes || topck_pos || topck_dist);
         JHQ_TRY(run_batch(ix, ix->wq.p, Bq, k, bp, ix->wout_d.p, ix->wout_i.p, dbg, ix->stream));
         JHQ_HIP(hipMemcpyAsync(ix->h_d, ix->wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
                                hipMemcpyDeviceToHost, ix->stream));
@@ -332,6 +332,10 @@ int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, 
         JHQ_HIP(hipStreamSynchronize(ix->stream));
         std::memcpy(dists + q0 * k, ix->h_d, static_cast<size_t>(Bq) * k * sizeof(float));
         std::memcpy(ids + q0 * k, ix->h_i, static_cast<size_t>(Bq) * k * sizeof(int32_t));
+        if (q_rot) {
+            JHQ_HIP(hipMemcpy(q_rot + q0 * d, ix->wqrot.p, static_cast<size_t>(Bq) * d * sizeof(float),
+                              hipMemcpyDeviceToHost));
+        }
         if (probes) {
             JHQ_HIP(hipMemcpy(probes + q0 * bp.P, ix->wprobes.p,
                               static_cast<size_t>(Bq) * bp.P * sizeof(int32_t),
@@ -602,13 +606,14 @@ int jhq_add(jhq_index* ix, const float* x, int64_t n) {
 
 int jhq_search(jhq_index* idx, const float* q, int64_t nq, int k, float* dists, int32_t* ids) {
     if (!q || !dists || !ids) return fail(JHQ_EINVAL, "null argument");
-    return search_host(idx, q, nq, k, dists, ids, nullptr, nullptr, nullptr);
+    return search_host(idx, q, nq, k, dists, ids, nullptr, nullptr, nullptr, nullptr);
 }
 
 int jhq_search_debug(jhq_index* idx, const float* q, int64_t nq, int k, float* dists,
-                     int32_t* ids, int32_t* probes, int32_t* topck_pos, float* topck_dist) {
+                     int32_t* ids, float* q_rot, int32_t* probes, int32_t* topck_pos,
+                     float* topck_dist) {
     if (!q || !dists || !ids) return fail(JHQ_EINVAL, "null argument");
-    return search_host(idx, q, nq, k, dists, ids, probes, topck_pos, topck_dist);
+    return search_host(idx, q, nq, k, dists, ids, q_rot, probes, topck_pos, topck_dist);
 }
 
 int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float* d_dists,

@@ -25,6 +25,13 @@ hipError_t gemm_nt_score(const float* A, int64_t lda, const float* Bm, int64_t l
 hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t ldb,
                           int64_t n, int m, int d, const float* norms,
                           unsigned long long* keys, hipStream_t s);
+// The same products on fp32 MFMA for the query side (rotation, centroid
+// scores); not a fixed summation order, so only distances and near-tie probe
+// choices depend on it, never the stored codes.
+hipError_t mfma_nt_store(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
+                         int K, float* C, int64_t ldc, hipStream_t s);
+hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
+                         int K, const float* norms, float* C, int64_t ldc, hipStream_t s);
 hipError_t fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
 hipError_t keys_to_assign(const unsigned long long* keys, int64_t n, int32_t* assign,
                           hipStream_t s);

@@ -20,6 +20,7 @@
 #include "kernels.h"
 
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <cstdint>
 
 // Scan workgroup size and code-load pipeline depth (subspaces in flight).
@@ -560,6 +561,144 @@ hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t 
                                                         norms, keys, s);
 }
 
+// ---------------------------------------------------------------------------
+// Query-side GEMMs on fp32 MFMA (v_mfma_f32_16x16x4f32):
+//   C[b][n] = sum_k A[b][k] * Bm[n][k]      (EPI_STORE: query rotation)
+//   C[b][n] = norms[n] - 2 * that           (EPI_SCORE: centroid scores)
+// Operand layout of the instruction: lane l supplies A[l%16][k_l] and
+// Bm[l%16][k_l] where lane group g = l/16 owns the k values; lane l receives
+// D[4*(l/16)+j][l%16], j < 4.  Each k index is assigned to one (lane group,
+// step) pair: group g walks its own contiguous quarter of the wave's K slice,
+// so each lane streams two contiguous runs (one A row, one Bm row) with
+// 128-bit loads.  One wave per 16x16 output tile and K slice; the S waves of a
+// workgroup split K and their partial tiles are added in LDS in wave order.
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int S, int EPI, bool VEC>
+__global__ void __launch_bounds__(64 * S)
+mfma_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
+               int64_t ldb, int nb, int N, int K, float* __restrict__ C, int64_t ldc,
+               const float* __restrict__ norms) {
+    __shared__ v4f red[S > 1 ? (S - 1) * 64 : 1];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int b0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+    const int Ks = (K + S - 1) / S;
+    const int kbeg = wv * Ks, kend = min(K, kbeg + Ks);
+    const int Kq = (Ks + 3) / 4;  // steps of this wave (every lane issues all of them)
+    const int ka = kbeg + g * Kq;
+    const int kz = min(kend, ka + Kq);
+    const bool arow = (b0 + r) < nb, brow = (n0 + r) < N;
+    const float* ap = A + (int64_t)(arow ? b0 + r : 0) * lda;
+    const float* bp = Bm + (int64_t)(brow ? n0 + r : 0) * ldb;
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    if (VEC) {
+        // K % (64*S) == 0, rows 16-byte aligned: every lane's run is whole
+        // float4s, fetched 4 deep (16 k-steps) with the next 4 in flight
+        // rows past the edge read the clamped row 0; they only feed output
+        // rows / columns that are never stored, so the loads stay unconditional
+        constexpr int D = 4;
+        const float4* a4 = (const float4*)(ap + ka);
+        const float4* b4 = (const float4*)(bp + ka);
+        const int n4 = Kq / 4;
+        float4 an[D], bn[D];
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            an[u] = a4[u];
+            bn[u] = b4[u];
+        }
+        for (int i = 0; i < n4; i += D) {
+            float4 ac[D], bc[D];
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                ac[u] = an[u];
+                bc[u] = bn[u];
+            }
+            if (i + D < n4) {
+#pragma unroll
+                for (int u = 0; u < D; u++) {
+                    an[u] = a4[i + D + u];
+                    bn[u] = b4[i + D + u];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u].x, bc[u].x, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u].y, bc[u].y, acc1, 0, 0, 0);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u].z, bc[u].z, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u].w, bc[u].w, acc1, 0, 0, 0);
+            }
+        }
+    } else {
+        for (int st = 0; st < Kq; st++) {
+            const int k = ka + st;
+            const bool ok = k < kz;
+            const float av = (arow && ok) ? ap[k] : 0.0f;
+            const float bv = (brow && ok) ? bp[k] : 0.0f;
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc0, 0, 0, 0);
+        }
+    }
+    v4f acc = acc0 + acc1;
+    if (S > 1) {
+        if (wv > 0) red[(wv - 1) * 64 + lane] = acc;
+        __syncthreads();
+        if (wv > 0) return;
+#pragma unroll
+        for (int w2 = 0; w2 < S - 1; w2++) acc += red[w2 * 64 + lane];
+    }
+    const int col = n0 + r;
+    if (col >= N) return;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int row = b0 + 4 * g + j;
+        if (row < nb) {
+            float v = acc[j];
+            if (EPI == EPI_SCORE) v = fmaf(-2.0f, v, norms[col]);
+            C[(int64_t)row * ldc + col] = v;
+        }
+    }
+}
+
+template <int EPI>
+static hipError_t launch_mfma(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb,
+                              int N, int K, float* C, int64_t ldc, const float* norms,
+                              hipStream_t s) {
+    if (nb <= 0 || N <= 0) return hipSuccess;
+    const int64_t tiles = (int64_t)((N + 15) / 16) * ((nb + 15) / 16);
+    if ((nb + 15) / 16 > 65535) return hipErrorInvalidValue;
+    int S = 1;
+    while (S < 8 && tiles * S < 2048 && K / (S * 2) >= 64) S *= 2;
+    const bool vec = (K % (64 * S) == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                     ((uintptr_t)A % 16 == 0) && ((uintptr_t)Bm % 16 == 0);
+    dim3 grid((N + 15) / 16, (nb + 15) / 16);
+#define JHQ_MFMA_LAUNCH(SS)                                                                     \
+    if (vec)                                                                                  \
+        hipLaunchKernelGGL((mfma_nt_kernel<SS, EPI, true>), grid, dim3(64 * SS), 0, s, A, lda, \
+                           Bm, ldb, nb, N, K, C, ldc, norms);                                 \
+    else                                                                                      \
+        hipLaunchKernelGGL((mfma_nt_kernel<SS, EPI, false>), grid, dim3(64 * SS), 0, s, A,     \
+                           lda, Bm, ldb, nb, N, K, C, ldc, norms);
+    switch (S) {
+        case 1: JHQ_MFMA_LAUNCH(1) break;
+        case 2: JHQ_MFMA_LAUNCH(2) break;
+        case 4: JHQ_MFMA_LAUNCH(4) break;
+        default: JHQ_MFMA_LAUNCH(8) break;
+    }
+#undef JHQ_MFMA_LAUNCH
+    return hipGetLastError();
+}
+
+hipError_t mfma_nt_store(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
+                         int K, float* C, int64_t ldc, hipStream_t s) {
+    return launch_mfma<EPI_STORE>(A, lda, Bm, ldb, nb, N, K, C, ldc, nullptr, s);
+}
+
+hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
+                         int K, const float* norms, float* C, int64_t ldc, hipStream_t s) {
+    return launch_mfma<EPI_SCORE>(A, lda, Bm, ldb, nb, N, K, C, ldc, norms, s);
+}
+
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
@@ -733,19 +872,17 @@ hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n, 
 // Streaming exact top-k.
 //
 // The candidates of one selection arrive in rounds: in each round every
-// thread of the workgroup supplies up to 4 (value, tag) pairs (value ~0u =
-// no candidate).  The exact top-k by (value, tag) ascending is kept as a short
+// thread of the workgroup supplies CPT (value, tag) pairs (value ~0u = no
+// candidate).  The exact top-k by (value, tag) ascending is kept as a short
 // list of survivors in LDS:
-//   - bound: in the first round a bound is derived from the round itself.
-//     Each wave finds the c-th smallest of its values (c = ceil(k / waves))
-//     by c rounds of wave-min; the largest of these is >= at least k values,
-//     so no candidate above it can be in the top k.  Later the bound is the
-//     k-th smallest survivor after each prune.
-//   - survivors (value <= bound) are appended with one ballot per wave;
-//   - when the survivor list passes half its capacity it is pruned to the
-//     exact top-k (rank selection for short lists, radix selection else);
-//   - if a round overflows the list, the round's values (kept in rbuf) and
-//     the survivors from before the round are selected together.
+//   - bound: in the first round each wave contributes its c smallest values
+//     (c rounds of wave-min) and the bound is the k-th smallest of that pool,
+//     so at least k candidates are <= it; later the bound is the k-th
+//     smallest survivor after each prune;
+//   - survivors (value <= bound) are appended with one atomic per wave;
+//   - when the list passes half its capacity it is pruned to the exact top-k;
+//   - if a round does not fit, what fit is pruned, the bound tightens and the
+//     rest of the round (still in registers) is appended again.
 // Every step is exact: a candidate is dropped only when k kept candidates
 // precede it in (value, tag) order.
 // ---------------------------------------------------------------------------
@@ -774,8 +911,9 @@ __device__ __forceinline__ void rank_select(const unsigned long long* in, int n,
 
 // Exact top-k of n keys in LDS (n >= k, the first k are real) into out[0..k).
 template <int NT>
-__device__ __forceinline__ void select_keys(const unsigned long long* in, int n, int k, unsigned long long* out,
-                            int* idx, unsigned long long* tmp, SelState* st) {
+__device__ __forceinline__ void select_keys(const unsigned long long* in, int n, int k,
+                                            unsigned long long* out, int* idx,
+                                            unsigned long long* tmp, SelState* st) {
     if ((int64_t)n * n <= (int64_t)NT * 512) {
         rank_select<NT>(in, n, k, out);
     } else {
@@ -792,7 +930,6 @@ __host__ __device__ constexpr int est_per_wave(int k, int nw) {
 }
 
 struct StreamSel {
-    uint32_t* rbuf;             // [NT*4] values of the current round
     unsigned long long* skeys;  // [scap] survivors
     unsigned long long* kout;   // [k]
     unsigned long long* ktmp;   // [k]
@@ -812,25 +949,40 @@ __device__ __forceinline__ void stream_begin(const StreamSel& S) {
     }
 }
 
-// One round.  o[j] / tg[j]: this thread's values and tags; tag_of(s) returns
-// the tag of round slot s (= thread*4 + j) for the overflow path.
-template <int NT, class TagOf>
-__device__ __forceinline__ void stream_round(const StreamSel& S, int k, const uint32_t (&o)[4],
-                             const uint32_t (&tg)[4], TagOf tag_of,
-                             unsigned long long* stats = nullptr) {
+// Prunes the survivor list skeys[0..n) to its exact top-k and tightens the
+// bound.  Called by every thread; ends with a barrier.
+template <int NT>
+__device__ __forceinline__ void stream_prune(const StreamSel& S, int n, int k) {
+    select_keys<NT>(S.skeys, n, k, S.kout, S.kidx, S.ktmp, S.st);
+    for (int i = threadIdx.x; i < k; i += NT) S.skeys[i] = S.kout[i];
+    if (threadIdx.x == 0) {
+        S.ctl[0] = k;
+        S.ctl[1] = (int)min((uint32_t)S.ctl[1], (uint32_t)(S.kout[k - 1] >> 32));
+        S.ctl[2] = 1;
+    }
+    __syncthreads();
+}
+
+// One round: o[j] / tg[j] are this thread's values and tags.
+template <int NT, int CPT>
+__device__ __forceinline__ void stream_round(const StreamSel& S, int k, const uint32_t (&o)[CPT],
+                                             const uint32_t (&tg)[CPT],
+                                             unsigned long long* stats = nullptr) {
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int sn_before = S.ctl[0];
     const uint32_t Tcur = (uint32_t)S.ctl[1];
     const bool est = S.ctl[2] == 0;
-    *(uint4*)(S.rbuf + tid * 4) = make_uint4(o[0], o[1], o[2], o[3]);
     if (est) {
         // each wave contributes its c smallest values; the bound is the k-th
         // smallest of the pooled values (>= k values are <= it)
         const int c = est_per_wave(k, NW);
-        uint32_t t0 = o[0], t1 = o[1], t2 = o[2], t3 = o[3];
+        uint32_t t[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; j++) t[j] = o[j];
         for (int it = 0; it < c; it++) {
-            const uint32_t lm = min(min(t0, t1), min(t2, t3));
+            uint32_t lm = t[0];
+#pragma unroll
+            for (int j = 1; j < CPT; j++) lm = min(lm, t[j]);
             uint32_t m = lm;
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) m = min(m, (uint32_t)__shfl_xor((int)m, off));
@@ -838,10 +990,14 @@ __device__ __forceinline__ void stream_round(const StreamSel& S, int k, const ui
             if (m == ~0u) continue;
             const unsigned long long bal = __ballot(lm == m);
             if (lane == __ffsll((long long)bal) - 1) {
-                if (t0 == m) t0 = ~0u;
-                else if (t1 == m) t1 = ~0u;
-                else if (t2 == m) t2 = ~0u;
-                else t3 = ~0u;
+                bool hit = false;
+#pragma unroll
+                for (int j = 0; j < CPT; j++) {
+                    if (!hit && t[j] == m) {
+                        t[j] = ~0u;
+                        hit = true;
+                    }
+                }
             }
         }
         if (tid == 0) S.ctl[3] = (int)~0u;
@@ -864,86 +1020,63 @@ __device__ __forceinline__ void stream_round(const StreamSel& S, int k, const ui
         }
         __syncthreads();
         T = min(T, (uint32_t)S.ctl[3]);
-    }
-    // append survivors: one atomic per wave
-    bool p[4];
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        p[j] = (o[j] != ~0u) && (o[j] <= T);
-        cnt += p[j] ? 1 : 0;
-    }
-    int incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off);
-        if (lane >= off) incl += t;
-    }
-    int wbase = 0;
-    if (lane == 63 && incl) wbase = atomicAdd(&S.ctl[0], incl);
-    wbase = __shfl(wbase, 63);
-    int at = wbase + incl - cnt;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        if (p[j]) {
-            if (at < S.scap) S.skeys[at] = ((unsigned long long)o[j] << 32) | tg[j];
-            at++;
+        if (tid == 0 && T != ~0u) {
+            S.ctl[1] = (int)T;
+            S.ctl[2] = 1;
         }
     }
-    if (tid == 0 && est && T != ~0u) {
-        S.ctl[1] = (int)T;
-        S.ctl[2] = 1;
-    }
-    __syncthreads();
-    const int n_after = S.ctl[0];
-#ifdef JHQ_PHASE_TIMING
-    const unsigned long long st0 = wall_clock64();
-    if (stats && threadIdx.x == 0) {
-        stats[0] += (n_after > S.scap) ? 1 : 0;
-        stats[1] += (n_after <= S.scap && n_after > k && 2 * n_after >= S.scap) ? 1 : 0;
-        stats[2] += (unsigned long long)n_after;
-    }
-#endif
-    if (n_after > S.scap) {
-        // overflow: survivors from before this round plus this round's values
-        const int kk = min(k, n_after);
-        const int nb = sn_before;
-        block_topk<NT>(
-            [&](int i) -> uint32_t {
-                if (i < nb) return (uint32_t)(S.skeys[i] >> 32);
-                const uint32_t v = S.rbuf[i - nb];
-                return v <= T ? v : ~0u;
-            },
-            [&](int i) -> uint32_t {
-                if (i < nb) return (uint32_t)(S.skeys[i] & 0xffffffffull);
-                return tag_of(i - nb);
-            },
-            nb + NT * 4, kk, S.kidx, S.ktmp, S.kout, S.st);
-        for (int i = tid; i < kk; i += NT) S.skeys[i] = S.kout[i];
-        if (tid == 0) {
-            S.ctl[0] = kk;
-            if (kk == k) {
-                S.ctl[1] = (int)(uint32_t)(S.kout[kk - 1] >> 32);
-                S.ctl[2] = 1;
+    uint32_t pend = 0u;
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+        if (o[j] != ~0u && o[j] <= T) pend |= 1u << j;
+    for (;;) {
+        // append the pending survivors: one atomic per wave
+        const int cnt = __popc(pend);
+        int incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t2 = __shfl_up(incl, off);
+            if (lane >= off) incl += t2;
+        }
+        int wbase = 0;
+        if (lane == 63 && incl) wbase = atomicAdd(&S.ctl[0], incl);
+        wbase = __shfl(wbase, 63);
+        int at = wbase + incl - cnt;
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            if ((pend >> j) & 1u) {
+                if (at < S.scap) {
+                    S.skeys[at] = ((unsigned long long)o[j] << 32) | tg[j];
+                    pend &= ~(1u << j);
+                }
+                at++;
             }
         }
         __syncthreads();
-    } else if (n_after > k && 2 * n_after >= S.scap) {
-        select_keys<NT>(S.skeys, n_after, k, S.kout, S.kidx, S.ktmp, S.st);
-        for (int i = tid; i < k; i += NT) S.skeys[i] = S.kout[i];
-        if (tid == 0) {
-            S.ctl[0] = k;
-            S.ctl[1] = (int)min((uint32_t)S.ctl[1], (uint32_t)(S.kout[k - 1] >> 32));
-            S.ctl[2] = 1;
-        }
-        __syncthreads();
-    }
+        const int n_after = S.ctl[0];
 #ifdef JHQ_PHASE_TIMING
-    if (stats && threadIdx.x == 0) stats[3] += wall_clock64() - st0;
+        if (stats && tid == 0) {
+            stats[0] += (n_after > S.scap) ? 1 : 0;
+            stats[1] += (n_after <= S.scap && n_after > k && 2 * n_after >= S.scap) ? 1 : 0;
+            stats[2] += (unsigned long long)n_after;
+        }
 #endif
+        if (n_after > S.scap) {
+            // did not fit: prune what is stored, tighten the bound, retry
+            stream_prune<NT>(S, S.scap, k);
+            const uint32_t T2 = (uint32_t)S.ctl[1];
+#pragma unroll
+            for (int j = 0; j < CPT; j++)
+                if (((pend >> j) & 1u) && o[j] > T2) pend &= ~(1u << j);
+            if (!__syncthreads_or(pend != 0u)) break;
+        } else {
+            if (n_after > k && 2 * n_after >= S.scap) stream_prune<NT>(S, n_after, k);
+            break;
+        }
+    }
 }
 
-// Finishes a selection: out = S.kout[0..kk) sorted ascending; returns kk.
+// Finishes a selection: S.kout[0..kk) sorted ascending; returns kk.
 template <int NT>
 __device__ __forceinline__ int stream_end(const StreamSel& S, int k) {
     const int n = S.ctl[0];
@@ -954,12 +1087,11 @@ __device__ __forceinline__ int stream_end(const StreamSel& S, int k) {
 
 static int stream_scap(int k) { return 4 * k < 512 ? 512 : (4 * k + 63) / 64 * 64; }
 
-
 __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
 
 // LDS bytes of a StreamSel (rounded to 16 so that what follows stays aligned).
 static size_t stream_lds_bytes(int NT, int k) {
-    return align16((size_t)NT * 4 * 4 + (size_t)stream_scap(k) * 8 + (size_t)k * (8 + 8 + 4) +
+    return align16((size_t)stream_scap(k) * 8 + (size_t)k * (8 + 8 + 4) +
                    (size_t)(NT / 64) * est_per_wave(k, NT / 64) * 4 + 16 + sizeof(SelState));
 }
 
@@ -968,8 +1100,7 @@ static size_t stream_lds_bytes(int NT, int k) {
 template <int NT>
 __device__ unsigned char* stream_carve(unsigned char* p, int k, StreamSel* S) {
     S->scap = (4 * k < 512 ? 512 : (4 * k + 63) / 64 * 64);
-    S->rbuf = (uint32_t*)p;
-    S->skeys = (unsigned long long*)(S->rbuf + NT * 4);
+    S->skeys = (unsigned long long*)p;
     S->kout = S->skeys + S->scap;
     S->ktmp = S->kout + k;
     S->kidx = (int*)(S->ktmp + k);
@@ -1008,7 +1139,7 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
             o[j] = i < nlist ? f2ord(row[i]) : ~0u;
             tg[j] = (uint32_t)i;
         }
-        stream_round<NT>(S, P, o, tg, [&](int s) { return (uint32_t)(r * NT * 4 + s); });
+        stream_round<NT, 4>(S, P, o, tg);
     }
     const int kk = stream_end<NT>(S, P);
     for (int i = tid; i < P; i += NT) {
@@ -1168,6 +1299,8 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
 //     streaming selection above -> partial[segment][ck] keys
 //     (ord(dist) << 32 | pos), unfilled = ~0.
 // ---------------------------------------------------------------------------
+constexpr int kScanCPT = 4;  // candidates per thread per round
+
 template <int NT, int SU>
 __global__ void __launch_bounds__(NT)
 scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
@@ -1176,10 +1309,12 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
                   const int32_t* __restrict__ list_off, const int32_t* __restrict__ list_padoff,
                   const uint8_t* __restrict__ codes_t, int ck,
                   unsigned long long* __restrict__ partial) {
+    constexpr int CPT = kScanCPT, TPG = kGroup / CPT;  // threads per group of 16
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;
     StreamSel S;
-    int* qpre = (int*)stream_carve<NT>(smem + (size_t)M * 256 * 4, ck, &S);
+    float* sq = (float*)stream_carve<NT>(smem + (size_t)M * 256 * 4, ck, &S);  // [d] query
+    int* qpre = (int*)(sq + ((d + 3) & ~3));
     int* spre = qpre + B + 1;
     int32_t* sg = spre + B + 1;     // per probe: group prefix [P+1],
     int32_t* spad0 = sg + P + 1;    // padded start, padded size,
@@ -1214,7 +1349,7 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
         const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
         const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
         __syncthreads();
-        // probe metadata and the query's rotated vector (staged in rbuf)
+        // probe metadata and the query's rotated vector
         for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
         for (int i = tid; i < P; i += NT) {
             const int l = probes[(int64_t)b * P + i];
@@ -1224,7 +1359,6 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
             soff[i] = o0;
             snl[i] = list_off[l + 1] - o0;
         }
-        float* sq = (float*)S.rbuf;
         for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
         stream_begin<NT>(S);
         __syncthreads();
@@ -1233,28 +1367,30 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
         __syncthreads();
         JHQ_PHASE(1);
 
-        const int nq4 = (gB - gA) * 4;
-        const int rounds = (nq4 + NT - 1) / NT;
-        auto probe_of = [&](int g) {
-            int plo = 0, phi = P - 1;  // last p with sg[p] <= g
-            while (plo < phi) {
-                const int mid = (plo + phi + 1) >> 1;
-                if (sg[mid] <= g) plo = mid;
-                else phi = mid - 1;
-            }
-            return plo;
-        };
+        const int ntask = (gB - gA) * TPG;
+        const int rounds = (ntask + NT - 1) / NT;
         for (int r = 0; r < rounds; r++) {
-            const int qd = r * NT + tid;
-            uint32_t o[4] = {~0u, ~0u, ~0u, ~0u}, tg[4] = {0u, 0u, 0u, 0u};
-            if (qd < nq4) {
-                const int gq = gA * 4 + qd;
-                const int g = gq >> 2, sub = gq & 3;
-                const int plo = probe_of(g);
+            const int t = r * NT + tid;
+            uint32_t o[CPT], tg[CPT];
+#pragma unroll
+            for (int j = 0; j < CPT; j++) {
+                o[j] = ~0u;
+                tg[j] = 0u;
+            }
+            if (t < ntask) {
+                const int g = gA + t / TPG, sub = t % TPG;
+                int plo = 0, phi = P - 1;  // last p with sg[p] <= g
+                while (plo < phi) {
+                    const int mid = (plo + phi + 1) >> 1;
+                    if (sg[mid] <= g) plo = mid;
+                    else phi = mid - 1;
+                }
                 const int npad = snpad[plo], nl = snl[plo];
-                const int c0 = (g - sg[plo]) * kGroup + sub * 4;
+                const int c0 = (g - sg[plo]) * kGroup + sub * CPT;
                 const uint8_t* base = codes_t + (int64_t)spad0[plo] * M + c0;
-                float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+                float a[CPT];
+#pragma unroll
+                for (int j = 0; j < CPT; j++) a[j] = 0.0f;
                 // the next SU subspaces' code words are in flight while the
                 // current SU are gathered from the LUT
                 const int MS = M - M % SU;
@@ -1272,10 +1408,10 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
 #pragma unroll
                     for (int u = 0; u < SU; u++) {
                         const float* lm = lut + (m + u) * 256;
-                        a0 += lm[wc[u] & 0xffu];
-                        a1 += lm[(wc[u] >> 8) & 0xffu];
-                        a2 += lm[(wc[u] >> 16) & 0xffu];
-                        a3 += lm[wc[u] >> 24];
+                        a[0] += lm[wc[u] & 0xffu];
+                        a[1] += lm[(wc[u] >> 8) & 0xffu];
+                        a[2] += lm[(wc[u] >> 16) & 0xffu];
+                        a[3] += lm[wc[u] >> 24];
                     }
 #pragma unroll
                     for (int u = 0; u < SU; u++) wc[u] = wn[u];
@@ -1283,37 +1419,27 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
                 for (int m = MS; m < M; m++) {
                     const uint32_t ww = *(const uint32_t*)(base + (int64_t)m * npad);
                     const float* lm = lut + m * 256;
-                    a0 += lm[ww & 0xffu];
-                    a1 += lm[(ww >> 8) & 0xffu];
-                    a2 += lm[(ww >> 16) & 0xffu];
-                    a3 += lm[ww >> 24];
+                    a[0] += lm[ww & 0xffu];
+                    a[1] += lm[(ww >> 8) & 0xffu];
+                    a[2] += lm[(ww >> 16) & 0xffu];
+                    a[3] += lm[ww >> 24];
                 }
                 const uint32_t p0 = (uint32_t)(soff[plo] + c0);
-                o[0] = (c0 + 0 < nl) ? f2ord(a0) : ~0u;
-                o[1] = (c0 + 1 < nl) ? f2ord(a1) : ~0u;
-                o[2] = (c0 + 2 < nl) ? f2ord(a2) : ~0u;
-                o[3] = (c0 + 3 < nl) ? f2ord(a3) : ~0u;
-                tg[0] = p0;
-                tg[1] = p0 + 1u;
-                tg[2] = p0 + 2u;
-                tg[3] = p0 + 3u;
+#pragma unroll
+                for (int j = 0; j < CPT; j++) {
+                    o[j] = (c0 + j < nl) ? f2ord(a[j]) : ~0u;
+                    tg[j] = p0 + (uint32_t)j;
+                }
             }
 #ifdef JHQ_PHASE_TIMING
             __syncthreads();  // attribute the wait for the slowest wave to the scan
 #endif
             JHQ_PHASE(2);
-            stream_round<NT>(
-                S, ck, o, tg,
-                [&](int s) -> uint32_t {
-                    const int gq = gA * 4 + r * NT + (s >> 2);
-                    const int g = gq >> 2;
-                    const int plo = probe_of(g);
-                    return (uint32_t)(soff[plo] + (g - sg[plo]) * kGroup + (gq & 3) * 4 + (s & 3));
-                },
+            stream_round<NT, CPT>(S, ck, o, tg,
 #ifdef JHQ_PHASE_TIMING
-                ph_acc + 4
+                                  ph_acc + 4
 #else
-                nullptr
+                                  nullptr
 #endif
             );
             JHQ_PHASE(3);
@@ -1344,10 +1470,9 @@ constexpr int kProbeNT = 512;
 
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out) {
     const size_t lds = (size_t)M * 256 * 4 + stream_lds_bytes(kScanNT, ck) +
-                       (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 + (size_t)K1D * 4 +
-                       (kScanNT / 64) * 4 + 64;
+                       (size_t)((d + 3) & ~3) * 4 + (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 +
+                       (size_t)K1D * 4 + (kScanNT / 64) * 4 + 64;
     if (lds > (size_t)kLdsBytes - 1024) return false;
-    if ((size_t)d * 4 > (size_t)kScanNT * 16) return false;  // q staged in the round buffer
     out->G = target_wg;
     out->lds = (int)lds;
     out->max_segments = target_wg + B;
@@ -1394,12 +1519,13 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
                    int Kr, int Br, int bpv, const uint8_t* __restrict__ list_res,
                    const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
                    float* __restrict__ out_d, int32_t* __restrict__ out_i,
-                   unsigned long long* __restrict__ topck_dbg) {
+                   unsigned long long* __restrict__ topck_dbg, int stage_cap) {
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
     unsigned char* p = stream_carve<NT>(smem, ck, &S);
     unsigned long long* fkeys = (unsigned long long*)p;  // [ck] final-candidate keys
-    int* qpre = (int*)(fkeys + ck);
+    unsigned long long* stage = fkeys + ck;              // [stage_cap] segment lists
+    int* qpre = (int*)(stage + stage_cap);
     int* spre = qpre + B + 1;
     int* cpos = spre + B + 1;
     float* cprim = (float*)(cpos + ck);
@@ -1419,25 +1545,59 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     __syncthreads();
     JHQ_PHASE(0);
 
-    // merge the query's segment lists: 4 keys per thread per round
-    const int nkeys = (s1 - s0) * ck;
+    // merge the query's segment lists into the exact top-ck
+    const int nseg = s1 - s0;
+    const int nkeys = nseg * ck;
     const unsigned long long* src = partial + (int64_t)s0 * ck;
-    const int rounds = (nkeys + NT * 4 - 1) / (NT * 4);
-    for (int r = 0; r < rounds; r++) {
-        uint32_t o[4], tg[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = r * NT * 4 + threadIdx.x * 4 + j;
-            const unsigned long long kk = i < nkeys ? src[i] : ~0ull;
-            o[j] = (uint32_t)(kk >> 32);
-            tg[j] = (uint32_t)(kk & 0xffffffffull);
+    int ksel;
+    if (nkeys <= stage_cap) {
+        // each list is sorted ascending (~0 padded): the rank of key x from
+        // list a at index i in the union is i + sum over the other lists of
+        // the number of keys below x (keys are distinct)
+        for (int i = tid; i < nkeys; i += NT) stage[i] = src[i];
+        if (tid == 0) S.ctl[0] = 0;
+        __syncthreads();
+        int nv = 0;
+        for (int i = tid; i < nkeys; i += NT) nv += stage[i] != ~0ull ? 1 : 0;
+        for (int off = 32; off > 0; off >>= 1) nv += __shfl_xor(nv, off);
+        if ((tid & 63) == 0 && nv) atomicAdd(&S.ctl[0], nv);
+        __syncthreads();
+        ksel = min(ck, S.ctl[0]);
+        for (int idx = tid; idx < nkeys; idx += NT) {
+            const unsigned long long x = stage[idx];
+            if (x == ~0ull) continue;
+            const int a = idx / ck;
+            int r = idx - a * ck;
+            for (int bl = 0; bl < nseg && r < ksel; bl++) {
+                if (bl == a) continue;
+                const unsigned long long* L = stage + bl * ck;
+                int lo = 0, hi = ck;  // first index with L[i] >= x
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (L[mid] < x) lo = mid + 1;
+                    else hi = mid;
+                }
+                r += lo;
+            }
+            if (r < ksel) S.kout[r] = x;
         }
-        stream_round<NT>(S, ck, o, tg, [&](int s) {
-            const int i = r * NT * 4 + s;
-            return (uint32_t)(src[i] & 0xffffffffull);
-        });
+        __syncthreads();
+    } else {
+        // many segments: streaming selection, 4 keys per thread per round
+        const int rounds = (nkeys + NT * 4 - 1) / (NT * 4);
+        for (int r = 0; r < rounds; r++) {
+            uint32_t o[4], tg[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = r * NT * 4 + threadIdx.x * 4 + j;
+                const unsigned long long kk = i < nkeys ? src[i] : ~0ull;
+                o[j] = (uint32_t)(kk >> 32);
+                tg[j] = (uint32_t)(kk & 0xffffffffull);
+            }
+            stream_round<NT, 4>(S, ck, o, tg);
+        }
+        ksel = stream_end<NT>(S, ck);
     }
-    const int ksel = stream_end<NT>(S, ck);
     JHQ_PHASE(1);
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
@@ -1557,13 +1717,15 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* qtot, i
                        int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s) {
     constexpr int NT = kRefineNT;
     if (k > ck) return hipErrorInvalidValue;
-    const size_t lds = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)(2 * (B + 1)) * 4 +
-                       (size_t)ck * 4 * 2 + (NT / 64) * 4 + (size_t)(d + d / 32 + 1) * 4 + 16;
+    const int stage_cap = std::max(4096, 8 * ck);
+    const size_t lds = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)stage_cap * 8 +
+                       (size_t)(2 * (B + 1)) * 4 + (size_t)ck * 4 * 2 + (NT / 64) * 4 +
+                       (size_t)(d + d / 32 + 1) * 4 + 16;
     static const int max_dyn = allow_max_lds((const void*)refine_topk_kernel<NT>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, qtot, B, sh.G,
                        ck, k, q_rot, d, res_c1d, Kr, Br, bpv, list_res, list_corr, list_ids, out_d,
-                       out_i, topck_dbg);
+                       out_i, topck_dbg, stage_cap);
     return hipGetLastError();
 }
 

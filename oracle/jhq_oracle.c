@@ -513,6 +513,14 @@ int o_ck(float alpha, int k) {
 int o_search(const o_index* ix, const float* q, int64_t nq, int k,
              float* out_dist, int32_t* out_ids,
              int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist) {
+    return o_search_ex(ix, q, NULL, NULL, nq, k, out_dist, out_ids, dbg_probes,
+                       dbg_topck_pos, dbg_topck_dist);
+}
+
+int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
+                const int32_t* probes_in, int64_t nq, int k,
+                float* out_dist, int32_t* out_ids,
+                int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist) {
     const int d = ix->d, M = ix->M, nlist = ix->nlist;
     const int nprobe = ix->nprobe < nlist ? ix->nprobe : nlist;
     const int ck = o_ck(ix->alpha, k);
@@ -530,12 +538,17 @@ int o_search(const o_index* ix, const float* q, int64_t nq, int k,
     for (int c = 0; c < nlist; c++) cids[c] = c;
 
     for (int64_t qi = 0; qi < nq; qi++) {
-        o_rotate(ix->P, q + qi * d, 1, d, q_rot);
-        /* centroid scores: ||c||^2 - 2<c,q> (search.cu:31-32) */
-        for (int c = 0; c < nlist; c++)
-            scores[c] = fmaf(-2.0f, dot_fma(q_rot, ix->cent + (int64_t)c * d, d),
-                             ix->cent_norms[c]);
-        o_select_topk_pairs(scores, cids, nlist, nprobe, pd, probes);
+        if (q_rot_in) memcpy(q_rot, q_rot_in + qi * d, (size_t)d * sizeof(float));
+        else o_rotate(ix->P, q + qi * d, 1, d, q_rot);
+        if (probes_in) {
+            memcpy(probes, probes_in + qi * nprobe, (size_t)nprobe * sizeof(int32_t));
+        } else {
+            /* centroid scores: ||c||^2 - 2<c,q> (search.cu:31-32) */
+            for (int c = 0; c < nlist; c++)
+                scores[c] = fmaf(-2.0f, dot_fma(q_rot, ix->cent + (int64_t)c * d, d),
+                                 ix->cent_norms[c]);
+            o_select_topk_pairs(scores, cids, nlist, nprobe, pd, probes);
+        }
         if (dbg_probes) memcpy(dbg_probes + qi * nprobe, probes, (size_t)nprobe * sizeof(int32_t));
 
         int64_t total = 0;

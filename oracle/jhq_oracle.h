@@ -129,6 +129,14 @@ typedef struct {
 int o_search(const o_index* ix, const float* q, int64_t nq, int k,
              float* out_dist, int32_t* out_ids,
              int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist);
+/* Stage-wise variant: if q_rot_in != NULL it holds the rotated queries
+ * [nq][d] to use instead of rotating q; if probes_in != NULL it holds the
+ * probed lists [nq][nprobe] to use instead of selecting them.  The rest of
+ * the pipeline is o_search's. */
+int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
+                const int32_t* probes_in, int64_t nq, int k,
+                float* out_dist, int32_t* out_ids,
+                int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist);
 /* ck = max(k, ceil(alpha * k)) (jhq_v14_streaming_add/search.cu:408) */
 int o_ck(float alpha, int k);
 

@@ -56,6 +56,8 @@ _SIGS = {
     "o_select_topk_pairs": (_I, [_VP, _VP, _I64, _I, _VP, _VP]),
     "o_ck": (_I, [_F, _I]),
     "o_search": (_I, [ctypes.POINTER(_OIndex), _VP, _I64, _I, _VP, _VP, _VP, _VP, _VP]),
+    "o_search_ex": (_I, [ctypes.POINTER(_OIndex), _VP, _VP, _VP, _I64, _I, _VP, _VP, _VP, _VP,
+                         _VP]),
 }
 
 _REF_SIGS = {
@@ -374,21 +376,30 @@ class OracleIndex:
          s.list_codes, s.list_res, s.list_corr) = [_p(a) for a in self._keep]
         return s
 
-    def search(self, q, k, debug=False):
+    def search(self, q, k, debug=False, q_rot=None, probes=None):
+        """Reference pipeline per query.  Stage-wise parity: q_rot [nq, d] replaces
+        the rotation and probes [nq, nprobe] replaces the probe selection."""
         q = _c(q, np.float32)
         nq = q.shape[0]
+        if q_rot is not None:
+            q_rot = _c(q_rot, np.float32)
+            assert q_rot.shape == (nq, self.d)
+        if probes is not None:
+            probes = _c(probes, np.int32)
+            assert probes.shape == (nq, self.nprobe)
         ck = ck_of(self.alpha, k)
         dists = np.empty((nq, k), np.float32)
         ids = np.empty((nq, k), np.int32)
-        probes = np.empty((nq, self.nprobe), np.int32) if debug else None
         tpos = np.empty((nq, ck), np.int32) if debug else None
         tdist = np.empty((nq, ck), np.float32) if debug else None
         s = self._struct()
-        lib().o_search(ctypes.byref(s), _p(q), nq, k, _p(dists), _p(ids),
-                       _p(probes) if debug else None, _p(tpos) if debug else None,
-                       _p(tdist) if debug else None)
+        pr_out = np.empty((nq, self.nprobe), np.int32) if debug else None
+        lib().o_search_ex(ctypes.byref(s), _p(q), _p(q_rot) if q_rot is not None else None,
+                          _p(probes) if probes is not None else None, nq, k, _p(dists),
+                          _p(ids), _p(pr_out) if debug else None, _p(tpos) if debug else None,
+                          _p(tdist) if debug else None)
         if debug:
-            return dict(dists=dists, ids=ids, probes=probes, topck_pos=tpos, topck_dist=tdist)
+            return dict(dists=dists, ids=ids, probes=pr_out, topck_pos=tpos, topck_dist=tdist)
         return dists, ids
 
 
