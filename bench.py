@@ -217,6 +217,19 @@ def main():
     achieved = scan_bytes_per_launch / (scan_us * 1e-6) / 1e9
     dominant = max(step_us, key=step_us.get)
 
+    # HBM traffic per scan launch: FETCH_SIZE + WRITE_SIZE from the committed
+    # rocprofv3 counter runs (scaled by the calibration kernel), when they were
+    # taken at the operating point chosen above
+    traffic, traffic_note = None, "no counter run at this operating point"
+    tpath = os.path.join(ROOT, "profiles", "scan_topck_cfg2_traffic.json")
+    if os.path.exists(tpath) and args.scale == 1.0:
+        with open(tpath) as f:
+            tj = json.load(f)
+        if tj.get("nprobe") == npb and float(tj.get("alpha")) == float(alpha):
+            traffic = int(tj["traffic_bytes_per_launch"])
+            traffic_note = ("bytes per launch from %s (FETCH_SIZE x %.2f + WRITE_SIZE x %.2f)"
+                            % (tj["source"], tj["fetch_scale"], tj["write_scale"]))
+
     # reference protocol: host arrays, warm-up + mean of 5 search() calls
     ix.search(hq, K)
     t0 = time.time()
@@ -262,7 +275,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_note": traffic_note,
             "algorithmic_bytes_per_launch": int(scan_bytes_per_launch),
             "avg_launch_us": round(scan_us, 2),
         },
@@ -273,8 +287,9 @@ def main():
 
 def profile_mode(torch, dev, ix, q, k, batch, nprobe, alpha, nbatches):
     """A short, fixed workload for rocprofv3 counter runs: `nbatches` search
-    batches over distinct queries, then one plain device-to-device copy of
-    256 MiB whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters."""
+    batches over distinct queries, then one elementwise float32 kernel that
+    reads and writes 256 MiB; its FETCH_SIZE / WRITE_SIZE readings calibrate
+    the counters."""
     ix.set_nprobe(nprobe)
     ix.set_alpha(alpha)
     out_d = torch.empty((batch, k), dtype=torch.float32, device=dev)
@@ -287,11 +302,11 @@ def profile_mode(torch, dev, ix, q, k, batch, nprobe, alpha, nbatches):
     torch.cuda.synchronize()
     tm, nb = ix.timing()
     ix.set_timing(False)
-    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-    src.fill_(1)
+    # calibration: an elementwise float32 kernel that reads and writes 256 MiB
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    dst.copy_(src)
+    torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
     # algorithmic scan bytes of the profiled batches
     L = ix.lists(include_payload=False)
@@ -304,7 +319,8 @@ def profile_mode(torch, dev, ix, q, k, batch, nprobe, alpha, nbatches):
     print(json.dumps({"profile_batches": nbatches, "nprobe": nprobe, "alpha": alpha,
                       "scan_bytes_per_launch": tot / nbatches,
                       "step_us_per_batch": {k2: round(v * 1000.0 / nb, 2) for k2, v in tm.items()},
-                      "copy_bytes": 256 << 20}), flush=True)
+                      "calibration_kernel": "torch.mul(float32[64Mi], 1.0)",
+                      "calibration_bytes_each_way": 256 << 20}), flush=True)
 
 
 def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds):
