@@ -74,7 +74,10 @@ def gen_mixture(torch, dev, n, d, ncomp, seed, means=None, scales=None, chunk=10
     return out, means, scales
 
 
-def ground_truth(torch, base, q, k=10, short=100, chunk=256):
+def ground_truth(torch, base, q, k=10, width=100, short=200, chunk=256):
+    """Exact L2 neighbours: an fp32 GEMM short list of `short`, re-ranked in
+    float64.  Returns the top-`width` ids (the reference's GT files are 100
+    wide, scripts/preprocess.py:231); column order is exact distance order."""
     bn = (base.double() ** 2).sum(1).float()
     gt = []
     for i in range(0, q.shape[0], chunk):
@@ -83,15 +86,26 @@ def ground_truth(torch, base, q, k=10, short=100, chunk=256):
         cand = s.topk(short, dim=1, largest=False).indices
         xb = base[cand].double()
         dd = ((xb - qq.double()[:, None, :]) ** 2).sum(2)
-        order = dd.argsort(dim=1, stable=True)[:, :k]
+        order = dd.argsort(dim=1, stable=True)[:, :width]
         gt.append(torch.gather(cand, 1, order).cpu().numpy())
     return np.concatenate(gt)
 
 
 def recall_at(ids, gt, k=10):
+    """Standard k@k recall: |returned top-k & true top-k| / k."""
     hits = 0
     for a, b in zip(ids, gt):
         hits += len(set(a[:k].tolist()) & set(b[:k].tolist()))
+    return hits / (len(ids) * k)
+
+
+def recall_ref_def(ids, gt, k=10):
+    """The reference demos' definition: a returned id counts if it is anywhere
+    in the ground-truth row (examples/demo_jhq_v14_streaming_add.cu:15-27,
+    which loops over the GT file's full width)."""
+    hits = 0
+    for a, b in zip(ids, gt):
+        hits += len(set(a[:k].tolist()) & set(b.tolist()))
     return hits / (len(ids) * k)
 
 
@@ -175,11 +189,21 @@ def main():
             run_steps(nb)
             torch.cuda.synchronize()
             dt = time.time() - t0
-            rec = recall_at(out_i.cpu().numpy(), gt, K)
-            sweep.append(dict(alpha=alpha, nprobe=npb, qps=NQ / dt, recall_at_10=rec))
-            log(f"sweep alpha={alpha:g} nprobe={npb} qps={NQ / dt:.0f} recall@10={rec:.4f}")
+            ids_np = out_i.cpu().numpy()
+            rec = recall_at(ids_np, gt, K)
+            rec_ref = recall_ref_def(ids_np, gt, K)
+            sweep.append(dict(alpha=alpha, nprobe=npb, qps=NQ / dt, recall_at_10=rec,
+                              recall_ref_def=rec_ref))
+            log(f"sweep alpha={alpha:g} nprobe={npb} qps={NQ / dt:.0f} recall@10={rec:.4f} "
+                f"(reference definition, 10@100: {rec_ref:.4f})")
     ok = [s for s in sweep if s["recall_at_10"] >= 0.95]
-    chosen = max(ok, key=lambda s: s["qps"]) if ok else max(sweep, key=lambda s: s["recall_at_10"])
+    gate_met = bool(ok)
+    if not ok:
+        # the quantizer's recall ceiling is below the gate on this data: take
+        # the fastest point within 0.001 of the best recall
+        best = max(s["recall_at_10"] for s in sweep)
+        ok = [s for s in sweep if s["recall_at_10"] >= best - 1e-3]
+    chosen = max(ok, key=lambda s: s["qps"])
     npb, alpha = chosen["nprobe"], chosen["alpha"]
     ix.set_nprobe(npb)
     ix.set_alpha(alpha)
@@ -196,6 +220,7 @@ def main():
     qps = queries_timed / elapsed
     ms_per_step = elapsed * 1000.0 / Kst
     rec = recall_at(out_i.cpu().numpy(), gt, K)
+    rec_ref = recall_ref_def(out_i.cpu().numpy(), gt, K)
     log(f"timed nprobe={npb} steps={Kst} qps={qps:.0f} ms/step={ms_per_step:.4f} recall={rec:.4f}")
 
     # per-kernel HIP-event times over one pass (events on the kernels' stream)
@@ -260,6 +285,13 @@ def main():
                         "k=10, batch=64, queries resident in HBM" % alpha,
             "N": N, "nq": NQ, "nlist": NLIST, "nprobe": npb, "alpha": alpha, "k": K,
             "batch": BATCH, "recall_at_10": round(rec, 4),
+            "recall_gate_0.95_met": gate_met,
+            "recall_at_10_reference_definition": round(rec_ref, 4),
+            "recall_note": ("standard 10@10 against exact L2; the reference's published recalls "
+                            "count a hit anywhere in a 100-wide GT row (10@100, reported "
+                            "alongside). With M=128 B=8 Br=4 the JHQ estimate itself caps "
+                            "10@10 below 0.95 on this data (refining every candidate reaches "
+                            "0.8865 on a 50K sample), so the gate is unmet at every nprobe/alpha"),
             "sweep": [{k2: (round(v, 4) if isinstance(v, float) else v) for k2, v in s.items()}
                       for s in sweep],
             "qps_host_to_host": round(qps_host, 1),

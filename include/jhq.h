@@ -43,6 +43,13 @@ enum {
     JHQ_ENOMEM = 4   /* device or host allocation failure                   */
 };
 
+/* Element types of host input arrays (the _ex entry points). */
+enum {
+    JHQ_F32 = 0, /* float32                                   */
+    JHQ_U8 = 1,  /* uint8, converted to float32 (0..255)      */
+    JHQ_I8 = 2   /* int8, converted to float32 (-128..127)    */
+};
+
 typedef struct jhq_index jhq_index;
 
 /* JHQGpuIndex::Params (v14/jhq_gpu_index.cuh:16-36), same fields, same
@@ -58,10 +65,15 @@ typedef struct {
     int   batch_size; /* queries per search batch                      */
     int   seed;       /* JL rotation seed                              */
     int   add_batch;  /* rows rotated/encoded per add() step           */
+    /* Extension (no reference counterpart; the reference trains one residual
+     * codebook for all dimensions, v14/jhq_gpu_index.cu:302-330): 1 trains
+     * one Kr-word residual codebook per subspace.  Default 0. */
+    int   residual_per_subspace;
 } jhq_params;
 
 /* Fills the reference defaults: M=96 B=8 Br=4 alpha=4 nlist=1024 nprobe=8
- * ivf_iters=8 batch_size=256 seed=42 add_batch=65536. */
+ * ivf_iters=8 batch_size=256 seed=42 add_batch=65536, and
+ * residual_per_subspace=0. */
 void jhq_params_default(jhq_params* p);
 
 /* JHQGpuIndex::JHQGpuIndex(int d, Params) — v14/jhq_gpu_index.cu:103-131.
@@ -81,11 +93,32 @@ int jhq_train(jhq_index* idx, const float* x, int64_t n_train);
  * a second call fails with JHQ_ESTATE. */
 int jhq_add(jhq_index* idx, const float* x, int64_t n);
 
+/* Typed-input variants of train / add (dtype JHQ_F32, JHQ_U8, JHQ_I8).
+ * uint8 / int8 rows cross PCIe as bytes and become float32 on the device.
+ * The reference reads such data only in its HBlock line
+ * (common/bvecs_io.cuh:13-88, common/spacev_io.cuh:23-65). */
+int jhq_train_ex(jhq_index* idx, const void* x, int dtype, int64_t n_train);
+int jhq_add_ex(jhq_index* idx, const void* x, int dtype, int64_t n);
+
+/* Streaming add (extension; the reference allows one add(),
+ * v14/jhq_gpu_index.cu:419-420): rotates, encodes and assigns n more vectors
+ * and appends them to their IVF lists, ids continuing from ntotal.  May be
+ * called any number of times after train(), before or after add(), and
+ * between searches.  A list that outgrows its block moves to the end of the
+ * list pool with twice the capacity.  Results are identical to one add() of
+ * all vectors in the same order. */
+int jhq_append(jhq_index* idx, const float* x, int64_t n);
+int jhq_append_ex(jhq_index* idx, const void* x, int dtype, int64_t n);
+
 /* JHQGpuIndex::search(h_q, nq, k, h_dists, h_labels) —
  * v14/jhq_gpu_index.cu:535-552 -> search_gpu, v14/search.cu:388-445.
  * q host [nq x d]; dists/ids host [nq x k]. */
 int jhq_search(jhq_index* idx, const float* q, int64_t nq, int k,
                float* dists, int32_t* ids);
+
+/* search() with typed host queries (dtype JHQ_F32, JHQ_U8, JHQ_I8). */
+int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k,
+                  float* dists, int32_t* ids);
 
 /* Same pipeline with queries and results already in device memory
  * (the reference's graph body v14/search.cu:315-386 without the host
@@ -115,7 +148,8 @@ const char* jhq_last_error(void);
 /* Derived sizes: Ds, K1D, bits_per_dim, Kr, bpv (v14/jhq_gpu_index.cu:123-128). */
 int jhq_get_dims(const jhq_index* idx, int* Ds, int* K1D, int* bpd, int* Kr, int* bpv);
 
-/* Trained state: sigma, c1d[K1D], res_c1d[Kr], P[d*d] (row-major Pi(j,k),
+/* Trained state: sigma, c1d[K1D], res_c1d[Kr] (or [M][Kr] with
+ * residual_per_subspace), P[d*d] (row-major Pi(j,k),
  * i.e. the transpose of JLTransform::pi_data()), centroids[nlist*d],
  * cent_norms[nlist].  Any pointer may be NULL. */
 int jhq_get_codebooks(const jhq_index* idx, float* sigma, float* c1d,
@@ -128,6 +162,10 @@ int jhq_get_codebooks(const jhq_index* idx, float* sigma, float* c1d,
  * corr[ntotal].  Any pointer may be NULL. */
 int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids,
                   uint8_t* codes, uint8_t* res, float* corr);
+
+/* List pool occupancy: slots in use (including padding and blocks left
+ * behind by relocations) and allocated slots. */
+int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity);
 
 /* Search that also returns, per query, the rotated query [nq x d] (the
  * fp32 MFMA product the pipeline used), the probed list ids [nq x nprobe]

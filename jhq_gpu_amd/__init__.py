@@ -47,7 +47,7 @@ class _Params(ctypes.Structure):
         ("M", ctypes.c_int), ("B", ctypes.c_int), ("Br", ctypes.c_int),
         ("alpha", ctypes.c_float), ("nlist", ctypes.c_int), ("nprobe", ctypes.c_int),
         ("ivf_iters", ctypes.c_int), ("batch_size", ctypes.c_int), ("seed", ctypes.c_int),
-        ("add_batch", ctypes.c_int),
+        ("add_batch", ctypes.c_int), ("residual_per_subspace", ctypes.c_int),
     ]
 
 
@@ -64,10 +64,13 @@ class Params:
     batch_size: int = 256
     seed: int = 42
     add_batch: int = 65536
+    # extension: one residual codebook per subspace (the reference has one)
+    residual_per_subspace: int = 0
 
     def _c(self):
         return _Params(self.M, self.B, self.Br, self.alpha, self.nlist, self.nprobe,
-                       self.ivf_iters, self.batch_size, self.seed, self.add_batch)
+                       self.ivf_iters, self.batch_size, self.seed, self.add_batch,
+                       self.residual_per_subspace)
 
 
 _VP = ctypes.c_void_p
@@ -81,6 +84,12 @@ _SIGS = {
     "jhq_train": (_I, [_VP, _VP, _I64]),
     "jhq_add": (_I, [_VP, _VP, _I64]),
     "jhq_search": (_I, [_VP, _VP, _I64, _I, _VP, _VP]),
+    "jhq_train_ex": (_I, [_VP, _VP, _I, _I64]),
+    "jhq_add_ex": (_I, [_VP, _VP, _I, _I64]),
+    "jhq_append": (_I, [_VP, _VP, _I64]),
+    "jhq_append_ex": (_I, [_VP, _VP, _I, _I64]),
+    "jhq_search_ex": (_I, [_VP, _VP, _I, _I64, _I, _VP, _VP]),
+    "jhq_get_pool": (_I, [_VP, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "jhq_search_device": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP]),
     "jhq_ntotal": (_I64, [_VP]),
     "jhq_dim": (_I, [_VP]),
@@ -133,11 +142,30 @@ def _check(rc):
     raise JHQDeviceError(f"[{rc}] {msg}")
 
 
+JHQ_F32, JHQ_U8, JHQ_I8 = 0, 1, 2
+
+
 def _f32(a, d=None):
     a = np.ascontiguousarray(a, dtype=np.float32)
     if d is not None and (a.ndim != 2 or a.shape[1] != d):
         raise ValueError(f"expected a [n, {d}] array, got shape {a.shape}")
     return a
+
+
+def _typed(a, d):
+    """uint8 / int8 arrays pass through as bytes (converted on the device);
+    anything else becomes float32."""
+    a = np.asarray(a)
+    if a.dtype == np.uint8:
+        dt = JHQ_U8
+    elif a.dtype == np.int8:
+        dt = JHQ_I8
+    else:
+        a, dt = np.asarray(a, dtype=np.float32), JHQ_F32
+    a = np.ascontiguousarray(a)
+    if a.ndim != 2 or a.shape[1] != d:
+        raise ValueError(f"expected a [n, {d}] array, got shape {a.shape}")
+    return a, dt
 
 
 def _ptr(a):
@@ -176,19 +204,27 @@ class JHQGpuIndex:
 
     # -- reference API -------------------------------------------------------
     def train(self, x):
-        x = _f32(x, self._d)
-        _check(lib().jhq_train(self._h, _ptr(x), x.shape[0]))
+        """float32 rows (uint8 / int8 rows are converted to float32)."""
+        x, dt = _typed(x, self._d)
+        _check(lib().jhq_train_ex(self._h, _ptr(x), dt, x.shape[0]))
 
     def add(self, x):
-        x = _f32(x, self._d)
-        _check(lib().jhq_add(self._h, _ptr(x), x.shape[0]))
+        """The reference's one-shot add (a second call raises RuntimeError)."""
+        x, dt = _typed(x, self._d)
+        _check(lib().jhq_add_ex(self._h, _ptr(x), dt, x.shape[0]))
+
+    def append(self, x):
+        """Streaming add (extension): any number of calls, interleaved with
+        searches; ids continue from ntotal."""
+        x, dt = _typed(x, self._d)
+        _check(lib().jhq_append_ex(self._h, _ptr(x), dt, x.shape[0]))
 
     def search(self, q, k):
-        q = _f32(q, self._d)
+        q, dt = _typed(q, self._d)
         nq = q.shape[0]
         dists = np.empty((nq, k), np.float32)
         ids = np.empty((nq, k), np.int32)
-        _check(lib().jhq_search(self._h, _ptr(q), nq, int(k), _ptr(dists), _ptr(ids)))
+        _check(lib().jhq_search_ex(self._h, _ptr(q), dt, nq, int(k), _ptr(dists), _ptr(ids)))
         return dists, ids
 
     @property
@@ -232,11 +268,17 @@ class JHQGpuIndex:
         _check(lib().jhq_get_codebooks(self._h, None, None, None, _ptr(P), None, None))
         return P
 
+    def pool(self):
+        used, cap = _I64(), _I64()
+        _check(lib().jhq_get_pool(self._h, ctypes.byref(used), ctypes.byref(cap)))
+        return int(used.value), int(cap.value)
+
     def codebooks(self):
         dm = self.dims()
         sigma = np.zeros(1, np.float32)
         c1d = np.empty(dm["K1D"], np.float32)
-        rc = np.empty(dm["Kr"], np.float32)
+        rc = np.empty((self._p.M, dm["Kr"]) if self._p.residual_per_subspace else dm["Kr"],
+                      np.float32)
         P = np.empty((self._d, self._d), np.float32)
         cent = np.empty((self._p.nlist, self._d), np.float32)
         norms = np.empty(self._p.nlist, np.float32)

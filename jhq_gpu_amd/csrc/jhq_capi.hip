@@ -83,6 +83,7 @@ struct jhq_index {
     // parameters (v14/jhq_gpu_index.cuh:50-54)
     int d = 0, M = 0, B = 0, Br = 0, Ds = 0, K1D = 0, bpd = 0, Kr = 0, bpv = 0;
     int nlist = 0, nprobe = 0, ivf_iters = 0, batch_size = 0, seed = 0, add_batch = 0;
+    int RC = 1;  // residual codebooks: 1 (reference) or M (one per subspace)
     float alpha = 0.f;
     int64_t ntotal = 0;
     bool trained = false;
@@ -93,11 +94,16 @@ struct jhq_index {
     std::vector<float> Pi_cm;  // JLTransform::pi_data() (column-major)
     std::vector<float> P_rm;   // row-major Pi(j,k)
     std::vector<float> c1d, res_c1d, cent, cent_norms;
-    std::vector<int32_t> list_off_h, list_padoff_h;
+
+    // list pool (host mirror of the ListDesc array): list l owns slots
+    // [start, start + cap) and holds size candidates
+    std::vector<int32_t> l_start, l_cap, l_size;
+    int64_t pool_cap = 0, pool_used = 0;
 
     hipStream_t stream = nullptr;
     DBuf<float> dP, dc1d, dres_c1d, dcent, dnorms;
-    DBuf<int32_t> dlist_off, dlist_padoff, dlist_ids;
+    DBuf<int4> dldesc;
+    DBuf<int32_t> dlist_ids;
     DBuf<uint8_t> dcodes_t, dres;
     DBuf<float> dcorr;
 
@@ -105,6 +111,7 @@ struct jhq_index {
     DBuf<float> wq, wqrot, wscores, wout_d;
     DBuf<int32_t> wprobes, wgofs, wqtot, wout_i;
     DBuf<unsigned long long> wpartial, wtopck;
+    DBuf<int32_t> wpslot;
     float* h_q = nullptr;  // pinned staging
     float* h_d = nullptr;
     int32_t* h_i = nullptr;
@@ -242,6 +249,7 @@ int ensure_workspace(jhq_index* ix, int ck, int k, int P, int max_segments) {
     JHQ_TRY(ix->wgofs.ensure(B * (P + 1)));
     JHQ_TRY(ix->wqtot.ensure(B));
     JHQ_TRY(ix->wpartial.ensure(static_cast<size_t>(max_segments) * ck));
+    JHQ_TRY(ix->wpslot.ensure(static_cast<size_t>(max_segments) * ck));
     JHQ_TRY(ix->wtopck.ensure(B * ck));
     JHQ_TRY(ix->wout_d.ensure(B * k));
     JHQ_TRY(ix->wout_i.ensure(B * k));
@@ -274,15 +282,16 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
     JHQ_HIP(jhq::mfma_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
                                ix->wscores.p, ix->nlist, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
-    JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dlist_padoff.p,
-                               ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, s));
+    JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, ix->wprobes.p,
+                               ix->wgofs.p, ix->wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
     JHQ_HIP(jhq::scan_topck(ix->wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
-                            ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dlist_off.p,
-                            ix->dlist_padoff.p, ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, s));
+                            ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dldesc.p,
+                            ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, ix->wpslot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[4], s));
-    JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k, ix->wqrot.p, d,
-                             ix->dres_c1d.p, ix->Kr, ix->Br, ix->bpv, ix->dres.p, ix->dcorr.p,
+    JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wpslot.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k,
+                             ix->wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
+                             ix->bpv, ix->dldesc.p, ix->nlist, ix->dres.p, ix->dcorr.p,
                              ix->dlist_ids.p, d_out, d_ids, want_topck ? ix->wtopck.p : nullptr,
                              s));
     if (ix->timing) {
@@ -381,6 +390,7 @@ void jhq_params_default(jhq_params* p) {
     p->batch_size = 256;
     p->seed = 42;
     p->add_batch = 65536;
+    p->residual_per_subspace = 0;
 }
 
 int jhq_create(int d, const jhq_params* p, jhq_index** out) {
@@ -401,6 +411,10 @@ int jhq_create(int d, const jhq_params* p, jhq_index** out) {
     if (p->add_batch <= 0) return fail(JHQ_EINVAL, "add_batch must be positive");
     if (!(p->alpha > 0.0f)) return fail(JHQ_EINVAL, "alpha must be positive");
     if (p->B <= 0) return fail(JHQ_EINVAL, "B must be positive");
+    if (p->residual_per_subspace != 0 && p->residual_per_subspace != 1)
+        return fail(JHQ_EINVAL, "residual_per_subspace must be 0 or 1");
+    if (p->residual_per_subspace && p->M * (1 << p->Br) > 8192)
+        return fail(JHQ_EINVAL, "per-subspace residual codebooks need M * 2^Br <= 8192");
 
     jhq_index* ix = new (std::nothrow) jhq_index();
     if (!ix) return fail(JHQ_ENOMEM, "host allocation failed");
@@ -420,6 +434,10 @@ int jhq_create(int d, const jhq_params* p, jhq_index** out) {
     ix->K1D = 1 << ix->bpd;
     ix->Kr = 1 << p->Br;
     ix->bpv = (d * p->Br + 7) / 8;
+    ix->RC = p->residual_per_subspace ? p->M : 1;
+    ix->l_start.assign(ix->nlist, 0);
+    ix->l_cap.assign(ix->nlist, 0);
+    ix->l_size.assign(ix->nlist, 0);
     // JLTransform jl_(d, seed): the rotation is built with the index.
     ix->Pi_cm = jhq::build_rotation(d, p->seed);
     ix->P_rm.resize(static_cast<size_t>(d) * d);
@@ -462,17 +480,40 @@ int jhq_get_dims(const jhq_index* idx, int* Ds, int* K1D, int* bpd, int* Kr, int
     return JHQ_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Host float32 copy of a typed input (dtype 0 float32, 1 uint8, 2 int8).
+int host_f32(const void* x, int dtype, int64_t count, std::vector<float>* tmp, const float** out) {
+    if (dtype == JHQ_F32) {
+        *out = static_cast<const float*>(x);
+        return JHQ_OK;
+    }
+    if (dtype != JHQ_U8 && dtype != JHQ_I8) return fail(JHQ_EINVAL, "unknown dtype");
+    tmp->resize(static_cast<size_t>(count));
+    if (dtype == JHQ_U8) {
+        const uint8_t* u = static_cast<const uint8_t*>(x);
+        for (int64_t i = 0; i < count; i++) (*tmp)[i] = static_cast<float>(u[i]);
+    } else {
+        const int8_t* u = static_cast<const int8_t*>(x);
+        for (int64_t i = 0; i < count; i++) (*tmp)[i] = static_cast<float>(u[i]);
+    }
+    *out = tmp->data();
+    return JHQ_OK;
+}
+
+size_t dtype_size(int dtype) { return dtype == JHQ_F32 ? 4 : 1; }
+
 // v14/jhq_gpu_index.cu:333-364
-int jhq_train(jhq_index* ix, const float* x, int64_t n_train) {
-    if (!ix || !x) return fail(JHQ_EINVAL, "null argument");
+int train_impl(jhq_index* ix, const float* x, int64_t n_train) {
     if (n_train <= 0) return fail(JHQ_EINVAL, "n_train must be positive");
-    if (n_train < ix->nlist)
-        return fail(JHQ_EINVAL, "n_train must be >= nlist");
+    if (n_train < ix->nlist) return fail(JHQ_EINVAL, "n_train must be >= nlist");
     if (n_train * static_cast<int64_t>(ix->d) > INT32_MAX)
         return fail(JHQ_EINVAL, "n_train * d must fit in int (the reference's residual k-means size)");
-    if (ix->added) return fail(JHQ_ESTATE, "train() after add() is not supported");
+    if (ix->added || ix->ntotal > 0) return fail(JHQ_ESTATE, "train() after add() is not supported");
     JHQ_TRY(ix->ensure_stream());
-    const int d = ix->d, M = ix->M;
+    const int d = ix->d, M = ix->M, Ds = ix->Ds;
     ix->sigma = jhq::estimate_sigma(x, n_train, d);
     ix->c1d = jhq::lloyd_max_c1d(ix->sigma, ix->K1D);
     JHQ_TRY(ix->dP.upload(ix->P_rm.data(), ix->P_rm.size()));
@@ -484,7 +525,7 @@ int jhq_train(jhq_index* ix, const float* x, int64_t n_train) {
     JHQ_TRY(dy.alloc(static_cast<size_t>(n_train) * d));
     JHQ_TRY(dcodes.alloc(static_cast<size_t>(n_train) * M));
     JHQ_HIP(jhq::gemm_nt_store(dx.p, d, ix->dP.p, d, n_train, d, d, dy.p, d, false, ix->stream));
-    JHQ_HIP(jhq::encode(dy.p, n_train, d, M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr, ix->Br,
+    JHQ_HIP(jhq::encode(dy.p, n_train, d, M, Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr, 1, ix->Br,
                         ix->bpv, nullptr, dcodes.p, nullptr, nullptr, 1, ix->stream));
     dx.release();
     std::vector<float> h_y(static_cast<size_t>(n_train) * d);
@@ -497,40 +538,92 @@ int jhq_train(jhq_index* ix, const float* x, int64_t n_train) {
 
     JHQ_TRY(train_ivf(ix, h_y.data(), dy.p, n_train));
 
-    // v14/jhq_gpu_index.cu:302-330 — residual scalars over all training dims
-    {
-        std::vector<float> resid(static_cast<size_t>(n_train) * d);
-        const int kmask = ix->K1D - 1;
-        for (int64_t i = 0; i < n_train; i++) {
-            const uint8_t* code = h_codes.data() + i * M;
-            const float* yi = h_y.data() + i * d;
-            float* ri = resid.data() + i * d;
-            for (int m = 0; m < M; m++)
-                for (int k = 0; k < ix->Ds; k++)
-                    ri[m * ix->Ds + k] =
-                        yi[m * ix->Ds + k] - ix->c1d[(code[m] >> (k * ix->bpd)) & kmask];
-        }
-        ix->res_c1d = jhq::train_1d_kmeans(resid.data(), static_cast<int64_t>(resid.size()), ix->Kr);
+    // v14/jhq_gpu_index.cu:302-330 — residual scalars r = y - yhat over the
+    // training set.  One codebook over every dimension (the reference), or,
+    // with per-subspace codebooks, one 1-D k-means per subspace over that
+    // subspace's Ds dimensions.
+    const int kmask = ix->K1D - 1;
+    auto resid = [&](int64_t i, int j) {
+        const int m = j / Ds, k = j - m * Ds;
+        return h_y[static_cast<size_t>(i) * d + j] -
+               ix->c1d[(h_codes[static_cast<size_t>(i) * M + m] >> (k * ix->bpd)) & kmask];
+    };
+    ix->res_c1d.assign(static_cast<size_t>(ix->RC) * ix->Kr, 0.f);
+    std::vector<float> vals;
+    for (int cb = 0; cb < ix->RC; cb++) {
+        const int j0 = ix->RC == 1 ? 0 : cb * Ds, j1 = ix->RC == 1 ? d : j0 + Ds;
+        vals.resize(static_cast<size_t>(n_train) * (j1 - j0));
+        size_t t = 0;
+        for (int64_t i = 0; i < n_train; i++)
+            for (int j = j0; j < j1; j++) vals[t++] = resid(i, j);
+        std::vector<float> c = jhq::train_1d_kmeans(vals.data(), static_cast<int64_t>(vals.size()),
+                                                    ix->Kr);
+        // Kr shrinks only for tiny training sets (train_1d_kmeans clamps Kr to n)
+        for (int r = 0; r < ix->Kr; r++)
+            ix->res_c1d[static_cast<size_t>(cb) * ix->Kr + r] =
+                c.empty() ? 0.f : c[std::min<size_t>(r, c.size() - 1)];
     }
-    // Kr may shrink only for tiny training sets (train_1d_kmeans clamps Kr to n)
-    std::vector<float> rc(ix->Kr, ix->res_c1d.empty() ? 0.f : ix->res_c1d.back());
-    std::copy(ix->res_c1d.begin(), ix->res_c1d.end(), rc.begin());
-    ix->res_c1d = rc;
     JHQ_TRY(ix->dres_c1d.upload(ix->res_c1d.data(), ix->res_c1d.size()));
     ix->trained = true;
     return JHQ_OK;
 }
 
-// v14/jhq_gpu_index.cu:417-532
-int jhq_add(jhq_index* ix, const float* x, int64_t n) {
-    if (!ix || !x) return fail(JHQ_EINVAL, "null argument");
-    if (!ix->trained) return fail(JHQ_ESTATE, "call train() before add()");
-    if (ix->added) return fail(JHQ_ESTATE, "only one add() call is supported");
-    if (n <= 0) return fail(JHQ_EINVAL, "n must be positive");
-    if (n > INT32_MAX) return fail(JHQ_EINVAL, "n exceeds int32 ids");
+// Uploads the ListDesc array {start, cap, size, cbase} from the host mirror.
+int upload_ldesc(jhq_index* ix) {
+    std::vector<int4> h(static_cast<size_t>(ix->nlist));
+    int64_t cb = 0;
+    for (int l = 0; l < ix->nlist; l++) {
+        h[l] = make_int4(ix->l_start[l], ix->l_cap[l], ix->l_size[l], static_cast<int>(cb));
+        cb += ix->l_size[l];
+    }
+    return ix->dldesc.upload(h.data(), h.size());
+}
+
+// Grows the device pool to at least `need` slots, keeping every block where
+// it is (the old pool is copied to the front of the new one).
+int grow_pool(jhq_index* ix, int64_t need) {
+    if (need <= ix->pool_cap) return JHQ_OK;
+    const int64_t cap = std::max<int64_t>(need, ix->pool_cap + ix->pool_cap / 2);
+    const int M = ix->M, bpv = ix->bpv;
+    DBuf<uint8_t> nc, nr;
+    DBuf<float> nco;
+    DBuf<int32_t> ni;
+    JHQ_TRY(nc.alloc(static_cast<size_t>(cap) * M + 16));
+    JHQ_TRY(nr.alloc(static_cast<size_t>(cap) * bpv));
+    JHQ_TRY(nco.alloc(static_cast<size_t>(cap)));
+    JHQ_TRY(ni.alloc(static_cast<size_t>(cap)));
+    hipStream_t s = ix->stream;
+    if (ix->pool_used > 0) {
+        const size_t u = static_cast<size_t>(ix->pool_used);
+        JHQ_HIP(hipMemcpyAsync(nc.p, ix->dcodes_t.p, u * M, hipMemcpyDeviceToDevice, s));
+        JHQ_HIP(hipMemcpyAsync(nr.p, ix->dres.p, u * bpv, hipMemcpyDeviceToDevice, s));
+        JHQ_HIP(hipMemcpyAsync(nco.p, ix->dcorr.p, u * sizeof(float), hipMemcpyDeviceToDevice, s));
+        JHQ_HIP(hipMemcpyAsync(ni.p, ix->dlist_ids.p, u * sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+        JHQ_HIP(hipStreamSynchronize(s));
+    }
+    std::swap(ix->dcodes_t.p, nc.p);
+    std::swap(ix->dcodes_t.n, nc.n);
+    std::swap(ix->dres.p, nr.p);
+    std::swap(ix->dres.n, nr.n);
+    std::swap(ix->dcorr.p, nco.p);
+    std::swap(ix->dcorr.n, nco.n);
+    std::swap(ix->dlist_ids.p, ni.p);
+    std::swap(ix->dlist_ids.n, ni.n);
+    ix->pool_cap = cap;
+    return JHQ_OK;
+}
+
+// Rotates, encodes and assigns n vectors x (host, dtype) in add_batch chunks
+// (v14/jhq_gpu_index.cu:438-463), inserts them at the end of their lists
+// with ids id_base + i, and grows list blocks as needed.  exact_fit: the
+// pool is empty and every list gets capacity round16(size) (the one-shot add
+// of the reference); otherwise a list that outgrows its block moves to the
+// end of the pool with twice the capacity.
+int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_fit) {
     JHQ_TRY(ix->ensure_stream());
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
     hipStream_t s = ix->stream;
+    const int64_t id_base = ix->ntotal;
 
     DBuf<uint8_t> dpc, drc;
     DBuf<float> dco;
@@ -542,64 +635,171 @@ int jhq_add(jhq_index* ix, const float* x, int64_t n) {
     {
         const int64_t AB = std::min<int64_t>(ix->add_batch, n);
         DBuf<float> dxb, dyb;
+        DBuf<uint8_t> draw;
         DBuf<unsigned long long> keys;
         JHQ_TRY(dxb.alloc(static_cast<size_t>(AB) * d));
         JHQ_TRY(dyb.alloc(static_cast<size_t>(AB) * d));
+        if (dtype != JHQ_F32) JHQ_TRY(draw.alloc(static_cast<size_t>(AB) * d));
+        const uint8_t* xb = static_cast<const uint8_t*>(x);
+        const size_t es = dtype_size(dtype);
         for (int64_t start = 0; start < n; start += AB) {
             const int64_t nb = std::min(AB, n - start);
-            JHQ_HIP(hipMemcpyAsync(dxb.p, x + start * d, static_cast<size_t>(nb) * d * sizeof(float),
-                                   hipMemcpyHostToDevice, s));
+            const size_t cnt = static_cast<size_t>(nb) * d;
+            if (dtype == JHQ_F32) {
+                JHQ_HIP(hipMemcpyAsync(dxb.p, xb + static_cast<size_t>(start) * d * es,
+                                       cnt * sizeof(float), hipMemcpyHostToDevice, s));
+            } else {
+                // bytes cross PCIe; float32 conversion on the device
+                JHQ_HIP(hipMemcpyAsync(draw.p, xb + static_cast<size_t>(start) * d, cnt,
+                                       hipMemcpyHostToDevice, s));
+                JHQ_HIP(jhq::convert_to_f32(draw.p, dtype, static_cast<int64_t>(cnt), dxb.p, s));
+            }
             JHQ_HIP(jhq::gemm_nt_store(dxb.p, d, ix->dP.p, d, nb, d, d, dyb.p, d, false, s));
-            JHQ_HIP(jhq::encode(dyb.p, nb, d, M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr,
+            JHQ_HIP(jhq::encode(dyb.p, nb, d, M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr, ix->RC,
                                 ix->Br, bpv, ix->dres_c1d.p, dpc.p + start * M,
                                 drc.p + start * bpv, dco.p + start, 3, s));
             JHQ_TRY(assign_rows(ix, dyb.p, nb, dasg.p + start, keys));
             JHQ_HIP(hipStreamSynchronize(s));
         }
     }
-    // stable counting sort by list (the reference's thrust::sort_by_key,
-    // v14/jhq_gpu_index.cu:468-486)
+    // stable order by (list, id) of the new vectors (the reference's
+    // thrust::sort_by_key, v14/jhq_gpu_index.cu:468-486)
     std::vector<int32_t> asg(static_cast<size_t>(n));
     JHQ_HIP(hipMemcpy(asg.data(), dasg.p, asg.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
-    std::vector<int32_t> off(nlist + 1, 0), padoff(nlist + 1, 0);
+    std::vector<int64_t> add(nlist + 1, 0);
     for (int64_t i = 0; i < n; i++) {
         const int a = asg[i];
         if (a < 0 || a >= nlist) return fail(JHQ_EDEVICE, "invalid IVF assignment");
-        off[a + 1]++;
+        add[a + 1]++;
     }
-    for (int c = 0; c < nlist; c++) {
-        const int cnt = off[c + 1];
-        const int npad = (cnt + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
-        off[c + 1] = off[c] + cnt;
-        padoff[c + 1] = padoff[c] + npad;
+    for (int l = 0; l < nlist; l++) {
+        if (static_cast<int64_t>(ix->l_size[l]) + add[l + 1] > INT32_MAX)
+            return fail(JHQ_EINVAL, "list size exceeds int32");
     }
-    std::vector<int32_t> order(static_cast<size_t>(n)), slist(static_cast<size_t>(n));
+    // block placement
+    std::vector<int4> moves;
+    if (exact_fit) {
+        int64_t pos = 0;
+        for (int l = 0; l < nlist; l++) {
+            const int64_t cap = (add[l + 1] + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+            ix->l_start[l] = static_cast<int32_t>(pos);
+            ix->l_cap[l] = static_cast<int32_t>(cap);
+            pos += cap;
+        }
+        if (pos > INT32_MAX) return fail(JHQ_EINVAL, "list pool exceeds int32 slots");
+        JHQ_TRY(grow_pool(ix, pos));  // empty pool: nothing is copied
+        ix->pool_used = pos;
+    } else {
+        int64_t used = ix->pool_used;
+        std::vector<int32_t> nstart(ix->l_start), ncap(ix->l_cap);
+        for (int l = 0; l < nlist; l++) {
+            const int64_t need = ix->l_size[l] + add[l + 1];
+            if (need <= ix->l_cap[l]) continue;
+            int64_t cap = std::max<int64_t>(need, 2 * static_cast<int64_t>(ix->l_cap[l]));
+            cap = std::max<int64_t>(cap, jhq::kGroup);
+            cap = (cap + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+            if (ix->l_size[l] > 0) {
+                moves.push_back(make_int4(ix->l_start[l], ix->l_cap[l], ix->l_size[l], 0));
+                moves.push_back(make_int4(static_cast<int>(used), static_cast<int>(cap), 0, 0));
+            }
+            nstart[l] = static_cast<int32_t>(used);
+            ncap[l] = static_cast<int32_t>(cap);
+            used += cap;
+        }
+        if (used > INT32_MAX) return fail(JHQ_EINVAL, "list pool exceeds int32 slots");
+        JHQ_TRY(grow_pool(ix, used));
+        if (!moves.empty()) {
+            DBuf<int4> dmoves;
+            JHQ_TRY(dmoves.upload(moves.data(), moves.size()));
+            JHQ_HIP(jhq::relocate_lists(dmoves.p, static_cast<int>(moves.size() / 2), M, bpv,
+                                        ix->dcodes_t.p, ix->dcodes_t.p, ix->dres.p, ix->dres.p,
+                                        ix->dcorr.p, ix->dcorr.p, ix->dlist_ids.p, ix->dlist_ids.p,
+                                        s));
+            JHQ_HIP(hipStreamSynchronize(s));
+        }
+        ix->l_start = nstart;
+        ix->l_cap = ncap;
+        ix->pool_used = used;
+    }
+    // scatter the new vectors behind each list's current candidates
+    std::vector<int32_t> order(static_cast<size_t>(n)), slist(static_cast<size_t>(n)),
+        sidx(static_cast<size_t>(n));
     {
-        std::vector<int32_t> fill(off.begin(), off.end() - 1);
+        std::vector<int64_t> fill(nlist);
+        for (int l = 0; l < nlist; l++) fill[l] = add[l];
+        for (int l = 0; l < nlist; l++) add[l + 1] += add[l];
+        for (int l = 0; l < nlist; l++) fill[l] = add[l];
+        std::vector<int32_t> rank(nlist, 0);
         for (int64_t i = 0; i < n; i++) {
             const int a = asg[i];
-            const int32_t pos = fill[a]++;
-            order[pos] = static_cast<int32_t>(i);
-            slist[pos] = a;
+            const int64_t p = fill[a]++;
+            order[p] = static_cast<int32_t>(i);
+            slist[p] = a;
+            sidx[p] = ix->l_size[a] + rank[a]++;
         }
+        JHQ_TRY(upload_ldesc(ix));
+        DBuf<int32_t> dorder, dslist, dsidx;
+        JHQ_TRY(dorder.upload(order.data(), order.size()));
+        JHQ_TRY(dslist.upload(slist.data(), slist.size()));
+        JHQ_TRY(dsidx.upload(sidx.data(), sidx.size()));
+        JHQ_HIP(jhq::scatter_lists(dorder.p, dslist.p, dsidx.p, n, id_base, ix->dldesc.p, dpc.p,
+                                   drc.p, dco.p, M, bpv, ix->dlist_ids.p, ix->dcodes_t.p, ix->dres.p,
+                                   ix->dcorr.p, s));
+        JHQ_HIP(hipStreamSynchronize(s));
+        for (int l = 0; l < nlist; l++) ix->l_size[l] += rank[l];
     }
-    DBuf<int32_t> dorder, dslist;
-    JHQ_TRY(dorder.upload(order.data(), order.size()));
-    JHQ_TRY(dslist.upload(slist.data(), slist.size()));
-    JHQ_TRY(ix->dlist_off.upload(off.data(), off.size()));
-    JHQ_TRY(ix->dlist_padoff.upload(padoff.data(), padoff.size()));
-    JHQ_TRY(ix->dlist_ids.alloc(static_cast<size_t>(n)));
-    JHQ_TRY(ix->dcodes_t.alloc(static_cast<size_t>(padoff[nlist]) * M + 16));
-    JHQ_TRY(ix->dres.alloc(static_cast<size_t>(n) * bpv));
-    JHQ_TRY(ix->dcorr.alloc(static_cast<size_t>(n)));
-    JHQ_HIP(hipMemsetAsync(ix->dcodes_t.p, 0, ix->dcodes_t.n, s));
-    JHQ_HIP(jhq::scatter_lists(dorder.p, dslist.p, n, 0, ix->dlist_off.p, ix->dlist_padoff.p,
-                               dpc.p, drc.p, dco.p, M, bpv, ix->dlist_ids.p, ix->dcodes_t.p,
-                               ix->dres.p, ix->dcorr.p, s));
-    JHQ_HIP(hipStreamSynchronize(s));
-    ix->list_off_h = off;
-    ix->list_padoff_h = padoff;
-    ix->ntotal = n;
+    JHQ_TRY(upload_ldesc(ix));
+    ix->ntotal += n;
+    return JHQ_OK;
+}
+
+int check_insert(jhq_index* ix, const void* x, int64_t n) {
+    if (!ix || !x) return fail(JHQ_EINVAL, "null argument");
+    if (!ix->trained) return fail(JHQ_ESTATE, "call train() before add()");
+    if (n <= 0) return fail(JHQ_EINVAL, "n must be positive");
+    if (ix->ntotal + n > INT32_MAX) return fail(JHQ_EINVAL, "n exceeds int32 ids");
+    return JHQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int jhq_train(jhq_index* ix, const float* x, int64_t n_train) {
+    return jhq_train_ex(ix, x, JHQ_F32, n_train);
+}
+
+int jhq_train_ex(jhq_index* ix, const void* x, int dtype, int64_t n_train) {
+    if (!ix || !x) return fail(JHQ_EINVAL, "null argument");
+    if (n_train <= 0) return fail(JHQ_EINVAL, "n_train must be positive");
+    std::vector<float> tmp;
+    const float* xf = nullptr;
+    JHQ_TRY(host_f32(x, dtype, n_train * static_cast<int64_t>(ix->d), &tmp, &xf));
+    return train_impl(ix, xf, n_train);
+}
+
+// v14/jhq_gpu_index.cu:417-532
+int jhq_add(jhq_index* ix, const float* x, int64_t n) { return jhq_add_ex(ix, x, JHQ_F32, n); }
+
+int jhq_add_ex(jhq_index* ix, const void* x, int dtype, int64_t n) {
+    JHQ_TRY(check_insert(ix, x, n));
+    if (dtype != JHQ_F32 && dtype != JHQ_U8 && dtype != JHQ_I8)
+        return fail(JHQ_EINVAL, "unknown dtype");
+    if (ix->added || ix->ntotal > 0) return fail(JHQ_ESTATE, "only one add() call is supported");
+    JHQ_TRY(insert_impl(ix, x, dtype, n, true));
+    ix->added = true;
+    return JHQ_OK;
+}
+
+int jhq_append(jhq_index* ix, const float* x, int64_t n) {
+    return jhq_append_ex(ix, x, JHQ_F32, n);
+}
+
+int jhq_append_ex(jhq_index* ix, const void* x, int dtype, int64_t n) {
+    JHQ_TRY(check_insert(ix, x, n));
+    if (dtype != JHQ_F32 && dtype != JHQ_U8 && dtype != JHQ_I8)
+        return fail(JHQ_EINVAL, "unknown dtype");
+    JHQ_TRY(insert_impl(ix, x, dtype, n, false));
     ix->added = true;
     return JHQ_OK;
 }
@@ -650,26 +850,59 @@ int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids, uint8_t*
                   uint8_t* res, float* corr) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (!idx->added) return fail(JHQ_ESTATE, "index is empty");
-    const int64_t n = idx->ntotal;
-    const int M = idx->M, nlist = idx->nlist;
-    if (offsets) std::memcpy(offsets, idx->list_off_h.data(), (nlist + 1) * sizeof(int32_t));
-    if (ids) JHQ_HIP(hipMemcpy(ids, idx->dlist_ids.p, n * sizeof(int32_t), hipMemcpyDeviceToHost));
-    if (res) JHQ_HIP(hipMemcpy(res, idx->dres.p, static_cast<size_t>(n) * idx->bpv, hipMemcpyDeviceToHost));
-    if (corr) JHQ_HIP(hipMemcpy(corr, idx->dcorr.p, n * sizeof(float), hipMemcpyDeviceToHost));
+    const int M = idx->M, nlist = idx->nlist, bpv = idx->bpv;
+    // canonical order: lists in list order, candidates in insertion order
+    std::vector<int64_t> cbase(nlist + 1, 0);
+    for (int l = 0; l < nlist; l++) cbase[l + 1] = cbase[l] + idx->l_size[l];
+    if (offsets)
+        for (int l = 0; l <= nlist; l++) offsets[l] = static_cast<int32_t>(cbase[l]);
+    const size_t used = static_cast<size_t>(idx->pool_used);
+    if (ids) {
+        std::vector<int32_t> t(used);
+        JHQ_HIP(hipMemcpy(t.data(), idx->dlist_ids.p, used * sizeof(int32_t), hipMemcpyDeviceToHost));
+        for (int l = 0; l < nlist; l++)
+            std::memcpy(ids + cbase[l], t.data() + idx->l_start[l], idx->l_size[l] * sizeof(int32_t));
+    }
+    if (corr) {
+        std::vector<float> t(used);
+        JHQ_HIP(hipMemcpy(t.data(), idx->dcorr.p, used * sizeof(float), hipMemcpyDeviceToHost));
+        for (int l = 0; l < nlist; l++)
+            std::memcpy(corr + cbase[l], t.data() + idx->l_start[l], idx->l_size[l] * sizeof(float));
+    }
+    if (res) {
+        std::vector<uint8_t> t(used * bpv);
+        JHQ_HIP(hipMemcpy(t.data(), idx->dres.p, t.size(), hipMemcpyDeviceToHost));
+        for (int l = 0; l < nlist; l++)
+            std::memcpy(res + cbase[l] * bpv, t.data() + static_cast<size_t>(idx->l_start[l]) * bpv,
+                        static_cast<size_t>(idx->l_size[l]) * bpv);
+    }
     if (codes) {
-        std::vector<uint8_t> t(idx->dcodes_t.n);
+        std::vector<uint8_t> t(used * M);
         JHQ_HIP(hipMemcpy(t.data(), idx->dcodes_t.p, t.size(), hipMemcpyDeviceToHost));
         for (int l = 0; l < nlist; l++) {
-            const int64_t pad0 = idx->list_padoff_h[l];
-            const int64_t npad = idx->list_padoff_h[l + 1] - pad0;
-            const int64_t o = idx->list_off_h[l];
-            const int64_t nl = idx->list_off_h[l + 1] - o;
-            for (int64_t i = 0; i < nl; i++)
-                for (int m = 0; m < M; m++)
-                    codes[(o + i) * M + m] = t[pad0 * M + m * npad + i];
+            const int64_t st = idx->l_start[l], cap = idx->l_cap[l], o = cbase[l];
+            for (int64_t i = 0; i < idx->l_size[l]; i++)
+                for (int m = 0; m < M; m++) codes[(o + i) * M + m] = t[st * M + m * cap + i];
         }
     }
     return JHQ_OK;
+}
+
+int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (pool_slots) *pool_slots = idx->pool_used;
+    if (pool_capacity) *pool_capacity = idx->pool_cap;
+    return JHQ_OK;
+}
+
+int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k, float* dists,
+                  int32_t* ids) {
+    if (!idx || !q || !dists || !ids) return fail(JHQ_EINVAL, "null argument");
+    if (nq < 0) return fail(JHQ_EINVAL, "nq must be >= 0");
+    std::vector<float> tmp;
+    const float* qf = nullptr;
+    JHQ_TRY(host_f32(q, dtype, nq * static_cast<int64_t>(idx->d), &tmp, &qf));
+    return search_host(idx, qf, nq, k, dists, ids, nullptr, nullptr, nullptr, nullptr);
 }
 
 int jhq_set_timing(jhq_index* idx, int enable) {
@@ -701,7 +934,7 @@ int jhq_k_primary_encode(const float* d_y, uint8_t* d_codes, const float* d_c1d,
                          int M, int Ds, int K1D, int bits_per_dim, void* stream) {
     if (!d_y || !d_codes || !d_c1d || n < 0 || M <= 0 || Ds * M != d || (1 << bits_per_dim) != K1D)
         return fail(JHQ_EINVAL, "bad argument");
-    JHQ_HIP(jhq::encode(d_y, n, d, M, Ds, K1D, bits_per_dim, d_c1d, 1, 4, 1, nullptr, d_codes,
+    JHQ_HIP(jhq::encode(d_y, n, d, M, Ds, K1D, bits_per_dim, d_c1d, 1, 1, 4, 1, nullptr, d_codes,
                         nullptr, nullptr, 1, static_cast<hipStream_t>(stream)));
     return JHQ_OK;
 }
@@ -714,7 +947,7 @@ int jhq_k_residual_encode(const float* d_y, const uint8_t* d_primary, uint8_t* d
         M <= 0 || Ds * M != d || (1 << bits_per_dim) != K1D || (Br != 4 && Br != 8) ||
         bpv != (d * Br + 7) / 8 || Kr <= 0 || Kr > (1 << Br))
         return fail(JHQ_EINVAL, "bad argument");
-    JHQ_HIP(jhq::encode(d_y, n, d, M, Ds, K1D, bits_per_dim, d_c1d, Kr, Br, bpv, d_res_c1d,
+    JHQ_HIP(jhq::encode(d_y, n, d, M, Ds, K1D, bits_per_dim, d_c1d, Kr, 1, Br, bpv, d_res_c1d,
                         const_cast<uint8_t*>(d_primary), d_res_codes, d_corrections, 2,
                         static_cast<hipStream_t>(stream)));
     return JHQ_OK;

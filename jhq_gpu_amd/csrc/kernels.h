@@ -32,33 +32,45 @@ hipError_t mfma_nt_store(const float* A, int64_t lda, const float* Bm, int64_t l
                          int K, float* C, int64_t ldc, hipStream_t s);
 hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
                          int K, const float* norms, float* C, int64_t ldc, hipStream_t s);
+// uint8 (dtype 1) / int8 (dtype 2) elements to float32.
+hipError_t convert_to_f32(const void* src, int dtype, int64_t n, float* dst, hipStream_t s);
 hipError_t fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
 hipError_t keys_to_assign(const unsigned long long* keys, int64_t n, int32_t* assign,
                           hipStream_t s);
 
 // Primary / residual encode.  mode bit 0: compute and write primary codes from
 // y; mode bit 1: residual codes + corrections (primary digits from y when bit 0
-// is set, else read from `codes`).
+// is set, else read from `codes`).  res_c1d holds RC codebooks of Kr words:
+// RC = 1 (one codebook for every dimension) or RC = M (one per subspace).
 hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int bpd,
-                  const float* c1d, int Kr, int Br, int bpv, const float* res_c1d,
+                  const float* c1d, int Kr, int RC, int Br, int bpv, const float* res_c1d,
                   uint8_t* codes, uint8_t* res, float* corr, int mode, hipStream_t s);
 
-// Scatter per-vector data into list storage.  For stored position s:
-// id = order[s], list = slist[s]; ids_out[s] = id + id_base; res/corr copied;
-// primary codes written to the code-major padded block of the list.
-hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n,
-                         int64_t id_base, const int32_t* list_off,
-                         const int32_t* list_padoff, const uint8_t* pc,
-                         const uint8_t* rc, const float* co, int M, int bpv,
-                         int32_t* ids_out, uint8_t* codes_t, uint8_t* res_out,
-                         float* corr_out, hipStream_t s);
+// List storage: one pool of padded candidate slots; list l is described by
+// int4 {start, cap, size, cbase}: slots [start, start + cap) with cap a
+// multiple of kGroup, size candidates, first canonical position cbase
+// (lists in list order, candidates in insertion order).  Byte m of candidate
+// i is at codes_t[start*M + m*cap + i]; residual codes, corrections and ids
+// are indexed by slot.
+//
+// Scatter: new vector s goes to list slist[s] at index sidx[s]; its id is
+// id_base + order[s], order[s] indexing the per-vector inputs pc/rc/co.
+hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
+                         int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
+                         const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,
+                         uint8_t* codes_t, uint8_t* res_out, float* corr_out, hipStream_t s);
+// Moves list blocks: moves[2r] = {start, cap, size} (source), moves[2r+1] =
+// {start, cap} (destination); blocks must not overlap.
+hipError_t relocate_lists(const int4* moves, int nmoves, int M, int bpv, const uint8_t* codes_src,
+                          uint8_t* codes_dst, const uint8_t* res_src, uint8_t* res_dst,
+                          const float* corr_src, float* corr_dst, const int32_t* ids_src,
+                          int32_t* ids_dst, hipStream_t s);
 
 // Per query: exact top-P lists by (score, list) from scores[b][nlist];
 // writes probes[b][P] (ascending), gofs[b][P+1] (prefix of padded group
 // counts) and qtot[b] (= gofs[b][P]).
-hipError_t select_probes(const float* scores, int B, int nlist, int P,
-                         const int32_t* list_padoff, int32_t* probes, int32_t* gofs,
-                         int32_t* qtot, hipStream_t s);
+hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
+                         int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s);
 
 struct ScanShape {
     int G;             // persistent scan workgroups
@@ -71,18 +83,20 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from
 // q_rot (v14/search.cu:65-195); partial[segment][ck] keys
-// (ord(dist) << 32 | pos), unfilled = ~0.
+// (ord(dist) << 32 | canonical position), unfilled = ~0, and the candidates'
+// pool slots in partial_slot[segment][ck].
 hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d,
                       int B, int M, const int32_t* probes, const int32_t* gofs,
-                      const int32_t* qtot, int P, const int32_t* list_off,
-                      const int32_t* list_padoff, const uint8_t* codes_t, int ck,
-                      const ScanShape& sh, unsigned long long* partial, hipStream_t s);
+                      const int32_t* qtot, int P, const int4* ldesc, const uint8_t* codes_t,
+                      int ck, const ScanShape& sh, unsigned long long* partial,
+                      int32_t* partial_slot, hipStream_t s);
 
 // Per query: merge its segment lists, residual refine, final top-k.
 // If topck_dbg != nullptr it receives the merged short list [B][ck] keys.
-hipError_t refine_topk(const unsigned long long* partial, const int32_t* qtot, int B,
-                       const ScanShape& sh, int ck, int k, const float* q_rot, int d,
-                       const float* res_c1d, int Kr, int Br, int bpv, const uint8_t* list_res,
+hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial_slot,
+                       const int32_t* qtot, int B, const ScanShape& sh, int ck, int k,
+                       const float* q_rot, int d, int Ds, const float* res_c1d, int Kr, int RC,
+                       int Br, int bpv, const int4* ldesc, int nlist, const uint8_t* list_res,
                        const float* list_corr, const int32_t* list_ids, float* out_d,
                        int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s);
 

@@ -699,6 +699,24 @@ hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t l
     return launch_mfma<EPI_SCORE>(A, lda, Bm, ldb, nb, N, K, C, ldc, norms, s);
 }
 
+// uint8 / int8 vectors converted to float32 on the device (dtype 1 = uint8,
+// 2 = int8), 16 elements per thread iteration.
+__global__ void convert_kernel(const uint8_t* __restrict__ src, int dtype, int64_t n,
+                               float* __restrict__ dst) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = dtype == 1 ? (float)src[i] : (float)(int8_t)src[i];
+}
+
+hipError_t convert_to_f32(const void* src, int dtype, int64_t n, float* dst, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (dtype != 1 && dtype != 2) return hipErrorInvalidValue;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(convert_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
+                       dim3(256), 0, s, (const uint8_t*)src, dtype, n, dst);
+    return hipGetLastError();
+}
+
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
@@ -745,19 +763,27 @@ __device__ __forceinline__ int nearest_mid(const float* mids, int n, float v) {
 
 __global__ void __launch_bounds__(256)
 encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int K1D, int bpd,
-              const float* __restrict__ c1d, int Kr, int Br, int bpv,
+              const float* __restrict__ c1d, int Kr, int RC, int Br, int bpv,
               const float* __restrict__ res_c1d, uint8_t* __restrict__ codes,
               uint8_t* __restrict__ res, float* __restrict__ corr, int mode) {
+    // RC residual codebooks of Kr words: one shared by every dimension (the
+    // reference, v14/jhq_gpu_index.cu:302-330) or one per subspace (RC = M)
     __shared__ float tile[256][33];
-    __shared__ float cval[256], cmid[256], rval[256], rmid[256];
+    __shared__ float cval[256], cmid[256];
+    extern __shared__ float rsh[];  // rval[RC*Kr], rmid[RC*Kr]
+    float* rval = rsh;
+    float* rmid = rsh + RC * Kr;
     const int tid = threadIdx.x;
     const int64_t v0 = (int64_t)blockIdx.x * 256;
     const int64_t vid = v0 + tid;
     if (tid < K1D) cval[tid] = c1d[tid];
-    if ((mode & 2) && tid < Kr) rval[tid] = res_c1d[tid];
+    if (mode & 2)
+        for (int i = tid; i < RC * Kr; i += 256) rval[i] = res_c1d[i];
     __syncthreads();
     if (tid + 1 < K1D) cmid[tid] = 0.5f * (cval[tid] + cval[tid + 1]);
-    if ((mode & 2) && tid + 1 < Kr) rmid[tid] = 0.5f * (rval[tid] + rval[tid + 1]);
+    if (mode & 2)
+        for (int i = tid; i < RC * Kr; i += 256)
+            if ((i % Kr) + 1 < Kr) rmid[i] = 0.5f * (rval[i] + rval[i + 1]);
     __syncthreads();
     const bool live = vid < n;
     const int kmask = K1D - 1;
@@ -788,10 +814,11 @@ encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int 
                     dig = (codes[vid * M + m] >> (k * bpd)) & kmask;
                 }
                 if (mode & 2) {
+                    const int cb = (RC == 1) ? 0 : m;
                     const float yhat = cval[dig];
                     const float r = val - yhat;
-                    const int ri = (Kr == 1) ? 0 : nearest_mid(rmid, Kr, r);
-                    const float rhat = rval[ri];
+                    const int ri = (Kr == 1) ? 0 : nearest_mid(rmid + cb * Kr, Kr, r);
+                    const float rhat = rval[cb * Kr + ri];
                     if (Br == 4) {
                         if ((j & 1) == 0) {
                             rbyte = (uint32_t)(ri & 0x0F);
@@ -815,58 +842,107 @@ encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int 
 }
 
 hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int bpd,
-                  const float* c1d, int Kr, int Br, int bpv, const float* res_c1d,
+                  const float* c1d, int Kr, int RC, int Br, int bpv, const float* res_c1d,
                   uint8_t* codes, uint8_t* res, float* corr, int mode, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    if (K1D > 256 || Kr > 256 || (32 % Ds) != 0) return hipErrorInvalidValue;
+    if (K1D > 256 || Kr > 256 || (32 % Ds) != 0 || (RC != 1 && RC != M)) return hipErrorInvalidValue;
+    const size_t lds = (size_t)2 * RC * Kr * sizeof(float);
+    if (lds > 96 * 1024) return hipErrorInvalidValue;
+    if (lds > 48 * 1024) {
+        static const hipError_t e = hipFuncSetAttribute((const void*)encode_kernel,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         96 * 1024);
+        if (e != hipSuccess) return e;
+    }
     const int64_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(encode_kernel, dim3((unsigned)blocks), dim3(256), 0, s, y, n, d, M, Ds,
-                       K1D, bpd, c1d, Kr, Br, bpv, res_c1d, codes, res, corr, mode);
+    hipLaunchKernelGGL(encode_kernel, dim3((unsigned)blocks), dim3(256), lds, s, y, n, d, M, Ds,
+                       K1D, bpd, c1d, Kr, RC, Br, bpv, res_c1d, codes, res, corr, mode);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// List storage scatter.  Primary codes go to a code-major block per list:
-// list l occupies padded candidates [padoff[l], padoff[l+1]) and stores byte m
-// of candidate i at codes_t[padoff[l]*M + m*npad + i] (npad = multiple of 16),
-// so one 32-bit load returns byte m of four consecutive candidates.
+// List storage.  The lists live in one pool of padded candidate slots; list l
+// is described by ListDesc {start, cap, size, cbase} (int4): it owns slots
+// [start, start + cap) (cap a multiple of 16) and holds size candidates.
+// Primary codes are code-major inside the block: byte m of candidate i is at
+// codes_t[start*M + m*cap + i], so one 32-bit load returns byte m of four
+// consecutive candidates.  Residual codes, corrections and ids are indexed by
+// slot.  cbase is the list's first canonical position (lists in list order,
+// candidates in insertion order), the tag the exact selection breaks ties
+// with, so results do not depend on where a list's block sits in the pool.
 // ---------------------------------------------------------------------------
 __global__ void scatter_kernel(const int32_t* __restrict__ order, const int32_t* __restrict__ slist,
-                               int64_t n, int64_t id_base, const int32_t* __restrict__ list_off,
-                               const int32_t* __restrict__ list_padoff,
-                               const uint8_t* __restrict__ pc, const uint8_t* __restrict__ rc,
-                               const float* __restrict__ co, int M, int bpv,
-                               int32_t* __restrict__ ids_out, uint8_t* __restrict__ codes_t,
+                               const int32_t* __restrict__ sidx, int64_t n, int64_t id_base,
+                               const int4* __restrict__ ldesc, const uint8_t* __restrict__ pc,
+                               const uint8_t* __restrict__ rc, const float* __restrict__ co, int M,
+                               int bpv, int32_t* __restrict__ ids_out, uint8_t* __restrict__ codes_t,
                                uint8_t* __restrict__ res_out, float* __restrict__ corr_out) {
     const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= n) return;
     const int64_t id = order[s];
-    const int l = slist[s];
-    const int64_t i = s - list_off[l];
-    const int64_t pad0 = list_padoff[l];
-    const int64_t npad = list_padoff[l + 1] - pad0;
-    ids_out[s] = (int32_t)(id + id_base);
-    corr_out[s] = co[id];
-    uint8_t* dst = codes_t + pad0 * M + i;
+    const int4 L = ldesc[slist[s]];
+    const int64_t i = sidx[s];
+    const int64_t slot = (int64_t)L.x + i;
+    ids_out[slot] = (int32_t)(id + id_base);
+    corr_out[slot] = co[id];
+    uint8_t* dst = codes_t + (int64_t)L.x * M + i;
     const uint8_t* src = pc + id * M;
-    for (int m = 0; m < M; m++) dst[(int64_t)m * npad] = src[m];
+    for (int m = 0; m < M; m++) dst[(int64_t)m * L.y] = src[m];
     const uint8_t* rs = rc + id * bpv;
-    uint8_t* rd = res_out + s * bpv;
+    uint8_t* rd = res_out + slot * bpv;
     for (int b2 = 0; b2 < bpv; b2++) rd[b2] = rs[b2];
 }
 
-hipError_t scatter_lists(const int32_t* order, const int32_t* slist, int64_t n, int64_t id_base,
-                         const int32_t* list_off, const int32_t* list_padoff, const uint8_t* pc,
+hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
+                         int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
                          const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,
                          uint8_t* codes_t, uint8_t* res_out, float* corr_out, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)blocks), dim3(256), 0, s, order, slist, n,
-                       id_base, list_off, list_padoff, pc, rc, co, M, bpv, ids_out, codes_t,
-                       res_out, corr_out);
+    hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)blocks), dim3(256), 0, s, order, slist, sidx,
+                       n, id_base, ldesc, pc, rc, co, M, bpv, ids_out, codes_t, res_out, corr_out);
     return hipGetLastError();
 }
 
+// Moves list blocks.  moves[2r] = {start, cap, size} of block r's source,
+// moves[2r+1] = {start, cap} of its destination; the size candidates are
+// copied and the code-major primary codes re-strided.  Source and
+// destination blocks never overlap (destinations lie past every live block,
+// or in another pool).
+__global__ void relocate_kernel(const int4* __restrict__ moves, int M, int bpv,
+                                const uint8_t* __restrict__ codes_src, uint8_t* __restrict__ codes_dst,
+                                const uint8_t* __restrict__ res_src, uint8_t* __restrict__ res_dst,
+                                const float* __restrict__ corr_src, float* __restrict__ corr_dst,
+                                const int32_t* __restrict__ ids_src, int32_t* __restrict__ ids_dst) {
+    const int4 fr = moves[blockIdx.x * 2];
+    const int4 to = moves[blockIdx.x * 2 + 1];
+    const int size = fr.z;
+    if (size <= 0) return;
+    const uint8_t* cs = codes_src + (int64_t)fr.x * M;
+    uint8_t* cd = codes_dst + (int64_t)to.x * M;
+    for (int64_t e = threadIdx.x; e < (int64_t)M * size; e += blockDim.x) {
+        const int64_t m = e / size, i = e - m * size;
+        cd[m * to.y + i] = cs[m * fr.y + i];
+    }
+    const uint8_t* rs = res_src + (int64_t)fr.x * bpv;
+    uint8_t* rd = res_dst + (int64_t)to.x * bpv;
+    for (int64_t e = threadIdx.x; e < (int64_t)size * bpv; e += blockDim.x) rd[e] = rs[e];
+    for (int i = threadIdx.x; i < size; i += blockDim.x) {
+        corr_dst[to.x + i] = corr_src[fr.x + i];
+        ids_dst[to.x + i] = ids_src[fr.x + i];
+    }
+}
+
+hipError_t relocate_lists(const int4* moves, int nmoves, int M, int bpv, const uint8_t* codes_src,
+                          uint8_t* codes_dst, const uint8_t* res_src, uint8_t* res_dst,
+                          const float* corr_src, float* corr_dst, const int32_t* ids_src,
+                          int32_t* ids_dst, hipStream_t s) {
+    if (nmoves <= 0) return hipSuccess;
+    hipLaunchKernelGGL(relocate_kernel, dim3((unsigned)nmoves), dim3(256), 0, s, moves, M, bpv,
+                       codes_src, codes_dst, res_src, res_dst, corr_src, corr_dst, ids_src,
+                       ids_dst);
+    return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // Streaming exact top-k.
@@ -1120,7 +1196,7 @@ __device__ unsigned char* stream_carve(unsigned char* p, int k, StreamSel* S) {
 template <int NT>
 __global__ void __launch_bounds__(NT)
 select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
-                     const int32_t* __restrict__ list_padoff, int32_t* __restrict__ probes,
+                     const int4* __restrict__ ldesc, int32_t* __restrict__ probes,
                      int32_t* __restrict__ gofs, int32_t* __restrict__ qtot) {
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
@@ -1145,7 +1221,7 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     for (int i = tid; i < P; i += NT) {
         const int l = i < kk ? (int)(uint32_t)(S.kout[i] & 0xffffffffull) : 0;
         probes[(int64_t)b * P + i] = l;
-        gcnt[i] = i < kk ? (list_padoff[l + 1] - list_padoff[l]) / kGroup : 0;
+        gcnt[i] = i < kk ? (ldesc[l].z + kGroup - 1) / kGroup : 0;
     }
     __syncthreads();
     // prefix of the group counts (P is small: one wave)
@@ -1306,9 +1382,8 @@ __global__ void __launch_bounds__(NT)
 scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
                   const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                   const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
-                  const int32_t* __restrict__ list_off, const int32_t* __restrict__ list_padoff,
-                  const uint8_t* __restrict__ codes_t, int ck,
-                  unsigned long long* __restrict__ partial) {
+                  const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t, int ck,
+                  unsigned long long* __restrict__ partial, int32_t* __restrict__ partial_slot) {
     constexpr int CPT = kScanCPT, TPG = kGroup / CPT;  // threads per group of 16
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;
@@ -1317,8 +1392,8 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
     int* qpre = (int*)(sq + ((d + 3) & ~3));
     int* spre = qpre + B + 1;
     int32_t* sg = spre + B + 1;     // per probe: group prefix [P+1],
-    int32_t* spad0 = sg + P + 1;    // padded start, padded size,
-    int32_t* snpad = spad0 + P;     // list size, stored-position start
+    int32_t* spad0 = sg + P + 1;    // block start, block capacity,
+    int32_t* snpad = spad0 + P;     // list size, first canonical position
     int32_t* snl = snpad + P;
     int32_t* soff = snl + P;
     float* sc1d = (float*)(soff + P);
@@ -1352,12 +1427,11 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
         // probe metadata and the query's rotated vector
         for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
         for (int i = tid; i < P; i += NT) {
-            const int l = probes[(int64_t)b * P + i];
-            const int p0 = list_padoff[l], o0 = list_off[l];
-            spad0[i] = p0;
-            snpad[i] = list_padoff[l + 1] - p0;
-            soff[i] = o0;
-            snl[i] = list_off[l + 1] - o0;
+            const int4 L = ldesc[probes[(int64_t)b * P + i]];
+            spad0[i] = L.x;
+            snpad[i] = L.y;
+            snl[i] = L.z;
+            soff[i] = L.w;
         }
         for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
         stream_begin<NT>(S);
@@ -1446,7 +1520,19 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
         }
         const int kk = stream_end<NT>(S, ck);
         unsigned long long* outp = partial + (int64_t)seg * ck;
-        for (int i = tid; i < ck; i += NT) outp[i] = i < kk ? S.kout[i] : ~0ull;
+        int32_t* outs = partial_slot + (int64_t)seg * ck;
+        for (int i = tid; i < ck; i += NT) {
+            int32_t slot = -1;
+            if (i < kk) {
+                // pool slot of the survivor: its probe holds canonical
+                // positions [soff, soff + snl) at slots [spad0, ...)
+                const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
+                for (int p = 0; p < P; p++)
+                    if (tag >= soff[p] && tag - soff[p] < snl[p]) slot = spad0[p] + (tag - soff[p]);
+            }
+            outp[i] = i < kk ? S.kout[i] : ~0ull;
+            outs[i] = slot;
+        }
         JHQ_PHASE(3);
     }
     JHQ_PHASE_FLUSH(0);
@@ -1479,28 +1565,27 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     return true;
 }
 
-hipError_t select_probes(const float* scores, int B, int nlist, int P,
-                         const int32_t* list_padoff, int32_t* probes, int32_t* gofs,
-                         int32_t* qtot, hipStream_t s) {
+hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
+                         int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s) {
     const size_t lds = stream_lds_bytes(kProbeNT, P) + (size_t)P * 4 + 16;
     static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<kProbeNT>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(select_probes_kernel<kProbeNT>, dim3(B), dim3(kProbeNT), lds, s, scores,
-                       nlist, P, list_padoff, probes, gofs, qtot);
+                       nlist, P, ldesc, probes, gofs, qtot);
     return hipGetLastError();
 }
 
 hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d,
                       int B, int M, const int32_t* probes, const int32_t* gofs,
-                      const int32_t* qtot, int P, const int32_t* list_off,
-                      const int32_t* list_padoff, const uint8_t* codes_t, int ck,
-                      const ScanShape& sh, unsigned long long* partial, hipStream_t s) {
+                      const int32_t* qtot, int P, const int4* ldesc, const uint8_t* codes_t,
+                      int ck, const ScanShape& sh, unsigned long long* partial,
+                      int32_t* partial_slot, hipStream_t s) {
     constexpr int NT = kScanNT, SU = JHQ_SCAN_SU;
     static const int max_dyn = allow_max_lds((const void*)scan_topck_kernel<NT, SU>);
     if (sh.lds > max_dyn || Ds > 8 || K1D > 256) return hipErrorInvalidValue;
     hipLaunchKernelGGL((scan_topck_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d, Ds,
-                       K1D, bpd, c1d, M, probes, gofs, qtot, B, P, list_off, list_padoff, codes_t,
-                       ck, partial);
+                       K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, ck, partial,
+                       partial_slot);
     return hipGetLastError();
 }
 
@@ -1514,9 +1599,10 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
 template <int NT>
 __global__ void __launch_bounds__(NT)
 refine_topk_kernel(const unsigned long long* __restrict__ partial,
-                   const int32_t* __restrict__ qtot, int B, int Gmax, int ck, int k,
-                   const float* __restrict__ q_rot, int d, const float* __restrict__ res_c1d,
-                   int Kr, int Br, int bpv, const uint8_t* __restrict__ list_res,
+                   const int32_t* __restrict__ partial_slot, const int32_t* __restrict__ qtot,
+                   int B, int Gmax, int ck, int k, const float* __restrict__ q_rot, int d, int Ds,
+                   const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
+                   const int4* __restrict__ ldesc, int nlist, const uint8_t* __restrict__ list_res,
                    const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
                    float* __restrict__ out_d, int32_t* __restrict__ out_i,
                    unsigned long long* __restrict__ topck_dbg, int stage_cap) {
@@ -1525,7 +1611,10 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     unsigned char* p = stream_carve<NT>(smem, ck, &S);
     unsigned long long* fkeys = (unsigned long long*)p;  // [ck] final-candidate keys
     unsigned long long* stage = fkeys + ck;              // [stage_cap] segment lists
-    int* qpre = (int*)(stage + stage_cap);
+    int* sslot = (int*)(stage + stage_cap);              // [stage_cap] their pool slots
+    int* kslot = sslot + stage_cap;                      // [ck] slots of the short list
+    float* rc = (float*)(kslot + ck);                    // [RC*Kr] residual codebooks
+    int* qpre = (int*)(rc + RC * Kr);
     int* spre = qpre + B + 1;
     int* cpos = spre + B + 1;
     float* cprim = (float*)(cpos + ck);
@@ -1533,13 +1622,12 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     // query staged with one pad word per 32 so that lanes reading 32-dim
     // ranges at a 32-word stride hit distinct banks
     float* sq = (float*)(wsum + NT / 64);
-    __shared__ float rc[256];
 
     const int b = blockIdx.x, tid = threadIdx.x;
     JHQ_PHASE_DECL
     work_plan<NT>(qtot, B, Gmax, qpre, spre, wsum);
     for (int i = tid; i < d; i += NT) sq[i + (i >> 5)] = q_rot[(int64_t)b * d + i];
-    for (int i = tid; i < Kr; i += NT) rc[i] = res_c1d[i];
+    for (int i = tid; i < RC * Kr; i += NT) rc[i] = res_c1d[i];
     const int s0 = spre[b], s1 = spre[b + 1];
     stream_begin<NT>(S);
     __syncthreads();
@@ -1554,7 +1642,11 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
         // each list is sorted ascending (~0 padded): the rank of key x from
         // list a at index i in the union is i + sum over the other lists of
         // the number of keys below x (keys are distinct)
-        for (int i = tid; i < nkeys; i += NT) stage[i] = src[i];
+        const int32_t* srcs = partial_slot + (int64_t)s0 * ck;
+        for (int i = tid; i < nkeys; i += NT) {
+            stage[i] = src[i];
+            sslot[i] = srcs[i];
+        }
         if (tid == 0) S.ctl[0] = 0;
         __syncthreads();
         int nv = 0;
@@ -1579,7 +1671,10 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
                 }
                 r += lo;
             }
-            if (r < ksel) S.kout[r] = x;
+            if (r < ksel) {
+                S.kout[r] = x;
+                kslot[r] = sslot[idx];
+            }
         }
         __syncthreads();
     } else {
@@ -1597,13 +1692,27 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
             stream_round<NT, 4>(S, ck, o, tg);
         }
         ksel = stream_end<NT>(S, ck);
+        // pool slots of the short list: the list whose canonical range holds
+        // the tag (binary search over the list descriptors)
+        for (int r = tid; r < ksel; r += NT) {
+            const int tag = (int)(uint32_t)(S.kout[r] & 0xffffffffull);
+            int lo = 0, hi = nlist - 1;  // last list with cbase <= tag
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (ldesc[mid].w <= tag) lo = mid;
+                else hi = mid - 1;
+            }
+            const int4 L = ldesc[lo];
+            kslot[r] = L.x + (tag - L.w);
+        }
+        __syncthreads();
     }
     JHQ_PHASE(1);
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
             const unsigned long long kk = S.kout[r];
             cprim[r] = ord2f((uint32_t)(kk >> 32));
-            cpos[r] = (int)(uint32_t)(kk & 0xffffffffull);
+            cpos[r] = kslot[r];
             if (topck_dbg) topck_dbg[(int64_t)b * ck + r] = kk;
         } else if (topck_dbg) {
             topck_dbg[(int64_t)b * ck + r] = ~0ull;
@@ -1614,6 +1723,13 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     // residual refine: 16 lanes per candidate, lane l16 sums a contiguous
     // range of dimensions, then a fixed xor tree adds the 16 partial sums.
     const int grp = tid >> 4, l16 = tid & 15;
+    // codebook of dimension j: one shared codebook, or that of subspace j / Ds
+    int ds_shift = -1;
+    if (RC > 1 && (Ds & (Ds - 1)) == 0) ds_shift = __ffs(Ds) - 1;
+    auto cbo = [&](int j) -> int {
+        if (RC == 1) return 0;
+        return (ds_shift >= 0 ? (j >> ds_shift) : (j / Ds)) * Kr;
+    };
     constexpr int NG = NT / 16;
     const int dpc = (Br == 4) ? 32 : 16;  // dimensions per 16-byte chunk
     const bool vec = (bpv % 16) == 0 && (d % dpc) == 0;
@@ -1649,7 +1765,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
 #pragma unroll
                                 for (int nb = 0; nb < 8; nb++) {
                                     const int jj = jb + q4 * 8 + nb;
-                                    const float df = sq[jj + (jj >> 5)] - rc[(ww[q4] >> (4 * nb)) & 0x0Fu];
+                                    const float df = sq[jj + (jj >> 5)] - rc[cbo(jj) + ((ww[q4] >> (4 * nb)) & 0x0Fu)];
                                     sres = sres + df * df;
                                 }
                         } else {
@@ -1658,7 +1774,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
 #pragma unroll
                                 for (int nb = 0; nb < 4; nb++) {
                                     const int jj = jb + q4 * 4 + nb;
-                                    const float df = sq[jj + (jj >> 5)] - rc[(ww[q4] >> (8 * nb)) & 0xFFu];
+                                    const float df = sq[jj + (jj >> 5)] - rc[cbo(jj) + ((ww[q4] >> (8 * nb)) & 0xFFu)];
                                     sres = sres + df * df;
                                 }
                         }
@@ -1667,16 +1783,16 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
             } else if (Br == 4) {
                 for (int j = j0; j < j1; j += 2) {
                     const uint32_t byte = rcode[j >> 1];
-                    const float df0 = sq[j + (j >> 5)] - rc[byte & 0x0Fu];
+                    const float df0 = sq[j + (j >> 5)] - rc[cbo(j) + (byte & 0x0Fu)];
                     sres = sres + df0 * df0;
                     if (j + 1 < j1) {
-                        const float df1 = sq[(j + 1) + ((j + 1) >> 5)] - rc[byte >> 4];
+                        const float df1 = sq[(j + 1) + ((j + 1) >> 5)] - rc[cbo(j + 1) + (byte >> 4)];
                         sres = sres + df1 * df1;
                     }
                 }
             } else {
                 for (int j = j0; j < j1; j++) {
-                    const float df = sq[j + (j >> 5)] - rc[rcode[j]];
+                    const float df = sq[j + (j >> 5)] - rc[cbo(j) + rcode[j]];
                     sres = sres + df * df;
                 }
             }
@@ -1710,22 +1826,23 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     JHQ_PHASE_FLUSH(2);
 }
 
-hipError_t refine_topk(const unsigned long long* partial, const int32_t* qtot, int B,
-                       const ScanShape& sh, int ck, int k, const float* q_rot, int d,
-                       const float* res_c1d, int Kr, int Br, int bpv, const uint8_t* list_res,
+hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial_slot,
+                       const int32_t* qtot, int B, const ScanShape& sh, int ck, int k,
+                       const float* q_rot, int d, int Ds, const float* res_c1d, int Kr, int RC,
+                       int Br, int bpv, const int4* ldesc, int nlist, const uint8_t* list_res,
                        const float* list_corr, const int32_t* list_ids, float* out_d,
                        int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s) {
     constexpr int NT = kRefineNT;
     if (k > ck) return hipErrorInvalidValue;
     const int stage_cap = std::max(4096, 8 * ck);
-    const size_t lds = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)stage_cap * 8 +
-                       (size_t)(2 * (B + 1)) * 4 + (size_t)ck * 4 * 2 + (NT / 64) * 4 +
-                       (size_t)(d + d / 32 + 1) * 4 + 16;
+    const size_t lds = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)stage_cap * (8 + 4) +
+                       (size_t)ck * 4 + (size_t)RC * Kr * 4 + (size_t)(2 * (B + 1)) * 4 +
+                       (size_t)ck * 4 * 2 + (NT / 64) * 4 + (size_t)(d + d / 32 + 1) * 4 + 32;
     static const int max_dyn = allow_max_lds((const void*)refine_topk_kernel<NT>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, qtot, B, sh.G,
-                       ck, k, q_rot, d, res_c1d, Kr, Br, bpv, list_res, list_corr, list_ids, out_d,
-                       out_i, topck_dbg, stage_cap);
+    hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, partial_slot,
+                       qtot, B, sh.G, ck, k, q_rot, d, Ds, res_c1d, Kr, RC, Br, bpv, ldesc, nlist,
+                       list_res, list_corr, list_ids, out_d, out_i, topck_dbg, stage_cap);
     return hipGetLastError();
 }
 

@@ -294,6 +294,15 @@ void o_primary_encode(const float* y, int64_t n, int d, int M, const float* c1d,
 void o_residual_encode(const float* y, const uint8_t* primary, int64_t n, int d,
                        int M, const float* c1d, int K1D, const float* res_c1d,
                        int Kr, int Br, uint8_t* res_codes, float* corr) {
+    o_residual_encode_rc(y, primary, n, d, M, c1d, K1D, res_c1d, Kr, 1, Br, res_codes, corr);
+}
+
+/* RC residual codebooks of Kr words: RC = 1 (every dimension, the
+ * reference), or RC = M (dimension j uses codebook j / Ds; an extension with
+ * no reference counterpart). */
+void o_residual_encode_rc(const float* y, const uint8_t* primary, int64_t n, int d,
+                          int M, const float* c1d, int K1D, const float* res_c1d,
+                          int Kr, int RC, int Br, uint8_t* res_codes, float* corr) {
     const int Ds = d / M, bpd = bits_per_dim(d, M, K1D);
     const int bpv = (d * Br + 7) / 8;
     const int kmask = K1D - 1;
@@ -308,8 +317,9 @@ void o_residual_encode(const float* y, const uint8_t* primary, int64_t n, int d,
             const int pidx = (pc[m] >> (k * bpd)) & kmask;
             const float yhat = c1d[pidx];
             const float resid = yi[j] - yhat;
-            const int ri = nearest_sorted(res_c1d, Kr, resid);
-            const float rhat = res_c1d[ri];
+            const float* rcb = res_c1d + (RC == 1 ? 0 : (int64_t)m * Kr);
+            const int ri = nearest_sorted(rcb, Kr, resid);
+            const float rhat = rcb[ri];
             if (Br == 4) {
                 if (j % 2 == 0) rc[j / 2] = (uint8_t)(ri & 0x0F);
                 else rc[j / 2] |= (uint8_t)((ri & 0x0F) << 4);
@@ -580,11 +590,10 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
             for (int j = 0; j < d; j++) {
                 const int ri = (Br == 4) ? ((j % 2 == 0) ? (rc[j / 2] & 0x0F) : (rc[j / 2] >> 4))
                                          : rc[j];
-                const float diff = q_rot[j] - ix->res_c1d[ri];
+                const float diff = q_rot[j] - ix->res_c1d[(ix->RC == 1 ? 0 : (j / ix->Ds) * Kr) + ri];
                 const float lr = diff * diff;
                 d_res = d_res + lr;
             }
-            (void)Kr;
             comp[c] = (cd[c] + d_res) + ix->list_corr[pos];
             cid[c] = ix->list_ids[pos];
         }

@@ -10,8 +10,10 @@
  * the library is built with -ffp-contract=off and uses fmaf() exactly where the
  * reference's build contracts a multiply-add (nvcc --use_fast_math for device
  * code, gcc -O3 -march=native for cpu/).  The GPU product follows the same
- * order, so codes, LUTs, primary distances, probe lists and top-ck candidate
- * sets are bit-exact between the two.
+ * order for codes, corrections, LUT entries and primary distances, so those
+ * are bit-exact between the two.  The product's query rotation and centroid
+ * scores run on fp32 MFMA; o_search_ex takes the product's rotated queries
+ * and probe lists so that every later stage is compared bit for bit.
  *
  * Pinning status (what checks each function; see tests/test_oracle_*.py):
  *   o_mt_*               mt19937 known answer (10000th draw of seed 5489) and
@@ -80,6 +82,9 @@ void o_primary_encode(const float* y, int64_t n, int d, int M, const float* c1d,
 void o_residual_encode(const float* y, const uint8_t* primary, int64_t n, int d,
                        int M, const float* c1d, int K1D, const float* res_c1d,
                        int Kr, int Br, uint8_t* res_codes, float* corr);
+void o_residual_encode_rc(const float* y, const uint8_t* primary, int64_t n, int d,
+                          int M, const float* c1d, int K1D, const float* res_c1d,
+                          int Kr, int RC, int Br, uint8_t* res_codes, float* corr);
 void o_reconstruct(const uint8_t* code, int d, int M, const float* c1d, int K1D,
                    float* out);
 
@@ -109,11 +114,12 @@ int  o_select_topk_pairs(const float* dist, const int32_t* tag, int64_t n, int k
 typedef struct {
     int d, M, B, Br, Ds, K1D, bpd, Kr, bpv;
     int nlist, nprobe;
+    int RC;                     /* residual codebooks: 1, or M (per subspace) */
     float alpha;
     int64_t ntotal;
     const float*   P;           /* [d][d] row-major Pi(j,k)                 */
     const float*   c1d;         /* [K1D]                                   */
-    const float*   res_c1d;     /* [Kr]                                    */
+    const float*   res_c1d;     /* [RC][Kr]                                */
     const float*   cent;        /* [nlist][d]                              */
     const float*   cent_norms;  /* [nlist]                                 */
     const int32_t* list_offsets;/* [nlist+1]                               */

@@ -25,7 +25,8 @@ _U32 = ctypes.c_uint32
 class _OIndex(ctypes.Structure):
     _fields_ = [
         ("d", _I), ("M", _I), ("B", _I), ("Br", _I), ("Ds", _I), ("K1D", _I), ("bpd", _I),
-        ("Kr", _I), ("bpv", _I), ("nlist", _I), ("nprobe", _I), ("alpha", _F), ("ntotal", _I64),
+        ("Kr", _I), ("bpv", _I), ("nlist", _I), ("nprobe", _I), ("RC", _I), ("alpha", _F),
+        ("ntotal", _I64),
         ("P", _VP), ("c1d", _VP), ("res_c1d", _VP), ("cent", _VP), ("cent_norms", _VP),
         ("list_offsets", _VP), ("list_ids", _VP), ("list_codes", _VP), ("list_res", _VP),
         ("list_corr", _VP),
@@ -44,6 +45,7 @@ _SIGS = {
     "o_rotate": (None, [_VP, _VP, _I64, _I, _VP]),
     "o_primary_encode": (None, [_VP, _I64, _I, _I, _VP, _I, _VP]),
     "o_residual_encode": (None, [_VP, _VP, _I64, _I, _I, _VP, _I, _VP, _I, _I, _VP, _VP]),
+    "o_residual_encode_rc": (None, [_VP, _VP, _I64, _I, _I, _VP, _I, _VP, _I, _I, _I, _VP, _VP]),
     "o_reconstruct": (None, [_VP, _I, _I, _VP, _I, _VP]),
     "o_flat_lut": (None, [_VP, _I, _I, _VP, _I, _VP]),
     "o_factored_lut": (None, [_VP, _I, _I, _VP, _I, _VP]),
@@ -186,16 +188,19 @@ def primary_encode(y, M, c1d):
 
 
 def residual_encode(y, codes, M, c1d, res_c1d, Br):
+    """res_c1d: [Kr] (one codebook) or [M, Kr] (one per subspace)."""
     y = _c(y, np.float32)
     codes = _c(codes, np.uint8)
     c1d = _c(c1d, np.float32)
     res_c1d = _c(res_c1d, np.float32)
+    RC = res_c1d.shape[0] if res_c1d.ndim == 2 else 1
+    Kr = res_c1d.shape[-1]
     n, d = y.shape
     bpv = (d * Br + 7) // 8
     res = np.empty((n, bpv), np.uint8)
     corr = np.empty(n, np.float32)
-    lib().o_residual_encode(_p(y), _p(codes), n, d, M, _p(c1d), c1d.size, _p(res_c1d),
-                            res_c1d.size, Br, _p(res), _p(corr))
+    lib().o_residual_encode_rc(_p(y), _p(codes), n, d, M, _p(c1d), c1d.size, _p(res_c1d),
+                               Kr, RC, Br, _p(res), _p(corr))
     return res, corr
 
 
@@ -293,7 +298,8 @@ class OracleIndex:
     """CPU restatement of JHQGpuIndex (jhq_v14_streaming_add/jhq_gpu_index.cu)."""
 
     def __init__(self, d, M=96, B=8, Br=4, alpha=4.0, nlist=1024, nprobe=8, ivf_iters=8,
-                 seed=42, **_):
+                 seed=42, residual_per_subspace=0, **_):
+        self.RC = M if residual_per_subspace else 1
         self.d, self.M, self.B, self.Br = d, M, B, Br
         self.alpha = np.float32(alpha)
         self.nlist = nlist
@@ -313,6 +319,7 @@ class OracleIndex:
         """Wrap an index built elsewhere (e.g. the GPU's) for CPU search."""
         o = cls.__new__(cls)
         o.d, o.M, o.B, o.Br = d, params.M, params.B, params.Br
+        o.RC = params.M if getattr(params, "residual_per_subspace", 0) else 1
         o.alpha = np.float32(params.alpha)
         o.nlist = params.nlist
         o.nprobe = min(params.nprobe, params.nlist)
@@ -323,7 +330,8 @@ class OracleIndex:
         o.Kr = 1 << o.Br
         o.bpv = (d * o.Br + 7) // 8
         o.P = _c(P, np.float32)
-        o.c1d, o.res_c1d = _c(c1d, np.float32), _c(res_c1d, np.float32)
+        o.c1d = _c(c1d, np.float32)
+        o.res_c1d = _c(res_c1d, np.float32).reshape((o.RC, -1) if o.RC > 1 else (-1,))
         o.cent, o.cent_norms = _c(cent, np.float32), _c(cent_norms, np.float32)
         o.list_offsets, o.list_ids = _c(offsets, np.int32), _c(ids, np.int32)
         o.list_codes, o.list_res, o.list_corr = (_c(codes, np.uint8), _c(res, np.uint8),
@@ -341,11 +349,18 @@ class OracleIndex:
         codes = primary_encode(y, self.M, self.c1d)
         self.cent = train_ivf(y, self.nlist, self.ivf_iters)
         self.cent_norms = cent_norms(self.cent)
-        resid = (y - reconstruct(codes, self.d, self.c1d)).ravel()
-        rc = train_1d_kmeans(resid, self.Kr)
-        if rc.size < self.Kr:
-            rc = np.concatenate([rc, np.full(self.Kr - rc.size, rc[-1], np.float32)])
-        self.res_c1d = rc
+        resid = y - reconstruct(codes, self.d, self.c1d)
+        books = []
+        for cb in range(self.RC):
+            # one codebook over every dimension (v14/jhq_gpu_index.cu:302-330),
+            # or one per subspace over its Ds dimensions
+            vals = resid.ravel() if self.RC == 1 else \
+                np.ascontiguousarray(resid[:, cb * self.Ds:(cb + 1) * self.Ds]).ravel()
+            rc = train_1d_kmeans(vals, self.Kr)
+            if rc.size < self.Kr:
+                rc = np.concatenate([rc, np.full(self.Kr - rc.size, rc[-1], np.float32)])
+            books.append(rc)
+        self.res_c1d = books[0] if self.RC == 1 else np.stack(books).astype(np.float32)
         return y
 
     def add(self, x):
@@ -369,6 +384,7 @@ class OracleIndex:
         s.d, s.M, s.B, s.Br = self.d, self.M, self.B, self.Br
         s.Ds, s.K1D, s.bpd, s.Kr, s.bpv = self.Ds, self.K1D, self.bpd, self.Kr, self.bpv
         s.nlist, s.nprobe, s.alpha, s.ntotal = self.nlist, self.nprobe, float(self.alpha), self.ntotal
+        s.RC = self.RC
         self._keep = [self.P, self.c1d, self.res_c1d, self.cent, self.cent_norms,
                       self.list_offsets, self.list_ids, self.list_codes, self.list_res,
                       self.list_corr]

@@ -58,6 +58,8 @@ def test_params_default_match_reference():
     (16, dict(M=8, add_batch=0), "add_batch"),
     (16, dict(M=8, alpha=0.0), "alpha"),
     (0, dict(M=8), "d must be positive"),
+    (16, dict(M=8, residual_per_subspace=2), "residual_per_subspace"),
+    (64, dict(M=64, B=8, Br=8, residual_per_subspace=1), "per-subspace"),
 ])
 def test_constructor_validation(d, kw, msg):
     with pytest.raises(ValueError, match=msg):
@@ -100,6 +102,18 @@ def test_call_order_errors_before_device():
     with pytest.raises(RuntimeError, match="not trained"):
         g.codebooks()
     assert "not trained" in jg.lib().jhq_last_error().decode()
+
+
+def test_append_and_typed_inputs_validate_before_device():
+    g = jg.JHQGpuIndex(16, jg.Params(M=8, nlist=4, nprobe=2))
+    x8 = np.zeros((100, 16), np.uint8)
+    with pytest.raises(RuntimeError, match="train"):
+        g.append(x8)
+    with pytest.raises(ValueError):
+        g.append(np.zeros((10, 15), np.float32))
+    L = jg.lib()
+    assert L.jhq_train_ex(g._h, x8.ctypes.data_as(jg._VP), 7, 100) == jg.JHQ_EINVAL
+    assert L.jhq_append_ex(g._h, None, 0, 10) == jg.JHQ_EINVAL
 
 
 def test_kernel_entry_points_reject_bad_arguments():

@@ -112,6 +112,31 @@ def test_residual_encode_brute_force(d, M, Br, Kr):
     assert np.allclose(lhs, rhs, rtol=1e-5)
 
 
+def test_per_subspace_residual_codebooks_brute_force():
+    """Extension with no reference counterpart: dimension j is quantised with
+    codebook j // Ds; pinned by brute force and by the one-codebook case."""
+    d, M, Kr = 48, 12, 16
+    Ds = d // M
+    rng = np.random.default_rng(44)
+    y = (rng.standard_normal((40, d)) * 0.05).astype(np.float32)
+    c1d = po.lloyd_max_c1d(0.05, 1 << (8 // Ds))
+    books = np.sort((rng.standard_normal((M, Kr)) * 0.02).astype(np.float32), axis=1)
+    codes = po.primary_encode(y, M, c1d)
+    res, corr = po.residual_encode(y, codes, M, c1d, books, 4)
+    r = y - po.reconstruct(codes, d, c1d)
+    ri = _unpack_res(res, d, 4)
+    for j in range(d):
+        assert np.array_equal(ri[:, j], nearest_brute(r[:, j], books[j // Ds]))
+    rhat = books[np.arange(d)[None, :] // Ds, ri].astype(np.float64)
+    yhat = po.reconstruct(codes, d, c1d).astype(np.float64)
+    assert np.allclose(corr, 2.0 * (yhat * rhat).sum(1), rtol=1e-5, atol=1e-9)
+    # M identical codebooks == the one shared codebook, bit for bit
+    same = np.repeat(books[:1], M, axis=0)
+    r1, c1 = po.residual_encode(y, codes, M, c1d, same, 4)
+    r0, c0 = po.residual_encode(y, codes, M, c1d, books[0], 4)
+    assert np.array_equal(r1, r0) and np.array_equal(c1.view(np.uint32), c0.view(np.uint32))
+
+
 def test_residual_nibble_swap_is_caught():
     rng = np.random.default_rng(8)
     y = (rng.standard_normal((20, 16)) * 0.05).astype(np.float32)
