@@ -163,6 +163,17 @@ int jhq_get_codebooks(const jhq_index* idx, float* sigma, float* c1d,
 int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids,
                   uint8_t* codes, uint8_t* res, float* corr);
 
+/* Index files (extension; the reference has no serialization).  jhq_save
+ * writes the parameters, the trained state and the lists in canonical order;
+ * jhq_load creates a new index from such a file (lists re-packed into a
+ * compact pool), ready to search and to append to.  Loading checks the magic,
+ * the version, the sizes and that the stored rotation equals the one its seed
+ * builds. */
+int jhq_save(const jhq_index* idx, const char* path);
+/* The index's current parameters (nprobe and alpha as last set). */
+int jhq_get_params(const jhq_index* idx, jhq_params* out);
+int jhq_load(const char* path, jhq_index** out);
+
 /* List pool occupancy: slots in use (including padding and blocks left
  * behind by relocations) and allocated slots. */
 int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity);

@@ -90,6 +90,9 @@ _SIGS = {
     "jhq_append_ex": (_I, [_VP, _VP, _I, _I64]),
     "jhq_search_ex": (_I, [_VP, _VP, _I, _I64, _I, _VP, _VP]),
     "jhq_get_pool": (_I, [_VP, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "jhq_save": (_I, [_VP, ctypes.c_char_p]),
+    "jhq_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_VP)]),
+    "jhq_get_params": (_I, [_VP, ctypes.POINTER(_Params)]),
     "jhq_search_device": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP]),
     "jhq_ntotal": (_I64, [_VP]),
     "jhq_dim": (_I, [_VP]),
@@ -267,6 +270,23 @@ class JHQGpuIndex:
         P = np.empty((self._d, self._d), np.float32)
         _check(lib().jhq_get_codebooks(self._h, None, None, None, _ptr(P), None, None))
         return P
+
+    def save(self, path):
+        """Writes the index (parameters, trained state, lists) to `path`."""
+        _check(lib().jhq_save(self._h, os.fsencode(path)))
+
+    @classmethod
+    def load(cls, path):
+        """A new index read from a file written by save()."""
+        h = _VP()
+        _check(lib().jhq_load(os.fsencode(path), ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self._h = h
+        self._d = int(lib().jhq_dim(h))
+        cp = _Params()
+        _check(lib().jhq_get_params(h, ctypes.byref(cp)))
+        self._p = Params(**{f: getattr(cp, f) for f, _ in _Params._fields_})
+        return self
 
     def pool(self):
         used, cap = _I64(), _I64()

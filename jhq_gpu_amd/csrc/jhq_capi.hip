@@ -888,6 +888,240 @@ int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids, uint8_t*
     return JHQ_OK;
 }
 
+// ---- index file: params, trained state, lists in canonical order ----------
+// Layout (little-endian): "JHQAMD01", u32 version, i32 d, jhq_params fields
+// (i32 except alpha f32), u8 trained, u8 added, i64 ntotal, f32 sigma,
+// f32 c1d[K1D], f32 res_c1d[RC*Kr], f32 P[d*d] (row-major Pi), f32
+// centroids[nlist*d], f32 norms[nlist], i32 sizes[nlist], i32 ids[ntotal],
+// u8 codes[ntotal*M], u8 res[ntotal*bpv], f32 corr[ntotal].
+}  // extern "C"
+
+namespace {
+
+constexpr char kMagic[8] = {'J', 'H', 'Q', 'A', 'M', 'D', '0', '1'};
+constexpr uint32_t kVersion = 1;
+
+struct FileW {
+    FILE* f;
+    bool ok = true;
+    void put(const void* p, size_t n) {
+        if (ok && n && std::fwrite(p, 1, n, f) != n) ok = false;
+    }
+    template <class T>
+    void put(const T& v) {
+        put(&v, sizeof(T));
+    }
+};
+
+struct FileR {
+    FILE* f;
+    bool ok = true;
+    void get(void* p, size_t n) {
+        if (ok && n && std::fread(p, 1, n, f) != n) ok = false;
+    }
+    template <class T>
+    void get(T& v) {
+        get(&v, sizeof(T));
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int jhq_get_params(const jhq_index* idx, jhq_params* out) {
+    if (!idx || !out) return fail(JHQ_EINVAL, "null argument");
+    out->M = idx->M;
+    out->B = idx->B;
+    out->Br = idx->Br;
+    out->alpha = idx->alpha;
+    out->nlist = idx->nlist;
+    out->nprobe = idx->nprobe;
+    out->ivf_iters = idx->ivf_iters;
+    out->batch_size = idx->batch_size;
+    out->seed = idx->seed;
+    out->add_batch = idx->add_batch;
+    out->residual_per_subspace = idx->RC > 1 ? 1 : 0;
+    return JHQ_OK;
+}
+
+int jhq_save(const jhq_index* idx, const char* path) {
+    if (!idx || !path) return fail(JHQ_EINVAL, "null argument");
+    if (!idx->trained) return fail(JHQ_ESTATE, "index is not trained");
+    const int64_t n = idx->ntotal;
+    const int nlist = idx->nlist;
+    std::vector<int32_t> offs(nlist + 1), ids(n);
+    std::vector<uint8_t> codes(static_cast<size_t>(n) * idx->M), res(static_cast<size_t>(n) * idx->bpv);
+    std::vector<float> corr(n);
+    if (n > 0) JHQ_TRY(jhq_get_lists(idx, offs.data(), ids.data(), codes.data(), res.data(), corr.data()));
+    FILE* f = std::fopen(path, "wb");
+    if (!f) return fail(JHQ_EINVAL, std::string("cannot open ") + path + " for writing");
+    FileW w{f};
+    w.put(kMagic, 8);
+    w.put(kVersion);
+    w.put(idx->d);
+    for (int v : {idx->M, idx->B, idx->Br}) w.put(v);
+    w.put(idx->alpha);
+    for (int v : {idx->nlist, idx->nprobe, idx->ivf_iters, idx->batch_size, idx->seed,
+                  idx->add_batch, idx->RC > 1 ? 1 : 0})
+        w.put(v);
+    const uint8_t tr = idx->trained ? 1 : 0, ad = idx->added ? 1 : 0;
+    w.put(tr);
+    w.put(ad);
+    w.put(n);
+    w.put(idx->sigma);
+    w.put(idx->c1d.data(), idx->c1d.size() * sizeof(float));
+    w.put(idx->res_c1d.data(), idx->res_c1d.size() * sizeof(float));
+    w.put(idx->P_rm.data(), idx->P_rm.size() * sizeof(float));
+    w.put(idx->cent.data(), idx->cent.size() * sizeof(float));
+    w.put(idx->cent_norms.data(), idx->cent_norms.size() * sizeof(float));
+    w.put(idx->l_size.data(), idx->l_size.size() * sizeof(int32_t));
+    w.put(ids.data(), ids.size() * sizeof(int32_t));
+    w.put(codes.data(), codes.size());
+    w.put(res.data(), res.size());
+    w.put(corr.data(), corr.size() * sizeof(float));
+    const bool closed = std::fclose(f) == 0;
+    if (!w.ok || !closed) return fail(JHQ_EINVAL, std::string("write to ") + path + " failed");
+    return JHQ_OK;
+}
+
+int jhq_load(const char* path, jhq_index** out) {
+    if (!path || !out) return fail(JHQ_EINVAL, "null argument");
+    *out = nullptr;
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return fail(JHQ_EINVAL, std::string("cannot open ") + path);
+    FileR r{f};
+    char magic[8];
+    uint32_t ver = 0;
+    int d = 0;
+    jhq_params p;
+    jhq_params_default(&p);
+    r.get(magic, 8);
+    r.get(ver);
+    r.get(d);
+    r.get(p.M);
+    r.get(p.B);
+    r.get(p.Br);
+    r.get(p.alpha);
+    for (int* v : {&p.nlist, &p.nprobe, &p.ivf_iters, &p.batch_size, &p.seed, &p.add_batch,
+                   &p.residual_per_subspace})
+        r.get(*v);
+    if (!r.ok || std::memcmp(magic, kMagic, 8) != 0 || ver != kVersion) {
+        std::fclose(f);
+        return fail(JHQ_EINVAL, std::string(path) + " is not a JHQ index file of this version");
+    }
+    const int nprobe_saved = p.nprobe;
+    jhq_index* ix = nullptr;
+    int rc = jhq_create(d, &p, &ix);
+    if (rc != JHQ_OK) {
+        std::fclose(f);
+        return rc;
+    }
+    ix->nprobe = nprobe_saved;
+    uint8_t tr = 0, ad = 0;
+    int64_t n = 0;
+    r.get(tr);
+    r.get(ad);
+    r.get(n);
+    r.get(ix->sigma);
+    ix->c1d.resize(ix->K1D);
+    ix->res_c1d.resize(static_cast<size_t>(ix->RC) * ix->Kr);
+    ix->cent.resize(static_cast<size_t>(ix->nlist) * d);
+    ix->cent_norms.resize(ix->nlist);
+    std::vector<float> P(static_cast<size_t>(d) * d);
+    r.get(ix->c1d.data(), ix->c1d.size() * sizeof(float));
+    r.get(ix->res_c1d.data(), ix->res_c1d.size() * sizeof(float));
+    r.get(P.data(), P.size() * sizeof(float));
+    r.get(ix->cent.data(), ix->cent.size() * sizeof(float));
+    r.get(ix->cent_norms.data(), ix->cent_norms.size() * sizeof(float));
+    std::vector<int32_t> sizes(ix->nlist), ids;
+    r.get(sizes.data(), sizes.size() * sizeof(int32_t));
+    const bool ok_n = r.ok && n >= 0 && n <= INT32_MAX;
+    int64_t tot = 0;
+    bool neg = false;
+    for (int32_t v : sizes) {
+        tot += v;
+        neg |= v < 0;
+    }
+    if (!ok_n || neg || tot != n || !tr) {
+        std::fclose(f);
+        delete ix;
+        return fail(JHQ_EINVAL, std::string(path) + ": truncated or inconsistent index file");
+    }
+    ids.resize(n);
+    std::vector<uint8_t> codes(static_cast<size_t>(n) * ix->M), res(static_cast<size_t>(n) * ix->bpv);
+    std::vector<float> corr(n);
+    r.get(ids.data(), ids.size() * sizeof(int32_t));
+    r.get(codes.data(), codes.size());
+    r.get(res.data(), res.size());
+    r.get(corr.data(), corr.size() * sizeof(float));
+    std::fclose(f);
+    if (!r.ok) {
+        delete ix;
+        return fail(JHQ_EINVAL, std::string(path) + ": truncated index file");
+    }
+    // the rotation is rebuilt from the seed at construction; the file's copy
+    // must agree (it is the same deterministic computation)
+    if (std::memcmp(P.data(), ix->P_rm.data(), P.size() * sizeof(float)) != 0) {
+        delete ix;
+        return fail(JHQ_EINVAL, std::string(path) + ": stored rotation differs from its seed's");
+    }
+    auto done = [&](int code) {
+        if (code != JHQ_OK) delete ix;
+        return code;
+    };
+    if ((rc = ix->ensure_stream()) != JHQ_OK ||
+        (rc = ix->dP.upload(ix->P_rm.data(), ix->P_rm.size())) != JHQ_OK ||
+        (rc = ix->dc1d.upload(ix->c1d.data(), ix->c1d.size())) != JHQ_OK ||
+        (rc = ix->dres_c1d.upload(ix->res_c1d.data(), ix->res_c1d.size())) != JHQ_OK ||
+        (rc = ix->dcent.upload(ix->cent.data(), ix->cent.size())) != JHQ_OK ||
+        (rc = ix->dnorms.upload(ix->cent_norms.data(), ix->cent_norms.size())) != JHQ_OK)
+        return done(rc);
+    ix->trained = true;
+    // compact pool: exact-fit blocks in list order (the one-shot add's layout)
+    const int M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
+    int64_t pos = 0;
+    for (int l = 0; l < nlist; l++) {
+        ix->l_start[l] = static_cast<int32_t>(pos);
+        ix->l_cap[l] = (sizes[l] + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+        ix->l_size[l] = sizes[l];
+        pos += ix->l_cap[l];
+    }
+    if (pos > INT32_MAX) return done(fail(JHQ_EINVAL, "list pool exceeds int32 slots"));
+    if (pos > 0) {
+        if ((rc = grow_pool(ix, pos)) != JHQ_OK) return done(rc);
+        ix->pool_used = pos;
+        std::vector<uint8_t> pc(static_cast<size_t>(pos) * M, 0), pr(static_cast<size_t>(pos) * bpv, 0);
+        std::vector<float> pco(static_cast<size_t>(pos), 0.f);
+        std::vector<int32_t> pid(static_cast<size_t>(pos), -1);
+        int64_t o = 0;
+        for (int l = 0; l < nlist; l++) {
+            const int64_t st = ix->l_start[l], cap = ix->l_cap[l];
+            for (int64_t i = 0; i < sizes[l]; i++, o++) {
+                for (int m = 0; m < M; m++) pc[st * M + m * cap + i] = codes[o * M + m];
+                std::memcpy(pr.data() + (st + i) * bpv, res.data() + o * bpv, bpv);
+                pco[st + i] = corr[o];
+                pid[st + i] = ids[o];
+            }
+        }
+        hipStream_t s = ix->stream;
+        if (hipMemcpyAsync(ix->dcodes_t.p, pc.data(), pc.size(), hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(ix->dres.p, pr.data(), pr.size(), hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(ix->dcorr.p, pco.data(), pco.size() * sizeof(float), hipMemcpyHostToDevice,
+                           s) != hipSuccess ||
+            hipMemcpyAsync(ix->dlist_ids.p, pid.data(), pid.size() * sizeof(int32_t),
+                           hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return done(fail(JHQ_EDEVICE, "index upload failed"));
+    }
+    rc = upload_ldesc(ix);
+    if (rc != JHQ_OK) return done(rc);
+    ix->ntotal = n;
+    ix->added = ad != 0;
+    *out = ix;
+    return JHQ_OK;
+}
+
 int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (pool_slots) *pool_slots = idx->pool_used;

@@ -116,6 +116,27 @@ def test_append_and_typed_inputs_validate_before_device():
     assert L.jhq_append_ex(g._h, None, 0, 10) == jg.JHQ_EINVAL
 
 
+def test_index_file_errors_before_device(tmp_path):
+    g = jg.JHQGpuIndex(16, jg.Params(M=8, nlist=4, nprobe=2))
+    with pytest.raises(RuntimeError, match="not trained"):
+        g.save(tmp_path / "untrained.jhq")
+    with pytest.raises(ValueError, match="cannot open"):
+        jg.JHQGpuIndex.load(tmp_path / "missing.jhq")
+    bad = tmp_path / "bad.jhq"
+    bad.write_bytes(b"NOTANIDX" + bytes(64))
+    with pytest.raises(ValueError, match="not a JHQ index file"):
+        jg.JHQGpuIndex.load(bad)
+    short = tmp_path / "short.jhq"
+    short.write_bytes(b"JHQAMD01")
+    with pytest.raises(ValueError, match="not a JHQ index file"):
+        jg.JHQGpuIndex.load(short)
+    p = jg.Params(M=8, nlist=4, nprobe=2)
+    got = jg.Params(**{f: getattr(p, f) for f in ("M", "B", "Br")})
+    cp = jg._Params()
+    assert jg.lib().jhq_get_params(g._h, ctypes.byref(cp)) == jg.JHQ_OK
+    assert (cp.M, cp.B, cp.Br, cp.nlist, cp.nprobe) == (got.M, got.B, got.Br, 4, 2)
+
+
 def test_kernel_entry_points_reject_bad_arguments():
     L = jg.lib()
     assert L.jhq_k_rotate(None, None, 4, 8, None, None) == jg.JHQ_EINVAL
