@@ -44,9 +44,15 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=0, help="timed steps (default: 5 passes)")
     ap.add_argument("--warmup", type=int, default=0, help="warmup steps (default: 1 pass)")
-    ap.add_argument("--nprobe", type=str, default="16,32,64")
-    ap.add_argument("--alpha", type=str, default="4,10",
-                    help="short-list factors swept (ck = max(k, ceil(alpha*k)))")
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                    help="BASELINE.json workload: 2 (default, the metric's config), 3 (100M "
+                         "uint8 D=128), 4 (100M int8 D=100), 5 (streaming add + search, D=768)")
+    ap.add_argument("--nprobe", type=str, default=None,
+                    help="nprobe values swept (default: 16,32,64 for config 2, the config's own "
+                         "value otherwise)")
+    ap.add_argument("--alpha", type=str, default=None,
+                    help="short-list factors swept (ck = max(k, ceil(alpha*k))); default 4,10 "
+                         "for config 2, 4 otherwise")
     ap.add_argument("--scale", type=float, default=1.0, help="fraction of N (debug only)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-batches", type=int, default=0,
@@ -54,7 +60,8 @@ def parse():
                          "first --nprobe/--alpha plus one 256 MiB device copy (the counter "
                          "calibration kernel), print per-step times and exit")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--seed", type=int, default=0x4A48510002)
+    ap.add_argument("--seed", type=int, default=None,
+                    help="data seed (default 0x4A48510000 + config)")
     return ap.parse_args()
 
 
@@ -116,12 +123,28 @@ def main():
               "single-GPU and multi-GPU sharding is design-only in this build.", file=sys.stderr)
         sys.exit(2)
     import torch
-    import jhq_gpu_amd as jg
     if not torch.cuda.is_available():
         print("no HIP device visible", file=sys.stderr)
         sys.exit(1)
-    dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.config == 2:
+        bench_cfg2(args)
+    elif args.config in (3, 4):
+        bench_bytes(args, LARGE[args.config])
+    else:
+        bench_streaming(args)
+
+
+def bench_cfg2(args):
+    import torch
+    import jhq_gpu_amd as jg
+    dev = torch.device("cuda:0")
+    if args.seed is None:
+        args.seed = 0x4A48510002
+    if args.nprobe is None:
+        args.nprobe = "16,32,64"
+    if args.alpha is None:
+        args.alpha = "4,10"
 
     N = int(1_000_000 * args.scale)
     D, NQ, NCOMP = 1024, 10_000, 10_000
@@ -313,6 +336,375 @@ def main():
             "avg_launch_us": round(scan_us, 2),
         },
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+# ---------------------------------------------------------------------------
+# configs 3 and 4: 100M byte vectors, the scan streaming codes from HBM
+# ---------------------------------------------------------------------------
+LARGE = {
+    3: dict(name="cfg3", N=100_000_000, D=128, NQ=10_000, NCOMP=65_536, NLIST=65_536,
+            NPROBE=64, M=16, BATCH=64, kind="uint8"),
+    4: dict(name="cfg4", N=100_000_000, D=100, NQ=10_000, NCOMP=32_768, NLIST=32_768,
+            NPROBE=48, M=25, BATCH=32, kind="int8"),
+}
+
+
+def gen_bytes(torch, dev, n, d, ncomp, seed, kind, means=None, chunk=2_000_000):
+    """Byte-valued mixture rows on the device.
+    uint8: component means ~ N(34, 60^2) per coordinate, per-coordinate std 20,
+    rounded and clipped to 0..255 (about 30% of coordinates become 0).
+    int8: means ~ N(0, 32^2), plus 16 * Student-t(nu=4) noise (a normal over
+    sqrt(chi2_4 / 4)), rounded and clipped to -128..127."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    if means is None:
+        mu, sd = (34.0, 60.0) if kind == "uint8" else (0.0, 32.0)
+        means = mu + sd * torch.randn(ncomp, d, device=dev, generator=g)
+    lo, hi, dt = (0, 255, torch.uint8) if kind == "uint8" else (-128, 127, torch.int8)
+    out = torch.empty(n, d, dtype=dt, device=dev)
+    for i in range(0, n, chunk):
+        m = min(chunk, n - i)
+        c = torch.randint(0, ncomp, (m,), device=dev, generator=g)
+        z = torch.randn(m, d, device=dev, generator=g)
+        if kind == "uint8":
+            x = means[c] + 20.0 * z
+        else:
+            chi = (torch.randn(m, d, 4, device=dev, generator=g) ** 2).sum(2)
+            x = means[c] + 16.0 * z / torch.sqrt(chi / 4.0)
+        out[i:i + m] = torch.clamp(torch.round(x), lo, hi).to(dt)
+        del x, z, c
+    return out, means
+
+
+def ground_truth_int(torch, base, q, width=100, bchunk=4_000_000, qchunk=1024):
+    """Exact L2 neighbours of integer-valued data: ||x||^2 - 2<q,x> in fp32 is
+    exact (every partial sum is an integer below 2^24 for these ranges), so an
+    fp32 GEMM over base chunks with a running top-`width` is exact up to
+    order among equal distances.  Returns (ids [nq, width], dists [nq, width])
+    with dists = ||q - x||^2."""
+    nq = q.shape[0]
+    qn = (q.double() ** 2).sum(1)
+    best_d = torch.full((nq, width), float("inf"), device=q.device)
+    best_i = torch.full((nq, width), -1, dtype=torch.int64, device=q.device)
+    for b0 in range(0, base.shape[0], bchunk):
+        xb = base[b0:b0 + bchunk].float()
+        xn = (xb * xb).sum(1)
+        for q0 in range(0, nq, qchunk):
+            qq = q[q0:q0 + qchunk]
+            s = torch.addmm(xn.expand(qq.shape[0], -1), qq, xb.T, alpha=-2.0)
+            dd, ii = s.topk(min(width, s.shape[1]), dim=1, largest=False)
+            cd = torch.cat([best_d[q0:q0 + qchunk], dd], 1)
+            ci = torch.cat([best_i[q0:q0 + qchunk], ii + b0], 1)
+            o = cd.topk(width, dim=1, largest=False).indices
+            best_d[q0:q0 + qchunk] = torch.gather(cd, 1, o)
+            best_i[q0:q0 + qchunk] = torch.gather(ci, 1, o)
+            del s, dd, ii, cd, ci
+        del xb, xn
+        log(f"ground truth: {min(b0 + bchunk, base.shape[0])} / {base.shape[0]} base rows")
+    # ascending order, then add ||q||^2 back
+    o = best_d.argsort(dim=1, stable=True)
+    best_d = torch.gather(best_d, 1, o).double() + qn[:, None]
+    best_i = torch.gather(best_i, 1, o)
+    return best_i.cpu().numpy(), best_d.cpu().numpy()
+
+
+def exact_dists(torch, base, q, ids):
+    """||q - x_id||^2 in float64 for returned ids (-1 -> inf)."""
+    t = torch.as_tensor(ids, device=q.device, dtype=torch.int64)
+    ok = t >= 0
+    x = base[t.clamp(min=0)].double()
+    d = ((x - q.double()[:, None, :]) ** 2).sum(2)
+    d[~ok] = float("inf")
+    return d.cpu().numpy()
+
+
+def recall_tie_aware(dist_ret, gt_d, k=10):
+    """Hits are returned ids whose exact distance is <= the k-th true distance
+    (integer data has exact ties, so id sets alone under-count)."""
+    kth = gt_d[:, k - 1:k]
+    return float(np.minimum((dist_ret[:, :k] <= kth * (1 + 1e-12)).sum(1), k).sum()) / (
+        dist_ret.shape[0] * k)
+
+
+def timed_search(torch, ix, q, out_d, out_i, k, batch, warmup, steps):
+    nq = q.shape[0]
+    nb = (nq + batch - 1) // batch
+
+    def run(nsteps):
+        for st in range(nsteps):
+            b = st % nb
+            q0, q1 = b * batch, min(nq, b * batch + batch)
+            ix.search_device(q[q0:q1], k, out_d[q0:q1], out_i[q0:q1])
+
+    run(warmup)
+    torch.cuda.synchronize()
+    t0 = time.time()
+    run(steps)
+    torch.cuda.synchronize()
+    el = time.time() - t0
+    nqt = sum(min(batch, nq - (st % nb) * batch) for st in range(steps))
+    return nqt / el, el * 1000.0 / steps
+
+
+def step_times(torch, ix, q, out_d, out_i, k, batch):
+    ix.set_timing(True)
+    timed_search(torch, ix, q, out_d, out_i, k, batch, 0, (q.shape[0] + batch - 1) // batch)
+    tm, nbat = ix.timing()
+    ix.set_timing(False)
+    return {k2: v * 1000.0 / nbat for k2, v in tm.items()}
+
+
+def scan_roofline(ix, hq, k, batch, step_us):
+    dbg = ix.search_debug(hq, k)
+    L = ix.lists(include_payload=False)
+    sizes = np.diff(L["offsets"]).astype(np.int64)
+    nb = (hq.shape[0] + batch - 1) // batch
+    per_launch = float(sizes[dbg["probes"]].sum()) * ix.params.M / nb
+    us = step_us["scan_topck"]
+    ach = per_launch / (us * 1e-6) / 1e9
+    return {
+        "kernel": "scan_topck_kernel",
+        "dominant_step": max(step_us, key=step_us.get),
+        "bound": "hbm",
+        "achieved": round(ach, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(ach / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "traffic_note": "no counter run at this operating point",
+        "algorithmic_bytes_per_launch": int(per_launch),
+        "avg_launch_us": round(us, 2),
+    }
+
+
+def bench_bytes(args, cf):
+    os.environ.setdefault("JHQ_VERBOSE", "1")  # progress lines during the long build
+    import torch
+    import jhq_gpu_amd as jg
+    dev = torch.device("cuda:0")
+    seed = args.seed if args.seed is not None else 0x4A48510000 + args.config
+    N = int(cf["N"] * args.scale)
+    D, NQ, M, K, BATCH = cf["D"], cf["NQ"], cf["M"], 10, cf["BATCH"]
+    NLIST = cf["NLIST"] if args.scale >= 1.0 else max(64, int(cf["NLIST"] * args.scale))
+    NCOMP = cf["NCOMP"] if args.scale >= 1.0 else max(64, int(cf["NCOMP"] * args.scale))
+    npb = int((args.nprobe or str(cf["NPROBE"])).split(",")[0])
+    alpha = float((args.alpha or "4").split(",")[0])
+
+    t0 = time.time()
+    base, means = gen_bytes(torch, dev, N, D, NCOMP, seed, cf["kind"])
+    qb, _ = gen_bytes(torch, dev, NQ, D, NCOMP, seed + 0x100, cf["kind"], means)
+    torch.cuda.synchronize()
+    zero_frac = float((base[:1_000_000] == 0).float().mean())
+    log(f"data {cf['kind']} N={N} D={D} gen {time.time() - t0:.1f}s zero fraction "
+        f"{zero_frac:.3f}")
+    t0 = time.time()
+    hb = base.cpu().numpy()
+    hq = qb.cpu().numpy()
+    qf = qb.float()
+    log(f"host copy {time.time() - t0:.1f}s")
+
+    t0 = time.time()
+    gt_i, gt_d = ground_truth_int(torch, base, qf)
+    torch.cuda.synchronize()
+    log(f"ground truth {time.time() - t0:.1f}s")
+
+    p = jg.Params(M=M, B=8, Br=4, alpha=alpha, nlist=NLIST, nprobe=npb, ivf_iters=8,
+                  batch_size=BATCH, seed=42)
+    ix = jg.JHQGpuIndex(D, p)
+    n_train = min(N, max(100_000, 16 * NLIST))
+    t0 = time.time()
+    ix.train(hb[:n_train])
+    t_train = time.time() - t0
+    log(f"train n={n_train} {t_train:.1f}s")
+    t0 = time.time()
+    ix.add(hb)
+    t_add = time.time() - t0
+    log(f"add {t_add:.1f}s ({N / t_add / 1e6:.2f} M vectors/s)")
+    del hb
+
+    out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
+    out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
+    nb = (NQ + BATCH - 1) // BATCH
+    W = args.warmup if args.warmup > 0 else nb
+    Kst = args.steps if args.steps > 0 else 3 * nb
+    qps, ms = timed_search(torch, ix, qf, out_d, out_i, K, BATCH, W, Kst)
+    ids = out_i.cpu().numpy()
+    rec = recall_at(ids, gt_i, K)
+    rec_tie = recall_tie_aware(exact_dists(torch, base, qf, ids), gt_d, K)
+    rec_ref = recall_ref_def(ids, gt_i, K)
+    log(f"timed nprobe={npb} steps={Kst} qps={qps:.0f} ms/step={ms:.4f} recall@10={rec:.4f} "
+        f"tie-aware={rec_tie:.4f} 10@100={rec_ref:.4f}")
+    step_us = step_times(torch, ix, qf, out_d, out_i, K, BATCH)
+    log("per-batch us: " + " ".join(f"{k2}={v:.1f}" for k2, v in step_us.items()))
+    roof = scan_roofline(ix, hq.astype(np.float32), K, BATCH, step_us)
+    used, cap = ix.pool()
+    line = {
+        "metric": f"QPS ({N // 1_000_000}Mx{D} {cf['kind']} IVF, nprobe {npb}, batch {BATCH}); "
+                  "ADC-scan HBM GB/s vs peak",
+        "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": Kst, "warmup": W,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": f"synthetic: seeded {NCOMP}-component {cf['kind']} mixture (torch Philox), "
+                f"zero fraction {zero_frac:.3f}",
+        "config": {
+            "workload": f"{cf['name']} IVF-JHQ N={N} D={D} {cf['kind']}, nlist={NLIST}, M={M} "
+                        f"B=8 Br=4, alpha={alpha:g}, k=10, batch={BATCH}, queries resident "
+                        "in HBM",
+            "N": N, "nq": NQ, "nlist": NLIST, "nprobe": npb, "alpha": alpha, "k": K,
+            "batch": BATCH, "n_train": n_train,
+            "recall_at_10": round(rec, 4), "recall_at_10_tie_aware": round(rec_tie, 4),
+            "recall_at_10_reference_definition": round(rec_ref, 4),
+            "build_s": {"train": round(t_train, 2), "add": round(t_add, 2)},
+            "pool_slots": [used, cap],
+            "step_us_per_batch": {k2: round(v, 2) for k2, v in step_us.items()},
+        },
+        "roofline": roof,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
+# ---------------------------------------------------------------------------
+# config 5: streaming add interleaved with search
+# ---------------------------------------------------------------------------
+def gen_mixture_chunks(torch, dev, n, d, ncomp, seed, chunk=1_000_000):
+    """gen_mixture for large n: same distribution, built chunk by chunk into
+    one device tensor."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    means = torch.randn(ncomp, d, device=dev, generator=g)
+    scales = torch.exp(torch.empty(ncomp, d, device=dev).uniform_(math.log(0.1), 0.0,
+                                                                 generator=g))
+    out = torch.empty(n, d, device=dev)
+    for i in range(0, n, chunk):
+        m = min(chunk, n - i)
+        c = torch.randint(0, ncomp, (m,), device=dev, generator=g)
+        x = means[c] + scales[c] * torch.randn(m, d, device=dev, generator=g)
+        out[i:i + m] = x / x.norm(dim=1, keepdim=True)
+    return out, means, scales
+
+
+def ground_truth_f32(torch, base, q, width=100, short=300, qchunk=128, bchunk=2_000_000):
+    """Exact L2 neighbours of float data: an fp32 GEMM short list of `short`
+    per base chunk, merged, then re-ranked in float64."""
+    nq = q.shape[0]
+    bn = torch.cat([(base[i:i + bchunk].double() ** 2).sum(1).float()
+                    for i in range(0, base.shape[0], bchunk)])
+    gt = []
+    for q0 in range(0, nq, qchunk):
+        qq = q[q0:q0 + qchunk]
+        s = torch.addmm(bn.expand(qq.shape[0], -1), qq, base.T, alpha=-2.0)
+        cand = s.topk(short, dim=1, largest=False).indices
+        del s
+        xb = base[cand].double()
+        dd = ((xb - qq.double()[:, None, :]) ** 2).sum(2)
+        o = dd.argsort(dim=1, stable=True)[:, :width]
+        gt.append(torch.gather(cand, 1, o).cpu().numpy())
+        if (q0 // qchunk) % 20 == 19:
+            log(f"ground truth: {q0 + qq.shape[0]} / {nq} queries")
+    return np.concatenate(gt)
+
+
+def bench_streaming(args):
+    os.environ.setdefault("JHQ_VERBOSE", "1")
+    import torch
+    import jhq_gpu_amd as jg
+    dev = torch.device("cuda:0")
+    seed = args.seed if args.seed is not None else 0x4A48510005
+    sc = args.scale
+    N0, NINS, INS_B = int(10_000_000 * sc), int(1_000_000 * sc), 10_000
+    D, NQ, M, K, BATCH, NCOMP = 768, 10_000, 96, 100, 128, 10_000
+    NLIST = 8192 if sc >= 1.0 else max(64, int(8192 * sc))
+    npb = int((args.nprobe or "32").split(",")[0])
+    alpha = float((args.alpha or "4").split(",")[0])
+
+    t0 = time.time()
+    base, means, scales = gen_mixture_chunks(torch, dev, N0 + NINS, D, NCOMP, seed)
+    q, _, _ = gen_mixture(torch, dev, NQ, D, NCOMP, seed + 0x100, means, scales)
+    torch.cuda.synchronize()
+    hb = base.cpu().numpy()
+    log(f"data N0={N0} inserts={NINS} D={D} gen+copy {time.time() - t0:.1f}s")
+
+    p = jg.Params(M=M, B=8, Br=4, alpha=alpha, nlist=NLIST, nprobe=npb, ivf_iters=8,
+                  batch_size=BATCH, seed=42, residual_per_subspace=1)
+    ix = jg.JHQGpuIndex(D, p)
+    n_train = min(N0, max(100_000, 16 * NLIST))
+    t0 = time.time()
+    ix.train(hb[:n_train])
+    t_train = time.time() - t0
+    t0 = time.time()
+    ix.add(hb[:N0])
+    t_add = time.time() - t0
+    log(f"train n={n_train} {t_train:.1f}s, initial add {t_add:.1f}s")
+
+    out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
+    out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
+    nb = (NQ + BATCH - 1) // BATCH
+    # interleave: one insert batch, then one search batch
+    t_ins = t_srch = 0.0
+    nsearched = 0
+    upto = N0
+    t_all = time.time()
+    for it in range(NINS // INS_B):
+        t0 = time.time()
+        ix.append(hb[upto:upto + INS_B])
+        t_ins += time.time() - t0
+        upto += INS_B
+        b = it % nb
+        q0, q1 = b * BATCH, min(NQ, b * BATCH + BATCH)
+        t0 = time.time()
+        ix.search_device(q[q0:q1], K, out_d[q0:q1], out_i[q0:q1])
+        torch.cuda.synchronize()
+        t_srch += time.time() - t0
+        nsearched += q1 - q0
+    t_all = time.time() - t_all
+    nbatches = NINS // INS_B
+    log(f"streaming: {nbatches} inserts of {INS_B} in {t_ins:.2f}s "
+        f"({NINS / max(t_ins, 1e-9):.0f} vectors/s), {nsearched} queries in {t_srch:.3f}s")
+    del hb
+
+    W = args.warmup if args.warmup > 0 else nb
+    Kst = args.steps if args.steps > 0 else 3 * nb
+    qps, ms = timed_search(torch, ix, q, out_d, out_i, K, BATCH, W, Kst)
+    t0 = time.time()
+    gt = ground_truth_f32(torch, base, q)
+    log(f"ground truth {time.time() - t0:.1f}s")
+    ids = out_i.cpu().numpy()
+    rec10 = recall_at(ids, gt, 10)
+    rec100 = recall_at(ids, gt, 100)
+    log(f"timed steps={Kst} qps={qps:.0f} ms/step={ms:.4f} recall@10={rec10:.4f} "
+        f"recall@100={rec100:.4f}")
+    step_us = step_times(torch, ix, q, out_d, out_i, K, BATCH)
+    log("per-batch us: " + " ".join(f"{k2}={v:.1f}" for k2, v in step_us.items()))
+    roof = scan_roofline(ix, q.cpu().numpy(), K, BATCH, step_us)
+    used, cap = ix.pool()
+    line = {
+        "metric": "QPS after streaming add (11Mx768 IVF, nprobe 32, k=100, batch 128); "
+                  "ADC-scan HBM GB/s vs peak",
+        "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": Kst, "warmup": W,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: seeded 10k-component Gaussian mixture, L2-normalised (torch Philox)",
+        "config": {
+            "workload": f"cfg5 streaming: N0={N0} + {NINS} appends of {INS_B} interleaved with "
+                        f"{BATCH}-query searches, D=768, nlist={NLIST}, M=96 per-subspace "
+                        f"residual codebooks, alpha={alpha:g}, k=100",
+            "N_final": upto, "nq": NQ, "nlist": NLIST, "nprobe": npb, "alpha": alpha, "k": K,
+            "batch": BATCH, "n_train": n_train,
+            "recall_at_10": round(rec10, 4), "recall_at_100": round(rec100, 4),
+            "streaming": {"insert_batches": nbatches, "insert_vectors_per_s":
+                          round(NINS / max(t_ins, 1e-9), 1),
+                          "insert_ms_per_batch": round(t_ins * 1000 / max(nbatches, 1), 3),
+                          "search_qps_interleaved": round(nsearched / max(t_srch, 1e-9), 1),
+                          "wall_s": round(t_all, 2)},
+            "build_s": {"train": round(t_train, 2), "initial_add": round(t_add, 2)},
+            "pool_slots": [used, cap],
+            "step_us_per_batch": {k2: round(v, 2) for k2, v in step_us.items()},
+        },
+        "roofline": roof,
+        "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
 

@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -21,6 +22,15 @@
 namespace {
 
 thread_local std::string g_err;
+
+// Progress lines on stderr for long builds, when JHQ_VERBOSE is set.
+bool verbose() {
+    static const bool v = [] {
+        const char* e = std::getenv("JHQ_VERBOSE");
+        return e && *e && *e != '0';
+    }();
+    return v;
+}
 
 int fail(int code, const std::string& msg) {
     g_err = msg;
@@ -210,6 +220,9 @@ int train_ivf(jhq_index* ix, const float* h_y, const float* d_y, int64_t n) {
     std::vector<double> sums(static_cast<size_t>(nlist) * d);
     std::vector<int64_t> counts(nlist);
     for (int iter = 0; iter < ix->ivf_iters; iter++) {
+        if (verbose())
+            std::fprintf(stderr, "[jhq] train: IVF k-means iteration %d/%d (nlist %d, n %lld)\n",
+                         iter + 1, ix->ivf_iters, nlist, static_cast<long long>(n));
         JHQ_TRY(upload_centroids(ix));
         JHQ_TRY(assign_rows(ix, d_y, n, dasg.p, keys));
         JHQ_HIP(hipMemcpyAsync(asg.data(), dasg.p, static_cast<size_t>(n) * sizeof(int32_t),
@@ -548,6 +561,9 @@ int train_impl(jhq_index* ix, const float* x, int64_t n_train) {
         return h_y[static_cast<size_t>(i) * d + j] -
                ix->c1d[(h_codes[static_cast<size_t>(i) * M + m] >> (k * ix->bpd)) & kmask];
     };
+    if (verbose())
+        std::fprintf(stderr, "[jhq] train: %d residual codebook(s) over %lld values each\n", ix->RC,
+                     static_cast<long long>(n_train) * (ix->RC == 1 ? d : Ds));
     ix->res_c1d.assign(static_cast<size_t>(ix->RC) * ix->Kr, 0.f);
     std::vector<float> vals;
     for (int cb = 0; cb < ix->RC; cb++) {
@@ -660,6 +676,9 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
                                 drc.p + start * bpv, dco.p + start, 3, s));
             JHQ_TRY(assign_rows(ix, dyb.p, nb, dasg.p + start, keys));
             JHQ_HIP(hipStreamSynchronize(s));
+            if (verbose() && (start / AB + 1) % 128 == 0)
+                std::fprintf(stderr, "[jhq] add: %lld / %lld vectors encoded and assigned\n",
+                             static_cast<long long>(start + nb), static_cast<long long>(n));
         }
     }
     // stable order by (list, id) of the new vectors (the reference's
