@@ -223,6 +223,14 @@ int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent,
                  const float* d_cent_norms, int nlist, int32_t* d_assign,
                  void* stream);
 
+/* select_probes_kernel — v14/search.cu:13-62: per query the P lists of
+ * smallest score (ties to the lower list id), in that order; gofs[b][P+1] is
+ * the prefix of ceil(list_size / 16) over the probes and qtot[b] its total.
+ * Any nlist (the reference holds a row in shared memory, v14/search.cu:22-33). */
+int jhq_k_select_probes(const float* d_scores, int B, int nlist, int P,
+                        const int32_t* d_list_sizes, int32_t* d_probes,
+                        int32_t* d_gofs, int32_t* d_qtot, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

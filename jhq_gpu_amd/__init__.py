@@ -110,6 +110,7 @@ _SIGS = {
     "jhq_k_residual_encode": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _I,
                                    _I, _I, _I, _VP]),
     "jhq_k_assign": (_I, [_VP, _I64, _I, _VP, _VP, _I, _VP, _VP]),
+    "jhq_k_select_probes": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
 }
 
 
@@ -385,3 +386,11 @@ def k_assign(y, cent, norms, assign, stream=None):
     n, d = y.shape
     _check(lib().jhq_k_assign(_dptr(y), int(n), int(d), _dptr(cent), _dptr(norms),
                               int(cent.shape[0]), _dptr(assign), _stream(stream)))
+
+
+def k_select_probes(scores, list_sizes, P, probes, gofs, qtot, stream=None):
+    """scores [B, nlist] float32, list_sizes [nlist] int32 (device tensors)."""
+    B, nlist = scores.shape
+    _check(lib().jhq_k_select_probes(_dptr(scores), int(B), int(nlist), int(P),
+                                     _dptr(list_sizes), _dptr(probes), _dptr(gofs), _dptr(qtot),
+                                     _stream(stream)))

@@ -629,12 +629,66 @@ int grow_pool(jhq_index* ix, int64_t need) {
     return JHQ_OK;
 }
 
+// Re-packs every list into a new pool: list l gets capacity
+// round16(need[l] * 5/4) (need = its size after the pending insert), blocks
+// are laid out in list order, dead blocks left by earlier moves are dropped,
+// and the pool keeps a quarter of headroom for lists that move later.
+int repack_pool(jhq_index* ix, const std::vector<int64_t>& need) {
+    const int nlist = ix->nlist, M = ix->M, bpv = ix->bpv;
+    std::vector<int32_t> nstart(nlist), ncap(nlist);
+    std::vector<int4> moves;
+    int64_t pos = 0;
+    for (int l = 0; l < nlist; l++) {
+        const int64_t want = need[l] > 0 ? need[l] + need[l] / 4 : 0;
+        const int64_t cap = (want + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+        if (ix->l_size[l] > 0) {
+            moves.push_back(make_int4(ix->l_start[l], ix->l_cap[l], ix->l_size[l], 0));
+            moves.push_back(make_int4(static_cast<int>(pos), static_cast<int>(cap), 0, 0));
+        }
+        nstart[l] = static_cast<int32_t>(pos);
+        ncap[l] = static_cast<int32_t>(cap);
+        pos += cap;
+        if (pos > INT32_MAX) return fail(JHQ_EINVAL, "list pool exceeds int32 slots");
+    }
+    const int64_t pcap = std::min<int64_t>(std::max<int64_t>(pos + pos / 4, 1), INT32_MAX);
+    DBuf<uint8_t> nc, nr;
+    DBuf<float> nco;
+    DBuf<int32_t> ni;
+    JHQ_TRY(nc.alloc(static_cast<size_t>(pcap) * M + 16));
+    JHQ_TRY(nr.alloc(static_cast<size_t>(pcap) * bpv));
+    JHQ_TRY(nco.alloc(static_cast<size_t>(pcap)));
+    JHQ_TRY(ni.alloc(static_cast<size_t>(pcap)));
+    hipStream_t s = ix->stream;
+    if (!moves.empty()) {
+        DBuf<int4> dmoves;
+        JHQ_TRY(dmoves.upload(moves.data(), moves.size()));
+        JHQ_HIP(jhq::relocate_lists(dmoves.p, static_cast<int>(moves.size() / 2), M, bpv,
+                                    ix->dcodes_t.p, nc.p, ix->dres.p, nr.p, ix->dcorr.p, nco.p,
+                                    ix->dlist_ids.p, ni.p, s));
+        JHQ_HIP(hipStreamSynchronize(s));
+    }
+    std::swap(ix->dcodes_t.p, nc.p);
+    std::swap(ix->dcodes_t.n, nc.n);
+    std::swap(ix->dres.p, nr.p);
+    std::swap(ix->dres.n, nr.n);
+    std::swap(ix->dcorr.p, nco.p);
+    std::swap(ix->dcorr.n, nco.n);
+    std::swap(ix->dlist_ids.p, ni.p);
+    std::swap(ix->dlist_ids.n, ni.n);
+    ix->l_start = nstart;
+    ix->l_cap = ncap;
+    ix->pool_cap = pcap;
+    ix->pool_used = pos;
+    return JHQ_OK;
+}
+
 // Rotates, encodes and assigns n vectors x (host, dtype) in add_batch chunks
 // (v14/jhq_gpu_index.cu:438-463), inserts them at the end of their lists
 // with ids id_base + i, and grows list blocks as needed.  exact_fit: the
 // pool is empty and every list gets capacity round16(size) (the one-shot add
 // of the reference); otherwise a list that outgrows its block moves to the
-// end of the pool with twice the capacity.
+// end of the pool with 1.5 times the capacity, and when the pool has no room
+// left for such moves every list is re-packed into a new pool instead.
 int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_fit) {
     JHQ_TRY(ix->ensure_stream());
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
@@ -714,7 +768,7 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         for (int l = 0; l < nlist; l++) {
             const int64_t need = ix->l_size[l] + add[l + 1];
             if (need <= ix->l_cap[l]) continue;
-            int64_t cap = std::max<int64_t>(need, 2 * static_cast<int64_t>(ix->l_cap[l]));
+            int64_t cap = std::max<int64_t>(need, ix->l_cap[l] + ix->l_cap[l] / 2);
             cap = std::max<int64_t>(cap, jhq::kGroup);
             cap = (cap + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
             if (ix->l_size[l] > 0) {
@@ -725,8 +779,18 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
             ncap[l] = static_cast<int32_t>(cap);
             used += cap;
         }
+        if (used > ix->pool_cap && ix->pool_used > 0) {
+            // no room for the moves: re-pack every list instead of growing
+            std::vector<int64_t> need(nlist);
+            for (int l = 0; l < nlist; l++) need[l] = ix->l_size[l] + add[l + 1];
+            JHQ_TRY(repack_pool(ix, need));
+            moves.clear();
+            nstart = ix->l_start;
+            ncap = ix->l_cap;
+            used = ix->pool_used;
+        }
         if (used > INT32_MAX) return fail(JHQ_EINVAL, "list pool exceeds int32 slots");
-        JHQ_TRY(grow_pool(ix, used));
+        JHQ_TRY(grow_pool(ix, used));  // only an empty pool grows here
         if (!moves.empty()) {
             DBuf<int4> dmoves;
             JHQ_TRY(dmoves.upload(moves.data(), moves.size()));
@@ -1218,6 +1282,30 @@ int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent, const 
     if (e == hipSuccess) e = jhq::keys_to_assign(keys, n, d_assign, s);
     (void)hipFreeAsync(keys, s);
     if (e != hipSuccess) return fail(JHQ_EDEVICE, std::string("assign: ") + hipGetErrorString(e));
+    return JHQ_OK;
+}
+
+int jhq_k_select_probes(const float* d_scores, int B, int nlist, int P,
+                        const int32_t* d_list_sizes, int32_t* d_probes, int32_t* d_gofs,
+                        int32_t* d_qtot, void* stream) {
+    if (!d_scores || !d_list_sizes || !d_probes || !d_gofs || !d_qtot || B <= 0 || nlist <= 0 ||
+        P <= 0 || P > nlist)
+        return fail(JHQ_EINVAL, "bad argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<int32_t> sizes(nlist);
+    JHQ_HIP(hipMemcpyAsync(sizes.data(), d_list_sizes, sizes.size() * 4, hipMemcpyDeviceToHost, s));
+    JHQ_HIP(hipStreamSynchronize(s));
+    std::vector<int4> h(nlist);
+    int64_t cb = 0;
+    for (int l = 0; l < nlist; l++) {
+        if (sizes[l] < 0) return fail(JHQ_EINVAL, "negative list size");
+        h[l] = make_int4(0, sizes[l], sizes[l], static_cast<int>(cb));
+        cb += sizes[l];
+    }
+    DBuf<int4> ld;
+    JHQ_TRY(ld.upload(h.data(), h.size()));
+    JHQ_HIP(jhq::select_probes(d_scores, B, nlist, P, ld.p, d_probes, d_gofs, d_qtot, s));
+    JHQ_HIP(hipStreamSynchronize(s));
     return JHQ_OK;
 }
 

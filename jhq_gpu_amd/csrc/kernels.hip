@@ -1193,31 +1193,136 @@ __device__ unsigned char* stream_carve(unsigned char* p, int k, StreamSel* S) {
 // per query; writes probes[b][P] ascending, gofs[b][P+1] (prefix of the
 // probed lists' padded group counts) and qtot[b] = gofs[b][P].
 // ---------------------------------------------------------------------------
+constexpr int kProbeFastP = 128;   // largest P served by the two-pass path
+constexpr int kProbeU = 8;         // float4 loads in flight per thread
+constexpr int kProbeSurv = 1024;   // short-list capacity of the two-pass path
+
+// The r-th smallest (1 <= r <= 64) of the wave's 64 lane values, bit by bit
+// from the top with ballots.
+__device__ __forceinline__ uint32_t wave_kth_u32(uint32_t v, int r) {
+    uint32_t res = 0u;
+    unsigned long long cand = ~0ull;
+    for (int bit = 31; bit >= 0; bit--) {
+        const unsigned long long zeros = cand & __ballot(((v >> bit) & 1u) == 0u);
+        const int nz = __popcll(zeros);
+        if (r <= nz) {
+            cand = zeros;
+        } else {
+            r -= nz;
+            cand &= ~zeros;
+            res |= 1u << bit;
+        }
+    }
+    return res;
+}
+
 template <int NT>
 __global__ void __launch_bounds__(NT)
 select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                      const int4* __restrict__ ldesc, int32_t* __restrict__ probes,
                      int32_t* __restrict__ gofs, int32_t* __restrict__ qtot) {
+    // Fast path (P <= kProbeFastP), two cheap passes over the row:
+    //   1. every thread takes the minimum ord(score) of its share; each wave
+    //      finds the ceil(P / waves)-th smallest of its 64 lane minima, and
+    //      the bound T is the largest of those, so at least P scores are <= T
+    //      (each counted lane minimum is one);
+    //   2. every score with ord <= T is appended to a short list as the key
+    //      (ord << 32 | list); its exact top P is the row's top P.
+    // A short list longer than kProbeSurv (many equal scores) falls back to
+    // streaming the row through the exact selector.
     extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int NW = NT / 64;
     StreamSel S;
-    int* gcnt = (int*)stream_carve<NT>(smem, P, &S);
-    const int b = blockIdx.x, tid = threadIdx.x;
+    unsigned char* tail = stream_carve<NT>(smem, P, &S);
+    int* gcnt = (int*)tail;
+    unsigned long long* surv = (unsigned long long*)(tail + align16((size_t)P * 4));  // [kProbeSurv]
+    uint32_t* wth = (uint32_t*)(surv + kProbeSurv);  // [NW]
+    int* scnt = (int*)(wth + NW);                    // [1]
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* row = scores + (int64_t)b * nlist;
+    JHQ_PHASE_DECL
     stream_begin<NT>(S);
+    if (tid == 0) *scnt = 0;
     __syncthreads();
-    const int rounds = (nlist + NT * 4 - 1) / (NT * 4);
-    for (int r = 0; r < rounds; r++) {
-        const int i0 = r * NT * 4 + tid * 4;
-        uint32_t o[4], tg[4];
+    JHQ_PHASE(0);
+    int kk = 0;
+    bool exact = false;
+    if (P <= kProbeFastP) {
+        const bool vec = (nlist & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0;
+        // visits every score of this thread's share: f(ord, list)
+        auto visit = [&](auto f) {
+            if (vec) {
+                const float4* r4 = reinterpret_cast<const float4*>(row);
+                const int n4 = nlist >> 2;
+                for (int base = 0; base < n4; base += NT * kProbeU) {
+                    float4 v[kProbeU];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = i0 + j;
-            o[j] = i < nlist ? f2ord(row[i]) : ~0u;
-            tg[j] = (uint32_t)i;
+                    for (int u = 0; u < kProbeU; u++) v[u] = r4[min(base + u * NT + tid, n4 - 1)];
+#pragma unroll
+                    for (int u = 0; u < kProbeU; u++) {
+                        const int i = base + u * NT + tid;
+                        if (i < n4) {
+                            f(f2ord(v[u].x), 4 * i);
+                            f(f2ord(v[u].y), 4 * i + 1);
+                            f(f2ord(v[u].z), 4 * i + 2);
+                            f(f2ord(v[u].w), 4 * i + 3);
+                        }
+                    }
+                }
+            } else {
+                for (int base = 0; base < nlist; base += NT * kProbeU * 4) {
+                    float v[kProbeU * 4];
+#pragma unroll
+                    for (int u = 0; u < kProbeU * 4; u++) v[u] = row[min(base + u * NT + tid, nlist - 1)];
+#pragma unroll
+                    for (int u = 0; u < kProbeU * 4; u++) {
+                        const int i = base + u * NT + tid;
+                        if (i < nlist) f(f2ord(v[u]), i);
+                    }
+                }
+            }
+        };
+        uint32_t mn = ~0u;
+        visit([&](uint32_t o, int) { mn = o < mn ? o : mn; });
+        JHQ_PHASE(1);
+        const uint32_t tw = wave_kth_u32(mn, (P + NW - 1) / NW);
+        if (lane == 0) wth[wv] = tw;
+        __syncthreads();
+        uint32_t T = 0u;
+#pragma unroll
+        for (int w = 0; w < NW; w++) T = wth[w] > T ? wth[w] : T;
+        JHQ_PHASE(2);
+        visit([&](uint32_t o, int i) {
+            if (o <= T) {
+                const int at = atomicAdd(scnt, 1);
+                if (at < kProbeSurv) surv[at] = ((unsigned long long)o << 32) | (uint32_t)i;
+            }
+        });
+        __syncthreads();
+        const int ns = *scnt;
+        if (ns <= kProbeSurv) {
+            rank_select<NT>(surv, ns, P, S.kout);
+            kk = P;
+            exact = true;
         }
-        stream_round<NT, 4>(S, P, o, tg);
+        JHQ_PHASE(3);
     }
-    const int kk = stream_end<NT>(S, P);
+    if (!exact) {
+        const int rounds = (nlist + NT * 4 - 1) / (NT * 4);
+        for (int r = 0; r < rounds; r++) {
+            const int i0 = r * NT * 4 + tid * 4;
+            uint32_t o[4], tg[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = i0 + j;
+                o[j] = i < nlist ? f2ord(row[i]) : ~0u;
+                tg[j] = (uint32_t)i;
+            }
+            stream_round<NT, 4>(S, P, o, tg);
+        }
+        kk = stream_end<NT>(S, P);
+        JHQ_PHASE(5);
+    }
     for (int i = tid; i < P; i += NT) {
         const int l = i < kk ? (int)(uint32_t)(S.kout[i] & 0xffffffffull) : 0;
         probes[(int64_t)b * P + i] = l;
@@ -1242,6 +1347,8 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
         }
         if (tid == 0) qtot[b] = carry;
     }
+    JHQ_PHASE(6);
+    JHQ_PHASE_FLUSH(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1554,6 +1661,7 @@ constexpr int kScanNT = JHQ_SCAN_NT;
 constexpr int kRefineNT = 512;
 constexpr int kProbeNT = 512;
 
+
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out) {
     const size_t lds = (size_t)M * 256 * 4 + stream_lds_bytes(kScanNT, ck) +
                        (size_t)((d + 3) & ~3) * 4 + (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 +
@@ -1567,7 +1675,8 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 
 hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
                          int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s) {
-    const size_t lds = stream_lds_bytes(kProbeNT, P) + (size_t)P * 4 + 16;
+    const size_t lds = stream_lds_bytes(kProbeNT, P) + align16((size_t)P * 4) +
+                       (size_t)kProbeSurv * 8 + (size_t)(kProbeNT / 64) * 4 + 16;
     static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<kProbeNT>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(select_probes_kernel<kProbeNT>, dim3(B), dim3(kProbeNT), lds, s, scores,

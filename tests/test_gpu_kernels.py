@@ -67,3 +67,54 @@ def test_assign_bit_exact_with_ties(gpu, n, d, nlist):
     jg.k_assign(_t(y, gpu), _t(cent, gpu), _t(norms, gpu), a)
     torch.cuda.synchronize()
     assert np.array_equal(a.cpu().numpy(), po.assign(y, cent, norms))
+
+
+@pytest.mark.parametrize("B,nlist,P", [(5, 100, 7), (4, 4096, 16), (3, 5000, 64), (2, 8191, 512),
+                                       (64, 65536, 64), (2, 65536, 1)])
+def test_select_probes_exact_with_ties(gpu, B, nlist, P):
+    """Probe lists in (score, list) order, exactly, through both the one-pass
+    selection and the sliced selection used for large nlist; scores with many
+    exact ties (small integers), so the tie rule decides most slots."""
+    import torch
+    rng = np.random.default_rng(B * nlist + P)
+    scores = rng.integers(-40, 40, (B, nlist)).astype(np.float32)
+    scores[scores == 0] = 0.5  # keep -0.0 / +0.0 out of the tie rule
+    scores[0, nlist // 2:] = -100.0  # the winners sit in the later slices
+    sizes = rng.integers(0, 50, nlist).astype(np.int32)
+    probes = torch.empty((B, P), dtype=torch.int32, device=gpu)
+    gofs = torch.empty((B, P + 1), dtype=torch.int32, device=gpu)
+    qtot = torch.empty((B,), dtype=torch.int32, device=gpu)
+    jg.k_select_probes(_t(scores, gpu), _t(sizes, gpu), P, probes, gofs, qtot)
+    torch.cuda.synchronize()
+    tags = np.arange(nlist, dtype=np.int32)
+    want = np.stack([po.select_topk_pairs(scores[b], tags, P)[1] for b in range(B)])
+    assert np.array_equal(probes.cpu().numpy(), want)
+    groups = (sizes[want] + 15) // 16
+    wg = np.concatenate([np.zeros((B, 1), np.int64), np.cumsum(groups, 1)], 1)
+    assert np.array_equal(gofs.cpu().numpy(), wg)
+    assert np.array_equal(qtot.cpu().numpy(), wg[:, -1])
+
+
+@pytest.mark.parametrize("nlist,P", [(65536, 64), (4100, 16), (8192, 128), (8192, 200)])
+def test_select_probes_clustered_top(gpu, nlist, P):
+    """The row's best lists packed into one stride class (lists 4*(5 + 512*j)
+    + r and 5 + 512*j, the share one thread reads in either load layout), so a
+    per-thread shortcut alone would lose some of them; the result must still
+    be the exact top P."""
+    import torch
+    B = 3
+    rng = np.random.default_rng(nlist + P)
+    scores = rng.standard_normal((B, nlist)).astype(np.float32) + 10.0
+    hot = np.array(sorted({4 * (5 + 512 * j) + r for j in range(64) for r in range(4)} |
+                          {5 + 512 * j for j in range(64)}))
+    hot = hot[hot < nlist]
+    scores[:, hot] = -rng.random((B, hot.size)).astype(np.float32)
+    sizes = rng.integers(0, 50, nlist).astype(np.int32)
+    probes = torch.empty((B, P), dtype=torch.int32, device=gpu)
+    gofs = torch.empty((B, P + 1), dtype=torch.int32, device=gpu)
+    qtot = torch.empty((B,), dtype=torch.int32, device=gpu)
+    jg.k_select_probes(_t(scores, gpu), _t(sizes, gpu), P, probes, gofs, qtot)
+    torch.cuda.synchronize()
+    tags = np.arange(nlist, dtype=np.int32)
+    want = np.stack([po.select_topk_pairs(scores[b], tags, P)[1] for b in range(B)])
+    assert np.array_equal(probes.cpu().numpy(), want)

@@ -58,6 +58,9 @@ def test_streaming_append_equals_one_shot(gpu, per_sub):
         _stagewise(g, o, q, k)
     used, cap = g.pool()
     assert used <= cap and used >= upto
+    # re-packing bounds the pool: a quarter of headroom per list plus a
+    # quarter for later moves, never the dead blocks of moved lists
+    assert cap <= 1.6 * upto + 20 * nlist
 
 
 def test_append_from_empty_and_add_guard(gpu):
