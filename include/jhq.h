@@ -105,8 +105,10 @@ int jhq_add_ex(jhq_index* idx, const void* x, int dtype, int64_t n);
  * and appends them to their IVF lists, ids continuing from ntotal.  May be
  * called any number of times after train(), before or after add(), and
  * between searches.  A list that outgrows its block moves to the end of the
- * list pool with twice the capacity.  Results are identical to one add() of
- * all vectors in the same order. */
+ * list pool with 1.5 times the capacity; when the pool has no room left for
+ * such moves, every list is re-packed into a new pool with a quarter of
+ * headroom each (blocks left behind by earlier moves are dropped).  Results
+ * are identical to one add() of all vectors in the same order. */
 int jhq_append(jhq_index* idx, const float* x, int64_t n);
 int jhq_append_ex(jhq_index* idx, const void* x, int dtype, int64_t n);
 
@@ -174,8 +176,8 @@ int jhq_save(const jhq_index* idx, const char* path);
 int jhq_get_params(const jhq_index* idx, jhq_params* out);
 int jhq_load(const char* path, jhq_index** out);
 
-/* List pool occupancy: slots in use (including padding and blocks left
- * behind by relocations) and allocated slots. */
+/* List pool occupancy: slots in use (including padding, headroom and blocks
+ * left behind by moves since the last re-pack) and allocated slots. */
 int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity);
 
 /* Search that also returns, per query, the rotated query [nq x d] (the
