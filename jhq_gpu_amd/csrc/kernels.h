@@ -76,6 +76,8 @@ struct ScanShape {
     int G;             // persistent scan workgroups
     int lds;           // dynamic LDS bytes of the scan kernel
     int max_segments;  // upper bound on top-ck lists per batch (partial rows)
+    int wave;          // 0: workgroup-synchronous selection; J: wave selection, 64*J-key buffers
+    int region;        // wave selection: bytes of the LUT / merge region
 };
 // LDS plan of the scan kernel; returns false if the byte LUT and the
 // selection buffers do not fit.

@@ -1645,6 +1645,286 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
     JHQ_PHASE_FLUSH(0);
 }
 
+// ---------------------------------------------------------------------------
+// Wave-level exact selection.  buf[0..n) holds distinct keys
+// (value << 32 | tag), n <= 64 * J; keeps the k smallest (k < n), compacted
+// to buf[0..k) in no particular order, and returns the k-th smallest key's
+// value.  The value is found bit by bit with ballots; among keys equal to it,
+// the needed number of smallest tags is found the same way.
+// ---------------------------------------------------------------------------
+template <int J>
+__device__ __forceinline__ uint32_t wave_prune(unsigned long long* buf, int n, int k) {
+    const int lane = threadIdx.x & 63;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    unsigned long long v[J], valid[J], cand[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int i = j * 64 + lane;
+        v[j] = i < n ? buf[i] : ~0ull;
+        valid[j] = __ballot(i < n);
+        cand[j] = valid[j];
+    }
+    uint32_t V = 0u;
+    int r = k;
+    for (int bit = 31; bit >= 0; bit--) {
+        unsigned long long z[J];
+        int nz = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            z[j] = cand[j] & __ballot((((uint32_t)(v[j] >> 32) >> bit) & 1u) == 0u);
+            nz += __popcll(z[j]);
+        }
+        if (r <= nz) {
+#pragma unroll
+            for (int j = 0; j < J; j++) cand[j] = z[j];
+        } else {
+            r -= nz;
+#pragma unroll
+            for (int j = 0; j < J; j++) cand[j] &= ~z[j];
+            V |= 1u << bit;
+        }
+    }
+    // cand: the keys whose value is V; the r smallest tags among them stay
+    int ceq = 0;
+#pragma unroll
+    for (int j = 0; j < J; j++) ceq += __popcll(cand[j]);
+    uint32_t Tt = ~0u;
+    if (ceq > r) {
+        Tt = 0u;
+        for (int bit = 31; bit >= 0; bit--) {
+            unsigned long long z[J];
+            int nz = 0;
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                z[j] = cand[j] & __ballot((((uint32_t)v[j] >> bit) & 1u) == 0u);
+                nz += __popcll(z[j]);
+            }
+            if (r <= nz) {
+#pragma unroll
+                for (int j = 0; j < J; j++) cand[j] = z[j];
+            } else {
+                r -= nz;
+#pragma unroll
+                for (int j = 0; j < J; j++) cand[j] &= ~z[j];
+                Tt |= 1u << bit;
+            }
+        }
+    }
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const uint32_t hi = (uint32_t)(v[j] >> 32), lo = (uint32_t)v[j];
+        const bool keep = ((valid[j] >> lane) & 1ull) && (hi < V || (hi == V && lo <= Tt));
+        const unsigned long long mk = __ballot(keep);
+        if (keep) buf[base + __popcll(mk & lt)] = v[j];
+        base += __popcll(mk);
+    }
+    return V;
+}
+
+// ---------------------------------------------------------------------------
+// ADC scan with wave-independent selection (same work plan, segments,
+// arithmetic and output as scan_topck_kernel).  Inside a segment the waves
+// take tasks of 16 groups (64 lanes x 4 candidates) from a counter, with no
+// workgroup barrier until the segment ends.  Each wave keeps its candidates
+// at or below min(own bound, shared bound) in its own LDS buffer; when the
+// buffer has no room for another 64 it is pruned to the wave's exact top-ck,
+// whose ck-th value becomes the wave's bound and lowers the shared bound (a
+// candidate above it has ck smaller candidates in that wave).  At the
+// segment's end every wave prunes to ck, the keys at or below the shared
+// bound are gathered where the LUT was, and one exact selection emits the
+// segment's top-ck.
+// ---------------------------------------------------------------------------
+template <int NT, int SU, int J>
+__global__ void __launch_bounds__(NT)
+scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
+                 const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
+                 const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
+                 const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t, int ck,
+                 int region_bytes, unsigned long long* __restrict__ partial,
+                 int32_t* __restrict__ partial_slot) {
+    // wave buffers of 64 * J keys (ck + 64 <= 64 * J)
+    constexpr int CPT = kScanCPT, TPG = kGroup / CPT, NW = NT / 64, wcap = 64 * J;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* lut = (float*)smem;                                  // or the merge keys
+    unsigned long long* merge = (unsigned long long*)smem;
+    unsigned long long* wbuf = (unsigned long long*)(smem + region_bytes);  // [NW][wcap]
+    unsigned long long* kout =
+        wbuf + max((size_t)NW * wcap, (size_t)((d + 3) & ~3) / 2);  // [ck]
+    unsigned long long* ktmp = kout + ck;                       // [ck]
+    int* kidx = (int*)(ktmp + ck);                              // [ck]
+    SelState* st = (SelState*)(kidx + ((ck + 3) & ~3));
+    int* ctl = (int*)(st + 1);                                  // Tg, merge count, task counter
+    float* sq = (float*)wbuf;  // the query, needed only until the LUT is built
+    int* qpre = ctl + 4;
+    int* spre = qpre + B + 1;
+    int32_t* sg = spre + B + 1;
+    int32_t* spad0 = sg + P + 1;
+    int32_t* snpad = spad0 + P;
+    int32_t* snl = snpad + P;
+    int32_t* soff = snl + P;
+    float* sc1d = (float*)(soff + P);
+    int* wsum = (int*)(sc1d + K1D);
+
+    const int tid = threadIdx.x, w = blockIdx.x, lane = tid & 63, wv = tid >> 6;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    unsigned long long* wb = wbuf + (size_t)wv * wcap;
+    for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
+    const int64_t T = qpre[B];
+    if (w >= G) return;
+    const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
+    int b;
+    {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (qpre[mid] <= x0) lo = mid;
+            else hi = mid - 1;
+        }
+        b = lo;
+    }
+    for (; b < B && qpre[b] < x1; b++) {
+        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
+        if (qb1 <= qb0) continue;
+        const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
+        const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
+        __syncthreads();
+        for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
+        for (int i = tid; i < P; i += NT) {
+            const int4 L = ldesc[probes[(int64_t)b * P + i]];
+            spad0[i] = L.x;
+            snpad[i] = L.y;
+            snl[i] = L.z;
+            soff[i] = L.w;
+        }
+        for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
+        if (tid == 0) {
+            ctl[0] = (int)~0u;  // shared bound
+            ctl[1] = 0;         // merge count
+            ctl[2] = 0;         // next task
+        }
+        __syncthreads();
+        build_lut_lds<NT>(sq, M, Ds, K1D, bpd, sc1d, lut);
+        __syncthreads();
+
+        const int ntask = (gB - gA + 15) / 16;
+        int nw = 0;          // keys in this wave's buffer (wave-uniform)
+        uint32_t Tw = ~0u;   // this wave's bound
+        for (;;) {
+            int t = 0;
+            if (lane == 0) t = atomicAdd(&ctl[2], 1);
+            t = __shfl(t, 0);
+            if (t >= ntask) break;
+            const int g = gA + t * 16 + (lane >> 2), sub = lane & (TPG - 1);
+            uint32_t o[CPT], tg[CPT];
+#pragma unroll
+            for (int j = 0; j < CPT; j++) {
+                o[j] = ~0u;
+                tg[j] = 0u;
+            }
+            if (g < gB) {
+                int plo = 0, phi = P - 1;
+                while (plo < phi) {
+                    const int mid = (plo + phi + 1) >> 1;
+                    if (sg[mid] <= g) plo = mid;
+                    else phi = mid - 1;
+                }
+                const int npad = snpad[plo], nl = snl[plo];
+                const int c0 = (g - sg[plo]) * kGroup + sub * CPT;
+                const uint8_t* base = codes_t + (int64_t)spad0[plo] * M + c0;
+                float a[CPT];
+#pragma unroll
+                for (int j = 0; j < CPT; j++) a[j] = 0.0f;
+                const int MS = M - M % SU;
+                uint32_t wc[SU], wn[SU];
+                if (MS > 0) {
+#pragma unroll
+                    for (int u = 0; u < SU; u++) wc[u] = *(const uint32_t*)(base + (int64_t)u * npad);
+                }
+                for (int m = 0; m < MS; m += SU) {
+                    if (m + SU < MS) {
+#pragma unroll
+                        for (int u = 0; u < SU; u++)
+                            wn[u] = *(const uint32_t*)(base + (int64_t)(m + SU + u) * npad);
+                    }
+#pragma unroll
+                    for (int u = 0; u < SU; u++) {
+                        const float* lm = lut + (m + u) * 256;
+                        a[0] += lm[wc[u] & 0xffu];
+                        a[1] += lm[(wc[u] >> 8) & 0xffu];
+                        a[2] += lm[(wc[u] >> 16) & 0xffu];
+                        a[3] += lm[wc[u] >> 24];
+                    }
+#pragma unroll
+                    for (int u = 0; u < SU; u++) wc[u] = wn[u];
+                }
+                for (int m = MS; m < M; m++) {
+                    const uint32_t ww = *(const uint32_t*)(base + (int64_t)m * npad);
+                    const float* lm = lut + m * 256;
+                    a[0] += lm[ww & 0xffu];
+                    a[1] += lm[(ww >> 8) & 0xffu];
+                    a[2] += lm[(ww >> 16) & 0xffu];
+                    a[3] += lm[ww >> 24];
+                }
+                const uint32_t p0 = (uint32_t)(soff[plo] + c0);
+#pragma unroll
+                for (int j = 0; j < CPT; j++) {
+                    o[j] = (c0 + j < nl) ? f2ord(a[j]) : ~0u;
+                    tg[j] = p0 + (uint32_t)j;
+                }
+            }
+            const uint32_t tgs = (uint32_t)ctl[0];
+#pragma unroll
+            for (int j = 0; j < CPT; j++) {
+                if (nw + 64 > wcap) {
+                    Tw = wave_prune<J>(wb, nw, ck);
+                    nw = ck;
+                    if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
+                }
+                const bool keep = o[j] != ~0u && o[j] <= min(Tw, tgs);
+                const unsigned long long mk = __ballot(keep);
+                if (keep) wb[nw + __popcll(mk & lt)] = ((unsigned long long)o[j] << 32) | tg[j];
+                nw += __popcll(mk);
+            }
+        }
+        if (nw > ck) {
+            Tw = wave_prune<J>(wb, nw, ck);
+            nw = ck;
+            if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
+        }
+        __syncthreads();  // every wave's tasks are done: the LUT area is free
+        const uint32_t Tf = (uint32_t)ctl[0];
+        for (int i0 = 0; i0 < nw; i0 += 64) {
+            const int i = i0 + lane;
+            const unsigned long long key = i < nw ? wb[i] : ~0ull;
+            const bool keep = i < nw && (uint32_t)(key >> 32) <= Tf;
+            const unsigned long long mk = __ballot(keep);
+            int at = 0;
+            if (lane == 0 && mk) at = atomicAdd(&ctl[1], __popcll(mk));
+            at = __shfl(at, 0);
+            if (keep) merge[at + __popcll(mk & lt)] = key;
+        }
+        __syncthreads();
+        const int n = ctl[1];
+        const int kk = min(ck, n);
+        if (kk > 0) select_keys<NT>(merge, n, kk, kout, kidx, ktmp, st);
+        __syncthreads();
+        unsigned long long* outp = partial + (int64_t)seg * ck;
+        int32_t* outs = partial_slot + (int64_t)seg * ck;
+        for (int i = tid; i < ck; i += NT) {
+            int32_t slot = -1;
+            if (i < kk) {
+                const int tag = (int)(uint32_t)(kout[i] & 0xffffffffull);
+                for (int p = 0; p < P; p++)
+                    if (tag >= soff[p] && tag - soff[p] < snl[p]) slot = spad0[p] + (tag - soff[p]);
+            }
+            outp[i] = i < kk ? kout[i] : ~0ull;
+            outs[i] = slot;
+        }
+    }
+}
+
 // Allows `kernel` the LDS left after its static allocation; returns the
 // largest dynamic LDS size it may be launched with (0 on failure).
 static int allow_max_lds(const void* kernel) {
@@ -1662,14 +1942,40 @@ constexpr int kRefineNT = 512;
 constexpr int kProbeNT = 512;
 
 
+// LDS of the wave-selection scan with wave buffers of 64 * J keys.
+static size_t scan_wave_lds(int M, int d, int P, int ck, int K1D, int B, int J, size_t* region) {
+    constexpr int NW = kScanNT / 64;
+    *region = align16(std::max((size_t)M * 256 * 4, (size_t)NW * ck * 8));
+    // the query vector shares the wave buffers
+    const size_t wb = std::max((size_t)NW * 64 * J * 8, (size_t)((d + 3) & ~3) * 4);
+    return *region + wb + (size_t)ck * 16 + (size_t)((ck + 3) & ~3) * 4 +
+           align16(sizeof(SelState)) + 16 + (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 +
+           (size_t)K1D * 4 + NW * 4 + 64;
+}
+
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out) {
+    out->G = target_wg;
+    out->max_segments = target_wg + B;
+    const int need = ck + 64;
+    const int J = need <= 128 ? 2 : need <= 192 ? 3 : need <= 256 ? 4 : need <= 384 ? 6
+                : need <= 512 ? 8 : 0;
+    if (J) {
+        size_t region = 0;
+        const size_t lds = scan_wave_lds(M, d, P, ck, K1D, B, J, &region);
+        if (lds <= (size_t)kLdsBytes - 1024) {
+            out->wave = J;
+            out->lds = (int)lds;
+            out->region = (int)region;
+            return true;
+        }
+    }
     const size_t lds = (size_t)M * 256 * 4 + stream_lds_bytes(kScanNT, ck) +
                        (size_t)((d + 3) & ~3) * 4 + (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 +
                        (size_t)K1D * 4 + (kScanNT / 64) * 4 + 64;
     if (lds > (size_t)kLdsBytes - 1024) return false;
-    out->G = target_wg;
+    out->wave = 0;
     out->lds = (int)lds;
-    out->max_segments = target_wg + B;
+    out->region = 0;
     return true;
 }
 
@@ -1690,8 +1996,26 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
                       int ck, const ScanShape& sh, unsigned long long* partial,
                       int32_t* partial_slot, hipStream_t s) {
     constexpr int NT = kScanNT, SU = JHQ_SCAN_SU;
+    if (Ds > 8 || K1D > 256) return hipErrorInvalidValue;
+    if (sh.wave) {
+        static const int mx[5] = {allow_max_lds((const void*)scan_wave_kernel<NT, SU, 2>),
+                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 3>),
+                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 4>),
+                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 6>),
+                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 8>)};
+        const int ji = sh.wave == 2 ? 0 : sh.wave == 3 ? 1 : sh.wave == 4 ? 2 : sh.wave == 6 ? 3 : 4;
+        if (sh.lds > mx[ji]) return hipErrorInvalidValue;
+        auto k = ji == 0 ? scan_wave_kernel<NT, SU, 2>
+                 : ji == 1 ? scan_wave_kernel<NT, SU, 3>
+                 : ji == 2 ? scan_wave_kernel<NT, SU, 4>
+                 : ji == 3 ? scan_wave_kernel<NT, SU, 6> : scan_wave_kernel<NT, SU, 8>;
+        hipLaunchKernelGGL(k, dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d, Ds, K1D, bpd, c1d, M,
+                           probes, gofs, qtot, B, P, ldesc, codes_t, ck, sh.region, partial,
+                           partial_slot);
+        return hipGetLastError();
+    }
     static const int max_dyn = allow_max_lds((const void*)scan_topck_kernel<NT, SU>);
-    if (sh.lds > max_dyn || Ds > 8 || K1D > 256) return hipErrorInvalidValue;
+    if (sh.lds > max_dyn) return hipErrorInvalidValue;
     hipLaunchKernelGGL((scan_topck_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d, Ds,
                        K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, ck, partial,
                        partial_slot);
