@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 // Scan workgroup size and code-load pipeline depth (subspaces in flight).
 #ifndef JHQ_SCAN_NT
@@ -1645,6 +1646,40 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
     JHQ_PHASE_FLUSH(0);
 }
 
+// The r-th smallest (1 <= r <= 64 * C) of the wave's 64 * C values, bit by
+// bit from the top with ballots.
+template <int C>
+__device__ __forceinline__ uint32_t wave_kth_u32(const uint32_t (&v)[C], int r) {
+    uint32_t res = 0u;
+    unsigned long long cand[C];
+#pragma unroll
+    for (int j = 0; j < C; j++) cand[j] = ~0ull;
+    for (int bit = 31; bit >= 0; bit--) {
+        unsigned long long z[C];
+        int nz = 0;
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            z[j] = cand[j] & __ballot(((v[j] >> bit) & 1u) == 0u);
+            nz += __popcll(z[j]);
+        }
+        if (r <= nz) {
+#pragma unroll
+            for (int j = 0; j < C; j++) cand[j] = z[j];
+        } else {
+            r -= nz;
+#pragma unroll
+            for (int j = 0; j < C; j++) cand[j] &= ~z[j];
+            res |= 1u << bit;
+        }
+    }
+    return res;
+}
+
+template <int CPT> struct CodeWord;
+template <> struct CodeWord<1> { using type = uint8_t; };
+template <> struct CodeWord<2> { using type = uint16_t; };
+template <> struct CodeWord<4> { using type = uint32_t; };
+
 // ---------------------------------------------------------------------------
 // Wave-level exact selection.  buf[0..n) holds distinct keys
 // (value << 32 | tag), n <= 64 * J; keeps the k smallest (k < n), compacted
@@ -1744,7 +1779,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                  int region_bytes, unsigned long long* __restrict__ partial,
                  int32_t* __restrict__ partial_slot) {
     // wave buffers of 64 * J keys (ck + 64 <= 64 * J)
-    constexpr int CPT = kScanCPT, TPG = kGroup / CPT, NW = NT / 64, wcap = 64 * J;
+    constexpr int NW = NT / 64, wcap = 64 * J;
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;                                  // or the merge keys
     unsigned long long* merge = (unsigned long long*)smem;
@@ -1769,9 +1804,11 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
     const int tid = threadIdx.x, w = blockIdx.x, lane = tid & 63, wv = tid >> 6;
     const unsigned long long lt = (1ull << lane) - 1ull;
     unsigned long long* wb = wbuf + (size_t)wv * wcap;
+    JHQ_PHASE_DECL
     for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
     const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
     const int64_t T = qpre[B];
+    JHQ_PHASE(0);
     if (w >= G) return;
     const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
     int b;
@@ -1807,19 +1844,18 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         __syncthreads();
         build_lut_lds<NT>(sq, M, Ds, K1D, bpd, sc1d, lut);
         __syncthreads();
+        JHQ_PHASE(1);
 
-        const int ntask = (gB - gA + 15) / 16;
         int nw = 0;          // keys in this wave's buffer (wave-uniform)
         uint32_t Tw = ~0u;   // this wave's bound
-        for (;;) {
-            int t = 0;
-            if (lane == 0) t = atomicAdd(&ctl[2], 1);
-            t = __shfl(t, 0);
-            if (t >= ntask) break;
-            const int g = gA + t * 16 + (lane >> 2), sub = lane & (TPG - 1);
-            uint32_t o[CPT], tg[CPT];
+        // one task: groups [g0, g0 + 64 / (16 / C)), C candidates per lane
+        auto task = [&](auto cc, int g0) {
+            constexpr int C = decltype(cc)::value, TP = kGroup / C;
+            using word_t = typename CodeWord<C>::type;
+            const int g = g0 + lane / TP, sub = lane % TP;
+            uint32_t o[C], tg[C];
 #pragma unroll
-            for (int j = 0; j < CPT; j++) {
+            for (int j = 0; j < C; j++) {
                 o[j] = ~0u;
                 tg[j] = 0u;
             }
@@ -1831,70 +1867,113 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                     else phi = mid - 1;
                 }
                 const int npad = snpad[plo], nl = snl[plo];
-                const int c0 = (g - sg[plo]) * kGroup + sub * CPT;
+                const int c0 = (g - sg[plo]) * kGroup + sub * C;
                 const uint8_t* base = codes_t + (int64_t)spad0[plo] * M + c0;
-                float a[CPT];
+                float a[C];
 #pragma unroll
-                for (int j = 0; j < CPT; j++) a[j] = 0.0f;
+                for (int j = 0; j < C; j++) a[j] = 0.0f;
                 const int MS = M - M % SU;
                 uint32_t wc[SU], wn[SU];
                 if (MS > 0) {
 #pragma unroll
-                    for (int u = 0; u < SU; u++) wc[u] = *(const uint32_t*)(base + (int64_t)u * npad);
+                    for (int u = 0; u < SU; u++) wc[u] = *(const word_t*)(base + (int64_t)u * npad);
                 }
                 for (int m = 0; m < MS; m += SU) {
                     if (m + SU < MS) {
 #pragma unroll
                         for (int u = 0; u < SU; u++)
-                            wn[u] = *(const uint32_t*)(base + (int64_t)(m + SU + u) * npad);
+                            wn[u] = *(const word_t*)(base + (int64_t)(m + SU + u) * npad);
                     }
 #pragma unroll
                     for (int u = 0; u < SU; u++) {
                         const float* lm = lut + (m + u) * 256;
-                        a[0] += lm[wc[u] & 0xffu];
-                        a[1] += lm[(wc[u] >> 8) & 0xffu];
-                        a[2] += lm[(wc[u] >> 16) & 0xffu];
-                        a[3] += lm[wc[u] >> 24];
+#pragma unroll
+                        for (int j = 0; j < C; j++) a[j] += lm[(wc[u] >> (8 * j)) & 0xffu];
                     }
 #pragma unroll
                     for (int u = 0; u < SU; u++) wc[u] = wn[u];
                 }
                 for (int m = MS; m < M; m++) {
-                    const uint32_t ww = *(const uint32_t*)(base + (int64_t)m * npad);
+                    const uint32_t ww = *(const word_t*)(base + (int64_t)m * npad);
                     const float* lm = lut + m * 256;
-                    a[0] += lm[ww & 0xffu];
-                    a[1] += lm[(ww >> 8) & 0xffu];
-                    a[2] += lm[(ww >> 16) & 0xffu];
-                    a[3] += lm[ww >> 24];
+#pragma unroll
+                    for (int j = 0; j < C; j++) a[j] += lm[(ww >> (8 * j)) & 0xffu];
                 }
                 const uint32_t p0 = (uint32_t)(soff[plo] + c0);
 #pragma unroll
-                for (int j = 0; j < CPT; j++) {
+                for (int j = 0; j < C; j++) {
                     o[j] = (c0 + j < nl) ? f2ord(a[j]) : ~0u;
                     tg[j] = p0 + (uint32_t)j;
                 }
             }
             const uint32_t tgs = (uint32_t)ctl[0];
 #pragma unroll
-            for (int j = 0; j < CPT; j++) {
+            for (int j = 0; j < C; j++) {
                 if (nw + 64 > wcap) {
                     Tw = wave_prune<J>(wb, nw, ck);
                     nw = ck;
                     if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
+#ifdef JHQ_PHASE_TIMING
+                    if (tid == 0) ph_acc[5] += 1;
+#endif
                 }
                 const bool keep = o[j] != ~0u && o[j] <= min(Tw, tgs);
                 const unsigned long long mk = __ballot(keep);
                 if (keep) wb[nw + __popcll(mk & lt)] = ((unsigned long long)o[j] << 32) | tg[j];
                 nw += __popcll(mk);
             }
+        };
+        // units of 8 groups: a wave takes two (a 4-candidates-per-lane task)
+        // while many remain, then one (2 per lane), so the waves finish close
+        // together
+        const int nunit = (gB - gA + 7) / 8;
+        for (;;) {
+            int t = 0, take = 1;
+            if (lane == 0) {
+                const int done = *(volatile int*)&ctl[2];
+                take = nunit - done > 4 * NW ? 2 : 1;
+                t = atomicAdd(&ctl[2], take);
+            }
+            t = __shfl(t, 0);
+            take = __shfl(take, 0);
+            if (t >= nunit) break;
+            if (take == 2 && t + 1 < nunit) {
+                task(std::integral_constant<int, 4>(), gA + t * 8);
+            } else {
+                task(std::integral_constant<int, 2>(), gA + t * 8);
+            }
+#ifdef JHQ_PHASE_TIMING
+            if (tid == 0) ph_acc[4] += 1;
+#endif
         }
         if (nw > ck) {
             Tw = wave_prune<J>(wb, nw, ck);
             nw = ck;
             if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
         }
+        JHQ_PHASE(6);
+        // a tighter bound for the merge: each wave's r-th smallest value, r =
+        // ceil(ck / waves); the largest of them has >= ck values at or below it
+        {
+            const int r = (ck + NW - 1) / NW;
+            uint32_t vals[J];
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const int i = j * 64 + lane;
+                vals[j] = i < nw ? (uint32_t)(wb[i] >> 32) : ~0u;
+            }
+            const uint32_t tw = nw >= r ? wave_kth_u32<J>(vals, r) : ~0u;
+            if (lane == 0) wsum[wv] = (int)tw;
+        }
         __syncthreads();  // every wave's tasks are done: the LUT area is free
-        const uint32_t Tf = (uint32_t)ctl[0];
+        JHQ_PHASE(2);
+        uint32_t Tf = (uint32_t)ctl[0];
+        {
+            uint32_t t3 = 0u;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) t3 = max(t3, (uint32_t)wsum[w2]);
+            Tf = min(Tf, t3);
+        }
         for (int i0 = 0; i0 < nw; i0 += 64) {
             const int i = i0 + lane;
             const unsigned long long key = i < nw ? wb[i] : ~0ull;
@@ -1922,7 +2001,12 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             outp[i] = i < kk ? kout[i] : ~0ull;
             outs[i] = slot;
         }
+#ifdef JHQ_PHASE_TIMING
+        if (tid == 0) ph_acc[7] += n;
+#endif
+        JHQ_PHASE(3);
     }
+    JHQ_PHASE_FLUSH(0);
 }
 
 // Allows `kernel` the LDS left after its static allocation; returns the
