@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <new>
 #include <string>
 #include <vector>
@@ -120,7 +121,7 @@ struct jhq_index {
     // search workspace (v14/search.cuh:24-46)
     DBuf<float> wq, wqrot, wscores, wout_d;
     DBuf<int32_t> wprobes, wgofs, wqtot, wout_i;
-    DBuf<unsigned long long> wpartial, wtopck;
+    DBuf<unsigned long long> wpartial, wtopck, wdump;
     DBuf<int32_t> wpslot;
     float* h_q = nullptr;  // pinned staging
     float* h_d = nullptr;
@@ -281,7 +282,16 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
-    return ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.max_segments);
+    JHQ_TRY(ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.max_segments));
+    if (bp->sh.dump) {
+        // a query's candidates are at most the padded sizes of the P largest lists
+        std::vector<int32_t> sz(ix->l_size);
+        std::partial_sort(sz.begin(), sz.begin() + bp->P, sz.end(), std::greater<int32_t>());
+        int64_t per_q = 0;
+        for (int i = 0; i < bp->P; i++) per_q += (sz[i] + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+        JHQ_TRY(ix->wdump.ensure(static_cast<size_t>(Bq) * std::max<int64_t>(per_q, 1)));
+    }
+    return JHQ_OK;
 }
 
 // One batch of Bq queries at d_q (device) through the whole pipeline
@@ -300,7 +310,8 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
     JHQ_HIP(jhq::scan_topck(ix->wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                             ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dldesc.p,
-                            ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, ix->wpslot.p, s));
+                            ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, ix->wpslot.p,
+                            ix->wdump.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[4], s));
     JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wpslot.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k,
                              ix->wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,

@@ -77,6 +77,10 @@ struct ScanShape {
     int lds;           // dynamic LDS bytes of the scan kernel
     int max_segments;  // upper bound on top-ck lists per batch (partial rows)
     int wave;          // 0: workgroup-synchronous selection; J: wave selection, 64*J-key buffers
+    int nt;            // threads per scan workgroup
+    int dump;          // 1: every distance to a buffer, then one selection per query (region
+                       // = that kernel's LDS); the buffer holds B * (groups of the P largest
+                       // lists) * 16 keys
     int region;        // wave selection: bytes of the LUT / merge region
 };
 // LDS plan of the scan kernel; returns false if the byte LUT and the
@@ -91,7 +95,7 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
                       int B, int M, const int32_t* probes, const int32_t* gofs,
                       const int32_t* qtot, int P, const int4* ldesc, const uint8_t* codes_t,
                       int ck, const ScanShape& sh, unsigned long long* partial,
-                      int32_t* partial_slot, hipStream_t s);
+                      int32_t* partial_slot, unsigned long long* dump, hipStream_t s);
 
 // Per query: merge its segment lists, residual refine, final top-k.
 // If topck_dbg != nullptr it receives the merged short list [B][ck] keys.

@@ -2009,6 +2009,236 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
     JHQ_PHASE_FLUSH(0);
 }
 
+// ---------------------------------------------------------------------------
+// Large short lists (ck beyond the wave buffers): the scan writes every
+// candidate's key (ord(dist) << 32 | canonical position; ~0 for padding) to
+// dump[qpre[b] * 16 + group * 16 + i], and select_query_kernel selects each
+// query's exact top-ck from them.  Same work plan, LUT and arithmetic as the
+// other scans.
+// ---------------------------------------------------------------------------
+template <int NT, int SU>
+__global__ void __launch_bounds__(NT)
+scan_dump_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
+                 const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
+                 const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
+                 const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t,
+                 unsigned long long* __restrict__ dump) {
+    constexpr int NW = NT / 64;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* lut = (float*)smem;
+    int* ctl = (int*)(smem + (size_t)M * 256 * 4);  // task counter
+    float* sq = (float*)(ctl + 4);
+    int* qpre = (int*)(sq + ((d + 3) & ~3));
+    int* spre = qpre + B + 1;
+    int32_t* sg = spre + B + 1;
+    int32_t* spad0 = sg + P + 1;
+    int32_t* snpad = spad0 + P;
+    int32_t* snl = snpad + P;
+    int32_t* soff = snl + P;
+    float* sc1d = (float*)(soff + P);
+    int* wsum = (int*)(sc1d + K1D);
+
+    const int tid = threadIdx.x, w = blockIdx.x, lane = tid & 63;
+    for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
+    const int64_t T = qpre[B];
+    if (w >= G) return;
+    const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
+    int b;
+    {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (qpre[mid] <= x0) lo = mid;
+            else hi = mid - 1;
+        }
+        b = lo;
+    }
+    for (; b < B && qpre[b] < x1; b++) {
+        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
+        if (qb1 <= qb0) continue;
+        const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
+        __syncthreads();
+        for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
+        for (int i = tid; i < P; i += NT) {
+            const int4 L = ldesc[probes[(int64_t)b * P + i]];
+            spad0[i] = L.x;
+            snpad[i] = L.y;
+            snl[i] = L.z;
+            soff[i] = L.w;
+        }
+        for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
+        if (tid == 0) ctl[0] = 0;
+        __syncthreads();
+        build_lut_lds<NT>(sq, M, Ds, K1D, bpd, sc1d, lut);
+        __syncthreads();
+        unsigned long long* qd = dump + qb0 * kGroup;
+        auto task = [&](auto cc, int g0) {
+            constexpr int C = decltype(cc)::value, TP = kGroup / C;
+            using word_t = typename CodeWord<C>::type;
+            const int g = g0 + lane / TP, sub = lane % TP;
+            if (g >= gB) return;
+            int plo = 0, phi = P - 1;
+            while (plo < phi) {
+                const int mid = (plo + phi + 1) >> 1;
+                if (sg[mid] <= g) plo = mid;
+                else phi = mid - 1;
+            }
+            const int npad = snpad[plo], nl = snl[plo];
+            const int c0 = (g - sg[plo]) * kGroup + sub * C;
+            const uint8_t* base = codes_t + (int64_t)spad0[plo] * M + c0;
+            float a[C];
+#pragma unroll
+            for (int j = 0; j < C; j++) a[j] = 0.0f;
+            const int MS = M - M % SU;
+            uint32_t wc[SU], wn[SU];
+            if (MS > 0) {
+#pragma unroll
+                for (int u = 0; u < SU; u++) wc[u] = *(const word_t*)(base + (int64_t)u * npad);
+            }
+            for (int m = 0; m < MS; m += SU) {
+                if (m + SU < MS) {
+#pragma unroll
+                    for (int u = 0; u < SU; u++)
+                        wn[u] = *(const word_t*)(base + (int64_t)(m + SU + u) * npad);
+                }
+#pragma unroll
+                for (int u = 0; u < SU; u++) {
+                    const float* lm = lut + (m + u) * 256;
+#pragma unroll
+                    for (int j = 0; j < C; j++) a[j] += lm[(wc[u] >> (8 * j)) & 0xffu];
+                }
+#pragma unroll
+                for (int u = 0; u < SU; u++) wc[u] = wn[u];
+            }
+            for (int m = MS; m < M; m++) {
+                const uint32_t ww = *(const word_t*)(base + (int64_t)m * npad);
+                const float* lm = lut + m * 256;
+#pragma unroll
+                for (int j = 0; j < C; j++) a[j] += lm[(ww >> (8 * j)) & 0xffu];
+            }
+            const uint32_t p0 = (uint32_t)(soff[plo] + c0);
+            unsigned long long* out = qd + (int64_t)g * kGroup + sub * C;
+#pragma unroll
+            for (int j = 0; j < C; j++)
+                out[j] = (c0 + j < nl) ? (((unsigned long long)f2ord(a[j]) << 32) | (p0 + j))
+                                       : ~0ull;
+        };
+        const int nunit = (gB - gA + 7) / 8;
+        for (;;) {
+            int t = 0, take = 1;
+            if (lane == 0) {
+                const int done = *(volatile int*)&ctl[0];
+                take = nunit - done > 4 * NW ? 2 : 1;
+                t = atomicAdd(&ctl[0], take);
+            }
+            t = __shfl(t, 0);
+            take = __shfl(take, 0);
+            if (t >= nunit) break;
+            if (take == 2 && t + 1 < nunit) task(std::integral_constant<int, 4>(), gA + t * 8);
+            else task(std::integral_constant<int, 2>(), gA + t * 8);
+        }
+    }
+}
+
+// Exact top-ck of each query's dumped keys (one workgroup per query), written
+// as the query's first segment list (sorted, ~0 padded) with pool slots; the
+// query's other segment lists are left empty.  Two passes: every thread takes
+// the minimum value of its share, the largest of the waves' ceil(ck / waves)-th
+// smallest lane minima bounds the ck-th smallest value, the keys at or below
+// it are gathered and selected exactly.  Too many (equal values) falls back to
+// streaming every key through the exact selector.
+constexpr int kDumpSurv = 8192;
+
+template <int NT>
+__global__ void __launch_bounds__(NT)
+select_query_kernel(const unsigned long long* __restrict__ dump, const int32_t* __restrict__ qtot,
+                    int B, int Gmax, int ck, const int32_t* __restrict__ probes, int P,
+                    const int4* __restrict__ ldesc, unsigned long long* __restrict__ partial,
+                    int32_t* __restrict__ partial_slot) {
+    constexpr int NW = NT / 64;
+    extern __shared__ __align__(16) unsigned char smem[];
+    StreamSel S;
+    unsigned char* p = stream_carve<NT>(smem, ck, &S);
+    unsigned long long* surv = (unsigned long long*)p;  // [kDumpSurv]
+    int* qpre = (int*)(surv + kDumpSurv);
+    int* spre = qpre + B + 1;
+    int* wsum = spre + B + 1;                            // [NW]
+    int* meta = wsum + NW;                               // [3P]: start, size, first position
+    int* scnt = meta + 3 * P;
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    work_plan<NT>(qtot, B, Gmax, qpre, spre, wsum);
+    for (int i = tid; i < P; i += NT) {
+        const int4 L = ldesc[probes[(int64_t)b * P + i]];
+        meta[3 * i] = L.x;
+        meta[3 * i + 1] = L.z;
+        meta[3 * i + 2] = L.w;
+    }
+    if (tid == 0) *scnt = 0;
+    stream_begin<NT>(S);
+    __syncthreads();
+    const int64_t n = (int64_t)(qpre[b + 1] - qpre[b]) * kGroup;
+    const unsigned long long* keys = dump + (int64_t)qpre[b] * kGroup;
+    uint32_t mn = ~0u;
+    for (int64_t i = tid; i < n; i += NT) mn = min(mn, (uint32_t)(keys[i] >> 32));
+    const int r = (ck + NW - 1) / NW;
+    uint32_t mv[1] = {mn};
+    const uint32_t tw = r <= 64 ? wave_kth_u32<1>(mv, r) : ~0u;
+    if (lane == 0) wsum[wv] = (int)tw;
+    __syncthreads();
+    uint32_t T = 0u;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; w2++) T = max(T, (uint32_t)wsum[w2]);
+    for (int64_t i0 = 0; i0 < n; i0 += NT) {
+        const int64_t i = i0 + tid;
+        const unsigned long long x = i < n ? keys[i] : ~0ull;
+        const bool keep = x != ~0ull && (uint32_t)(x >> 32) <= T;
+        const unsigned long long mk = __ballot(keep);
+        int at = 0;
+        if (lane == 0 && mk) at = atomicAdd(scnt, __popcll(mk));
+        at = __shfl(at, 0);
+        if (keep && at + __popcll(mk & lt) < kDumpSurv) surv[at + __popcll(mk & lt)] = x;
+    }
+    __syncthreads();
+    const int ns = *scnt;
+    int kk = 0;
+    if (ns <= kDumpSurv) {
+        kk = min(ck, ns);
+        if (kk > 0) select_keys<NT>(surv, ns, kk, S.kout, S.kidx, S.ktmp, S.st);
+    } else {
+        for (int64_t r0 = 0; r0 < n; r0 += (int64_t)NT * 4) {
+            uint32_t o[4], tg[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int64_t i = r0 + (int64_t)tid * 4 + j;
+                const unsigned long long x = i < n ? keys[i] : ~0ull;
+                o[j] = (uint32_t)(x >> 32);
+                tg[j] = (uint32_t)x;
+            }
+            stream_round<NT, 4>(S, ck, o, tg);
+        }
+        kk = stream_end<NT>(S, ck);
+    }
+    __syncthreads();
+    const int s0 = spre[b], s1 = spre[b + 1];
+    for (int i = tid; i < ck; i += NT) {
+        int32_t slot = -1;
+        if (i < kk) {
+            const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
+            for (int q = 0; q < P; q++)
+                if (tag >= meta[3 * q + 2] && tag - meta[3 * q + 2] < meta[3 * q + 1])
+                    slot = meta[3 * q] + (tag - meta[3 * q + 2]);
+        }
+        partial[(int64_t)s0 * ck + i] = i < kk ? S.kout[i] : ~0ull;
+        partial_slot[(int64_t)s0 * ck + i] = slot;
+    }
+    for (int64_t i = (int64_t)(s0 + 1) * ck + tid; i < (int64_t)s1 * ck; i += NT) {
+        partial[i] = ~0ull;
+        partial_slot[i] = -1;
+    }
+}
+
 // Allows `kernel` the LDS left after its static allocation; returns the
 // largest dynamic LDS size it may be launched with (0 on failure).
 static int allow_max_lds(const void* kernel) {
@@ -2027,8 +2257,9 @@ constexpr int kProbeNT = 512;
 
 
 // LDS of the wave-selection scan with wave buffers of 64 * J keys.
-static size_t scan_wave_lds(int M, int d, int P, int ck, int K1D, int B, int J, size_t* region) {
-    constexpr int NW = kScanNT / 64;
+static size_t scan_wave_lds(int NT, int M, int d, int P, int ck, int K1D, int B, int J,
+                            size_t* region) {
+    const int NW = NT / 64;
     *region = align16(std::max((size_t)M * 256 * 4, (size_t)NW * ck * 8));
     // the query vector shares the wave buffers
     const size_t wb = std::max((size_t)NW * 64 * J * 8, (size_t)((d + 3) & ~3) * 4);
@@ -2043,11 +2274,42 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     const int need = ck + 64;
     const int J = need <= 128 ? 2 : need <= 192 ? 3 : need <= 256 ? 4 : need <= 384 ? 6
                 : need <= 512 ? 8 : 0;
-    if (J) {
+    out->dump = 0;
+    // short lists up to 128: selection inside the scan, 16 waves per workgroup
+    if (J && J <= 3) {
         size_t region = 0;
-        const size_t lds = scan_wave_lds(M, d, P, ck, K1D, B, J, &region);
+        const size_t lds = scan_wave_lds(kScanNT, M, d, P, ck, K1D, B, J, &region);
         if (lds <= (size_t)kLdsBytes - 1024) {
             out->wave = J;
+            out->nt = kScanNT;
+            out->lds = (int)lds;
+            out->region = (int)region;
+            return true;
+        }
+    }
+    // longer ones: every distance to HBM, then one exact selection per query
+    {
+        const size_t lds = (size_t)M * 256 * 4 + 16 + (size_t)((d + 3) & ~3) * 4 +
+                           (size_t)(2 * (B + 1) + (P + 1) + 4 * P) * 4 + (size_t)K1D * 4 +
+                           (kScanNT / 64) * 4 + 64;
+        const size_t lds2 = stream_lds_bytes(kScanNT, ck) + (size_t)kDumpSurv * 8 +
+                            (size_t)(2 * (B + 1)) * 4 + (kScanNT / 64) * 4 + (size_t)P * 12 + 32;
+        if (lds <= (size_t)kLdsBytes - 1024 && lds2 <= (size_t)kLdsBytes - 1024) {
+            out->dump = 1;
+            out->wave = 0;
+            out->nt = kScanNT;
+            out->lds = (int)lds;
+            out->region = (int)lds2;
+            return true;
+        }
+    }
+    // 16 waves per workgroup if the LDS allows, else 8 (large ck)
+    for (int nt = kScanNT; J && nt >= 512; nt /= 2) {
+        size_t region = 0;
+        const size_t lds = scan_wave_lds(nt, M, d, P, ck, K1D, B, J, &region);
+        if (lds <= (size_t)kLdsBytes - 1024) {
+            out->wave = J;
+            out->nt = nt;
             out->lds = (int)lds;
             out->region = (int)region;
             return true;
@@ -2058,6 +2320,7 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
                        (size_t)K1D * 4 + (kScanNT / 64) * 4 + 64;
     if (lds > (size_t)kLdsBytes - 1024) return false;
     out->wave = 0;
+    out->nt = kScanNT;
     out->lds = (int)lds;
     out->region = 0;
     return true;
@@ -2078,24 +2341,38 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
                       int B, int M, const int32_t* probes, const int32_t* gofs,
                       const int32_t* qtot, int P, const int4* ldesc, const uint8_t* codes_t,
                       int ck, const ScanShape& sh, unsigned long long* partial,
-                      int32_t* partial_slot, hipStream_t s) {
+                      int32_t* partial_slot, unsigned long long* dump, hipStream_t s) {
     constexpr int NT = kScanNT, SU = JHQ_SCAN_SU;
     if (Ds > 8 || K1D > 256) return hipErrorInvalidValue;
+    if (sh.dump) {
+        static const int mxd = allow_max_lds((const void*)scan_dump_kernel<NT, SU>);
+        static const int mxs = allow_max_lds((const void*)select_query_kernel<NT>);
+        if (!dump || sh.lds > mxd || sh.region > mxs) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((scan_dump_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d,
+                           Ds, K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, dump);
+        hipLaunchKernelGGL(select_query_kernel<NT>, dim3(B), dim3(NT), sh.region, s,
+                           (const unsigned long long*)dump, qtot, B, sh.G, ck, probes, P, ldesc,
+                           partial, partial_slot);
+        return hipGetLastError();
+    }
     if (sh.wave) {
-        static const int mx[5] = {allow_max_lds((const void*)scan_wave_kernel<NT, SU, 2>),
-                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 3>),
-                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 4>),
-                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 6>),
-                                  allow_max_lds((const void*)scan_wave_kernel<NT, SU, 8>)};
+        using KFn = void (*)(const float*, int, int, int, int, const float*, int, const int32_t*,
+                             const int32_t*, const int32_t*, int, int, const int4*, const uint8_t*,
+                             int, int, unsigned long long*, int32_t*);
+        static const KFn kf[2][5] = {
+            {scan_wave_kernel<NT, SU, 2>, scan_wave_kernel<NT, SU, 3>, scan_wave_kernel<NT, SU, 4>,
+             scan_wave_kernel<NT, SU, 6>, scan_wave_kernel<NT, SU, 8>},
+            {scan_wave_kernel<NT / 2, SU, 2>, scan_wave_kernel<NT / 2, SU, 3>,
+             scan_wave_kernel<NT / 2, SU, 4>, scan_wave_kernel<NT / 2, SU, 6>,
+             scan_wave_kernel<NT / 2, SU, 8>}};
+        static int mx[2][5] = {{-1, -1, -1, -1, -1}, {-1, -1, -1, -1, -1}};
         const int ji = sh.wave == 2 ? 0 : sh.wave == 3 ? 1 : sh.wave == 4 ? 2 : sh.wave == 6 ? 3 : 4;
-        if (sh.lds > mx[ji]) return hipErrorInvalidValue;
-        auto k = ji == 0 ? scan_wave_kernel<NT, SU, 2>
-                 : ji == 1 ? scan_wave_kernel<NT, SU, 3>
-                 : ji == 2 ? scan_wave_kernel<NT, SU, 4>
-                 : ji == 3 ? scan_wave_kernel<NT, SU, 6> : scan_wave_kernel<NT, SU, 8>;
-        hipLaunchKernelGGL(k, dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d, Ds, K1D, bpd, c1d, M,
-                           probes, gofs, qtot, B, P, ldesc, codes_t, ck, sh.region, partial,
-                           partial_slot);
+        const int ni = sh.nt == NT ? 0 : 1;
+        if (mx[ni][ji] < 0) mx[ni][ji] = allow_max_lds((const void*)kf[ni][ji]);
+        if (sh.lds > mx[ni][ji]) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(kf[ni][ji], dim3(sh.G), dim3(sh.nt), sh.lds, s, q_rot, d, Ds, K1D, bpd,
+                           c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, ck, sh.region,
+                           partial, partial_slot);
         return hipGetLastError();
     }
     static const int max_dyn = allow_max_lds((const void*)scan_topck_kernel<NT, SU>);
