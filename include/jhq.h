@@ -193,8 +193,8 @@ int jhq_search_debug(jhq_index* idx, const float* q, int64_t nq, int k,
  * step list of jhq_v13_step_timing/search.cu:424-491).  When enabled,
  * every search batch records events; jhq_get_timing returns accumulated
  * milliseconds per step and the number of batches:
- *   ms[0] rotate  ms[1] centroid scores  ms[2] select probes
- *   ms[3] byte LUT + ADC scan + top-ck  ms[4] merge + refine + final top-k
+ *   ms[0] query rotation + centroid scores (one product)  ms[1] select probes
+ *   ms[2] byte LUT + ADC scan + top-ck  ms[3] merge + refine + final top-k
  * Events are recorded on the stream the kernels run on. */
 int jhq_set_timing(jhq_index* idx, int enable);
 int jhq_get_timing(const jhq_index* idx, double* ms, int n_ms, int64_t* batches);

@@ -27,7 +27,7 @@ _LIB_PATH = os.path.join(_HERE, "libjhq_amd.so")
 _lib = None
 
 JHQ_OK, JHQ_EINVAL, JHQ_ESTATE, JHQ_EDEVICE, JHQ_ENOMEM = 0, 1, 2, 3, 4
-STEP_NAMES = ("rotate", "centroid_scores", "select_probes", "scan_topck", "refine_topk")
+STEP_NAMES = ("query_gemm", "select_probes", "scan_topck", "refine_topk")
 
 
 class JHQError(RuntimeError):

@@ -86,7 +86,7 @@ struct DBuf {
     }
 };
 
-constexpr int kSteps = 5;
+constexpr int kSteps = 4;
 
 }  // namespace
 
@@ -117,6 +117,10 @@ struct jhq_index {
     DBuf<int32_t> dlist_ids;
     DBuf<uint8_t> dcodes_t, dres;
     DBuf<float> dcorr;
+
+    // query GEMM operand [Pi ; centroids * Pi] ((d + nlist) x d): one product
+    // gives the rotated query and the centroid dots
+    DBuf<float> dqmat;
 
     // search workspace (v14/search.cuh:24-46)
     DBuf<float> wq, wqrot, wscores, wout_d;
@@ -202,6 +206,26 @@ int upload_centroids(jhq_index* ix) {
     compute_norms(ix);
     JHQ_TRY(ix->dcent.upload(ix->cent.data(), ix->cent.size()));
     JHQ_TRY(ix->dnorms.upload(ix->cent_norms.data(), ix->cent_norms.size()));
+    return JHQ_OK;
+}
+
+// dqmat = [Pi ; cent * Pi]: row j < d is Pi's row j, row d + l is centroid l
+// taken back to the unrotated space (sum_j cent[l][j] Pi(j, k), a fixed-order
+// fmaf chain), so that <q, row d + l> = <c_l, Pi q>.  Only where the
+// 64-row MFMA product applies (d % 64 == 0).
+int build_query_matrix(jhq_index* ix) {
+    const int d = ix->d, nlist = ix->nlist;
+    ix->dqmat.release();
+    if (!jhq::mfma_q_ok(d, d, d)) return JHQ_OK;
+    JHQ_TRY(ix->ensure_stream());
+    JHQ_TRY(ix->dqmat.alloc(static_cast<size_t>(d + nlist) * d));
+    DBuf<float> dpt;
+    JHQ_TRY(dpt.upload(ix->Pi_cm.data(), ix->Pi_cm.size()));  // row k = (Pi(0,k), Pi(1,k), ...)
+    JHQ_HIP(hipMemcpyAsync(ix->dqmat.p, ix->dP.p, static_cast<size_t>(d) * d * sizeof(float),
+                           hipMemcpyDeviceToDevice, ix->stream));
+    JHQ_HIP(jhq::gemm_nt_store(ix->dcent.p, d, dpt.p, d, nlist, d, d,
+                               ix->dqmat.p + static_cast<size_t>(d) * d, d, false, ix->stream));
+    JHQ_HIP(hipStreamSynchronize(ix->stream));
     return JHQ_OK;
 }
 
@@ -300,19 +324,25 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
               int32_t* d_ids, bool want_topck, hipStream_t s) {
     const int d = ix->d;
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
-    JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, ix->wqrot.p, d, s));
+    if (ix->dqmat.p) {
+        // rotation and centroid dots in one tiled product
+        JHQ_HIP(jhq::mfma_q(d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, ix->wqrot.p, d,
+                            ix->wscores.p, ix->nlist, ix->dnorms.p, s));
+    } else {
+        // d not a multiple of 64: the 16-row kernels
+        JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, ix->wqrot.p, d, s));
+        JHQ_HIP(jhq::mfma_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
+                                   ix->wscores.p, ix->nlist, s));
+    }
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
-    JHQ_HIP(jhq::mfma_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
-                               ix->wscores.p, ix->nlist, s));
-    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, ix->wprobes.p,
                                ix->wgofs.p, ix->wqtot.p, s));
-    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     JHQ_HIP(jhq::scan_topck(ix->wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                             ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dldesc.p,
                             ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, ix->wpslot.p,
                             ix->wdump.p, s));
-    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[4], s));
+    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
     JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wpslot.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k,
                              ix->wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
                              ix->bpv, ix->dldesc.p, ix->nlist, ix->dres.p, ix->dcorr.p,
@@ -591,6 +621,7 @@ int train_impl(jhq_index* ix, const float* x, int64_t n_train) {
                 c.empty() ? 0.f : c[std::min<size_t>(r, c.size() - 1)];
     }
     JHQ_TRY(ix->dres_c1d.upload(ix->res_c1d.data(), ix->res_c1d.size()));
+    JHQ_TRY(build_query_matrix(ix));
     ix->trained = true;
     return JHQ_OK;
 }
@@ -1169,7 +1200,8 @@ int jhq_load(const char* path, jhq_index** out) {
         (rc = ix->dc1d.upload(ix->c1d.data(), ix->c1d.size())) != JHQ_OK ||
         (rc = ix->dres_c1d.upload(ix->res_c1d.data(), ix->res_c1d.size())) != JHQ_OK ||
         (rc = ix->dcent.upload(ix->cent.data(), ix->cent.size())) != JHQ_OK ||
-        (rc = ix->dnorms.upload(ix->cent_norms.data(), ix->cent_norms.size())) != JHQ_OK)
+        (rc = ix->dnorms.upload(ix->cent_norms.data(), ix->cent_norms.size())) != JHQ_OK ||
+        (rc = build_query_matrix(ix)) != JHQ_OK)
         return done(rc);
     ix->trained = true;
     // compact pool: exact-fit blocks in list order (the one-shot add's layout)

@@ -28,6 +28,14 @@ hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t 
 // The same products on fp32 MFMA for the query side (rotation, centroid
 // scores); not a fixed summation order, so only distances and near-tie probe
 // choices depend on it, never the stored codes.
+// Query product against Bm (N rows of K): columns < nrot are stored to C1,
+// the others become scores norms[c] - 2 * dot in C2 (column c - nrot).
+// fp32 MFMA, 64 rows x 16 columns per wave.  mfma_q_ok: K % 64 == 0 and
+// lda, ldb multiples of 4 (A and Bm must also be 16-byte aligned).
+bool mfma_q_ok(int K, int64_t lda, int64_t ldb);
+hipError_t mfma_q(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N, int K,
+                  int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2, const float* norms,
+                  hipStream_t s);
 hipError_t mfma_nt_store(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
                          int K, float* C, int64_t ldc, hipStream_t s);
 hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,

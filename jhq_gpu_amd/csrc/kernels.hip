@@ -661,6 +661,134 @@ mfma_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
     }
 }
 
+// ---------------------------------------------------------------------------
+// Query-side product against Bm = [Pi ; centroids Pi] (the centroids taken
+// back to the unrotated space, so the scores need not wait for the rotation):
+// C[row][col] = sum_k A[row][k] * Bm[col][k]; columns below nrot are the
+// rotated query (stored to C1), the rest centroid scores norms[c] - 2 * dot
+// (stored to C2 at column c - nrot).  Like mfma_nt_kernel (each lane streams
+// its own rows' k-runs as float4, S waves split K and add in a fixed order
+// through LDS), but a wave covers 64 rows x 16 columns (four 16x16 MFMA
+// tiles sharing each B fragment), so Bm is read once per 64 rows.
+// Requires K % (64 * S) == 0, lda and ldb multiples of 4, aligned A and Bm.
+// ---------------------------------------------------------------------------
+template <int S>
+__global__ void __launch_bounds__(64 * S)
+mfma_q_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
+              int64_t ldb, int nb, int N, int K, int nrot, float* __restrict__ C1, int64_t ld1,
+              float* __restrict__ C2, int64_t ld2, const float* __restrict__ norms) {
+    constexpr int RT = 4, D = 2;
+    __shared__ v4f red[S > 1 ? (S - 1) * 64 * RT : 1];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int b0 = blockIdx.y * 64, n0 = blockIdx.x * 16;
+    // lane (r, g) reads the float4 at k = wv*Ks + 16t + 4g of its rows, so
+    // the four k-groups of a row read 64 contiguous bytes per load; every
+    // k of the wave's range is summed once whatever its MFMA k-slot
+    const int Ks = K / S;
+    const int ka = wv * Ks + 4 * g;
+    const float4* a4[RT];
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const int row = b0 + 16 * i + r;
+        a4[i] = (const float4*)(A + (int64_t)(row < nb ? row : 0) * lda + ka);
+    }
+    const int col = n0 + r;
+    const float4* b4 = (const float4*)(Bm + (int64_t)(col < N ? col : 0) * ldb + ka);
+    v4f acc0[RT], acc1[RT];
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        acc0[i] = v4f{0.f, 0.f, 0.f, 0.f};
+        acc1[i] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    const int n4 = Ks / 16;
+    float4 an[D][RT], bn[D];
+#pragma unroll
+    for (int u = 0; u < D; u++) {
+        bn[u] = b4[4 * u];
+#pragma unroll
+        for (int i = 0; i < RT; i++) an[u][i] = a4[i][4 * u];
+    }
+    for (int it = 0; it < n4; it += D) {
+        float4 ac[D][RT], bc[D];
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            bc[u] = bn[u];
+#pragma unroll
+            for (int i = 0; i < RT; i++) ac[u][i] = an[u][i];
+        }
+        if (it + D < n4) {
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                bn[u] = b4[4 * (it + D + u)];
+#pragma unroll
+                for (int i = 0; i < RT; i++) an[u][i] = a4[i][4 * (it + D + u)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                acc0[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].x, bc[u].x, acc0[i], 0, 0, 0);
+                acc1[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].y, bc[u].y, acc1[i], 0, 0, 0);
+                acc0[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].z, bc[u].z, acc0[i], 0, 0, 0);
+                acc1[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].w, bc[u].w, acc1[i], 0, 0, 0);
+            }
+        }
+    }
+    v4f acc[RT];
+#pragma unroll
+    for (int i = 0; i < RT; i++) acc[i] = acc0[i] + acc1[i];
+    if (S > 1) {
+        if (wv > 0)
+#pragma unroll
+            for (int i = 0; i < RT; i++) red[((wv - 1) * RT + i) * 64 + lane] = acc[i];
+        __syncthreads();
+        if (wv > 0) return;
+#pragma unroll
+        for (int w2 = 0; w2 < S - 1; w2++)
+#pragma unroll
+            for (int i = 0; i < RT; i++) acc[i] += red[(w2 * RT + i) * 64 + lane];
+    }
+    if (col >= N) return;
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = b0 + 16 * i + 4 * g + j;
+            if (row < nb) {
+                const float v = acc[i][j];
+                if (col < nrot) C1[(int64_t)row * ld1 + col] = v;
+                else C2[(int64_t)row * ld2 + (col - nrot)] = fmaf(-2.0f, v, norms[col - nrot]);
+            }
+        }
+    }
+}
+
+bool mfma_q_ok(int K, int64_t lda, int64_t ldb) {
+    return K % 64 == 0 && lda % 4 == 0 && ldb % 4 == 0;
+}
+
+hipError_t mfma_q(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N, int K,
+                  int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2, const float* norms,
+                  hipStream_t s) {
+    if (nb <= 0 || N <= 0) return hipSuccess;
+    if (!mfma_q_ok(K, lda, ldb) || ((uintptr_t)A & 15) || ((uintptr_t)Bm & 15) ||
+        (nb + 63) / 64 > 65535)
+        return hipErrorInvalidValue;
+    const int64_t tiles = (int64_t)((N + 15) / 16) * ((nb + 63) / 64);
+    int S = 1;
+    while (S < 8 && tiles * S < 2048 && K % (64 * S * 2) == 0 && K / (S * 2) >= 64) S *= 2;
+    dim3 grid((N + 15) / 16, (nb + 63) / 64);
+    switch (S) {
+        case 1: hipLaunchKernelGGL(mfma_q_kernel<1>, grid, dim3(64), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
+        case 2: hipLaunchKernelGGL(mfma_q_kernel<2>, grid, dim3(128), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
+        case 4: hipLaunchKernelGGL(mfma_q_kernel<4>, grid, dim3(256), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
+        default: hipLaunchKernelGGL(mfma_q_kernel<8>, grid, dim3(512), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
+    }
+    return hipGetLastError();
+}
+
 template <int EPI>
 static hipError_t launch_mfma(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb,
                               int N, int K, float* C, int64_t ldc, const float* norms,
