@@ -8,9 +8,9 @@ uniform weights) and L2-normalised.  IVF nlist=4096 trained on the first
 100,000 base vectors (the reference demo's protocol), M=128, B=8, Br=4,
 alpha=4, k=10, query batch 64.  Ground truth is exact L2 brute force.
 
-A "step" is one batch of 64 queries through the whole search path (rotate,
-centroid scores, probe selection, byte LUT, ADC scan + top-ck, refine +
-final top-k) with queries and results resident in device memory.  The nprobe
+A "step" is one batch of 64 queries through the whole search path (query
+rotation and centroid scores, probe selection, byte LUT, ADC scan + top-ck,
+refine + final top-k) with queries and results resident in device memory.  The nprobe
 sweep {16, 32, 64} picks the fastest setting with recall@10 >= 0.95; `value`
 is that setting's queries/s over exactly --steps timed steps.
 
@@ -268,12 +268,16 @@ def bench_cfg2(args):
     # HBM traffic per scan launch: FETCH_SIZE + WRITE_SIZE from the committed
     # rocprofv3 counter runs (scaled by the calibration kernel), when they were
     # taken at the operating point chosen above
+    kernel, _ = ix.scan_plan(K)
     traffic, traffic_note = None, "no counter run at this operating point"
-    tpath = os.path.join(ROOT, "profiles", "scan_topck_cfg2_traffic.json")
-    if os.path.exists(tpath) and args.scale == 1.0:
-        with open(tpath) as f:
+    pdir = os.path.join(ROOT, "profiles")
+    for fn in sorted(os.listdir(pdir)) if os.path.isdir(pdir) else []:
+        if not fn.endswith("_traffic.json") or args.scale != 1.0:
+            continue
+        with open(os.path.join(pdir, fn)) as f:
             tj = json.load(f)
-        if tj.get("nprobe") == npb and float(tj.get("alpha")) == float(alpha):
+        if (tj.get("kernel") == kernel and tj.get("nprobe") == npb
+                and float(tj.get("alpha")) == float(alpha) and tj.get("workload", "").startswith("cfg2")):
             traffic = int(tj["traffic_bytes_per_launch"])
             traffic_note = ("bytes per launch from %s (FETCH_SIZE x %.2f + WRITE_SIZE x %.2f)"
                             % (tj["source"], tj["fetch_scale"], tj["write_scale"]))
@@ -323,7 +327,7 @@ def bench_cfg2(args):
             "step_us_per_batch": {k2: round(v, 2) for k2, v in step_us.items()},
         },
         "roofline": {
-            "kernel": "scan_topck_kernel",
+            "kernel": kernel,
             "dominant_step": dominant,
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -464,8 +468,9 @@ def scan_roofline(ix, hq, k, batch, step_us):
     per_launch = float(sizes[dbg["probes"]].sum()) * ix.params.M / nb
     us = step_us["scan_topck"]
     ach = per_launch / (us * 1e-6) / 1e9
+    kernel, _ = ix.scan_plan(k)
     return {
-        "kernel": "scan_topck_kernel",
+        "kernel": kernel + (" + select_query_kernel" if kernel == "scan_dump_kernel" else ""),
         "dominant_step": max(step_us, key=step_us.get),
         "bound": "hbm",
         "achieved": round(ach, 1),

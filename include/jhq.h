@@ -176,6 +176,12 @@ int jhq_save(const jhq_index* idx, const char* path);
 int jhq_get_params(const jhq_index* idx, jhq_params* out);
 int jhq_load(const char* path, jhq_index** out);
 
+/* Which scan a search with this k runs: 0 workgroup-synchronous selection
+ * (scan_topck_kernel), 1 wave-level selection (scan_wave_kernel), 2 every
+ * distance to a buffer then one selection per query (scan_dump_kernel +
+ * select_query_kernel); and the short-list length ck. */
+int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list);
+
 /* List pool occupancy: slots in use (including padding, headroom and blocks
  * left behind by moves since the last re-pack) and allocated slots. */
 int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity);

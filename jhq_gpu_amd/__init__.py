@@ -93,6 +93,7 @@ _SIGS = {
     "jhq_save": (_I, [_VP, ctypes.c_char_p]),
     "jhq_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_VP)]),
     "jhq_get_params": (_I, [_VP, ctypes.POINTER(_Params)]),
+    "jhq_get_plan": (_I, [_VP, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "jhq_search_device": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP]),
     "jhq_ntotal": (_I64, [_VP]),
     "jhq_dim": (_I, [_VP]),
@@ -288,6 +289,13 @@ class JHQGpuIndex:
         _check(lib().jhq_get_params(h, ctypes.byref(cp)))
         self._p = Params(**{f: getattr(cp, f) for f, _ in _Params._fields_})
         return self
+
+    def scan_plan(self, k):
+        """(scan kernel name, short-list length ck) a search with this k uses."""
+        kind, ck = _I(), _I()
+        _check(lib().jhq_get_plan(self._h, int(k), ctypes.byref(kind), ctypes.byref(ck)))
+        names = ("scan_topck_kernel", "scan_wave_kernel", "scan_dump_kernel")
+        return names[kind.value], int(ck.value)
 
     def pool(self):
         used, cap = _I64(), _I64()

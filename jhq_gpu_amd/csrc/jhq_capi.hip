@@ -1248,6 +1248,18 @@ int jhq_load(const char* path, jhq_index** out) {
     return JHQ_OK;
 }
 
+int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list) {
+    if (!idx || k <= 0) return fail(JHQ_EINVAL, "bad argument");
+    const int ck = ceil_ck(idx->alpha, k);
+    const int P = std::min(idx->nprobe, idx->nlist);
+    jhq::ScanShape sh{};
+    if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh))
+        return fail(JHQ_EINVAL, "no scan plan fits in LDS");
+    if (scan_kind) *scan_kind = sh.dump ? 2 : sh.wave ? 1 : 0;
+    if (short_list) *short_list = ck;
+    return JHQ_OK;
+}
+
 int jhq_get_pool(const jhq_index* idx, int64_t* pool_slots, int64_t* pool_capacity) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (pool_slots) *pool_slots = idx->pool_used;
