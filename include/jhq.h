@@ -179,7 +179,8 @@ int jhq_load(const char* path, jhq_index** out);
 /* Which scan a search with this k runs: 0 workgroup-synchronous selection
  * (scan_topck_kernel), 1 wave-level selection (scan_wave_kernel), 2 every
  * distance to a buffer then one selection per query (scan_dump_kernel +
- * select_query_kernel); and the short-list length ck. */
+ * select_query_kernel), 3 wave-level selection with lanes skewed across
+ * subspaces (scan_skew_kernel); and the short-list length ck. */
 int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list);
 
 /* List pool occupancy: slots in use (including padding, headroom and blocks

@@ -294,7 +294,7 @@ class JHQGpuIndex:
         """(scan kernel name, short-list length ck) a search with this k uses."""
         kind, ck = _I(), _I()
         _check(lib().jhq_get_plan(self._h, int(k), ctypes.byref(kind), ctypes.byref(ck)))
-        names = ("scan_topck_kernel", "scan_wave_kernel", "scan_dump_kernel")
+        names = ("scan_topck_kernel", "scan_wave_kernel", "scan_dump_kernel", "scan_skew_kernel")
         return names[kind.value], int(ck.value)
 
     def pool(self):

@@ -116,6 +116,7 @@ struct jhq_index {
     DBuf<int4> dldesc;
     DBuf<int32_t> dlist_ids;
     DBuf<uint8_t> dcodes_t, dres;
+    DBuf<uint8_t> dcodes_s;  // lane-skewed rows of the primary codes (skew scan)
     DBuf<float> dcorr;
 
     // query GEMM operand [Pi ; centroids * Pi] ((d + nlist) x d): one product
@@ -302,7 +303,8 @@ struct BatchPlan {
 int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
-    if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh))
+    if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
+                        ix->dcodes_s.p != nullptr))
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
@@ -341,7 +343,7 @@ int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& b
     JHQ_HIP(jhq::scan_topck(ix->wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                             ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dldesc.p,
                             ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, ix->wpslot.p,
-                            ix->wdump.p, s));
+                            ix->wdump.p, ix->dcodes_s.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
     JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wpslot.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k,
                              ix->wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
@@ -637,6 +639,21 @@ int upload_ldesc(jhq_index* ix) {
     return ix->dldesc.upload(h.data(), h.size());
 }
 
+// The skew scan's copy of the codes (M a multiple of 32, at most 128).
+bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128; }
+
+int rebuild_skew(jhq_index* ix) {
+    if (!skew_eligible(ix) || ix->pool_cap <= 0) return JHQ_OK;
+    const size_t need = static_cast<size_t>(ix->pool_cap) * ix->M;
+    if (ix->dcodes_s.n < need) JHQ_TRY(ix->dcodes_s.alloc(need));
+    int max_cap = 0;
+    for (int l = 0; l < ix->nlist; l++) max_cap = std::max(max_cap, ix->l_cap[l]);
+    JHQ_HIP(jhq::skew_codes(ix->dldesc.p, ix->nlist, max_cap, ix->dcodes_t.p, ix->M,
+                            ix->dcodes_s.p, ix->stream));
+    JHQ_HIP(hipStreamSynchronize(ix->stream));
+    return JHQ_OK;
+}
+
 // Grows the device pool to at least `need` slots, keeping every block where
 // it is (the old pool is copied to the front of the new one).
 int grow_pool(jhq_index* ix, int64_t need) {
@@ -874,6 +891,7 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         for (int l = 0; l < nlist; l++) ix->l_size[l] += rank[l];
     }
     JHQ_TRY(upload_ldesc(ix));
+    JHQ_TRY(rebuild_skew(ix));
     ix->ntotal += n;
     return JHQ_OK;
 }
@@ -1241,6 +1259,7 @@ int jhq_load(const char* path, jhq_index** out) {
             return done(fail(JHQ_EDEVICE, "index upload failed"));
     }
     rc = upload_ldesc(ix);
+    if (rc == JHQ_OK) rc = rebuild_skew(ix);
     if (rc != JHQ_OK) return done(rc);
     ix->ntotal = n;
     ix->added = ad != 0;
@@ -1253,9 +1272,10 @@ int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list) {
     const int ck = ceil_ck(idx->alpha, k);
     const int P = std::min(idx->nprobe, idx->nlist);
     jhq::ScanShape sh{};
-    if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh))
+    if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh,
+                        idx->dcodes_s.p != nullptr))
         return fail(JHQ_EINVAL, "no scan plan fits in LDS");
-    if (scan_kind) *scan_kind = sh.dump ? 2 : sh.wave ? 1 : 0;
+    if (scan_kind) *scan_kind = sh.dump ? 2 : sh.skew ? 3 : sh.wave ? 1 : 0;
     if (short_list) *short_list = ck;
     return JHQ_OK;
 }

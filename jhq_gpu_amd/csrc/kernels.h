@@ -63,6 +63,11 @@ hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int 
 //
 // Scatter: new vector s goes to list slist[s] at index sidx[s]; its id is
 // id_base + order[s], order[s] indexing the per-vector inputs pc/rc/co.
+// Lane-skewed rows of the primary codes (row[t] = code[(t - i mod 32) mod M]
+// for candidate i of each list, at skew[(start + i) * M]); every capacity
+// slot of every list, max_cap >= the largest capacity.  M % 4 == 0.
+hipError_t skew_codes(const int4* ldesc, int nlist, int max_cap, const uint8_t* codes_t, int M,
+                      uint8_t* skew, hipStream_t s);
 hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
                          int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
                          const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,
@@ -86,6 +91,7 @@ struct ScanShape {
     int max_segments;  // upper bound on top-ck lists per batch (partial rows)
     int wave;          // 0: workgroup-synchronous selection; J: wave selection, 64*J-key buffers
     int nt;            // threads per scan workgroup
+    int skew;          // M / 4 when the lane-skewed scan runs (needs the skewed codes)
     int dump;          // 1: every distance to a buffer, then one selection per query (region
                        // = that kernel's LDS); the buffer holds B * (groups of the P largest
                        // lists) * 16 keys
@@ -93,7 +99,8 @@ struct ScanShape {
 };
 // LDS plan of the scan kernel; returns false if the byte LUT and the
 // selection buffers do not fit.
-bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out);
+bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
+               bool skew = false);
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from
 // q_rot (v14/search.cu:65-195); partial[segment][ck] keys
@@ -103,7 +110,7 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
                       int B, int M, const int32_t* probes, const int32_t* gofs,
                       const int32_t* qtot, int P, const int4* ldesc, const uint8_t* codes_t,
                       int ck, const ScanShape& sh, unsigned long long* partial,
-                      int32_t* partial_slot, unsigned long long* dump, hipStream_t s);
+                      int32_t* partial_slot, unsigned long long* dump, const uint8_t* skew, hipStream_t s);
 
 // Per query: merge its segment lists, residual refine, final top-k.
 // If topck_dbg != nullptr it receives the merged short list [B][ck] keys.

@@ -1022,6 +1022,44 @@ __global__ void scatter_kernel(const int32_t* __restrict__ order, const int32_t*
     for (int b2 = 0; b2 < bpv; b2++) rd[b2] = rs[b2];
 }
 
+// ---------------------------------------------------------------------------
+// Lane-skewed copy of the primary codes, for the scan that runs each lane a
+// fixed number of subspaces behind its neighbours.  Candidate i of a list
+// (pool slot start + i) gets a row of M bytes at skew[(start + i) * M]:
+//   row[t] = code[(t - (i mod 32)) mod M]
+// so that at step t the lane holding i reads subspace t - (i mod 32) from
+// row position t.  One thread per (list, candidate); the codes are read from
+// the code-major blocks (codes_t[start * M + m * cap + i]).
+// ---------------------------------------------------------------------------
+__global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t,
+                                  int M, uint8_t* __restrict__ skew) {
+    const int4 L = ldesc[blockIdx.x];
+    const int i = blockIdx.y * blockDim.x + threadIdx.x;
+    if (i >= L.y) return;  // capacity: padding rows are written too
+    const uint8_t* src = codes_t + (int64_t)L.x * M + i;
+    uint8_t* dst = skew + ((int64_t)L.x + i) * M;
+    const int s = i & 31;
+    for (int t0 = 0; t0 < M; t0 += 4) {
+        uint32_t w = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            int m = t0 + e - s;
+            if (m < 0) m += M;
+            w |= (uint32_t)src[(int64_t)m * L.y] << (8 * e);
+        }
+        *(uint32_t*)(dst + t0) = w;
+    }
+}
+
+hipError_t skew_codes(const int4* ldesc, int nlist, int max_cap, const uint8_t* codes_t, int M,
+                      uint8_t* skew, hipStream_t s) {
+    if (nlist <= 0 || max_cap <= 0) return hipSuccess;
+    if (M % 4 != 0 || (max_cap + 255) / 256 > 65535) return hipErrorInvalidValue;
+    dim3 grid(nlist, (max_cap + 255) / 256);
+    hipLaunchKernelGGL(skew_codes_kernel, grid, dim3(256), 0, s, ldesc, codes_t, M, skew);
+    return hipGetLastError();
+}
+
 hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
                          int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
                          const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,
@@ -1546,7 +1584,7 @@ __device__ int work_plan(const int32_t* __restrict__ qtot, int B, int Gmax, int*
 // one low-nibble prefix and expands the high nibble as a binary tree (34
 // fmas for 16 entries instead of 128); every entry is still the same chain.
 // ---------------------------------------------------------------------------
-template <int NT>
+template <int NT, bool TR = false>
 __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, int K1D, int bpd,
                                               const float* sc1d, float* lut) {
     const int tpm = NT / M > 0 ? NT / M : 1;
@@ -1579,7 +1617,10 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
                     }
                 }
 #pragma unroll
-                for (int h = 0; h < 16; h++) lm[p + 16 * h] = t[h];
+                for (int h = 0; h < 16; h++) {
+                    if (TR) lut[(p + 16 * h) * M + m] = t[h];
+                    else lm[p + 16 * h] = t[h];
+                }
             }
         } else {
             for (int v = part; v < 256; v += tpm) {
@@ -1591,7 +1632,8 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
                         sacc = fmaf(df, df, sacc);
                     }
                 }
-                lm[v] = sacc;
+                if (TR) lut[v * M + m] = sacc;
+                else lm[v] = sacc;
             }
         }
     }
@@ -2137,6 +2179,362 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
     JHQ_PHASE_FLUSH(0);
 }
 
+// chunks of a code row requested ahead of the one being consumed
+#ifndef JHQ_SKEW_D
+#define JHQ_SKEW_D 2
+#endif
+// LUT reads per group of steps, and groups of reads in flight ahead of the adds
+#ifndef JHQ_SKEW_GS
+#define JHQ_SKEW_GS 4
+#endif
+#ifndef JHQ_SKEW_LA
+#define JHQ_SKEW_LA 3
+#endif
+// ---------------------------------------------------------------------------
+// ADC scan with lanes skewed across subspaces (M a multiple of 32, MW = M/4).
+// Random byte-LUT gathers conflict on LDS banks when every lane reads the same
+// subspace's table.  Here the LUT is laid out [v][m] (bank = m mod 32) and lane
+// l runs s = l mod 32 steps behind step t: at step t it adds subspace t - s of
+// its candidate, so the 32 lane classes hit 32 different banks.  Each lane
+// still adds its candidate's subspaces in ascending order from 0.0f, exactly
+// the unskewed sum:
+//   - a period is M steps over one candidate per lane (64 per wave: two
+//     32-aligned rows of up to two lists, lanes 0-31 and 32-63); at steps
+//     t >= s it adds subspaces 0 .. M-1-s of the current candidate, at steps
+//     t < s of the NEXT period subspaces M-s .. M-1 of it, then its sum is
+//     final (the lane class of candidate i is i mod 32, so it never changes);
+//   - the codes come from the skewed copy (row[t] = code[(t - s) mod M]),
+//     streamed in 32-byte chunks; the previous row's first chunk stays in
+//     registers for the tails;
+//   - which lanes read a tail at step t < 32, and which finish a sum there,
+//     are lane masks built on the scalar unit (no per-step compares);
+//   - after the last period a drain of up to 31 steps finishes the tails.
+// Work plan, segments, wave selection, merge and output are scan_wave_kernel's.
+// ---------------------------------------------------------------------------
+template <int NT, int MW, int J>
+__global__ void __launch_bounds__(NT)
+scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
+                 const float* __restrict__ c1d, const int32_t* __restrict__ probes,
+                 const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
+                 const int4* __restrict__ ldesc, const uint8_t* __restrict__ skew, int ck,
+                 int region_bytes, unsigned long long* __restrict__ partial,
+                 int32_t* __restrict__ partial_slot) {
+    constexpr int M = MW * 4, NW = NT / 64, wcap = 64 * J;
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* lut = (float*)smem;                                  // [256][M], or the merge keys
+    unsigned long long* merge = (unsigned long long*)smem;
+    unsigned long long* wbuf = (unsigned long long*)(smem + region_bytes);  // [NW][wcap]
+    unsigned long long* kout =
+        wbuf + max((size_t)NW * wcap, (size_t)((d + 3) & ~3) / 2);  // [ck]
+    unsigned long long* ktmp = kout + ck;                       // [ck]
+    int* kidx = (int*)(ktmp + ck);                              // [ck]
+    SelState* st = (SelState*)(kidx + ((ck + 3) & ~3));
+    int* ctl = (int*)(st + 1);                                  // Tg, merge count, task counter
+    float* sq = (float*)wbuf;  // the query, needed only until the LUT is built
+    int* qpre = ctl + 4;
+    int* spre = qpre + B + 1;
+    int32_t* sg = spre + B + 1;
+    int32_t* spad0 = sg + P + 1;
+    int32_t* snpad = spad0 + P;
+    int32_t* snl = snpad + P;
+    int32_t* soff = snl + P;
+    int32_t* sru = soff + P;      // [P+1] first row unit of each probe in the segment
+    int32_t* sr0 = sru + P + 1;   // [P] first row of each probe in the segment
+    float* sc1d = (float*)(sr0 + P);
+    int* wsum = (int*)(sc1d + K1D);
+
+    const int tid = threadIdx.x, w = blockIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int s = lane & 31;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    unsigned long long* wb = wbuf + (size_t)wv * wcap;
+    JHQ_PHASE_DECL
+    for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
+    const int64_t T = qpre[B];
+    JHQ_PHASE(0);
+    if (w >= G) return;
+    const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
+    int b;
+    {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (qpre[mid] <= x0) lo = mid;
+            else hi = mid - 1;
+        }
+        b = lo;
+    }
+    for (; b < B && qpre[b] < x1; b++) {
+        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
+        if (qb1 <= qb0) continue;
+        const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
+        const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
+        __syncthreads();
+        for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
+        for (int i = tid; i < P; i += NT) {
+            const int4 L = ldesc[probes[(int64_t)b * P + i]];
+            spad0[i] = L.x;
+            snpad[i] = L.y;
+            snl[i] = L.z;
+            soff[i] = L.w;
+        }
+        for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
+        if (tid == 0) {
+            ctl[0] = (int)~0u;
+            ctl[1] = 0;
+            ctl[2] = 0;
+        }
+        __syncthreads();
+        // rows (32 candidates) of each probe that meet the segment's groups
+        for (int i = tid; i < P; i += NT) {
+            const int lo = max(gA, sg[i]), hi = min(gB, sg[i + 1]);
+            sr0[i] = lo < hi ? (lo - sg[i]) >> 1 : 0;
+        }
+        block_exclusive_scan<NT>(
+            [&](int i) {
+                const int lo = max(gA, sg[i]), hi = min(gB, sg[i + 1]);
+                return lo < hi ? ((hi - sg[i] + 1) >> 1) - ((lo - sg[i]) >> 1) : 0;
+            },
+            P, sru, wsum);
+        build_lut_lds<NT, true>(sq, M, Ds, K1D, bpd, sc1d, lut);
+        __syncthreads();
+        JHQ_PHASE(1);
+
+        const int nunit = sru[P];
+        const int ntask = (nunit + 1) >> 1;
+        int nw = 0;
+        uint32_t Tw = ~0u;
+        // rows are streamed in chunks of 8 words (32 steps), chunk c + D
+        // requested while chunk c is consumed; pw keeps the first chunk of the
+        // previous row (its tail steps t < s <= 31 read nothing else).  The
+        // steps run in groups of GS: the LUT reads of group g + LA are issued
+        // before the adds of group g, so at most (LA + 1) * GS read results
+        // are live at a time (the compiler would otherwise issue a whole
+        // period's reads first and hold all of them in registers).
+        constexpr int C = MW / 8, D = C < JHQ_SKEW_D ? C : JHQ_SKEW_D;
+        constexpr int GS = JHQ_SKEW_GS, LA = JHQ_SKEW_LA, NG = M / GS;
+        uint32_t wr[C + D][8], pw[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) pw[j] = 0u;
+        float acc = 0.0f;
+        uint32_t ptag = 0u;
+        bool pvalid = false;
+        const float* lb = lut - s;  // lane base: lut[v*M + m] = lb[v*M + t] with m = t - s
+        auto append = [&](bool keep, uint32_t o, uint32_t tg) {
+            if (nw + 64 > wcap) {
+                Tw = wave_prune<J>(wb, nw, ck);
+                nw = ck;
+                if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
+            }
+            const uint32_t tgs = (uint32_t)ctl[0];
+            keep = keep && o <= min(Tw, tgs);
+            const unsigned long long mk = __ballot(keep);
+            if (keep) wb[nw + __popcll(mk & lt)] = ((unsigned long long)o << 32) | tg;
+            nw += __popcll(mk);
+        };
+        // the lane's candidate of task t: unit 2t + half, row r of probe p
+        auto locate = [&](int t, bool& valid, uint32_t& tag, int64_t& slot) {
+            const int u = 2 * t + (lane >> 5);
+            valid = false;
+            tag = 0u;
+            slot = 0;
+            if (t < ntask && u < nunit) {
+                int plo = 0, phi = P - 1;  // last probe with sru <= u
+                while (plo < phi) {
+                    const int mid = (plo + phi + 1) >> 1;
+                    if (sru[mid] <= u) plo = mid;
+                    else phi = mid - 1;
+                }
+                const int r = sr0[plo] + (u - sru[plo]);
+                const int i = 32 * r + s;
+                const int gi = sg[plo] + (i >> 4);
+                valid = i < snl[plo] && gi >= gA && gi < gB;
+                tag = (uint32_t)(soff[plo] + i);
+                slot = valid ? (int64_t)spad0[plo] + i : 0;
+            }
+        };
+        auto grab = [&]() {
+            int t = 0;
+            if (lane == 0) t = atomicAdd(&ctl[2], 1);
+            return __shfl(t, 0);
+        };
+        auto load_chunk = [&](int64_t slot, int c, uint32_t (&dst)[8]) {
+            const uint4* rp = (const uint4*)(skew + slot * M + 32 * c);
+            const uint4 a = rp[0], b2 = rp[1];
+            dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
+            dst[4] = b2.x; dst[5] = b2.y; dst[6] = b2.z; dst[7] = b2.w;
+        };
+        int t = grab();
+        bool valid;
+        uint32_t tag;
+        int64_t slot;
+        locate(t, valid, tag, slot);
+        if (t < ntask) {
+#pragma unroll
+            for (int c = 0; c < D; c++) load_chunk(slot, c, wr[c]);
+        }
+        while (t < ntask) {
+            const int tn = grab();
+            bool nvalid;
+            uint32_t ntag;
+            int64_t nslot;
+            locate(tn, nvalid, ntag, nslot);
+            const bool more = tn < ntask;
+            float fin = 0.0f;
+            // Lane masks of the chunk-0 steps, built on the scalar unit: lanes
+            // 32h + s with s > t read a tail at step t (tmask), the lanes with
+            // s == t finish their previous candidate there (fmask).  The seeds
+            // are opaque so the masks are rebuilt each period, not hoisted.
+            uint32_t tseed = 0xfffffffeu, fseed = 1u;
+            asm volatile("" : "+s"(tseed), "+s"(fseed));
+            auto rep2 = [](uint32_t m) { return ((unsigned long long)m << 32) | m; };
+            // byte offsets of the lane's LUT base for a head and a tail read
+            // (opaque: one select of two registers per step)
+            using lds_byte = __attribute__((address_space(3))) const char;
+            lds_byte* ph = (lds_byte*)lut - 4 * s;
+            lds_byte* pt = ph + 4 * M;
+            asm volatile("" : "+v"(ph), "+v"(pt));
+            // LUT reads of steps GS*g .. GS*g+GS-1.  In chunk 0 a lane with
+            // t < s reads the previous candidate's subspace M + t - s
+            auto fetch = [&](int g, float (&dst)[GS]) {
+#pragma unroll
+                for (int i = 0; i < GS; i++) {
+                    const int tt = GS * g + i, c = tt >> 5, j = (tt >> 2) & 7, e = tt & 3;
+                    if (c == 0) {
+                        const bool tail = __builtin_amdgcn_inverse_ballot_w64(rep2(tseed << tt));
+                        uint32_t v = __builtin_amdgcn_ubfe(tail ? pw[j] : wr[0][j], 8 * e, 8);
+                        asm("" : "+v"(v));
+                        dst[i] = *(const __attribute__((address_space(3))) float*)(
+                            (tail ? pt : ph) + v * (4 * M) + 4 * tt);
+                    } else {
+                        uint32_t v = __builtin_amdgcn_ubfe(wr[c][j], 8 * e, 8);
+                        asm("" : "+v"(v));
+                        dst[i] = *(const __attribute__((address_space(3))) float*)(
+                            ph + v * (4 * M) + 4 * tt);
+                    }
+                }
+            };
+            // adds of steps GS*g .. GS*g+GS-1, in step order; at t == s the
+            // previous candidate's sum is final and the current one starts from 0
+            auto accum = [&](int g, const float (&src)[GS]) {
+#pragma unroll
+                for (int i = 0; i < GS; i++) {
+                    const int tt = GS * g + i;
+                    if (tt < 32) {
+                        const bool first = __builtin_amdgcn_inverse_ballot_w64(rep2(fseed << tt));
+                        fin = first ? acc : fin;
+                        acc = first ? 0.0f : acc;
+                    }
+                    acc += src[i];
+                }
+            };
+            // the reads run LA groups ahead of the adds
+            float vq[LA + 1][GS];
+#pragma unroll
+            for (int g = 0; g < LA; g++) fetch(g, vq[g]);
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                if ((g * GS) % 32 == 0) {
+                    const int c = g * GS / 32 + D;  // chunk to request
+                    if (c < C) load_chunk(slot, c, wr[c]);
+                    else if (more) load_chunk(nslot, c - C, wr[c]);
+                }
+                if (g + LA < NG) fetch(g + LA, vq[(g + LA) % (LA + 1)]);
+                accum(g, vq[g % (LA + 1)]);
+                asm volatile("" : "+v"(acc));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) pw[j] = wr[0][j];
+#pragma unroll
+            for (int c = 0; c < D; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) wr[c][j] = wr[C + c][j];
+            append(pvalid, f2ord(fin), ptag);
+            ptag = tag;
+            pvalid = valid;
+            tag = ntag;
+            valid = nvalid;
+            slot = nslot;
+            t = tn;
+        }
+        {
+            // drain: the tails of the last candidates
+            float fin = acc;
+            int sv = s;
+            asm volatile("" : "+v"(sv));
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int tt = 4 * j + e;
+                    if (tt < sv) acc += lb[((pw[j] >> (8 * e)) & 0xffu) * M + tt + M];
+                    if (tt == sv) fin = acc;
+                }
+            }
+            append(pvalid, f2ord(fin), ptag);
+        }
+        if (nw > ck) {
+            Tw = wave_prune<J>(wb, nw, ck);
+            nw = ck;
+            if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
+        }
+        {
+            const int r = (ck + NW - 1) / NW;
+            uint32_t vals[J];
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const int i = j * 64 + lane;
+                vals[j] = i < nw ? (uint32_t)(wb[i] >> 32) : ~0u;
+            }
+            const uint32_t tw = nw >= r ? wave_kth_u32<J>(vals, r) : ~0u;
+            if (lane == 0) wsum[wv] = (int)tw;
+        }
+        JHQ_PHASE(6);
+        __syncthreads();  // every wave's tasks are done: the LUT area is free
+        JHQ_PHASE(2);
+        uint32_t Tf = (uint32_t)ctl[0];
+        {
+            uint32_t t3 = 0u;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) t3 = max(t3, (uint32_t)wsum[w2]);
+            Tf = min(Tf, t3);
+        }
+        for (int i0 = 0; i0 < nw; i0 += 64) {
+            const int i = i0 + lane;
+            const unsigned long long key = i < nw ? wb[i] : ~0ull;
+            const bool keep = i < nw && (uint32_t)(key >> 32) <= Tf;
+            const unsigned long long mk = __ballot(keep);
+            int at = 0;
+            if (lane == 0 && mk) at = atomicAdd(&ctl[1], __popcll(mk));
+            at = __shfl(at, 0);
+            if (keep) merge[at + __popcll(mk & lt)] = key;
+        }
+        __syncthreads();
+        const int n = ctl[1];
+        const int kk = min(ck, n);
+        if (kk > 0) select_keys<NT>(merge, n, kk, kout, kidx, ktmp, st);
+        __syncthreads();
+        unsigned long long* outp = partial + (int64_t)seg * ck;
+        int32_t* outs = partial_slot + (int64_t)seg * ck;
+        for (int i = tid; i < ck; i += NT) {
+            int32_t slot = -1;
+            if (i < kk) {
+                const int tag = (int)(uint32_t)(kout[i] & 0xffffffffull);
+                for (int p = 0; p < P; p++)
+                    if (tag >= soff[p] && tag - soff[p] < snl[p]) slot = spad0[p] + (tag - soff[p]);
+            }
+            outp[i] = i < kk ? kout[i] : ~0ull;
+            outs[i] = slot;
+        }
+#ifdef JHQ_PHASE_TIMING
+        if (tid == 0) ph_acc[7] += n;
+#endif
+        JHQ_PHASE(3);
+    }
+    JHQ_PHASE_FLUSH(0);
+}
+
 // ---------------------------------------------------------------------------
 // Large short lists (ck beyond the wave buffers): the scan writes every
 // candidate's key (ord(dist) << 32 | canonical position; ~0 for padding) to
@@ -2380,6 +2778,7 @@ static int allow_max_lds(const void* kernel) {
 }
 
 constexpr int kScanNT = JHQ_SCAN_NT;
+constexpr int kSkewNT = 512;  // 8 waves: the scan loop's registers fit without spills
 constexpr int kRefineNT = 512;
 constexpr int kProbeNT = 512;
 
@@ -2396,15 +2795,31 @@ static size_t scan_wave_lds(int NT, int M, int d, int P, int ck, int K1D, int B,
            (size_t)K1D * 4 + NW * 4 + 64;
 }
 
-bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out) {
+bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
+               bool skew) {
     out->G = target_wg;
     out->max_segments = target_wg + B;
+    out->skew = 0;
     const int need = ck + 64;
     const int J = need <= 128 ? 2 : need <= 192 ? 3 : need <= 256 ? 4 : need <= 384 ? 6
                 : need <= 512 ? 8 : 0;
     out->dump = 0;
     // short lists up to 128: selection inside the scan, 16 waves per workgroup
     if (J && J <= 3) {
+        // lanes skewed across subspaces: M a multiple of 32, at most 128
+        if (skew && M % 32 == 0 && M <= 128) {
+            size_t region = 0;
+            const size_t lds = scan_wave_lds(kSkewNT, M, d, P, ck, K1D, B, J, &region) +
+                               (size_t)(2 * P + 1) * 4;
+            if (lds <= (size_t)kLdsBytes - 1024) {
+                out->wave = J;
+                out->skew = M / 4;
+                out->nt = kSkewNT;
+                out->lds = (int)lds;
+                out->region = (int)region;
+                return true;
+            }
+        }
         size_t region = 0;
         const size_t lds = scan_wave_lds(kScanNT, M, d, P, ck, K1D, B, J, &region);
         if (lds <= (size_t)kLdsBytes - 1024) {
@@ -2469,9 +2884,31 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
                       int B, int M, const int32_t* probes, const int32_t* gofs,
                       const int32_t* qtot, int P, const int4* ldesc, const uint8_t* codes_t,
                       int ck, const ScanShape& sh, unsigned long long* partial,
-                      int32_t* partial_slot, unsigned long long* dump, hipStream_t s) {
+                      int32_t* partial_slot, unsigned long long* dump, const uint8_t* skew,
+                      hipStream_t s) {
     constexpr int NT = kScanNT, SU = JHQ_SCAN_SU;
     if (Ds > 8 || K1D > 256) return hipErrorInvalidValue;
+    if (sh.skew) {
+        using KFn = void (*)(const float*, int, int, int, int, const float*, const int32_t*,
+                             const int32_t*, const int32_t*, int, int, const int4*,
+                             const uint8_t*, int, int, unsigned long long*, int32_t*);
+        constexpr int NS = kSkewNT;
+        static const KFn kf[4][2] = {
+            {scan_skew_kernel<NS, 8, 2>, scan_skew_kernel<NS, 8, 3>},
+            {scan_skew_kernel<NS, 16, 2>, scan_skew_kernel<NS, 16, 3>},
+            {scan_skew_kernel<NS, 24, 2>, scan_skew_kernel<NS, 24, 3>},
+            {scan_skew_kernel<NS, 32, 2>, scan_skew_kernel<NS, 32, 3>}};
+        static int mx[4][2] = {{-1, -1}, {-1, -1}, {-1, -1}, {-1, -1}};
+        const int mi = sh.skew / 8 - 1, ji = sh.wave - 2;
+        if (!skew || mi < 0 || mi > 3 || ji < 0 || ji > 1 || sh.skew * 4 != M)
+            return hipErrorInvalidValue;
+        if (mx[mi][ji] < 0) mx[mi][ji] = allow_max_lds((const void*)kf[mi][ji]);
+        if (sh.lds > mx[mi][ji]) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(kf[mi][ji], dim3(sh.G), dim3(NS), sh.lds, s, q_rot, d, Ds, K1D, bpd,
+                           c1d, probes, gofs, qtot, B, P, ldesc, skew, ck, sh.region, partial,
+                           partial_slot);
+        return hipGetLastError();
+    }
     if (sh.dump) {
         static const int mxd = allow_max_lds((const void*)scan_dump_kernel<NT, SU>);
         static const int mxs = allow_max_lds((const void*)select_query_kernel<NT>);

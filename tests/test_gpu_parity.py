@@ -37,6 +37,9 @@ CASES = [
     ("flat_many_chunks", 32, 8, 8, 4, 1, 1, 4.0, 20000, 6, 10, 1),
     # k=100 with alpha=4: ck=400 short list
     ("k100_ck400", 64, 16, 8, 4, 8, 4, 4.0, 6000, 12, 100, 16),
+    # M a multiple of 32: lanes skewed across subspaces (K1D=4; ck=100)
+    ("m64_ds4_ck100", 256, 64, 8, 4, 16, 5, 10.0, 3000, 20, 10, 32),
+    ("m96_d768", 768, 96, 8, 4, 8, 3, 4.0, 2500, 16, 10, 16),
 ]
 IDS = [c[0] for c in CASES]
 
