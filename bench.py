@@ -8,11 +8,13 @@ uniform weights) and L2-normalised.  IVF nlist=4096 trained on the first
 100,000 base vectors (the reference demo's protocol), M=128, B=8, Br=4,
 alpha=4, k=10, query batch 64.  Ground truth is exact L2 brute force.
 
-A "step" is one batch of 64 queries through the whole search path (query
-rotation and centroid scores, probe selection, byte LUT, ADC scan + top-ck,
-refine + final top-k) with queries and results resident in device memory.  The nprobe
-sweep {16, 32, 64} picks the fastest setting with recall@10 >= 0.95; `value`
-is that setting's queries/s over exactly --steps timed steps.
+A "step" is one device search call over the 10,000 queries, resident in device
+memory with their results: the engine runs them in batches of 64 through the
+whole search path (query rotation and centroid scores, probe selection, byte
+LUT, ADC scan + top-ck, refine + final top-k), alternating two workspaces on
+two streams so one batch's refine overlaps the next batch's query product.
+The nprobe sweep {16, 32, 64} picks the fastest setting with recall@10 >= 0.95;
+`value` is that setting's queries/s over exactly --steps timed steps.
 
 Also reported: per-kernel HIP-event times, the ADC scan's HBM roofline
 fraction, the reference's host-to-host QPS protocol, and the CPU baseline
@@ -42,8 +44,10 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=0, help="timed steps (default: 5 passes)")
-    ap.add_argument("--warmup", type=int, default=0, help="warmup steps (default: 1 pass)")
+    ap.add_argument("--steps", type=int, default=0,
+                    help="timed steps, each one pass over the query set (default: 10; 3 for "
+                         "configs 3-5)")
+    ap.add_argument("--warmup", type=int, default=0, help="warmup steps (default: 1)")
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="BASELINE.json workload: 2 (default, the metric's config), 3 (100M "
                          "uint8 D=128), 4 (100M int8 D=100), 5 (streaming add + search, D=768)")
@@ -196,22 +200,19 @@ def bench_cfg2(args):
 
     def run_steps(nsteps):
         for s in range(nsteps):
-            b = s % nb
-            q0 = b * BATCH
-            q1 = min(NQ, q0 + BATCH)
-            ix.search_device(q[q0:q1], K, out_d[q0:q1], out_i[q0:q1])
+            ix.search_device(q, K, out_d, out_i)
 
     sweep = []
     for alpha in alphas:
         ix.set_alpha(alpha)
         for npb in nprobes:
             ix.set_nprobe(npb)
-            run_steps(nb)
+            run_steps(1)
             torch.cuda.synchronize()
             t0 = time.time()
-            run_steps(nb)
+            run_steps(2)
             torch.cuda.synchronize()
-            dt = time.time() - t0
+            dt = (time.time() - t0) / 2
             ids_np = out_i.cpu().numpy()
             rec = recall_at(ids_np, gt, K)
             rec_ref = recall_ref_def(ids_np, gt, K)
@@ -231,24 +232,24 @@ def bench_cfg2(args):
     ix.set_nprobe(npb)
     ix.set_alpha(alpha)
 
-    W = args.warmup if args.warmup > 0 else nb
-    Kst = args.steps if args.steps > 0 else 5 * nb
+    W = args.warmup if args.warmup > 0 else 1
+    Kst = args.steps if args.steps > 0 else 10
     run_steps(W)
     torch.cuda.synchronize()
     t0 = time.time()
     run_steps(Kst)
     torch.cuda.synchronize()
     elapsed = time.time() - t0
-    queries_timed = sum(min(BATCH, NQ - (s % nb) * BATCH) for s in range(Kst))
-    qps = queries_timed / elapsed
+    qps = NQ * Kst / elapsed
     ms_per_step = elapsed * 1000.0 / Kst
     rec = recall_at(out_i.cpu().numpy(), gt, K)
     rec_ref = recall_ref_def(out_i.cpu().numpy(), gt, K)
     log(f"timed nprobe={npb} steps={Kst} qps={qps:.0f} ms/step={ms_per_step:.4f} recall={rec:.4f}")
 
-    # per-kernel HIP-event times over one pass (events on the kernels' stream)
+    # per-kernel HIP-event times over one pass (events on the kernels' stream;
+    # timing runs the batches one after another on one stream)
     ix.set_timing(True)
-    run_steps(nb)
+    run_steps(1)
     torch.cuda.synchronize()
     tm, nbat = ix.timing()
     ix.set_timing(False)
@@ -433,14 +434,13 @@ def recall_tie_aware(dist_ret, gt_d, k=10):
 
 
 def timed_search(torch, ix, q, out_d, out_i, k, batch, warmup, steps):
+    """Queries/s and ms per step; a step is one device search over all of q
+    (the engine batches it by its batch_size)."""
     nq = q.shape[0]
-    nb = (nq + batch - 1) // batch
 
     def run(nsteps):
         for st in range(nsteps):
-            b = st % nb
-            q0, q1 = b * batch, min(nq, b * batch + batch)
-            ix.search_device(q[q0:q1], k, out_d[q0:q1], out_i[q0:q1])
+            ix.search_device(q, k, out_d, out_i)
 
     run(warmup)
     torch.cuda.synchronize()
@@ -448,13 +448,12 @@ def timed_search(torch, ix, q, out_d, out_i, k, batch, warmup, steps):
     run(steps)
     torch.cuda.synchronize()
     el = time.time() - t0
-    nqt = sum(min(batch, nq - (st % nb) * batch) for st in range(steps))
-    return nqt / el, el * 1000.0 / steps
+    return nq * steps / el, el * 1000.0 / steps
 
 
 def step_times(torch, ix, q, out_d, out_i, k, batch):
     ix.set_timing(True)
-    timed_search(torch, ix, q, out_d, out_i, k, batch, 0, (q.shape[0] + batch - 1) // batch)
+    timed_search(torch, ix, q, out_d, out_i, k, batch, 0, 1)
     tm, nbat = ix.timing()
     ix.set_timing(False)
     return {k2: v * 1000.0 / nbat for k2, v in tm.items()}
@@ -532,8 +531,8 @@ def bench_bytes(args, cf):
     out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
     nb = (NQ + BATCH - 1) // BATCH
-    W = args.warmup if args.warmup > 0 else nb
-    Kst = args.steps if args.steps > 0 else 3 * nb
+    W = args.warmup if args.warmup > 0 else 1
+    Kst = args.steps if args.steps > 0 else 3
     qps, ms = timed_search(torch, ix, qf, out_d, out_i, K, BATCH, W, Kst)
     ids = out_i.cpu().numpy()
     rec = recall_at(ids, gt_i, K)
@@ -670,8 +669,8 @@ def bench_streaming(args):
         f"({NINS / max(t_ins, 1e-9):.0f} vectors/s), {nsearched} queries in {t_srch:.3f}s")
     del hb
 
-    W = args.warmup if args.warmup > 0 else nb
-    Kst = args.steps if args.steps > 0 else 3 * nb
+    W = args.warmup if args.warmup > 0 else 1
+    Kst = args.steps if args.steps > 0 else 3
     qps, ms = timed_search(torch, ix, q, out_d, out_i, K, BATCH, W, Kst)
     t0 = time.time()
     gt = ground_truth_f32(torch, base, q)

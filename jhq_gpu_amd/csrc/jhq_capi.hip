@@ -88,6 +88,15 @@ struct DBuf {
 
 constexpr int kSteps = 4;
 
+// Per-batch search buffers (v14/search.cuh:24-46).  The index keeps two sets:
+// consecutive batches of one device search alternate between them on two
+// streams, so one batch's refine overlaps the next batch's query product.
+struct Workspace {
+    DBuf<float> wq, wqrot, wscores, wout_d;
+    DBuf<int32_t> wprobes, wgofs, wqtot, wout_i, wpslot;
+    DBuf<unsigned long long> wpartial, wtopck, wdump;
+};
+
 }  // namespace
 
 struct jhq_index {
@@ -123,11 +132,10 @@ struct jhq_index {
     // gives the rotated query and the centroid dots
     DBuf<float> dqmat;
 
-    // search workspace (v14/search.cuh:24-46)
-    DBuf<float> wq, wqrot, wscores, wout_d;
-    DBuf<int32_t> wprobes, wgofs, wqtot, wout_i;
-    DBuf<unsigned long long> wpartial, wtopck, wdump;
-    DBuf<int32_t> wpslot;
+    // search workspaces; ws[1] and the lane streams serve pipelined batches
+    Workspace ws[2];
+    hipStream_t lane[2] = {};
+    hipEvent_t lane_ev[3] = {};  // fork, lane 0 done, lane 1 done
     float* h_q = nullptr;  // pinned staging
     float* h_d = nullptr;
     int32_t* h_i = nullptr;
@@ -144,7 +152,18 @@ struct jhq_index {
         if (h_i) (void)hipHostFree(h_i);
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
+        for (auto& e : lane_ev)
+            if (e) (void)hipEventDestroy(e);
+        for (auto& l : lane)
+            if (l) (void)hipStreamDestroy(l);
         if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    int ensure_lanes() {
+        if (lane[1]) return JHQ_OK;
+        for (auto& l : lane) JHQ_HIP(hipStreamCreate(&l));
+        for (auto& e : lane_ev) JHQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        return JHQ_OK;
     }
 
     int ensure_stream() {
@@ -279,19 +298,19 @@ int train_ivf(jhq_index* ix, const float* h_y, const float* d_y, int64_t n) {
     return upload_centroids(ix);
 }
 
-int ensure_workspace(jhq_index* ix, int ck, int k, int P, int max_segments) {
+int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_segments) {
     const size_t B = static_cast<size_t>(ix->batch_size);
-    JHQ_TRY(ix->wq.ensure(B * ix->d));
-    JHQ_TRY(ix->wqrot.ensure(B * ix->d));
-    JHQ_TRY(ix->wscores.ensure(B * ix->nlist));
-    JHQ_TRY(ix->wprobes.ensure(B * P));
-    JHQ_TRY(ix->wgofs.ensure(B * (P + 1)));
-    JHQ_TRY(ix->wqtot.ensure(B));
-    JHQ_TRY(ix->wpartial.ensure(static_cast<size_t>(max_segments) * ck));
-    JHQ_TRY(ix->wpslot.ensure(static_cast<size_t>(max_segments) * ck));
-    JHQ_TRY(ix->wtopck.ensure(B * ck));
-    JHQ_TRY(ix->wout_d.ensure(B * k));
-    JHQ_TRY(ix->wout_i.ensure(B * k));
+    JHQ_TRY(w.wq.ensure(B * ix->d));
+    JHQ_TRY(w.wqrot.ensure(B * ix->d));
+    JHQ_TRY(w.wscores.ensure(B * ix->nlist));
+    JHQ_TRY(w.wprobes.ensure(B * P));
+    JHQ_TRY(w.wgofs.ensure(B * (P + 1)));
+    JHQ_TRY(w.wqtot.ensure(B));
+    JHQ_TRY(w.wpartial.ensure(static_cast<size_t>(max_segments) * ck));
+    JHQ_TRY(w.wpslot.ensure(static_cast<size_t>(max_segments) * ck));
+    JHQ_TRY(w.wtopck.ensure(B * ck));
+    JHQ_TRY(w.wout_d.ensure(B * k));
+    JHQ_TRY(w.wout_i.ensure(B * k));
     return JHQ_OK;
 }
 
@@ -300,7 +319,7 @@ struct BatchPlan {
     jhq::ScanShape sh;
 };
 
-int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
+int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws = 1) {
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
     if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
@@ -308,47 +327,49 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp) {
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
-    JHQ_TRY(ensure_workspace(ix, bp->ck, k, bp->P, bp->sh.max_segments));
+    for (int i = 0; i < nws; i++)
+        JHQ_TRY(ensure_workspace(ix, ix->ws[i], bp->ck, k, bp->P, bp->sh.max_segments));
     if (bp->sh.dump) {
         // a query's candidates are at most the padded sizes of the P largest lists
         std::vector<int32_t> sz(ix->l_size);
         std::partial_sort(sz.begin(), sz.begin() + bp->P, sz.end(), std::greater<int32_t>());
         int64_t per_q = 0;
         for (int i = 0; i < bp->P; i++) per_q += (sz[i] + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
-        JHQ_TRY(ix->wdump.ensure(static_cast<size_t>(Bq) * std::max<int64_t>(per_q, 1)));
+        for (int i = 0; i < nws; i++)
+            JHQ_TRY(ix->ws[i].wdump.ensure(static_cast<size_t>(Bq) * std::max<int64_t>(per_q, 1)));
     }
     return JHQ_OK;
 }
 
 // One batch of Bq queries at d_q (device) through the whole pipeline
 // (the graph body of v14/search.cu:315-386).
-int run_batch(jhq_index* ix, const float* d_q, int Bq, int k, const BatchPlan& bp, float* d_out,
-              int32_t* d_ids, bool want_topck, hipStream_t s) {
+int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, const BatchPlan& bp,
+              float* d_out, int32_t* d_ids, bool want_topck, hipStream_t s) {
     const int d = ix->d;
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
     if (ix->dqmat.p) {
         // rotation and centroid dots in one tiled product
-        JHQ_HIP(jhq::mfma_q(d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, ix->wqrot.p, d,
-                            ix->wscores.p, ix->nlist, ix->dnorms.p, s));
+        JHQ_HIP(jhq::mfma_q(d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, w.wqrot.p, d,
+                            w.wscores.p, ix->nlist, ix->dnorms.p, s));
     } else {
         // d not a multiple of 64: the 16-row kernels
-        JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, ix->wqrot.p, d, s));
-        JHQ_HIP(jhq::mfma_nt_score(ix->wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
-                                   ix->wscores.p, ix->nlist, s));
+        JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, w.wqrot.p, d, s));
+        JHQ_HIP(jhq::mfma_nt_score(w.wqrot.p, d, ix->dcent.p, d, Bq, ix->nlist, d, ix->dnorms.p,
+                                   w.wscores.p, ix->nlist, s));
     }
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
-    JHQ_HIP(jhq::select_probes(ix->wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, ix->wprobes.p,
-                               ix->wgofs.p, ix->wqtot.p, s));
+    JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
+                               w.wgofs.p, w.wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
-    JHQ_HIP(jhq::scan_topck(ix->wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
-                            ix->wprobes.p, ix->wgofs.p, ix->wqtot.p, bp.P, ix->dldesc.p,
-                            ix->dcodes_t.p, bp.ck, bp.sh, ix->wpartial.p, ix->wpslot.p,
-                            ix->wdump.p, ix->dcodes_s.p, s));
+    JHQ_HIP(jhq::scan_topck(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
+                            w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
+                            ix->dcodes_t.p, bp.ck, bp.sh, w.wpartial.p, w.wpslot.p,
+                            w.wdump.p, ix->dcodes_s.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
-    JHQ_HIP(jhq::refine_topk(ix->wpartial.p, ix->wpslot.p, ix->wqtot.p, Bq, bp.sh, bp.ck, k,
-                             ix->wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
+    JHQ_HIP(jhq::refine_topk(w.wpartial.p, w.wpslot.p, w.wqtot.p, Bq, bp.sh, bp.ck, k,
+                             w.wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
                              ix->bpv, ix->dldesc.p, ix->nlist, ix->dres.p, ix->dcorr.p,
-                             ix->dlist_ids.p, d_out, d_ids, want_topck ? ix->wtopck.p : nullptr,
+                             ix->dlist_ids.p, d_out, d_ids, want_topck ? w.wtopck.p : nullptr,
                              s));
     if (ix->timing) {
         JHQ_HIP(hipEventRecord(ix->ev[kSteps], s));
@@ -386,29 +407,30 @@ int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, 
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
         const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
         std::memcpy(ix->h_q, q + q0 * d, static_cast<size_t>(Bq) * d * sizeof(float));
-        JHQ_HIP(hipMemcpyAsync(ix->wq.p, ix->h_q, static_cast<size_t>(Bq) * d * sizeof(float),
+        JHQ_HIP(hipMemcpyAsync(ix->ws[0].wq.p, ix->h_q, static_cast<size_t>(Bq) * d * sizeof(float),
                                hipMemcpyHostToDevice, ix->stream));
         const bool dbg = (q_rot || probes || topck_pos || topck_dist);
-        JHQ_TRY(run_batch(ix, ix->wq.p, Bq, k, bp, ix->wout_d.p, ix->wout_i.p, dbg, ix->stream));
-        JHQ_HIP(hipMemcpyAsync(ix->h_d, ix->wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
+        JHQ_TRY(run_batch(ix, ix->ws[0], ix->ws[0].wq.p, Bq, k, bp, ix->ws[0].wout_d.p,
+                          ix->ws[0].wout_i.p, dbg, ix->stream));
+        JHQ_HIP(hipMemcpyAsync(ix->h_d, ix->ws[0].wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
                                hipMemcpyDeviceToHost, ix->stream));
-        JHQ_HIP(hipMemcpyAsync(ix->h_i, ix->wout_i.p, static_cast<size_t>(Bq) * k * sizeof(int32_t),
+        JHQ_HIP(hipMemcpyAsync(ix->h_i, ix->ws[0].wout_i.p, static_cast<size_t>(Bq) * k * sizeof(int32_t),
                                hipMemcpyDeviceToHost, ix->stream));
         JHQ_HIP(hipStreamSynchronize(ix->stream));
         std::memcpy(dists + q0 * k, ix->h_d, static_cast<size_t>(Bq) * k * sizeof(float));
         std::memcpy(ids + q0 * k, ix->h_i, static_cast<size_t>(Bq) * k * sizeof(int32_t));
         if (q_rot) {
-            JHQ_HIP(hipMemcpy(q_rot + q0 * d, ix->wqrot.p, static_cast<size_t>(Bq) * d * sizeof(float),
+            JHQ_HIP(hipMemcpy(q_rot + q0 * d, ix->ws[0].wqrot.p, static_cast<size_t>(Bq) * d * sizeof(float),
                               hipMemcpyDeviceToHost));
         }
         if (probes) {
-            JHQ_HIP(hipMemcpy(probes + q0 * bp.P, ix->wprobes.p,
+            JHQ_HIP(hipMemcpy(probes + q0 * bp.P, ix->ws[0].wprobes.p,
                               static_cast<size_t>(Bq) * bp.P * sizeof(int32_t),
                               hipMemcpyDeviceToHost));
         }
         if (topck_pos || topck_dist) {
             tk.resize(static_cast<size_t>(Bq) * bp.ck);
-            JHQ_HIP(hipMemcpy(tk.data(), ix->wtopck.p, tk.size() * sizeof(unsigned long long),
+            JHQ_HIP(hipMemcpy(tk.data(), ix->ws[0].wtopck.p, tk.size() * sizeof(unsigned long long),
                               hipMemcpyDeviceToHost));
             for (size_t i = 0; i < tk.size(); i++) {
                 const unsigned long long kk = tk[i];
@@ -965,12 +987,33 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     if (!d_q || !d_dists || !d_ids) return fail(JHQ_EINVAL, "null argument");
     if (nq == 0) return JHQ_OK;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ix->stream;
+    const int Bmax = ix->batch_size;
+    // several batches: alternate two workspaces on two streams forked from s
+    // and joined back into it (step timing keeps one stream)
+    const bool pipe = nq > Bmax && !ix->timing;
     BatchPlan bp;
-    JHQ_TRY(plan_batch(ix, ix->batch_size, k, &bp));
-    for (int64_t q0 = 0; q0 < nq; q0 += ix->batch_size) {
-        const int Bq = static_cast<int>(std::min<int64_t>(ix->batch_size, nq - q0));
-        JHQ_TRY(run_batch(ix, d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k, d_ids + q0 * k, false,
-                          s));
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, pipe ? 2 : 1));
+    if (!pipe) {
+        for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
+            const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
+            JHQ_TRY(run_batch(ix, ix->ws[0], d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k,
+                              d_ids + q0 * k, false, s));
+        }
+        return JHQ_OK;
+    }
+    JHQ_TRY(ix->ensure_lanes());
+    JHQ_HIP(hipEventRecord(ix->lane_ev[0], s));
+    for (int l = 0; l < 2; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
+    int64_t bi = 0;
+    for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
+        const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
+        const int l = static_cast<int>(bi & 1);
+        JHQ_TRY(run_batch(ix, ix->ws[l], d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k,
+                          d_ids + q0 * k, false, ix->lane[l]));
+    }
+    for (int l = 0; l < 2; l++) {
+        JHQ_HIP(hipEventRecord(ix->lane_ev[1 + l], ix->lane[l]));
+        JHQ_HIP(hipStreamWaitEvent(s, ix->lane_ev[1 + l], 0));
     }
     return JHQ_OK;
 }

@@ -673,7 +673,7 @@ mfma_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
 // Requires K % (64 * S) == 0, lda and ldb multiples of 4, aligned A and Bm.
 // ---------------------------------------------------------------------------
 template <int S>
-__global__ void __launch_bounds__(64 * S)
+__global__ void __launch_bounds__(64 * S, 4)  // 4 waves per SIMD: two 8-wave groups per CU
 mfma_q_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
               int64_t ldb, int nb, int N, int K, int nrot, float* __restrict__ C1, int64_t ld1,
               float* __restrict__ C2, int64_t ld2, const float* __restrict__ norms) {
@@ -3095,6 +3095,80 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     int chk = (d + 15) / 16;
     if (vec) chk = (chk + dpc - 1) / dpc * dpc;
     else chk += chk & 1;
+    // the residual distance of one 16-byte chunk (dpc dimensions from jb)
+    auto chunk = [&](const uint4& w, int jb, float& sres) {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        if (Br == 4) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+                for (int nb = 0; nb < 8; nb++) {
+                    const int jj = jb + q4 * 8 + nb;
+                    const float df = sq[jj + (jj >> 5)] - rc[cbo(jj) + ((ww[q4] >> (4 * nb)) & 0x0Fu)];
+                    sres = sres + df * df;
+                }
+        } else {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++) {
+                    const int jj = jb + q4 * 4 + nb;
+                    const float df = sq[jj + (jj >> 5)] - rc[cbo(jj) + ((ww[q4] >> (8 * nb)) & 0xFFu)];
+                    sres = sres + df * df;
+                }
+        }
+    };
+    if (vec && chk / dpc <= 4) {
+        // at most 4 chunks per lane: the next round's chunks, correction and
+        // id are loaded while this round is summed
+        const int j0 = l16 * chk, j1 = (j0 + chk) < d ? (j0 + chk) : d;
+        const int nch = j1 > j0 ? (j1 - j0) / dpc : 0;
+        uint4 wc[4], wn[4];
+        float corr_c = 0.0f, corr_n = 0.0f;
+        int id_c = 0, id_n = 0;
+        auto fetch = [&](int base, uint4 (&w)[4], float& corr, int& id) {
+            const int c = base + grp;
+            if (c < ksel) {
+                const int pos = cpos[c];
+                const uint4* rp = (const uint4*)(list_res + (int64_t)pos * bpv + (j0 * Br) / 8);
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (u < nch) w[u] = rp[u];
+                if (l16 == 0) {
+                    corr = list_corr[pos];
+                    id = list_ids[pos];
+                }
+            }
+        };
+        fetch(0, wc, corr_c, id_c);
+        for (int base = 0; base < ksel; base += NG) {
+            if (base + NG < ksel) fetch(base + NG, wn, corr_n, id_n);
+            const int c = base + grp;
+            const bool valid = c < ksel;
+            float sres = 0.0f;
+            // j0 opaque per round: the LDS addresses of the 4 chunks' dimensions
+            // are formed here instead of being hoisted out of the loop
+            int jv = j0;
+            asm volatile("" : "+v"(jv));
+            if (valid) {
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (u < nch) chunk(wc[u], jv + u * dpc, sres);
+            }
+            sres = sres + __shfl_xor(sres, 8);
+            sres = sres + __shfl_xor(sres, 4);
+            sres = sres + __shfl_xor(sres, 2);
+            sres = sres + __shfl_xor(sres, 1);
+            if (valid && l16 == 0) {
+                const float comp = (cprim[c] + sres) + corr_c;
+                fkeys[c] = ((unsigned long long)f2ord(comp) << 32) | (uint32_t)id_c;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) wc[u] = wn[u];
+            corr_c = corr_n;
+            id_c = id_n;
+        }
+    } else
     for (int base = 0; base < ksel; base += NG) {
         const int c = base + grp;
         const bool valid = c < ksel;
@@ -3116,27 +3190,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
                         if (c4 + u >= nch) break;
-                        const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-                        const int jb = j0 + (c4 + u) * dpc;
-                        if (Br == 4) {
-#pragma unroll
-                            for (int q4 = 0; q4 < 4; q4++)
-#pragma unroll
-                                for (int nb = 0; nb < 8; nb++) {
-                                    const int jj = jb + q4 * 8 + nb;
-                                    const float df = sq[jj + (jj >> 5)] - rc[cbo(jj) + ((ww[q4] >> (4 * nb)) & 0x0Fu)];
-                                    sres = sres + df * df;
-                                }
-                        } else {
-#pragma unroll
-                            for (int q4 = 0; q4 < 4; q4++)
-#pragma unroll
-                                for (int nb = 0; nb < 4; nb++) {
-                                    const int jj = jb + q4 * 4 + nb;
-                                    const float df = sq[jj + (jj >> 5)] - rc[cbo(jj) + ((ww[q4] >> (8 * nb)) & 0xFFu)];
-                                    sres = sres + df * df;
-                                }
-                        }
+                        chunk(wv[u], j0 + (c4 + u) * dpc, sres);
                     }
                 }
             } else if (Br == 4) {

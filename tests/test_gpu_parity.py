@@ -176,6 +176,34 @@ def test_search_device_matches_host(gpu, case):
     assert np.array_equal(_bits(od.cpu().numpy()), _bits(d1))
 
 
+@pytest.mark.parametrize("name", ["ds8_k1d2", "m64_ds4_ck100", "k100_ck400"])
+def test_search_device_pipelined_batches(gpu, name):
+    """A device search over many batches (two workspaces on two streams,
+    joined into the caller's stream) returns what one call per batch and the
+    host search return, including a ragged last batch."""
+    import torch
+    case = CASES[IDS.index(name)]
+    g, o, base, q, k = _build(case)
+    batch = case[-1]
+    qq = np.ascontiguousarray(np.tile(q, (1 + 5 * batch // q.shape[0], 1))[:5 * batch + 3])
+    d1, i1 = g.search(qq, k)
+    qt = torch.from_numpy(qq).to(gpu)
+    od = torch.full((qq.shape[0], k), -1.0, dtype=torch.float32, device=gpu)
+    oi = torch.full((qq.shape[0], k), -2, dtype=torch.int32, device=gpu)
+    s = torch.cuda.current_stream()
+    for rep in range(2):
+        g.search_device(qt, k, od, oi, stream=s)
+        got_i, got_d = oi.cpu().numpy(), od.cpu().numpy()  # ordered after the join
+        assert np.array_equal(got_i, i1), rep
+        assert np.array_equal(_bits(got_d), _bits(d1)), rep
+    od2 = torch.empty_like(od)
+    oi2 = torch.empty_like(oi)
+    for b0 in range(0, qq.shape[0], batch):
+        g.search_device(qt[b0:b0 + batch], k, od2[b0:b0 + batch], oi2[b0:b0 + batch], stream=s)
+    assert np.array_equal(oi2.cpu().numpy(), i1)
+    assert np.array_equal(_bits(od2.cpu().numpy()), _bits(d1))
+
+
 def test_k_larger_than_candidates(gpu):
     """Unfilled slots are (+inf, -1) like v14/search.cu:284-286."""
     g, o, base, q, _ = _build(CASES[3])
