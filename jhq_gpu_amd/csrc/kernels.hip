@@ -2313,9 +2313,16 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         // period's reads first and hold all of them in registers).
         constexpr int C = MW / 8, D = C < JHQ_SKEW_D ? C : JHQ_SKEW_D;
         constexpr int GS = JHQ_SKEW_GS, LA = JHQ_SKEW_LA, NG = M / GS;
-        uint32_t wr[C + D][8], pw[8];
+        static_assert(LA <= 3 && LA * GS <= 15, "reads in flight exceed the LDS counter");
+        uint32_t wr[C + D][8], pw[8], tbm[8];
+        // tbm[j]: the bytes of word j (steps 4j .. 4j+3) that are tail steps
+        // (t < s) of this lane
 #pragma unroll
-        for (int j = 0; j < 8; j++) pw[j] = 0u;
+        for (int j = 0; j < 8; j++) {
+            pw[j] = 0u;
+            const int nt = min(max(s - 4 * j, 0), 4);
+            tbm[j] = nt == 4 ? ~0u : (1u << (8 * nt)) - 1u;
+        }
         float acc = 0.0f;
         uint32_t ptag = 0u;
         bool pvalid = false;
@@ -2402,7 +2409,9 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                     const int tt = GS * g + i, c = tt >> 5, j = (tt >> 2) & 7, e = tt & 3;
                     if (c == 0) {
                         const bool tail = __builtin_amdgcn_inverse_ballot_w64(rep2(tseed << tt));
-                        uint32_t v = __builtin_amdgcn_ubfe(tail ? pw[j] : wr[0][j], 8 * e, 8);
+                        // the word's tail bytes from the previous row, the rest from this one
+                        const uint32_t w = (pw[j] & tbm[j]) | (wr[0][j] & ~tbm[j]);
+                        uint32_t v = __builtin_amdgcn_ubfe(w, 8 * e, 8);
                         asm("" : "+v"(v));
                         dst[i] = *(const __attribute__((address_space(3))) float*)(
                             (tail ? pt : ph) + v * (4 * M) + 4 * tt);
@@ -2440,6 +2449,16 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                     else if (more) load_chunk(nslot, c - C, wr[c]);
                 }
                 if (g + LA < NG) fetch(g + LA, vq[(g + LA) % (LA + 1)]);
+                // one wait for the group's reads: the reads of the next groups
+                // (at most LA * GS) may still be in flight
+                __builtin_amdgcn_sched_barrier(0);
+                switch (g + LA < NG ? LA : NG - 1 - g) {
+                    case 3: __builtin_amdgcn_s_waitcnt(0xc07f | (3 * GS) << 8); break;
+                    case 2: __builtin_amdgcn_s_waitcnt(0xc07f | (2 * GS) << 8); break;
+                    case 1: __builtin_amdgcn_s_waitcnt(0xc07f | (1 * GS) << 8); break;
+                    default: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 accum(g, vq[g % (LA + 1)]);
                 asm volatile("" : "+v"(acc));
                 __builtin_amdgcn_sched_barrier(0);
