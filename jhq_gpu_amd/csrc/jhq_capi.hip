@@ -136,10 +136,10 @@ struct jhq_index {
     Workspace ws[2];
     hipStream_t lane[2] = {};
     hipEvent_t lane_ev[3] = {};  // fork, lane 0 done, lane 1 done
-    float* h_q = nullptr;  // pinned staging
-    float* h_d = nullptr;
-    int32_t* h_i = nullptr;
-    size_t h_q_n = 0, h_d_n = 0, h_i_n = 0;
+    float* h_q[2] = {};  // pinned staging, one set per lane
+    float* h_d[2] = {};
+    int32_t* h_i[2] = {};
+    size_t h_q_n[2] = {}, h_d_n[2] = {}, h_i_n[2] = {};
 
     bool timing = false;
     hipEvent_t ev[kSteps + 1] = {};
@@ -147,9 +147,11 @@ struct jhq_index {
     int64_t tbatches = 0;
 
     ~jhq_index() {
-        if (h_q) (void)hipHostFree(h_q);
-        if (h_d) (void)hipHostFree(h_d);
-        if (h_i) (void)hipHostFree(h_i);
+        for (int l = 0; l < 2; l++) {
+            if (h_q[l]) (void)hipHostFree(h_q[l]);
+            if (h_d[l]) (void)hipHostFree(h_d[l]);
+            if (h_i[l]) (void)hipHostFree(h_i[l]);
+        }
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
         for (auto& e : lane_ev)
@@ -392,33 +394,89 @@ int check_searchable(jhq_index* ix, int64_t nq, int k) {
     return JHQ_OK;
 }
 
+int ensure_host_staging(jhq_index* ix, int l, int Bmax, int k) {
+    JHQ_TRY(ensure_pinned(ix->h_q[l], ix->h_q_n[l], static_cast<size_t>(Bmax) * ix->d));
+    JHQ_TRY(ensure_pinned(ix->h_d[l], ix->h_d_n[l], static_cast<size_t>(Bmax) * k));
+    JHQ_TRY(ensure_pinned(ix->h_i[l], ix->h_i_n[l], static_cast<size_t>(Bmax) * k));
+    return JHQ_OK;
+}
+
+// Host arrays over several batches: the batches alternate between two lanes
+// (workspace, pinned staging, stream).  While one lane's batch runs, the host
+// copies the other lane's finished results out and its next queries in.
+int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, float* dists,
+                          int32_t* ids) {
+    const int d = ix->d;
+    const int Bmax = ix->batch_size;
+    BatchPlan bp;
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, 2));
+    JHQ_TRY(ix->ensure_lanes());
+    for (int l = 0; l < 2; l++) JHQ_TRY(ensure_host_staging(ix, l, Bmax, k));
+    JHQ_HIP(hipEventRecord(ix->lane_ev[0], ix->stream));
+    for (int l = 0; l < 2; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
+    int64_t pend_q0[2] = {-1, -1};
+    int pend_b[2] = {0, 0};
+    auto collect = [&](int l) -> int {
+        if (pend_q0[l] < 0) return JHQ_OK;
+        JHQ_HIP(hipEventSynchronize(ix->lane_ev[1 + l]));
+        std::memcpy(dists + pend_q0[l] * k, ix->h_d[l], static_cast<size_t>(pend_b[l]) * k * sizeof(float));
+        std::memcpy(ids + pend_q0[l] * k, ix->h_i[l], static_cast<size_t>(pend_b[l]) * k * sizeof(int32_t));
+        pend_q0[l] = -1;
+        return JHQ_OK;
+    };
+    int64_t bi = 0;
+    for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
+        const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
+        const int l = static_cast<int>(bi & 1);
+        Workspace& w = ix->ws[l];
+        hipStream_t st = ix->lane[l];
+        JHQ_TRY(collect(l));  // the lane's previous batch is done: its buffers are free
+        std::memcpy(ix->h_q[l], q + q0 * d, static_cast<size_t>(Bq) * d * sizeof(float));
+        JHQ_HIP(hipMemcpyAsync(w.wq.p, ix->h_q[l], static_cast<size_t>(Bq) * d * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+        JHQ_TRY(run_batch(ix, w, w.wq.p, Bq, k, bp, w.wout_d.p, w.wout_i.p, false, st));
+        JHQ_HIP(hipMemcpyAsync(ix->h_d[l], w.wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
+                               hipMemcpyDeviceToHost, st));
+        JHQ_HIP(hipMemcpyAsync(ix->h_i[l], w.wout_i.p, static_cast<size_t>(Bq) * k * sizeof(int32_t),
+                               hipMemcpyDeviceToHost, st));
+        JHQ_HIP(hipEventRecord(ix->lane_ev[1 + l], st));
+        pend_q0[l] = q0;
+        pend_b[l] = Bq;
+    }
+    // the older pending batch first
+    const int first = static_cast<int>(bi & 1);
+    JHQ_TRY(collect(first));
+    JHQ_TRY(collect(first ^ 1));
+    for (int l = 0; l < 2; l++) JHQ_HIP(hipStreamWaitEvent(ix->stream, ix->lane_ev[1 + l], 0));
+    return JHQ_OK;
+}
+
 int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, int32_t* ids,
                 float* q_rot, int32_t* probes, int32_t* topck_pos, float* topck_dist) {
     JHQ_TRY(check_searchable(ix, nq, k));
     if (nq == 0) return JHQ_OK;
     const int d = ix->d;
     const int Bmax = ix->batch_size;
+    const bool dbg = (q_rot || probes || topck_pos || topck_dist);
+    if (!dbg && !ix->timing && nq > Bmax) return search_host_pipelined(ix, q, nq, k, dists, ids);
     BatchPlan bp;
     JHQ_TRY(plan_batch(ix, Bmax, k, &bp));
-    JHQ_TRY(ensure_pinned(ix->h_q, ix->h_q_n, static_cast<size_t>(Bmax) * d));
-    JHQ_TRY(ensure_pinned(ix->h_d, ix->h_d_n, static_cast<size_t>(Bmax) * k));
-    JHQ_TRY(ensure_pinned(ix->h_i, ix->h_i_n, static_cast<size_t>(Bmax) * k));
+    JHQ_TRY(ensure_host_staging(ix, 0, Bmax, k));
     std::vector<unsigned long long> tk;
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
         const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
-        std::memcpy(ix->h_q, q + q0 * d, static_cast<size_t>(Bq) * d * sizeof(float));
-        JHQ_HIP(hipMemcpyAsync(ix->ws[0].wq.p, ix->h_q, static_cast<size_t>(Bq) * d * sizeof(float),
+        std::memcpy(ix->h_q[0], q + q0 * d, static_cast<size_t>(Bq) * d * sizeof(float));
+        JHQ_HIP(hipMemcpyAsync(ix->ws[0].wq.p, ix->h_q[0], static_cast<size_t>(Bq) * d * sizeof(float),
                                hipMemcpyHostToDevice, ix->stream));
-        const bool dbg = (q_rot || probes || topck_pos || topck_dist);
         JHQ_TRY(run_batch(ix, ix->ws[0], ix->ws[0].wq.p, Bq, k, bp, ix->ws[0].wout_d.p,
                           ix->ws[0].wout_i.p, dbg, ix->stream));
-        JHQ_HIP(hipMemcpyAsync(ix->h_d, ix->ws[0].wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
+        JHQ_HIP(hipMemcpyAsync(ix->h_d[0], ix->ws[0].wout_d.p, static_cast<size_t>(Bq) * k * sizeof(float),
                                hipMemcpyDeviceToHost, ix->stream));
-        JHQ_HIP(hipMemcpyAsync(ix->h_i, ix->ws[0].wout_i.p, static_cast<size_t>(Bq) * k * sizeof(int32_t),
+        JHQ_HIP(hipMemcpyAsync(ix->h_i[0], ix->ws[0].wout_i.p, static_cast<size_t>(Bq) * k * sizeof(int32_t),
                                hipMemcpyDeviceToHost, ix->stream));
         JHQ_HIP(hipStreamSynchronize(ix->stream));
-        std::memcpy(dists + q0 * k, ix->h_d, static_cast<size_t>(Bq) * k * sizeof(float));
-        std::memcpy(ids + q0 * k, ix->h_i, static_cast<size_t>(Bq) * k * sizeof(int32_t));
+        std::memcpy(dists + q0 * k, ix->h_d[0], static_cast<size_t>(Bq) * k * sizeof(float));
+        std::memcpy(ids + q0 * k, ix->h_i[0], static_cast<size_t>(Bq) * k * sizeof(int32_t));
         if (q_rot) {
             JHQ_HIP(hipMemcpy(q_rot + q0 * d, ix->ws[0].wqrot.p, static_cast<size_t>(Bq) * d * sizeof(float),
                               hipMemcpyDeviceToHost));
