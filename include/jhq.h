@@ -114,7 +114,8 @@ int jhq_append_ex(jhq_index* idx, const void* x, int dtype, int64_t n);
 
 /* JHQGpuIndex::search(h_q, nq, k, h_dists, h_labels) —
  * v14/jhq_gpu_index.cu:535-552 -> search_gpu, v14/search.cu:388-445.
- * q host [nq x d]; dists/ids host [nq x k]. */
+ * q host [nq x d]; dists/ids host [nq x k].  Over several batches the
+ * host copies of one batch overlap the kernels of the next. */
 int jhq_search(jhq_index* idx, const float* q, int64_t nq, int k,
                float* dists, int32_t* ids);
 
@@ -124,7 +125,10 @@ int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k,
 
 /* Same pipeline with queries and results already in device memory
  * (the reference's graph body v14/search.cu:315-386 without the host
- * copies around it).  Returns after the work is enqueued on `stream`. */
+ * copies around it).  Returns after the work is enqueued on `stream`.
+ * More than batch_size queries: the batches alternate between two internal
+ * streams forked from `stream` and joined back into it, so the call is
+ * stream-ordered on `stream` like a single launch. */
 int jhq_search_device(jhq_index* idx, const float* d_q, int64_t nq, int k,
                       float* d_dists, int32_t* d_ids, void* stream);
 
