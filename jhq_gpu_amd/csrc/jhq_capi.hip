@@ -125,7 +125,12 @@ struct jhq_index {
     DBuf<int4> dldesc;
     DBuf<int32_t> dlist_ids;
     DBuf<uint8_t> dcodes_t, dres;
-    DBuf<uint8_t> dcodes_s;  // lane-skewed rows of the primary codes (skew scan)
+    // lane-skewed rows of the primary codes, written when a search plan takes
+    // the skewed scan; per list, the block start and row count they hold
+    DBuf<uint8_t> dcodes_s;
+    bool skew_stale = true;
+    std::vector<int32_t> skew_start, skew_rows;
+    DBuf<int32_t> dskew_from;
     DBuf<float> dcorr;
 
     // query GEMM operand [Pi ; centroids * Pi] ((d + nlist) x d): one product
@@ -316,6 +321,40 @@ int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_
     return JHQ_OK;
 }
 
+bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128; }
+
+// Brings the skewed copy up to date: rows appended since the last refresh,
+// and every row of a list whose block moved (or of every list when the copy
+// had to grow).  Synchronous, so any stream may read the copy afterwards.
+int refresh_skew(jhq_index* ix) {
+    if (!ix->skew_stale) return JHQ_OK;
+    const int nl = ix->nlist;
+    const size_t need = static_cast<size_t>(std::max<int64_t>(ix->pool_cap, 1)) * ix->M;
+    if (ix->dcodes_s.n < need || static_cast<int>(ix->skew_start.size()) != nl) {
+        if (ix->dcodes_s.n < need) JHQ_TRY(ix->dcodes_s.alloc(need));
+        ix->skew_start.assign(nl, -1);
+        ix->skew_rows.assign(nl, 0);
+    }
+    std::vector<int32_t> from(nl);
+    int max_rows = 0;
+    for (int l = 0; l < nl; l++) {
+        from[l] = ix->skew_start[l] == ix->l_start[l] ? std::min(ix->skew_rows[l], ix->l_size[l]) : 0;
+        max_rows = std::max(max_rows, ix->l_size[l] - from[l]);
+    }
+    if (max_rows > 0) {
+        JHQ_TRY(ix->dskew_from.ensure(nl));
+        JHQ_HIP(hipMemcpyAsync(ix->dskew_from.p, from.data(), nl * sizeof(int32_t),
+                               hipMemcpyHostToDevice, ix->stream));
+        JHQ_HIP(jhq::skew_codes(ix->dldesc.p, ix->dskew_from.p, nl, max_rows, ix->dcodes_t.p, ix->M,
+                                ix->dcodes_s.p, ix->stream));
+        JHQ_HIP(hipStreamSynchronize(ix->stream));
+    }
+    ix->skew_start = ix->l_start;
+    ix->skew_rows = ix->l_size;
+    ix->skew_stale = false;
+    return JHQ_OK;
+}
+
 struct BatchPlan {
     int ck, P;
     jhq::ScanShape sh;
@@ -325,10 +364,11 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws = 1) {
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
     if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
-                        ix->dcodes_s.p != nullptr))
+                        skew_eligible(ix)))
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
+    if (bp->sh.skew) JHQ_TRY(refresh_skew(ix));
     for (int i = 0; i < nws; i++)
         JHQ_TRY(ensure_workspace(ix, ix->ws[i], bp->ck, k, bp->P, bp->sh.max_segments));
     if (bp->sh.dump) {
@@ -720,20 +760,6 @@ int upload_ldesc(jhq_index* ix) {
 }
 
 // The skew scan's copy of the codes (M a multiple of 32, at most 128).
-bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128; }
-
-int rebuild_skew(jhq_index* ix) {
-    if (!skew_eligible(ix) || ix->pool_cap <= 0) return JHQ_OK;
-    const size_t need = static_cast<size_t>(ix->pool_cap) * ix->M;
-    if (ix->dcodes_s.n < need) JHQ_TRY(ix->dcodes_s.alloc(need));
-    int max_cap = 0;
-    for (int l = 0; l < ix->nlist; l++) max_cap = std::max(max_cap, ix->l_cap[l]);
-    JHQ_HIP(jhq::skew_codes(ix->dldesc.p, ix->nlist, max_cap, ix->dcodes_t.p, ix->M,
-                            ix->dcodes_s.p, ix->stream));
-    JHQ_HIP(hipStreamSynchronize(ix->stream));
-    return JHQ_OK;
-}
-
 // Grows the device pool to at least `need` slots, keeping every block where
 // it is (the old pool is copied to the front of the new one).
 int grow_pool(jhq_index* ix, int64_t need) {
@@ -830,6 +856,7 @@ int repack_pool(jhq_index* ix, const std::vector<int64_t>& need) {
 // left for such moves every list is re-packed into a new pool instead.
 int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_fit) {
     JHQ_TRY(ix->ensure_stream());
+    ix->skew_stale = true;
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
     hipStream_t s = ix->stream;
     const int64_t id_base = ix->ntotal;
@@ -971,7 +998,6 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         for (int l = 0; l < nlist; l++) ix->l_size[l] += rank[l];
     }
     JHQ_TRY(upload_ldesc(ix));
-    JHQ_TRY(rebuild_skew(ix));
     ix->ntotal += n;
     return JHQ_OK;
 }
@@ -1360,7 +1386,6 @@ int jhq_load(const char* path, jhq_index** out) {
             return done(fail(JHQ_EDEVICE, "index upload failed"));
     }
     rc = upload_ldesc(ix);
-    if (rc == JHQ_OK) rc = rebuild_skew(ix);
     if (rc != JHQ_OK) return done(rc);
     ix->ntotal = n;
     ix->added = ad != 0;
@@ -1374,7 +1399,7 @@ int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list) {
     const int P = std::min(idx->nprobe, idx->nlist);
     jhq::ScanShape sh{};
     if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh,
-                        idx->dcodes_s.p != nullptr))
+                        skew_eligible(idx)))
         return fail(JHQ_EINVAL, "no scan plan fits in LDS");
     if (scan_kind) *scan_kind = sh.dump ? 2 : sh.skew ? 3 : sh.wave ? 1 : 0;
     if (short_list) *short_list = ck;

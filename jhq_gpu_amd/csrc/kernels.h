@@ -64,10 +64,11 @@ hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int 
 // Scatter: new vector s goes to list slist[s] at index sidx[s]; its id is
 // id_base + order[s], order[s] indexing the per-vector inputs pc/rc/co.
 // Lane-skewed rows of the primary codes (row[t] = code[(t - i mod 32) mod M]
-// for candidate i of each list, at skew[(start + i) * M]); every capacity
-// slot of every list, max_cap >= the largest capacity.  M % 4 == 0.
-hipError_t skew_codes(const int4* ldesc, int nlist, int max_cap, const uint8_t* codes_t, int M,
-                      uint8_t* skew, hipStream_t s);
+// for candidate i of each list, at skew[(start + i) * M]); rows from[l] ..
+// size-1 of list l (from: device [nlist]), max_rows >= the largest
+// size - from[l].  M % 4 == 0.
+hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
+                      const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s);
 hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
                          int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
                          const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,

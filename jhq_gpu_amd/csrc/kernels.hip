@@ -1028,14 +1028,16 @@ __global__ void scatter_kernel(const int32_t* __restrict__ order, const int32_t*
 // (pool slot start + i) gets a row of M bytes at skew[(start + i) * M]:
 //   row[t] = code[(t - (i mod 32)) mod M]
 // so that at step t the lane holding i reads subspace t - (i mod 32) from
-// row position t.  One thread per (list, candidate); the codes are read from
-// the code-major blocks (codes_t[start * M + m * cap + i]).
+// row position t.  Rows from[l] .. size-1 of list l are written (the rows
+// before from[l] are current); one thread per row, the codes read from the
+// code-major blocks (codes_t[start * M + m * cap + i]).
 // ---------------------------------------------------------------------------
-__global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t,
-                                  int M, uint8_t* __restrict__ skew) {
+__global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const int32_t* __restrict__ from,
+                                  const uint8_t* __restrict__ codes_t, int M,
+                                  uint8_t* __restrict__ skew) {
     const int4 L = ldesc[blockIdx.x];
-    const int i = blockIdx.y * blockDim.x + threadIdx.x;
-    if (i >= L.y) return;  // capacity: padding rows are written too
+    const int i = from[blockIdx.x] + blockIdx.y * blockDim.x + threadIdx.x;
+    if (i >= L.z) return;
     const uint8_t* src = codes_t + (int64_t)L.x * M + i;
     uint8_t* dst = skew + ((int64_t)L.x + i) * M;
     const int s = i & 31;
@@ -1051,12 +1053,12 @@ __global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const uint8_t*
     }
 }
 
-hipError_t skew_codes(const int4* ldesc, int nlist, int max_cap, const uint8_t* codes_t, int M,
-                      uint8_t* skew, hipStream_t s) {
-    if (nlist <= 0 || max_cap <= 0) return hipSuccess;
-    if (M % 4 != 0 || (max_cap + 255) / 256 > 65535) return hipErrorInvalidValue;
-    dim3 grid(nlist, (max_cap + 255) / 256);
-    hipLaunchKernelGGL(skew_codes_kernel, grid, dim3(256), 0, s, ldesc, codes_t, M, skew);
+hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
+                      const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s) {
+    if (nlist <= 0 || max_rows <= 0) return hipSuccess;
+    if (M % 4 != 0 || (max_rows + 255) / 256 > 65535) return hipErrorInvalidValue;
+    dim3 grid(nlist, (max_rows + 255) / 256);
+    hipLaunchKernelGGL(skew_codes_kernel, grid, dim3(256), 0, s, ldesc, from, codes_t, M, skew);
     return hipGetLastError();
 }
 

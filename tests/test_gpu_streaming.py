@@ -63,6 +63,32 @@ def test_streaming_append_equals_one_shot(gpu, per_sub):
     assert cap <= 1.6 * upto + 20 * nlist
 
 
+@pytest.mark.parametrize("d,M", [(128, 32), (256, 64)], ids=["m32", "m64"])
+def test_streaming_append_skewed_scan(gpu, d, M):
+    """M a multiple of 32: the search takes the skewed scan, whose row copy
+    of the codes is brought up to date before each search (appended rows,
+    moved lists, a re-packed pool)."""
+    nlist, nprobe, k = 16, 5, 10
+    base, q = queries_and_base(6000, 24, d, 40, seed=733 + M)
+    g, o = _pair(d, M, nlist, nprobe, 0)
+    g.train(base[:2000])
+    o.train(base[:2000])
+    assert g.scan_plan(k)[0] == "scan_skew_kernel"
+    g.add(base[:1000])
+    upto = 1000
+    o.add(base[:upto])
+    _stagewise(g, o, q, k)
+    for n in (3, 600, 1, 2500, 31, 1865):
+        g.append(base[upto:upto + n])
+        upto += n
+        o.add(base[:upto])
+        _lists_equal(g, o)
+        _stagewise(g, o, q, k)
+        d1, i1 = g.search(q, k)
+        d2, i2 = g.search(q, k)  # no change between: the copy is current
+        assert np.array_equal(i1, i2) and np.array_equal(_bits(d1), _bits(d2))
+
+
 def test_append_from_empty_and_add_guard(gpu):
     d, M, nlist, nprobe, k = 32, 8, 8, 3, 5
     base, q = queries_and_base(3000, 12, d, 16, seed=77)
