@@ -2825,22 +2825,25 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     const int J = need <= 128 ? 2 : need <= 192 ? 3 : need <= 256 ? 4 : need <= 384 ? 6
                 : need <= 512 ? 8 : 0;
     out->dump = 0;
+    // lanes skewed across subspaces (M a multiple of 32, at most 128), short
+    // lists up to 128.  Longer ones take the dump path below: with ck = 400
+    // (config 5) the skewed scan's 512-key wave buffers prune too often and
+    // it is slower (1124 against 872 us per batch of 128)
+    if (J && J <= 3 && skew && M % 32 == 0 && M <= 128) {
+        size_t region = 0;
+        const size_t lds = scan_wave_lds(kSkewNT, M, d, P, ck, K1D, B, J, &region) +
+                           (size_t)(2 * P + 1) * 4;
+        if (lds <= (size_t)kLdsBytes - 1024) {
+            out->wave = J;
+            out->skew = M / 4;
+            out->nt = kSkewNT;
+            out->lds = (int)lds;
+            out->region = (int)region;
+            return true;
+        }
+    }
     // short lists up to 128: selection inside the scan, 16 waves per workgroup
     if (J && J <= 3) {
-        // lanes skewed across subspaces: M a multiple of 32, at most 128
-        if (skew && M % 32 == 0 && M <= 128) {
-            size_t region = 0;
-            const size_t lds = scan_wave_lds(kSkewNT, M, d, P, ck, K1D, B, J, &region) +
-                               (size_t)(2 * P + 1) * 4;
-            if (lds <= (size_t)kLdsBytes - 1024) {
-                out->wave = J;
-                out->skew = M / 4;
-                out->nt = kSkewNT;
-                out->lds = (int)lds;
-                out->region = (int)region;
-                return true;
-            }
-        }
         size_t region = 0;
         const size_t lds = scan_wave_lds(kScanNT, M, d, P, ck, K1D, B, J, &region);
         if (lds <= (size_t)kLdsBytes - 1024) {

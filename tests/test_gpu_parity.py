@@ -40,6 +40,8 @@ CASES = [
     # M a multiple of 32: lanes skewed across subspaces (K1D=4; ck=100)
     ("m64_ds4_ck100", 256, 64, 8, 4, 16, 5, 10.0, 3000, 20, 10, 32),
     ("m96_d768", 768, 96, 8, 4, 8, 3, 4.0, 2500, 16, 10, 16),
+    # k=100, alpha=4 with M=32: ck=400 takes the dump scan and per-query selection
+    ("m32_ck400", 128, 32, 8, 4, 8, 4, 4.0, 6000, 12, 100, 16),
 ]
 IDS = [c[0] for c in CASES]
 
