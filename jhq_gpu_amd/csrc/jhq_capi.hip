@@ -256,53 +256,39 @@ int build_query_matrix(jhq_index* ix) {
     return JHQ_OK;
 }
 
-// v14/jhq_gpu_index.cu:228-299 — coarse k-means in rotated space.
-int train_ivf(jhq_index* ix, const float* h_y, const float* d_y, int64_t n) {
+// v14/jhq_gpu_index.cu:228-299 — coarse k-means in rotated space, on the
+// device: init rows c * n / nlist; each iteration assigns with the current
+// centroids and norms, then takes the means (double, ascending rows) or
+// reseeds empty lists.  The host copies are read back at the end.
+int train_ivf(jhq_index* ix, const float* d_y, int64_t n) {
     const int d = ix->d, nlist = ix->nlist;
-    ix->cent.assign(static_cast<size_t>(nlist) * d, 0.f);
-    for (int c = 0; c < nlist; c++) {
-        const int64_t src = static_cast<int64_t>(c) * n / nlist;
-        std::memcpy(ix->cent.data() + static_cast<int64_t>(c) * d, h_y + src * d,
-                    static_cast<size_t>(d) * sizeof(float));
-    }
+    hipStream_t s = ix->stream;
+    JHQ_TRY(ix->dcent.alloc(static_cast<size_t>(nlist) * d));
+    JHQ_TRY(ix->dnorms.alloc(static_cast<size_t>(nlist)));
+    JHQ_HIP(jhq::kmeans_init(d_y, d, n, nlist, ix->dcent.p, s));
     DBuf<int32_t> dasg;
     DBuf<unsigned long long> keys;
+    DBuf<unsigned char> scratch;
     JHQ_TRY(dasg.alloc(static_cast<size_t>(n)));
-    std::vector<int32_t> asg(static_cast<size_t>(n));
-    std::vector<double> sums(static_cast<size_t>(nlist) * d);
-    std::vector<int64_t> counts(nlist);
+    const size_t sb = jhq::kmeans_scratch_bytes(n, nlist);
+    JHQ_TRY(scratch.alloc(sb));
     for (int iter = 0; iter < ix->ivf_iters; iter++) {
         if (verbose())
             std::fprintf(stderr, "[jhq] train: IVF k-means iteration %d/%d (nlist %d, n %lld)\n",
                          iter + 1, ix->ivf_iters, nlist, static_cast<long long>(n));
-        JHQ_TRY(upload_centroids(ix));
+        JHQ_HIP(jhq::kmeans_norms(ix->dcent.p, d, nlist, ix->dnorms.p, s));
         JHQ_TRY(assign_rows(ix, d_y, n, dasg.p, keys));
-        JHQ_HIP(hipMemcpyAsync(asg.data(), dasg.p, static_cast<size_t>(n) * sizeof(int32_t),
-                               hipMemcpyDeviceToHost, ix->stream));
-        JHQ_HIP(hipStreamSynchronize(ix->stream));
-        std::fill(sums.begin(), sums.end(), 0.0);
-        std::fill(counts.begin(), counts.end(), 0);
-        for (int64_t i = 0; i < n; i++) {
-            const int c = asg[i];
-            counts[c]++;
-            double* sc = sums.data() + static_cast<int64_t>(c) * d;
-            const float* yi = h_y + i * d;
-            for (int j = 0; j < d; j++) sc[j] += yi[j];
-        }
-        for (int c = 0; c < nlist; c++) {
-            float* cc = ix->cent.data() + static_cast<int64_t>(c) * d;
-            if (counts[c] == 0) {
-                const int64_t src = (static_cast<int64_t>(c) * 1103515245 +
-                                     static_cast<int64_t>(iter) * 12345) % n;
-                std::memcpy(cc, h_y + src * d, static_cast<size_t>(d) * sizeof(float));
-                continue;
-            }
-            const double inv = 1.0 / static_cast<double>(counts[c]);
-            const double* sc = sums.data() + static_cast<int64_t>(c) * d;
-            for (int j = 0; j < d; j++) cc[j] = static_cast<float>(sc[j] * inv);
-        }
+        JHQ_HIP(jhq::kmeans_update(dasg.p, d_y, d, n, nlist, iter, ix->dcent.p, scratch.p, sb, s));
     }
-    return upload_centroids(ix);
+    JHQ_HIP(jhq::kmeans_norms(ix->dcent.p, d, nlist, ix->dnorms.p, s));
+    ix->cent.resize(static_cast<size_t>(nlist) * d);
+    ix->cent_norms.resize(static_cast<size_t>(nlist));
+    JHQ_HIP(hipMemcpyAsync(ix->cent.data(), ix->dcent.p, ix->cent.size() * sizeof(float),
+                           hipMemcpyDeviceToHost, s));
+    JHQ_HIP(hipMemcpyAsync(ix->cent_norms.data(), ix->dnorms.p, ix->cent_norms.size() * sizeof(float),
+                           hipMemcpyDeviceToHost, s));
+    JHQ_HIP(hipStreamSynchronize(s));
+    return JHQ_OK;
 }
 
 int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_segments) {
@@ -712,7 +698,7 @@ int train_impl(jhq_index* ix, const float* x, int64_t n_train) {
                            ix->stream));
     JHQ_HIP(hipStreamSynchronize(ix->stream));
 
-    JHQ_TRY(train_ivf(ix, h_y.data(), dy.p, n_train));
+    JHQ_TRY(train_ivf(ix, dy.p, n_train));
 
     // v14/jhq_gpu_index.cu:302-330 — residual scalars r = y - yhat over the
     // training set.  One codebook over every dimension (the reference), or,

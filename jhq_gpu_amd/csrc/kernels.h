@@ -54,6 +54,18 @@ hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int 
                   const float* c1d, int Kr, int RC, int Br, int bpv, const float* res_c1d,
                   uint8_t* codes, uint8_t* res, float* corr, int mode, hipStream_t s);
 
+// Coarse k-means on the device (kmeans.hip).  kmeans_init: centroid c =
+// row c * n / nlist of y [n x d].  kmeans_update: the means of the rows of
+// each list given the assignment asg [n], summed in double in ascending row
+// order, an empty list reseeded from row (c * 1103515245 + iter * 12345) % n;
+// scratch of kmeans_scratch_bytes(n, nlist) bytes.  kmeans_norms: ||c||^2 in
+// double, j ascending.
+hipError_t kmeans_init(const float* y, int d, int64_t n, int nlist, float* cent, hipStream_t s);
+size_t kmeans_scratch_bytes(int64_t n, int nlist);
+hipError_t kmeans_update(const int32_t* asg, const float* y, int d, int64_t n, int nlist, int iter,
+                         float* cent, void* scratch, size_t scratch_bytes, hipStream_t s);
+hipError_t kmeans_norms(const float* cent, int d, int nlist, float* norms, hipStream_t s);
+
 // List storage: one pool of padded candidate slots; list l is described by
 // int4 {start, cap, size, cbase}: slots [start, start + cap) with cap a
 // multiple of kGroup, size candidates, first canonical position cbase
