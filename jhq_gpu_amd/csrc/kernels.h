@@ -109,6 +109,7 @@ struct ScanShape {
                        // = that kernel's LDS); the buffer holds B * (groups of the P largest
                        // lists) * 16 keys
     int region;        // wave selection: bytes of the LUT / merge region
+    int ov;            // work plan: virtual groups per query (the cost of a segment)
 };
 // LDS plan of the scan kernel; returns false if the byte LUT and the
 // selection buffers do not fit.

@@ -1559,17 +1559,25 @@ __device__ void block_exclusive_scan(F f, int B, int* out, int* wsum) {
     __syncthreads();
 }
 
-// Returns the number of workgroups that take part: min(G, T), so that every
-// participating workgroup owns at least one group.
+// Each query's span starts with ov virtual groups, which stand for the cost of
+// a segment (its LUT build and merge): a workgroup whose range crosses into a
+// new query gets that many fewer real groups.  In these units query b spans
+// [qpre[b] + b*ov, qpre[b+1] + (b+1)*ov), its real groups the last qtot[b]
+// of them, and T = qpre[B] + B*ov.  Returns the number of workgroups that
+// take part: min(G, T).
+__device__ __forceinline__ int64_t plan_span(const int* qpre, int b, int ov) {
+    return (int64_t)qpre[b] + (int64_t)b * ov;
+}
+
 template <int NT>
-__device__ int work_plan(const int32_t* __restrict__ qtot, int B, int Gmax, int* qpre, int* spre,
-                         int* wsum) {
+__device__ int work_plan(const int32_t* __restrict__ qtot, int B, int Gmax, int ov, int* qpre,
+                         int* spre, int* wsum) {
     block_exclusive_scan<NT>([&](int b) { return (int)qtot[b]; }, B, qpre, wsum);
-    const int64_t T = qpre[B];
+    const int64_t T = plan_span(qpre, B, ov);
     const int G = (int)min<int64_t>(Gmax, T);
     block_exclusive_scan<NT>(
         [&](int b) {
-            const int64_t a = qpre[b], e = qpre[b + 1];
+            const int64_t a = plan_span(qpre, b, ov) + ov, e = plan_span(qpre, b + 1, ov);
             if (e <= a) return 0;
             return wg_of_group(e - 1, T, G) - wg_of_group(a, T, G) + 1;
         },
@@ -1663,7 +1671,8 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
                   const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                   const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
                   const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t, int ck,
-                  unsigned long long* __restrict__ partial, int32_t* __restrict__ partial_slot) {
+                  unsigned long long* __restrict__ partial, int32_t* __restrict__ partial_slot,
+                  int ov) {
     constexpr int CPT = kScanCPT, TPG = kGroup / CPT;  // threads per group of 16
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;
@@ -1682,8 +1691,8 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
     const int tid = threadIdx.x, w = blockIdx.x;
     JHQ_PHASE_DECL
     for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
-    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
-    const int64_t T = qpre[B];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, ov, qpre, spre, wsum);
+    const int64_t T = plan_span(qpre, B, ov);
     JHQ_PHASE(0);
     if (w >= G) return;
     const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
@@ -1693,14 +1702,15 @@ scan_topck_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int b
         int lo = 0, hi = B - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (qpre[mid] <= x0) lo = mid;
+            if (plan_span(qpre, mid, ov) <= x0) lo = mid;
             else hi = mid - 1;
         }
         b = lo;
     }
-    for (; b < B && qpre[b] < x1; b++) {
-        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
-        if (qb1 <= qb0) continue;
+    for (; b < B && plan_span(qpre, b, ov) < x1; b++) {
+        // the query's real groups, in plan units
+        const int64_t qb0 = plan_span(qpre, b, ov) + ov, qb1 = plan_span(qpre, b + 1, ov);
+        if (qb1 <= qb0 || qb1 <= x0 || qb0 >= x1) continue;
         const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
         const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
         __syncthreads();
@@ -1949,7 +1959,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                  const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
                  const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t, int ck,
                  int region_bytes, unsigned long long* __restrict__ partial,
-                 int32_t* __restrict__ partial_slot) {
+                 int32_t* __restrict__ partial_slot, int ov) {
     // wave buffers of 64 * J keys (ck + 64 <= 64 * J)
     constexpr int NW = NT / 64, wcap = 64 * J;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1978,8 +1988,8 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
     unsigned long long* wb = wbuf + (size_t)wv * wcap;
     JHQ_PHASE_DECL
     for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
-    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
-    const int64_t T = qpre[B];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, ov, qpre, spre, wsum);
+    const int64_t T = plan_span(qpre, B, ov);
     JHQ_PHASE(0);
     if (w >= G) return;
     const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
@@ -1988,14 +1998,15 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         int lo = 0, hi = B - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (qpre[mid] <= x0) lo = mid;
+            if (plan_span(qpre, mid, ov) <= x0) lo = mid;
             else hi = mid - 1;
         }
         b = lo;
     }
-    for (; b < B && qpre[b] < x1; b++) {
-        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
-        if (qb1 <= qb0) continue;
+    for (; b < B && plan_span(qpre, b, ov) < x1; b++) {
+        // the query's real groups, in plan units
+        const int64_t qb0 = plan_span(qpre, b, ov) + ov, qb1 = plan_span(qpre, b + 1, ov);
+        if (qb1 <= qb0 || qb1 <= x0 || qb0 >= x1) continue;
         const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
         const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
         __syncthreads();
@@ -2182,6 +2193,9 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 }
 
 // chunks of a code row requested ahead of the one being consumed
+#ifndef JHQ_PLAN_OV
+#define JHQ_PLAN_OV 11000
+#endif
 #ifndef JHQ_SKEW_D
 #define JHQ_SKEW_D 2
 #endif
@@ -2220,7 +2234,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                  const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
                  const int4* __restrict__ ldesc, const uint8_t* __restrict__ skew, int ck,
                  int region_bytes, unsigned long long* __restrict__ partial,
-                 int32_t* __restrict__ partial_slot) {
+                 int32_t* __restrict__ partial_slot, int ov) {
     constexpr int M = MW * 4, NW = NT / 64, wcap = 64 * J;
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;                                  // [256][M], or the merge keys
@@ -2251,8 +2265,8 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
     unsigned long long* wb = wbuf + (size_t)wv * wcap;
     JHQ_PHASE_DECL
     for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
-    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
-    const int64_t T = qpre[B];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, ov, qpre, spre, wsum);
+    const int64_t T = plan_span(qpre, B, ov);
     JHQ_PHASE(0);
     if (w >= G) return;
     const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
@@ -2261,14 +2275,15 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         int lo = 0, hi = B - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (qpre[mid] <= x0) lo = mid;
+            if (plan_span(qpre, mid, ov) <= x0) lo = mid;
             else hi = mid - 1;
         }
         b = lo;
     }
-    for (; b < B && qpre[b] < x1; b++) {
-        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
-        if (qb1 <= qb0) continue;
+    for (; b < B && plan_span(qpre, b, ov) < x1; b++) {
+        // the query's real groups, in plan units
+        const int64_t qb0 = plan_span(qpre, b, ov) + ov, qb1 = plan_span(qpre, b + 1, ov);
+        if (qb1 <= qb0 || qb1 <= x0 || qb0 >= x1) continue;
         const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
         const int seg = spre[b] + (w - wg_of_group(qb0, T, G));
         __syncthreads();
@@ -2569,7 +2584,7 @@ scan_dump_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                  const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                  const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B, int P,
                  const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t,
-                 unsigned long long* __restrict__ dump) {
+                 unsigned long long* __restrict__ dump, int ov) {
     constexpr int NW = NT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     float* lut = (float*)smem;
@@ -2587,8 +2602,8 @@ scan_dump_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 
     const int tid = threadIdx.x, w = blockIdx.x, lane = tid & 63;
     for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
-    const int G = work_plan<NT>(qtot, B, gridDim.x, qpre, spre, wsum);
-    const int64_t T = qpre[B];
+    const int G = work_plan<NT>(qtot, B, gridDim.x, ov, qpre, spre, wsum);
+    const int64_t T = plan_span(qpre, B, ov);
     if (w >= G) return;
     const int64_t x0 = T * w / G, x1 = T * (w + 1) / G;
     int b;
@@ -2596,14 +2611,15 @@ scan_dump_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         int lo = 0, hi = B - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (qpre[mid] <= x0) lo = mid;
+            if (plan_span(qpre, mid, ov) <= x0) lo = mid;
             else hi = mid - 1;
         }
         b = lo;
     }
-    for (; b < B && qpre[b] < x1; b++) {
-        const int64_t qb0 = qpre[b], qb1 = qpre[b + 1];
-        if (qb1 <= qb0) continue;
+    for (; b < B && plan_span(qpre, b, ov) < x1; b++) {
+        // the query's real groups, in plan units
+        const int64_t qb0 = plan_span(qpre, b, ov) + ov, qb1 = plan_span(qpre, b + 1, ov);
+        if (qb1 <= qb0 || qb1 <= x0 || qb0 >= x1) continue;
         const int gA = (int)(max(x0, qb0) - qb0), gB = (int)(min(x1, qb1) - qb0);
         __syncthreads();
         for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
@@ -2619,7 +2635,7 @@ scan_dump_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         __syncthreads();
         build_lut_lds<NT>(sq, M, Ds, K1D, bpd, sc1d, lut);
         __syncthreads();
-        unsigned long long* qd = dump + qb0 * kGroup;
+        unsigned long long* qd = dump + (int64_t)qpre[b] * kGroup;  // real groups of query b
         auto task = [&](auto cc, int g0) {
             constexpr int C = decltype(cc)::value, TP = kGroup / C;
             using word_t = typename CodeWord<C>::type;
@@ -2702,7 +2718,7 @@ __global__ void __launch_bounds__(NT)
 select_query_kernel(const unsigned long long* __restrict__ dump, const int32_t* __restrict__ qtot,
                     int B, int Gmax, int ck, const int32_t* __restrict__ probes, int P,
                     const int4* __restrict__ ldesc, unsigned long long* __restrict__ partial,
-                    int32_t* __restrict__ partial_slot) {
+                    int32_t* __restrict__ partial_slot, int ov) {
     constexpr int NW = NT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
@@ -2715,7 +2731,7 @@ select_query_kernel(const unsigned long long* __restrict__ dump, const int32_t* 
     int* scnt = meta + 3 * P;
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const unsigned long long lt = (1ull << lane) - 1ull;
-    work_plan<NT>(qtot, B, Gmax, qpre, spre, wsum);
+    work_plan<NT>(qtot, B, Gmax, ov, qpre, spre, wsum);
     for (int i = tid; i < P; i += NT) {
         const int4 L = ldesc[probes[(int64_t)b * P + i]];
         meta[3 * i] = L.x;
@@ -2820,6 +2836,9 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
                bool skew) {
     out->G = target_wg;
     out->max_segments = target_wg + B;
+    // a segment's LUT build and merge cost about as much as JHQ_PLAN_OV / M
+    // groups of the scan (12 us against 0.14 us per group at M = 128)
+    out->ov = std::max(0, JHQ_PLAN_OV / std::max(M, 1));
     out->skew = 0;
     const int need = ck + 64;
     const int J = need <= 128 ? 2 : need <= 192 ? 3 : need <= 256 ? 4 : need <= 384 ? 6
@@ -2915,7 +2934,7 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
     if (sh.skew) {
         using KFn = void (*)(const float*, int, int, int, int, const float*, const int32_t*,
                              const int32_t*, const int32_t*, int, int, const int4*,
-                             const uint8_t*, int, int, unsigned long long*, int32_t*);
+                             const uint8_t*, int, int, unsigned long long*, int32_t*, int);
         constexpr int NS = kSkewNT;
         static const KFn kf[4][2] = {
             {scan_skew_kernel<NS, 8, 2>, scan_skew_kernel<NS, 8, 3>},
@@ -2930,7 +2949,7 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
         if (sh.lds > mx[mi][ji]) return hipErrorInvalidValue;
         hipLaunchKernelGGL(kf[mi][ji], dim3(sh.G), dim3(NS), sh.lds, s, q_rot, d, Ds, K1D, bpd,
                            c1d, probes, gofs, qtot, B, P, ldesc, skew, ck, sh.region, partial,
-                           partial_slot);
+                           partial_slot, sh.ov);
         return hipGetLastError();
     }
     if (sh.dump) {
@@ -2938,16 +2957,17 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
         static const int mxs = allow_max_lds((const void*)select_query_kernel<NT>);
         if (!dump || sh.lds > mxd || sh.region > mxs) return hipErrorInvalidValue;
         hipLaunchKernelGGL((scan_dump_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d,
-                           Ds, K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, dump);
+                           Ds, K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, dump,
+                           sh.ov);
         hipLaunchKernelGGL(select_query_kernel<NT>, dim3(B), dim3(NT), sh.region, s,
                            (const unsigned long long*)dump, qtot, B, sh.G, ck, probes, P, ldesc,
-                           partial, partial_slot);
+                           partial, partial_slot, sh.ov);
         return hipGetLastError();
     }
     if (sh.wave) {
         using KFn = void (*)(const float*, int, int, int, int, const float*, int, const int32_t*,
                              const int32_t*, const int32_t*, int, int, const int4*, const uint8_t*,
-                             int, int, unsigned long long*, int32_t*);
+                             int, int, unsigned long long*, int32_t*, int);
         static const KFn kf[2][5] = {
             {scan_wave_kernel<NT, SU, 2>, scan_wave_kernel<NT, SU, 3>, scan_wave_kernel<NT, SU, 4>,
              scan_wave_kernel<NT, SU, 6>, scan_wave_kernel<NT, SU, 8>},
@@ -2961,14 +2981,14 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
         if (sh.lds > mx[ni][ji]) return hipErrorInvalidValue;
         hipLaunchKernelGGL(kf[ni][ji], dim3(sh.G), dim3(sh.nt), sh.lds, s, q_rot, d, Ds, K1D, bpd,
                            c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, ck, sh.region,
-                           partial, partial_slot);
+                           partial, partial_slot, sh.ov);
         return hipGetLastError();
     }
     static const int max_dyn = allow_max_lds((const void*)scan_topck_kernel<NT, SU>);
     if (sh.lds > max_dyn) return hipErrorInvalidValue;
     hipLaunchKernelGGL((scan_topck_kernel<NT, SU>), dim3(sh.G), dim3(NT), sh.lds, s, q_rot, d, Ds,
                        K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, ck, partial,
-                       partial_slot);
+                       partial_slot, sh.ov);
     return hipGetLastError();
 }
 
@@ -2988,7 +3008,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
                    const int4* __restrict__ ldesc, int nlist, const uint8_t* __restrict__ list_res,
                    const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
                    float* __restrict__ out_d, int32_t* __restrict__ out_i,
-                   unsigned long long* __restrict__ topck_dbg, int stage_cap) {
+                   unsigned long long* __restrict__ topck_dbg, int stage_cap, int ov) {
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
     unsigned char* p = stream_carve<NT>(smem, ck, &S);
@@ -3008,7 +3028,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
 
     const int b = blockIdx.x, tid = threadIdx.x;
     JHQ_PHASE_DECL
-    work_plan<NT>(qtot, B, Gmax, qpre, spre, wsum);
+    work_plan<NT>(qtot, B, Gmax, ov, qpre, spre, wsum);
     for (int i = tid; i < d; i += NT) sq[i + (i >> 5)] = q_rot[(int64_t)b * d + i];
     for (int i = tid; i < RC * Kr; i += NT) rc[i] = res_c1d[i];
     const int s0 = spre[b], s1 = spre[b + 1];
@@ -3279,7 +3299,8 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, partial_slot,
                        qtot, B, sh.G, ck, k, q_rot, d, Ds, res_c1d, Kr, RC, Br, bpv, ldesc, nlist,
-                       list_res, list_corr, list_ids, out_d, out_i, topck_dbg, stage_cap);
+                       list_res, list_corr, list_ids, out_d, out_i, topck_dbg, stage_cap,
+                       sh.ov);
     return hipGetLastError();
 }
 
