@@ -2194,7 +2194,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 
 // chunks of a code row requested ahead of the one being consumed
 #ifndef JHQ_PLAN_OV
-#define JHQ_PLAN_OV 11000
+#define JHQ_PLAN_OV 22000
 #endif
 #ifndef JHQ_SKEW_D
 #define JHQ_SKEW_D 2
@@ -2836,8 +2836,9 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
                bool skew) {
     out->G = target_wg;
     out->max_segments = target_wg + B;
-    // a segment's LUT build and merge cost about as much as JHQ_PLAN_OV / M
-    // groups of the scan (12 us against 0.14 us per group at M = 128)
+    // a segment (its LUT build, merge and first loads of a new query's lists)
+    // costs about as much as JHQ_PLAN_OV / M groups of the scan: 172 groups at
+    // M = 128, the best of 0 / 43 / 86 / 172 / 258 / 344 / 516 at config 2
     out->ov = std::max(0, JHQ_PLAN_OV / std::max(M, 1));
     out->skew = 0;
     const int need = ck + 64;
