@@ -2450,6 +2450,9 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                         const bool first = __builtin_amdgcn_inverse_ballot_w64(rep2(fseed << tt));
                         fin = first ? acc : fin;
                         acc = first ? 0.0f : acc;
+                        // selected here: deferred, the 32 selects keep every step's
+                        // sum and lane mask live to the end of the period
+                        asm volatile("" : "+v"(fin));
                     }
                     acc += src[i];
                 }
