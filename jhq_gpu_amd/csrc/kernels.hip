@@ -2356,19 +2356,18 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             if (keep) wb[nw + __popcll(mk & lt)] = ((unsigned long long)o << 32) | tg;
             nw += __popcll(mk);
         };
-        // the lane's candidate of task t: unit 2t + half, row r of probe p
+        // the lane's candidate of task t: unit 2t + half, row r of probe p.
+        // A wave's tasks increase, so the probe is found by stepping forward
+        // from the previous one (the last probe with sru <= u)
+        int pcur = 0;
         auto locate = [&](int t, bool& valid, uint32_t& tag, int64_t& slot) {
             const int u = 2 * t + (lane >> 5);
             valid = false;
             tag = 0u;
             slot = 0;
             if (t < ntask && u < nunit) {
-                int plo = 0, phi = P - 1;  // last probe with sru <= u
-                while (plo < phi) {
-                    const int mid = (plo + phi + 1) >> 1;
-                    if (sru[mid] <= u) plo = mid;
-                    else phi = mid - 1;
-                }
+                while (pcur + 1 < P && sru[pcur + 1] <= u) pcur++;
+                const int plo = pcur;
                 const int r = sr0[plo] + (u - sru[plo]);
                 const int i = 32 * r + s;
                 const int gi = sg[plo] + (i >> 4);
@@ -2380,7 +2379,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         auto grab = [&]() {
             int t = 0;
             if (lane == 0) t = atomicAdd(&ctl[2], 1);
-            return __shfl(t, 0);
+            return __builtin_amdgcn_readfirstlane(t);  // lane 0 is active: every lane is
         };
         auto load_chunk = [&](int64_t slot, int c, uint32_t (&dst)[8]) {
             const uint4* rp = (const uint4*)(skew + slot * M + 32 * c);
