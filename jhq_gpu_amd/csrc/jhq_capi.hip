@@ -88,6 +88,14 @@ struct DBuf {
 
 constexpr int kSteps = 4;
 
+// Search lanes (workspace, stream, pinned staging) that consecutive batches
+// of one call alternate between.
+#ifndef JHQ_LANES
+#define JHQ_LANES 2
+#endif
+constexpr int kLanes = JHQ_LANES;
+static_assert(kLanes >= 1, "at least one lane");
+
 // Per-batch search buffers (v14/search.cuh:24-46).  The index keeps two sets:
 // consecutive batches of one device search alternate between them on two
 // streams, so one batch's refine overlaps the next batch's query product.
@@ -138,13 +146,13 @@ struct jhq_index {
     DBuf<float> dqmat;
 
     // search workspaces; ws[1] and the lane streams serve pipelined batches
-    Workspace ws[2];
-    hipStream_t lane[2] = {};
-    hipEvent_t lane_ev[3] = {};  // fork, lane 0 done, lane 1 done
-    float* h_q[2] = {};  // pinned staging, one set per lane
-    float* h_d[2] = {};
-    int32_t* h_i[2] = {};
-    size_t h_q_n[2] = {}, h_d_n[2] = {}, h_i_n[2] = {};
+    Workspace ws[kLanes];
+    hipStream_t lane[kLanes] = {};
+    hipEvent_t lane_ev[kLanes + 1] = {};  // fork, then each lane's last batch done
+    float* h_q[kLanes] = {};  // pinned staging, one set per lane
+    float* h_d[kLanes] = {};
+    int32_t* h_i[kLanes] = {};
+    size_t h_q_n[kLanes] = {}, h_d_n[kLanes] = {}, h_i_n[kLanes] = {};
 
     bool timing = false;
     hipEvent_t ev[kSteps + 1] = {};
@@ -152,7 +160,7 @@ struct jhq_index {
     int64_t tbatches = 0;
 
     ~jhq_index() {
-        for (int l = 0; l < 2; l++) {
+        for (int l = 0; l < kLanes; l++) {
             if (h_q[l]) (void)hipHostFree(h_q[l]);
             if (h_d[l]) (void)hipHostFree(h_d[l]);
             if (h_i[l]) (void)hipHostFree(h_i[l]);
@@ -167,7 +175,7 @@ struct jhq_index {
     }
 
     int ensure_lanes() {
-        if (lane[1]) return JHQ_OK;
+        if (lane[kLanes - 1]) return JHQ_OK;
         for (auto& l : lane) JHQ_HIP(hipStreamCreate(&l));
         for (auto& e : lane_ev) JHQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         return JHQ_OK;
@@ -435,13 +443,17 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
     const int d = ix->d;
     const int Bmax = ix->batch_size;
     BatchPlan bp;
-    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, 2));
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, kLanes));
     JHQ_TRY(ix->ensure_lanes());
-    for (int l = 0; l < 2; l++) JHQ_TRY(ensure_host_staging(ix, l, Bmax, k));
+    for (int l = 0; l < kLanes; l++) JHQ_TRY(ensure_host_staging(ix, l, Bmax, k));
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], ix->stream));
-    for (int l = 0; l < 2; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
-    int64_t pend_q0[2] = {-1, -1};
-    int pend_b[2] = {0, 0};
+    for (int l = 0; l < kLanes; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
+    int64_t pend_q0[kLanes];
+    int pend_b[kLanes];
+    for (int l = 0; l < kLanes; l++) {
+        pend_q0[l] = -1;
+        pend_b[l] = 0;
+    }
     auto collect = [&](int l) -> int {
         if (pend_q0[l] < 0) return JHQ_OK;
         JHQ_HIP(hipEventSynchronize(ix->lane_ev[1 + l]));
@@ -453,7 +465,7 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
     int64_t bi = 0;
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
         const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
-        const int l = static_cast<int>(bi & 1);
+        const int l = static_cast<int>(bi % kLanes);
         Workspace& w = ix->ws[l];
         hipStream_t st = ix->lane[l];
         JHQ_TRY(collect(l));  // the lane's previous batch is done: its buffers are free
@@ -469,11 +481,10 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
         pend_q0[l] = q0;
         pend_b[l] = Bq;
     }
-    // the older pending batch first
-    const int first = static_cast<int>(bi & 1);
-    JHQ_TRY(collect(first));
-    JHQ_TRY(collect(first ^ 1));
-    for (int l = 0; l < 2; l++) JHQ_HIP(hipStreamWaitEvent(ix->stream, ix->lane_ev[1 + l], 0));
+    // the pending batches, oldest first
+    for (int j = 0; j < kLanes; j++) JHQ_TRY(collect(static_cast<int>((bi + j) % kLanes)));
+    for (int l = 0; l < kLanes; l++)
+        JHQ_HIP(hipStreamWaitEvent(ix->stream, ix->lane_ev[1 + l], 0));
     return JHQ_OK;
 }
 
@@ -1062,7 +1073,7 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     // and joined back into it (step timing keeps one stream)
     const bool pipe = nq > Bmax && !ix->timing;
     BatchPlan bp;
-    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, pipe ? 2 : 1));
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, pipe ? kLanes : 1));
     if (!pipe) {
         for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
             const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
@@ -1073,15 +1084,15 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     }
     JHQ_TRY(ix->ensure_lanes());
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], s));
-    for (int l = 0; l < 2; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
+    for (int l = 0; l < kLanes; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
     int64_t bi = 0;
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
         const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
-        const int l = static_cast<int>(bi & 1);
+        const int l = static_cast<int>(bi % kLanes);
         JHQ_TRY(run_batch(ix, ix->ws[l], d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k,
                           d_ids + q0 * k, false, ix->lane[l]));
     }
-    for (int l = 0; l < 2; l++) {
+    for (int l = 0; l < kLanes; l++) {
         JHQ_HIP(hipEventRecord(ix->lane_ev[1 + l], ix->lane[l]));
         JHQ_HIP(hipStreamWaitEvent(s, ix->lane_ev[1 + l], 0));
     }

@@ -2396,8 +2396,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 #pragma unroll
             for (int c = 0; c < D; c++) load_chunk(slot, c, wr[c]);
         }
-        // one period: this row's M steps (and the previous row's tails)
-        auto period = [&]() {
+        while (t < ntask) {
             const int tn = grab();
             bool nvalid;
             uint32_t ntag;
@@ -2496,13 +2495,6 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             valid = nvalid;
             slot = nslot;
             t = tn;
-        };
-        // two periods per iteration: the row chunks and the previous-row copy
-        // then rotate through registers without copies at the loop edge
-        while (t < ntask) {
-            period();
-            if (t >= ntask) break;
-            period();
         }
         {
             // drain: the tails of the last candidates
