@@ -76,7 +76,8 @@ hipError_t kmeans_norms(const float* cent, int d, int nlist, float* norms, hipSt
 // Scatter: new vector s goes to list slist[s] at index sidx[s]; its id is
 // id_base + order[s], order[s] indexing the per-vector inputs pc/rc/co.
 // Lane-skewed rows of the primary codes (row[t] = code[(t - i mod 32) mod M]
-// for candidate i of each list, at skew[(start + i) * M]); rows from[l] ..
+// for candidate i of each list, at skew[(start + i) * M], the wrapped bytes
+// t < i mod 32 stored as code + 1 mod 256); rows from[l] ..
 // size-1 of list l (from: device [nlist]), max_rows >= the largest
 // size - from[l].  M % 4 == 0.
 hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,

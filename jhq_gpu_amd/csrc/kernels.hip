@@ -672,6 +672,9 @@ mfma_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
 // tiles sharing each B fragment), so Bm is read once per 64 rows.
 // Requires K % (64 * S) == 0, lda and ldb multiples of 4, aligned A and Bm.
 // ---------------------------------------------------------------------------
+#ifndef JHQ_Q_SMAX
+#define JHQ_Q_SMAX 8
+#endif
 template <int S>
 __global__ void __launch_bounds__(64 * S, 4)  // 4 waves per SIMD: two 8-wave groups per CU
 mfma_q_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
@@ -778,7 +781,8 @@ hipError_t mfma_q(const float* A, int64_t lda, const float* Bm, int64_t ldb, int
         return hipErrorInvalidValue;
     const int64_t tiles = (int64_t)((N + 15) / 16) * ((nb + 63) / 64);
     int S = 1;
-    while (S < 8 && tiles * S < 2048 && K % (64 * S * 2) == 0 && K / (S * 2) >= 64) S *= 2;
+    while (S < JHQ_Q_SMAX && tiles * S < 2048 && K % (64 * S * 2) == 0 && K / (S * 2) >= 64)
+        S *= 2;
     dim3 grid((N + 15) / 16, (nb + 63) / 64);
     switch (S) {
         case 1: hipLaunchKernelGGL(mfma_q_kernel<1>, grid, dim3(64), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
@@ -1026,9 +1030,13 @@ __global__ void scatter_kernel(const int32_t* __restrict__ order, const int32_t*
 // Lane-skewed copy of the primary codes, for the scan that runs each lane a
 // fixed number of subspaces behind its neighbours.  Candidate i of a list
 // (pool slot start + i) gets a row of M bytes at skew[(start + i) * M]:
-//   row[t] = code[(t - (i mod 32)) mod M]
-// so that at step t the lane holding i reads subspace t - (i mod 32) from
-// row position t.  Rows from[l] .. size-1 of list l are written (the rows
+//   row[t] = code[t - s]                 for t >= s = i mod 32,
+//   row[t] = (code[M + t - s] + 1) mod 256 for t < s,
+// so that at step t the lane holding i reads subspace t - s from row
+// position t.  The tail bytes (t < s, read one period later, with the next
+// candidate's head bytes) are raised by one LUT row: their LUT address
+// (v + 1) * M + t - s is then the head bytes' formula, and code 255 wraps to
+// the copy of row 255's last subspaces kept just below the LUT.  Rows from[l] .. size-1 of list l are written (the rows
 // before from[l] are current); one thread per row, the codes read from the
 // code-major blocks (codes_t[start * M + m * cap + i]).
 // ---------------------------------------------------------------------------
@@ -1046,8 +1054,10 @@ __global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const int32_t*
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             int m = t0 + e - s;
+            // tail bytes (t < s) hold code + 1 (mod 256)
+            const uint32_t inc = m < 0 ? 1u : 0u;
             if (m < 0) m += M;
-            w |= (uint32_t)src[(int64_t)m * L.y] << (8 * e);
+            w |= ((src[(int64_t)m * L.y] + inc) & 0xffu) << (8 * e);
         }
         *(uint32_t*)(dst + t0) = w;
     }
@@ -1364,7 +1374,10 @@ __device__ unsigned char* stream_carve(unsigned char* p, int k, StreamSel* S) {
 // ---------------------------------------------------------------------------
 constexpr int kProbeFastP = 128;   // largest P served by the two-pass path
 constexpr int kProbeU = 8;         // float4 loads in flight per thread
-constexpr int kProbeSurv = 1024;   // short-list capacity of the two-pass path
+#ifndef JHQ_PROBE_SURV
+#define JHQ_PROBE_SURV 1024
+#endif
+constexpr int kProbeSurv = JHQ_PROBE_SURV;   // short-list capacity of the two-pass path
 
 // The r-th smallest (1 <= r <= 64) of the wave's 64 lane values, bit by bit
 // from the top with ballots.
@@ -1593,6 +1606,8 @@ __device__ int work_plan(const int32_t* __restrict__ qtot, int B, int Gmax, int 
 // 4 bits share the first 4 steps of their fma chain, so each thread finishes
 // one low-nibble prefix and expands the high nibble as a binary tree (34
 // fmas for 16 entries instead of 128); every entry is still the same chain.
+// TR: layout [v][m] (lut[v*M + m]), plus lut[m - M] = lut[255][m] for the
+// last 32 subspaces (the skewed scan reads row 255's tail there).
 // ---------------------------------------------------------------------------
 template <int NT, bool TR = false>
 __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, int K1D, int bpd,
@@ -1631,6 +1646,7 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
                     if (TR) lut[(p + 16 * h) * M + m] = t[h];
                     else lm[p + 16 * h] = t[h];
                 }
+                if (TR && p == 15 && m >= M - 32) lut[m - M] = t[15];
             }
         } else {
             for (int v = part; v < 256; v += tpm) {
@@ -1644,6 +1660,7 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
                 }
                 if (TR) lut[v * M + m] = sacc;
                 else lm[v] = sacc;
+                if (TR && v == 255 && m >= M - 32) lut[m - M] = sacc;
             }
         }
     }
@@ -2192,6 +2209,8 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
     JHQ_PHASE_FLUSH(0);
 }
 
+// bytes below the skewed scan's LUT: row 255's last 32 subspaces
+constexpr int kSkewPad = 128;
 // chunks of a code row requested ahead of the one being consumed
 #ifndef JHQ_PLAN_OV
 #define JHQ_PLAN_OV 22000
@@ -2221,9 +2240,11 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 //     final (the lane class of candidate i is i mod 32, so it never changes);
 //   - the codes come from the skewed copy (row[t] = code[(t - s) mod M]),
 //     streamed in 32-byte chunks; the previous row's first chunk stays in
-//     registers for the tails;
-//   - which lanes read a tail at step t < 32, and which finish a sum there,
-//     are lane masks built on the scalar unit (no per-step compares);
+//     registers for the tails.  Its tail bytes hold code + 1, so a tail read
+//     (subspace M + t - s of code v) and a head read (subspace t - s) share
+//     one address, lane base + byte * 4M + 4t;
+//   - which lanes finish a sum at step t < 32 is a lane mask built on the
+//     scalar unit (no per-step compares);
 //   - after the last period a drain of up to 31 steps finishes the tails.
 // Work plan, segments, wave selection, merge and output are scan_wave_kernel's.
 // ---------------------------------------------------------------------------
@@ -2237,7 +2258,8 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                  int32_t* __restrict__ partial_slot, int ov) {
     constexpr int M = MW * 4, NW = NT / 64, wcap = 64 * J;
     extern __shared__ __align__(16) unsigned char smem[];
-    float* lut = (float*)smem;                                  // [256][M], or the merge keys
+    // [256][M] after kSkewPad bytes that hold row 255's wrapped tail, or the merge keys
+    float* lut = (float*)(smem + kSkewPad);
     unsigned long long* merge = (unsigned long long*)smem;
     unsigned long long* wbuf = (unsigned long long*)(smem + region_bytes);  // [NW][wcap]
     unsigned long long* kout =
@@ -2404,33 +2426,32 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             locate(tn, nvalid, ntag, nslot);
             const bool more = tn < ntask;
             float fin = 0.0f;
-            // Lane masks of the chunk-0 steps, built on the scalar unit: lanes
-            // 32h + s with s > t read a tail at step t (tmask), the lanes with
-            // s == t finish their previous candidate there (fmask).  The seeds
-            // are opaque so the masks are rebuilt each period, not hoisted.
-            uint32_t tseed = 0xfffffffeu, fseed = 1u;
-            asm volatile("" : "+s"(tseed), "+s"(fseed));
-            auto rep2 = [](uint32_t m) { return ((unsigned long long)m << 32) | m; };
-            // byte offsets of the lane's LUT base for a head and a tail read
-            // (opaque: one select of two registers per step)
+            // Lane mask of the chunk-0 steps, built on the scalar unit: lanes
+            // 32h + s with s == t finish their previous candidate at step t
+            // (bits t and 32 + t).  The seed is opaque so the masks are
+            // rebuilt each period, not hoisted.
+            unsigned long long fseed = 0x100000001ull;
+            asm volatile("" : "+s"(fseed));
+            // byte offset of the lane's LUT base (opaque: not folded into
+            // per-step constants)
             using lds_byte = __attribute__((address_space(3))) const char;
             lds_byte* ph = (lds_byte*)lut - 4 * s;
-            lds_byte* pt = ph + 4 * M;
-            asm volatile("" : "+v"(ph), "+v"(pt));
+            asm volatile("" : "+v"(ph));
             // LUT reads of steps GS*g .. GS*g+GS-1.  In chunk 0 a lane with
-            // t < s reads the previous candidate's subspace M + t - s
+            // t < s reads the previous candidate's subspace M + t - s, its
+            // byte raised by one row: the same address formula
             auto fetch = [&](int g, float (&dst)[GS]) {
 #pragma unroll
                 for (int i = 0; i < GS; i++) {
                     const int tt = GS * g + i, c = tt >> 5, j = (tt >> 2) & 7, e = tt & 3;
                     if (c == 0) {
-                        const bool tail = __builtin_amdgcn_inverse_ballot_w64(rep2(tseed << tt));
                         // the word's tail bytes from the previous row, the rest from this one
-                        const uint32_t w = (pw[j] & tbm[j]) | (wr[0][j] & ~tbm[j]);
+                        uint32_t w;
+                        asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(w) : "v"(tbm[j]), "v"(pw[j]), "v"(wr[0][j]));
                         uint32_t v = __builtin_amdgcn_ubfe(w, 8 * e, 8);
                         asm("" : "+v"(v));
                         dst[i] = *(const __attribute__((address_space(3))) float*)(
-                            (tail ? pt : ph) + v * (4 * M) + 4 * tt);
+                            ph + v * (4 * M) + 4 * tt);
                     } else {
                         uint32_t v = __builtin_amdgcn_ubfe(wr[c][j], 8 * e, 8);
                         asm("" : "+v"(v));
@@ -2446,7 +2467,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                 for (int i = 0; i < GS; i++) {
                     const int tt = GS * g + i;
                     if (tt < 32) {
-                        const bool first = __builtin_amdgcn_inverse_ballot_w64(rep2(fseed << tt));
+                        const bool first = __builtin_amdgcn_inverse_ballot_w64(fseed << tt);
                         fin = first ? acc : fin;
                         acc = first ? 0.0f : acc;
                         // selected here: deferred, the 32 selects keep every step's
@@ -2506,7 +2527,8 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int tt = 4 * j + e;
-                    if (tt < sv) acc += lb[((pw[j] >> (8 * e)) & 0xffu) * M + tt + M];
+                    // the tail byte is code + 1: row v - 1, subspace M + tt - s
+                    if (tt < sv) acc += lb[((pw[j] >> (8 * e)) & 0xffu) * M + tt];
                     if (tt == sv) fin = acc;
                 }
             }
@@ -2824,9 +2846,9 @@ constexpr int kProbeNT = 512;
 
 // LDS of the wave-selection scan with wave buffers of 64 * J keys.
 static size_t scan_wave_lds(int NT, int M, int d, int P, int ck, int K1D, int B, int J,
-                            size_t* region) {
+                            size_t* region, int lut_pad = 0) {
     const int NW = NT / 64;
-    *region = align16(std::max((size_t)M * 256 * 4, (size_t)NW * ck * 8));
+    *region = align16(std::max((size_t)lut_pad + (size_t)M * 256 * 4, (size_t)NW * ck * 8));
     // the query vector shares the wave buffers
     const size_t wb = std::max((size_t)NW * 64 * J * 8, (size_t)((d + 3) & ~3) * 4);
     return *region + wb + (size_t)ck * 16 + (size_t)((ck + 3) & ~3) * 4 +
@@ -2853,7 +2875,7 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     // it is slower (1124 against 872 us per batch of 128)
     if (J && J <= 3 && skew && M % 32 == 0 && M <= 128) {
         size_t region = 0;
-        const size_t lds = scan_wave_lds(kSkewNT, M, d, P, ck, K1D, B, J, &region) +
+        const size_t lds = scan_wave_lds(kSkewNT, M, d, P, ck, K1D, B, J, &region, kSkewPad) +
                            (size_t)(2 * P + 1) * 4;
         if (lds <= (size_t)kLdsBytes - 1024) {
             out->wave = J;
