@@ -323,7 +323,7 @@ bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128
 int refresh_skew(jhq_index* ix) {
     if (!ix->skew_stale) return JHQ_OK;
     const int nl = ix->nlist;
-    const size_t need = static_cast<size_t>(std::max<int64_t>(ix->pool_cap, 1)) * ix->M;
+    const size_t need = static_cast<size_t>(jhq::skew_bytes(std::max<int64_t>(ix->pool_cap, 1), ix->M));
     if (ix->dcodes_s.n < need || static_cast<int>(ix->skew_start.size()) != nl) {
         if (ix->dcodes_s.n < need) JHQ_TRY(ix->dcodes_s.alloc(need));
         ix->skew_start.assign(nl, -1);

@@ -76,12 +76,14 @@ hipError_t kmeans_norms(const float* cent, int d, int nlist, float* norms, hipSt
 // Scatter: new vector s goes to list slist[s] at index sidx[s]; its id is
 // id_base + order[s], order[s] indexing the per-vector inputs pc/rc/co.
 // Lane-skewed rows of the primary codes (row[t] = code[(t - i mod 32) mod M]
-// for candidate i of each list, at skew[(start + i) * M], the wrapped bytes
-// t < i mod 32 stored as code + 1 mod 256); rows from[l] ..
+// for candidate i of each list, the wrapped bytes t < i mod 32 stored as
+// code + 1 mod 256), in blocks of 16 slots stored piece by piece (16 bytes of
+// each slot's row per piece); skew_bytes(pool_cap, M) bytes.  Rows from[l] ..
 // size-1 of list l (from: device [nlist]), max_rows >= the largest
-// size - from[l].  M % 4 == 0.
+// size - from[l].  M % 32 == 0, M <= 256.
 hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
                       const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s);
+int64_t skew_bytes(int64_t pool_cap, int M);
 hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
                          int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
                          const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,

@@ -1029,46 +1029,62 @@ __global__ void scatter_kernel(const int32_t* __restrict__ order, const int32_t*
 // ---------------------------------------------------------------------------
 // Lane-skewed copy of the primary codes, for the scan that runs each lane a
 // fixed number of subspaces behind its neighbours.  Candidate i of a list
-// (pool slot start + i) gets a row of M bytes at skew[(start + i) * M]:
+// (pool slot p = start + i) gets M bytes
 //   row[t] = code[t - s]                 for t >= s = i mod 32,
 //   row[t] = (code[M + t - s] + 1) mod 256 for t < s,
 // so that at step t the lane holding i reads subspace t - s from row
 // position t.  The tail bytes (t < s, read one period later, with the next
 // candidate's head bytes) are raised by one LUT row: their LUT address
 // (v + 1) * M + t - s is then the head bytes' formula, and code 255 wraps to
-// the copy of row 255's last subspaces kept just below the LUT.  Rows from[l] .. size-1 of list l are written (the rows
-// before from[l] are current); one thread per row, the codes read from the
-// code-major blocks (codes_t[start * M + m * cap + i]).
+// the copy of row 255's last subspaces kept just below the LUT.
+// The rows are stored in blocks of 16 slots (list starts and capacities are
+// multiples of 16), piece by piece: the 16 bytes row[16q .. 16q+15] of slot p
+// are at skew_piece(p, q) = ((p / 16) * (M / 16) + q) * 256 + (p mod 16) * 16,
+// so the 64 lanes of a wave reading one piece of their candidates (four
+// blocks of 16 consecutive slots) touch four 256-byte runs.
+// Rows from[l] .. size-1 of list l are written (with the rest of the first
+// block, whose rows are current anyway); one thread per piece, the codes read
+// from the code-major blocks (codes_t[start * M + m * cap + i]).
 // ---------------------------------------------------------------------------
+__host__ __device__ inline int64_t skew_piece(int64_t p, int q, int M) {
+    return ((p >> 4) * (M >> 4) + q) * 256 + (p & 15) * 16;
+}
+
 __global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const int32_t* __restrict__ from,
                                   const uint8_t* __restrict__ codes_t, int M,
                                   uint8_t* __restrict__ skew) {
     const int4 L = ldesc[blockIdx.x];
-    const int i = from[blockIdx.x] + blockIdx.y * blockDim.x + threadIdx.x;
-    if (i >= L.z) return;
+    const int q = threadIdx.x >> 4;
+    const int i = (from[blockIdx.x] & ~15) + blockIdx.y * 16 + (threadIdx.x & 15);
+    if (q >= M / 16 || i >= L.z) return;
     const uint8_t* src = codes_t + (int64_t)L.x * M + i;
-    uint8_t* dst = skew + ((int64_t)L.x + i) * M;
     const int s = i & 31;
-    for (int t0 = 0; t0 < M; t0 += 4) {
-        uint32_t w = 0u;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        w[k] = 0u;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            int m = t0 + e - s;
+            int m = 16 * q + 4 * k + e - s;
             // tail bytes (t < s) hold code + 1 (mod 256)
             const uint32_t inc = m < 0 ? 1u : 0u;
             if (m < 0) m += M;
-            w |= ((src[(int64_t)m * L.y] + inc) & 0xffu) << (8 * e);
+            w[k] |= ((src[(int64_t)m * L.y] + inc) & 0xffu) << (8 * e);
         }
-        *(uint32_t*)(dst + t0) = w;
     }
+    *(uint4*)(skew + skew_piece((int64_t)L.x + i, q, M)) = make_uint4(w[0], w[1], w[2], w[3]);
 }
+
+int64_t skew_bytes(int64_t pool_cap, int M) { return (pool_cap + 15) / 16 * 16 * M; }
 
 hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
                       const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s) {
     if (nlist <= 0 || max_rows <= 0) return hipSuccess;
-    if (M % 4 != 0 || (max_rows + 255) / 256 > 65535) return hipErrorInvalidValue;
-    dim3 grid(nlist, (max_rows + 255) / 256);
-    hipLaunchKernelGGL(skew_codes_kernel, grid, dim3(256), 0, s, ldesc, from, codes_t, M, skew);
+    // one block of threads per 16 slots; from[l] is rounded down to 16
+    const int64_t gy = ((int64_t)max_rows + 15 + 15) / 16;
+    if (M % 32 != 0 || M > 256 || gy > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(skew_codes_kernel, dim3(nlist, (unsigned)gy), dim3(M), 0, s, ldesc, from,
+                       codes_t, M, skew);
     return hipGetLastError();
 }
 
@@ -2216,7 +2232,7 @@ constexpr int kSkewPad = 128;
 #define JHQ_PLAN_OV 22000
 #endif
 #ifndef JHQ_SKEW_D
-#define JHQ_SKEW_D 2
+#define JHQ_SKEW_D 1
 #endif
 // LUT reads per group of steps, and groups of reads in flight ahead of the adds
 #ifndef JHQ_SKEW_GS
@@ -2404,8 +2420,9 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             return __builtin_amdgcn_readfirstlane(t);  // lane 0 is active: every lane is
         };
         auto load_chunk = [&](int64_t slot, int c, uint32_t (&dst)[8]) {
-            const uint4* rp = (const uint4*)(skew + slot * M + 32 * c);
-            const uint4 a = rp[0], b2 = rp[1];
+            // pieces 2c and 2c + 1 of the slot's row
+            const uint8_t* rp = skew + skew_piece(slot, 2 * c, M);
+            const uint4 a = *(const uint4*)rp, b2 = *(const uint4*)(rp + 256);
             dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
             dst[4] = b2.x; dst[5] = b2.y; dst[6] = b2.z; dst[7] = b2.w;
         };
@@ -2839,7 +2856,13 @@ static int allow_max_lds(const void* kernel) {
 }
 
 constexpr int kScanNT = JHQ_SCAN_NT;
-constexpr int kSkewNT = 512;  // 8 waves: the scan loop's registers fit without spills
+// 12 waves, three per SIMD: the loop's ~150 registers fit (at most 168 at three
+// waves per SIMD) and a third wave hides more of the LDS latency than two (8
+// waves: 467 K against 493 K queries/s at config 2; 16 waves spill)
+#ifndef JHQ_SKEW_NT
+#define JHQ_SKEW_NT 768
+#endif
+constexpr int kSkewNT = JHQ_SKEW_NT;
 constexpr int kRefineNT = 512;
 constexpr int kProbeNT = 512;
 
