@@ -1622,12 +1622,42 @@ __device__ int work_plan(const int32_t* __restrict__ qtot, int B, int Gmax, int 
 // 4 bits share the first 4 steps of their fma chain, so each thread finishes
 // one low-nibble prefix and expands the high nibble as a binary tree (34
 // fmas for 16 entries instead of 128); every entry is still the same chain.
-// TR: layout [v][m] (lut[v*M + m]), plus lut[m - M] = lut[255][m] for the
+// TR = 1: layout [v][m] (lut[v*M + m]), plus lut[m - M] = lut[255][m] for the
 // last 32 subspaces (the skewed scan reads row 255's tail there).
+// TR = 2 (M = 128): the skewed scan's parity layout, lut_parity_index().
 // ---------------------------------------------------------------------------
-template <int NT, bool TR = false>
+// Parity layout of a 128-subspace LUT for the skewed scan (float index from
+// the LUT base; the caller reserves 16 floats below it):
+//   odd m:  (v, m) at v*64 + m/2                  (table O, 64 KB)
+//   even m: (v, m) at kParE + v*64 + m/2          (table E, after a 64-byte gap)
+// Row v of either table is 256 bytes, so a lane's LDS address is one byte
+// permute of its code byte (v at bits 8-15, the table at bit 16, a lane
+// offset in bits 0-7).  Row 255's entries for m = 128 + d (d = -31 .. -1),
+// which a wrapped tail byte (v + 1 = 0) reads one row below row 0, are
+// copied to (d - 1) / 2 (odd m, below table O) and kParE + d / 2 (even m, in
+// the gap).
+constexpr int kParE = (65536 + 64) / 4;
+__host__ __device__ constexpr int lut_parity_index(int v, int m) {
+    return (m & 1 ? 0 : kParE) + v * 64 + (m >> 1);
+}
+template <int NT, int TR = 0>
 __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, int K1D, int bpd,
                                               const float* sc1d, float* lut) {
+    // one entry of the chosen layout (and its wrapped copy)
+    auto put = [&](int v, int m, float x) {
+        if (TR == 2) {
+            lut[lut_parity_index(v, m)] = x;
+            if (v == 255 && m >= 97) {
+                const int d = m - 128;
+                lut[m & 1 ? (d - 1) / 2 : kParE + d / 2] = x;
+            }
+        } else if (TR == 1) {
+            lut[v * M + m] = x;
+            if (v == 255 && m >= M - 32) lut[m - M] = x;
+        } else {
+            lut[m * 256 + v] = x;
+        }
+    };
     const int tpm = NT / M > 0 ? NT / M : 1;
     const int part = threadIdx.x % tpm;
     const int kmask = K1D - 1;
@@ -1635,7 +1665,6 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
         float qv[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) qv[k] = k < Ds ? sq[m * Ds + k] : 0.0f;
-        float* lm = lut + m * 256;
         if (K1D == 2 && Ds == 8) {
             const float c0 = sc1d[0], c1 = sc1d[1];
             for (int p = part; p < 16; p += tpm) {
@@ -1658,11 +1687,7 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
                     }
                 }
 #pragma unroll
-                for (int h = 0; h < 16; h++) {
-                    if (TR) lut[(p + 16 * h) * M + m] = t[h];
-                    else lm[p + 16 * h] = t[h];
-                }
-                if (TR && p == 15 && m >= M - 32) lut[m - M] = t[15];
+                for (int h = 0; h < 16; h++) put(p + 16 * h, m, t[h]);
             }
         } else {
             for (int v = part; v < 256; v += tpm) {
@@ -1674,9 +1699,7 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
                         sacc = fmaf(df, df, sacc);
                     }
                 }
-                if (TR) lut[v * M + m] = sacc;
-                else lm[v] = sacc;
-                if (TR && v == 255 && m >= M - 32) lut[m - M] = sacc;
+                put(v, m, sacc);
             }
         }
     }
@@ -2274,8 +2297,10 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                  int32_t* __restrict__ partial_slot, int ov) {
     constexpr int M = MW * 4, NW = NT / 64, wcap = 64 * J;
     extern __shared__ __align__(16) unsigned char smem[];
-    // [256][M] after kSkewPad bytes that hold row 255's wrapped tail, or the merge keys
-    float* lut = (float*)(smem + kSkewPad);
+    // the LUT ([256][M] after kSkewPad bytes that hold row 255's wrapped tail,
+    // or at M = 128 the parity layout after 64 bytes), or the merge keys
+    constexpr bool PAR = MW == 32;
+    float* lut = (float*)(smem + (PAR ? 64 : kSkewPad));
     unsigned long long* merge = (unsigned long long*)smem;
     unsigned long long* wbuf = (unsigned long long*)(smem + region_bytes);  // [NW][wcap]
     unsigned long long* kout =
@@ -2351,7 +2376,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                 return lo < hi ? ((hi - sg[i] + 1) >> 1) - ((lo - sg[i]) >> 1) : 0;
             },
             P, sru, wsum);
-        build_lut_lds<NT, true>(sq, M, Ds, K1D, bpd, sc1d, lut);
+        build_lut_lds<NT, PAR ? 2 : 1>(sq, M, Ds, K1D, bpd, sc1d, lut);
         __syncthreads();
         JHQ_PHASE(1);
 
@@ -2454,6 +2479,28 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             using lds_byte = __attribute__((address_space(3))) const char;
             lds_byte* ph = (lds_byte*)lut - 4 * s;
             asm volatile("" : "+v"(ph));
+            // parity layout: at step t the lane reads subspace m = t - s of
+            // table O (m odd) or E, at byte (O or E) + v*256 + 2m - 2(m&1) from
+            // the LUT base.  With d = t - s and q = d & 1 that is
+            //   lutbase + 2t + [byte 2: 1 - q][byte 1: v][byte 0: cq],
+            //   cq = 64 (1 - q) + 64 - 2s - 2q   (0 .. 128),
+            // where lutbase = smem + 64 and the 64-byte gap before E are folded
+            // into cq: one byte permute of the lane constant kp[t & 1] and the
+            // code word per step.  A tail byte (v + 1) lands on row v's
+            // subspace 128 + d the same way (2 * 128 = 256 bytes = one row).
+            uint32_t kp[2];
+#pragma unroll
+            for (int par = 0; par < 2; par++) {
+                const int q = par ^ (s & 1);
+                kp[par] = ((uint32_t)(1 - q) << 16) | (uint32_t)(64 * (1 - q) + 64 - 2 * s - 2 * q);
+            }
+            asm volatile("" : "+v"(kp[0]), "+v"(kp[1]));
+            // the permute gives the byte address from smem, which is LDS address 0
+            // (this kernel has no static LDS; the launch checks it)
+            auto par_read = [&](uint32_t w, int tt) {
+                const uint32_t a = __builtin_amdgcn_perm(kp[tt & 1], w, 0x0c060004u | ((uint32_t)(tt & 3) << 8));
+                return *(const __attribute__((address_space(3))) float*)((lds_byte*)(uintptr_t)a + 2 * tt);
+            };
             // LUT reads of steps GS*g .. GS*g+GS-1.  In chunk 0 a lane with
             // t < s reads the previous candidate's subspace M + t - s, its
             // byte raised by one row: the same address formula
@@ -2461,7 +2508,13 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 #pragma unroll
                 for (int i = 0; i < GS; i++) {
                     const int tt = GS * g + i, c = tt >> 5, j = (tt >> 2) & 7, e = tt & 3;
-                    if (c == 0) {
+                    if (PAR) {
+                        uint32_t w = wr[c][j];
+                        // chunk 0: the word's tail bytes from the previous row
+                        if (c == 0)
+                            asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(w) : "v"(tbm[j]), "v"(pw[j]), "v"(wr[0][j]));
+                        dst[i] = par_read(w, tt);
+                    } else if (c == 0) {
                         // the word's tail bytes from the previous row, the rest from this one
                         uint32_t w;
                         asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(w) : "v"(tbm[j]), "v"(pw[j]), "v"(wr[0][j]));
@@ -2545,7 +2598,18 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                 for (int e = 0; e < 4; e++) {
                     const int tt = 4 * j + e;
                     // the tail byte is code + 1: row v - 1, subspace M + tt - s
-                    if (tt < sv) acc += lb[((pw[j] >> (8 * e)) & 0xffu) * M + tt];
+                    if (tt < sv) {
+                        if (PAR) {
+                            const int q = (tt & 1) ^ (s & 1);
+                            const uint32_t k = ((uint32_t)(1 - q) << 16) |
+                                               (uint32_t)(64 * (1 - q) + 64 - 2 * s - 2 * q);
+                            const uint32_t a = __builtin_amdgcn_perm(k, pw[j], 0x0c060004u | ((uint32_t)e << 8));
+                            acc += *(const __attribute__((address_space(3))) float*)(
+                                (const __attribute__((address_space(3))) char*)(uintptr_t)a + 2 * tt);
+                        } else {
+                            acc += lb[((pw[j] >> (8 * e)) & 0xffu) * M + tt];
+                        }
+                    }
                     if (tt == sv) fin = acc;
                 }
             }
@@ -2845,6 +2909,12 @@ select_query_kernel(const unsigned long long* __restrict__ dump, const int32_t* 
 
 // Allows `kernel` the LDS left after its static allocation; returns the
 // largest dynamic LDS size it may be launched with (0 on failure).
+static int static_lds(const void* kernel) {
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return -1;
+    return (int)fa.sharedSizeBytes;
+}
+
 static int allow_max_lds(const void* kernel) {
     hipFuncAttributes fa;
     if (hipFuncGetAttributes(&fa, kernel) != hipSuccess) return 0;
@@ -2993,7 +3063,11 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
         const int mi = sh.skew / 8 - 1, ji = sh.wave - 2;
         if (!skew || mi < 0 || mi > 3 || ji < 0 || ji > 1 || sh.skew * 4 != M)
             return hipErrorInvalidValue;
-        if (mx[mi][ji] < 0) mx[mi][ji] = allow_max_lds((const void*)kf[mi][ji]);
+        if (mx[mi][ji] < 0) {
+            mx[mi][ji] = allow_max_lds((const void*)kf[mi][ji]);
+            // M = 128 addresses its LUT from LDS address 0: no static LDS
+            if (mi == 3 && static_lds((const void*)kf[mi][ji]) != 0) mx[mi][ji] = 0;
+        }
         if (sh.lds > mx[mi][ji]) return hipErrorInvalidValue;
         hipLaunchKernelGGL(kf[mi][ji], dim3(sh.G), dim3(NS), sh.lds, s, q_rot, d, Ds, K1D, bpd,
                            c1d, probes, gofs, qtot, B, P, ldesc, skew, ck, sh.region, partial,
