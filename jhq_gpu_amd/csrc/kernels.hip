@@ -2257,6 +2257,10 @@ constexpr int kSkewPad = 128;
 #ifndef JHQ_SKEW_D
 #define JHQ_SKEW_D 1
 #endif
+// probe lookup in registers for up to 64 probes (0: always through LDS)
+#ifndef JHQ_SKEW_PREG
+#define JHQ_SKEW_PREG 1
+#endif
 // LUT reads per group of steps, and groups of reads in flight ahead of the adds
 #ifndef JHQ_SKEW_GS
 #define JHQ_SKEW_GS 4
@@ -2407,28 +2411,58 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         uint32_t ptag = 0u;
         bool pvalid = false;
         const float* lb = lut - s;  // lane base: lut[v*M + m] = lb[v*M + t] with m = t - s
-        auto append = [&](bool keep, uint32_t o, uint32_t tg) {
+        // tgs: the workgroup bound ctl[0], read a period early (a stale bound
+        // only keeps more keys)
+        auto append = [&](bool keep, uint32_t o, uint32_t tg, uint32_t tgs) {
             if (nw + 64 > wcap) {
                 Tw = wave_prune<J>(wb, nw, ck);
                 nw = ck;
                 if (lane == 0) atomicMin((unsigned int*)&ctl[0], Tw);
             }
-            const uint32_t tgs = (uint32_t)ctl[0];
             keep = keep && o <= min(Tw, tgs);
             const unsigned long long mk = __ballot(keep);
             if (keep) wb[nw + __popcll(mk & lt)] = ((unsigned long long)o << 32) | tg;
             nw += __popcll(mk);
         };
-        // the lane's candidate of task t: unit 2t + half, row r of probe p.
-        // A wave's tasks increase, so the probe is found by stepping forward
-        // from the previous one (the last probe with sru <= u)
+        // the lane's candidate of task t: unit u = 2t + half, row r of probe
+        // p, the last probe with sru[p] <= u; i = 32 r + s.  Up to 64 probes
+        // live in registers, lane p holding probe p's
+        //   sru, A = 32 (sr0 - sru), soff + A, spad0 + A, snl - A, sg + A / 16
+        // so that i = A + 32u + s needs no LDS round trip: p by ballot,
+        // the rest by readlane.  More probes step forward through LDS from the
+        // previous one (a wave's tasks increase).
+        const bool preg = JHQ_SKEW_PREG && P <= 64;
+        int q_sru = 0x7fffffff, q_T = 0, q_S = 0, q_N = 0, q_G = 0;
+        if (preg && lane < P) {
+            const int A = 32 * (sr0[lane] - sru[lane]);
+            q_sru = sru[lane];
+            q_T = soff[lane] + A;
+            q_S = spad0[lane] + A;
+            q_N = snl[lane] - A;
+            q_G = sg[lane] + A / 16;
+        }
         int pcur = 0;
         auto locate = [&](int t, bool& valid, uint32_t& tag, int64_t& slot) {
             const int u = 2 * t + (lane >> 5);
             valid = false;
             tag = 0u;
             slot = 0;
-            if (t < ntask && u < nunit) {
+            if (preg) {
+                const int p0 = __popcll(__ballot(q_sru <= 2 * t)) - 1;
+                const int p1 = __popcll(__ballot(q_sru <= 2 * t + 1)) - 1;
+                // both halves' values (uniform), then a per-lane select
+                const int T0 = __builtin_amdgcn_readlane(q_T, p0), T1 = __builtin_amdgcn_readlane(q_T, p1);
+                const int S0 = __builtin_amdgcn_readlane(q_S, p0), S1 = __builtin_amdgcn_readlane(q_S, p1);
+                const int N0 = __builtin_amdgcn_readlane(q_N, p0), N1 = __builtin_amdgcn_readlane(q_N, p1);
+                const int G0 = __builtin_amdgcn_readlane(q_G, p0), G1 = __builtin_amdgcn_readlane(q_G, p1);
+                const bool h = lane >= 32;
+                const int T = h ? T1 : T0, S = h ? S1 : S0, N = h ? N1 : N0, G = h ? G1 : G0;
+                const int iu = 32 * u + s;
+                const int gi = G + 2 * u + (s >> 4);
+                valid = t < ntask && u < nunit && iu < N && gi >= gA && gi < gB;
+                tag = (uint32_t)(T + iu);
+                slot = valid ? (int64_t)S + iu : 0;
+            } else if (t < ntask && u < nunit) {
                 while (pcur + 1 < P && sru[pcur + 1] <= u) pcur++;
                 const int plo = pcur;
                 const int r = sr0[plo] + (u - sru[plo]);
@@ -2439,6 +2473,8 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                 slot = valid ? (int64_t)spad0[plo] + i : 0;
             }
         };
+        // tasks from a counter (a fixed wv, wv + NW, ... assignment measured 2%
+        // slower: the waves do not advance at the same rate)
         auto grab = [&]() {
             int t = 0;
             if (lane == 0) t = atomicAdd(&ctl[2], 1);
@@ -2466,6 +2502,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             uint32_t ntag;
             int64_t nslot;
             locate(tn, nvalid, ntag, nslot);
+            const uint32_t tgs = *(volatile __attribute__((address_space(3))) uint32_t*)ctl;
             const bool more = tn < ntask;
             float fin = 0.0f;
             // Lane mask of the chunk-0 steps, built on the scalar unit: lanes
@@ -2579,7 +2616,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             for (int c = 0; c < D; c++)
 #pragma unroll
                 for (int j = 0; j < 8; j++) wr[c][j] = wr[C + c][j];
-            append(pvalid, f2ord(fin), ptag);
+            append(pvalid, f2ord(fin), ptag, tgs);
             ptag = tag;
             pvalid = valid;
             tag = ntag;
@@ -2613,7 +2650,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                     if (tt == sv) fin = acc;
                 }
             }
-            append(pvalid, f2ord(fin), ptag);
+            append(pvalid, f2ord(fin), ptag, *(volatile __attribute__((address_space(3))) uint32_t*)ctl);
         }
         if (nw > ck) {
             Tw = wave_prune<J>(wb, nw, ck);

@@ -42,6 +42,10 @@ CASES = [
     ("m96_d768", 768, 96, 8, 4, 8, 3, 4.0, 2500, 16, 10, 16),
     # k=100, alpha=4 with M=32: ck=400 takes the dump scan and per-query selection
     ("m32_ck400", 128, 32, 8, 4, 8, 4, 4.0, 6000, 12, 100, 16),
+    # skewed scan with more probes than a wave has lanes (probe lookup through LDS)
+    ("m32_p80", 64, 32, 8, 4, 96, 80, 4.0, 4000, 12, 10, 16),
+    # skewed scan at M=128 (parity LUT) with exactly 64 probes (lookup in registers)
+    ("m128_p64", 256, 128, 8, 4, 64, 64, 4.0, 3000, 10, 10, 16),
 ]
 IDS = [c[0] for c in CASES]
 
@@ -204,6 +208,13 @@ def test_search_device_pipelined_batches(gpu, name):
         g.search_device(qt[b0:b0 + batch], k, od2[b0:b0 + batch], oi2[b0:b0 + batch], stream=s)
     assert np.array_equal(oi2.cpu().numpy(), i1)
     assert np.array_equal(_bits(od2.cpu().numpy()), _bits(d1))
+
+
+@pytest.mark.parametrize("name", ["m64_ds4_ck100", "m96_d768", "m32_p80", "m128_p64"])
+def test_skewed_scan_taken(gpu, name):
+    """The M % 32 == 0 cases above exercise the skewed scan (not a fallback)."""
+    g, _, _, _, k = _build(CASES[IDS.index(name)])
+    assert g.scan_plan(k)[0] == "scan_skew_kernel"
 
 
 def test_k_larger_than_candidates(gpu):
