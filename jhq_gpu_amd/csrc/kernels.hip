@@ -1658,10 +1658,17 @@ __device__ __forceinline__ void build_lut_lds(const float* sq, int M, int Ds, in
             lut[m * 256 + v] = x;
         }
     };
-    const int tpm = NT / M > 0 ? NT / M : 1;
-    const int part = threadIdx.x % tpm;
+    // threads to subspaces: for [m][v] a group of tpm threads shares m (a
+    // wave's writes are runs of consecutive v); for the [v][m] layouts
+    // consecutive threads take consecutive m (consecutive banks; threads
+    // that share m would write one bank, 64 or 128 words apart)
+    const int tid = threadIdx.x;
+    const bool mfast = TR != 0 && NT >= M;
+    const int tpm = mfast ? NT / M : (NT / M > 0 ? NT / M : 1);
+    const int part = mfast ? tid / M : tid % tpm;
     const int kmask = K1D - 1;
-    for (int m = threadIdx.x / tpm; m < M; m += NT / tpm) {
+    for (int m = mfast ? (part < tpm ? tid % M : M) : tid / tpm; m < M;
+         m += mfast ? M : NT / tpm) {
         float qv[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) qv[k] = k < Ds ? sq[m * Ds + k] : 0.0f;
