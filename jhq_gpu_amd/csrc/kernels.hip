@@ -2273,7 +2273,7 @@ constexpr int kSkewPad = 128;
 #define JHQ_SKEW_GS 4
 #endif
 #ifndef JHQ_SKEW_LA
-#define JHQ_SKEW_LA 3
+#define JHQ_SKEW_LA 2
 #endif
 // ---------------------------------------------------------------------------
 // ADC scan with lanes skewed across subspaces (M a multiple of 32, MW = M/4).
