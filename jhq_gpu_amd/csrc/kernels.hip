@@ -2487,6 +2487,17 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             if (lane == 0) t = atomicAdd(&ctl[2], 1);
             return __builtin_amdgcn_readfirstlane(t);  // lane 0 is active: every lane is
         };
+        // a task taken one period before it is needed: the counter's reply
+        // arrives while the period runs (read with readfirstlane a period later)
+        auto grab_ahead = [&]() {
+            // the counter through an opaque LDS pointer: the atomic optimizer
+            // (uniform address) would wait for the reply on the spot
+            __attribute__((address_space(3))) int* cp = (__attribute__((address_space(3))) int*)(ctl + 2);
+            asm volatile("" : "+v"(cp));
+            int t = 0;
+            if (lane == 0) t = __hip_atomic_fetch_add(cp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return t;
+        };
         auto load_chunk = [&](int64_t slot, int c, uint32_t (&dst)[8]) {
             // pieces 2c and 2c + 1 of the slot's row
             const uint8_t* rp = skew + skew_piece(slot, 2 * c, M);
@@ -2495,6 +2506,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             dst[4] = b2.x; dst[5] = b2.y; dst[6] = b2.z; dst[7] = b2.w;
         };
         int t = grab();
+        int tahead = grab_ahead();
         bool valid;
         uint32_t tag;
         int64_t slot;
@@ -2503,8 +2515,11 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 #pragma unroll
             for (int c = 0; c < D; c++) load_chunk(slot, c, wr[c]);
         }
+        // tasks come from the counter in increasing order per wave, so when
+        // t >= ntask the task taken ahead is past the end too
         while (t < ntask) {
-            const int tn = grab();
+            const int tn = __builtin_amdgcn_readfirstlane(tahead);
+            tahead = grab_ahead();
             bool nvalid;
             uint32_t ntag;
             int64_t nslot;
