@@ -2259,7 +2259,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 constexpr int kSkewPad = 128;
 // chunks of a code row requested ahead of the one being consumed
 #ifndef JHQ_PLAN_OV
-#define JHQ_PLAN_OV 22000
+#define JHQ_PLAN_OV 40000
 #endif
 #ifndef JHQ_SKEW_D
 #define JHQ_SKEW_D 1
@@ -3013,8 +3013,10 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     out->G = target_wg;
     out->max_segments = target_wg + B;
     // a segment (its LUT build, merge and first loads of a new query's lists)
-    // costs about as much as JHQ_PLAN_OV / M groups of the scan: 172 groups at
-    // M = 128, the best of 0 / 43 / 86 / 172 / 258 / 344 / 516 at config 2
+    // costs about as much as JHQ_PLAN_OV / M groups of the scan: 312 groups at
+    // M = 128 (12-wave skewed scan; of 86 / 125 / 172 / 234 / 312 / 390 / 507
+    // at config 2 the larger weights run the scan faster, and 312 keeps the
+    // alpha = 4 pipeline at its best)
     out->ov = std::max(0, JHQ_PLAN_OV / std::max(M, 1));
     out->skew = 0;
     const int need = ck + 64;
