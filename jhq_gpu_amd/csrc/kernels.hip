@@ -672,9 +672,6 @@ mfma_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
 // tiles sharing each B fragment), so Bm is read once per 64 rows.
 // Requires K % (64 * S) == 0, lda and ldb multiples of 4, aligned A and Bm.
 // ---------------------------------------------------------------------------
-#ifndef JHQ_Q_SMAX
-#define JHQ_Q_SMAX 8
-#endif
 template <int S, int CT>
 __global__ void __launch_bounds__(64 * S, CT > 1 ? 1 : 4)  // CT = 1: two 8-wave groups per CU
 mfma_q_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
@@ -810,8 +807,7 @@ hipError_t mfma_q(const float* A, int64_t lda, const float* Bm, int64_t ldb, int
         return hipErrorInvalidValue;
     const int64_t tiles = (int64_t)((N + 15) / 16) * ((nb + 63) / 64);
     int S = 1;
-    while (S < JHQ_Q_SMAX && tiles * S < 2048 && K % (64 * S * 2) == 0 && K / (S * 2) >= 64)
-        S *= 2;
+    while (S < 8 && tiles * S < 2048 && K % (64 * S * 2) == 0 && K / (S * 2) >= 64) S *= 2;
     dim3 grid((N + 15) / 16, (nb + 63) / 64);
     switch (S) {
         case 1: hipLaunchKernelGGL((mfma_q_kernel<1, 1>), grid, dim3(64), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
@@ -1427,10 +1423,7 @@ __device__ unsigned char* stream_carve(unsigned char* p, int k, StreamSel* S) {
 // ---------------------------------------------------------------------------
 constexpr int kProbeFastP = 128;   // largest P served by the two-pass path
 constexpr int kProbeU = 8;         // float4 loads in flight per thread
-#ifndef JHQ_PROBE_SURV
-#define JHQ_PROBE_SURV 1024
-#endif
-constexpr int kProbeSurv = JHQ_PROBE_SURV;   // short-list capacity of the two-pass path
+constexpr int kProbeSurv = 1024;   // short-list capacity of the two-pass path
 
 // The r-th smallest (1 <= r <= 64) of the wave's 64 lane values, bit by bit
 // from the top with ballots.
