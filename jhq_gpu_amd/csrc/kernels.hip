@@ -2325,7 +2325,13 @@ constexpr int kSkewPad = 128;
 //     one address, lane base + byte * 4M + 4t;
 //   - which lanes finish a sum at step t < 32 is a lane mask built on the
 //     scalar unit (no per-step compares);
-//   - after the last period a drain of up to 31 steps finishes the tails.
+//   - after the last period a drain of up to 31 steps finishes the tails;
+//   - at M = 128 the LUT is split by subspace parity into two tables of
+//     256-byte rows (lut_parity_index), so a gather's LDS address is one byte
+//     permute of the code word and a per-lane constant;
+//   - up to 64 probes of a segment live across the wave's lanes, so a task's
+//     candidate is found without LDS reads; the next task is taken from the
+//     counter a period ahead.
 // Work plan, segments, wave selection, merge and output are scan_wave_kernel's.
 // ---------------------------------------------------------------------------
 template <int NT, int MW, int J>
