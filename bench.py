@@ -642,6 +642,7 @@ def bench_streaming(args):
     ix.add(hb[:N0])
     t_add = time.time() - t0
     log(f"train n={n_train} {t_train:.1f}s, initial add {t_add:.1f}s")
+    ix.reserve(K)  # device searches with k=100 run in the reserved workspace
 
     out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)

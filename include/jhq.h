@@ -125,12 +125,27 @@ int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k,
 
 /* Same pipeline with queries and results already in device memory
  * (the reference's graph body v14/search.cu:315-386 without the host
- * copies around it).  Returns after the work is enqueued on `stream`.
+ * copies around it).  Returns after the work is enqueued on `stream`:
+ * it allocates nothing and does not synchronise with the host.  It runs in
+ * the workspace reserved for k <= k_max (jhq_reserve; add(), append(),
+ * load() and the setters reserve k_max = 10 at the index's batch_size,
+ * nprobe and alpha) and fails with JHQ_ESTATE for a larger k.
  * More than batch_size queries: the batches alternate between two internal
  * streams forked from `stream` and joined back into it, so the call is
- * stream-ordered on `stream` like a single launch. */
+ * stream-ordered on `stream` like a single launch.  Consecutive device
+ * searches are ordered after each other whatever their streams; add,
+ * append, host searches, setters and destroy wait for the last one. */
 int jhq_search_device(jhq_index* idx, const float* d_q, int64_t nq, int k,
                       float* d_dists, int32_t* d_ids, void* stream);
+
+/* Preallocates the search workspace (both pipeline lanes, pinned staging)
+ * for searches with k <= k_max at the current batch_size, nprobe and alpha
+ * — the reference's alloc_workspace (v14/jhq_gpu_index.cu:166-206, called at
+ * the end of add(), :531) with the ck/k capacities realloc_ck_buffers
+ * (v14/search.cu:294-313) grows on demand.  k_max only ever grows.  Host
+ * searches with a larger k grow the workspace themselves, like the
+ * reference; device searches do not. */
+int jhq_reserve(jhq_index* idx, int k_max);
 
 /* JHQGpuIndex::ntotal() / dim() — v14/jhq_gpu_index.cuh:46-47 */
 int64_t jhq_ntotal(const jhq_index* idx);

@@ -95,6 +95,7 @@ _SIGS = {
     "jhq_get_params": (_I, [_VP, ctypes.POINTER(_Params)]),
     "jhq_get_plan": (_I, [_VP, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "jhq_search_device": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP]),
+    "jhq_reserve": (_I, [_VP, _I]),
     "jhq_ntotal": (_I64, [_VP]),
     "jhq_dim": (_I, [_VP]),
     "jhq_set_nprobe": (_I, [_VP, _I]),
@@ -253,8 +254,14 @@ class JHQGpuIndex:
         _check(lib().jhq_set_alpha(self._h, float(alpha)))
         self._p.alpha = float(alpha)
 
+    def reserve(self, k_max):
+        """Preallocates the search workspace for k <= k_max (device searches
+        with a larger k raise RuntimeError)."""
+        _check(lib().jhq_reserve(self._h, int(k_max)))
+
     def search_device(self, q, k, out_dists, out_ids, stream=None):
-        """q, out_dists, out_ids: torch device tensors (or int addresses)."""
+        """q, out_dists, out_ids: torch device tensors (or int addresses).
+        Enqueue-only: k must be within the reserved workspace (reserve())."""
         nq = int(q.shape[0])
         s = None
         if stream is not None:

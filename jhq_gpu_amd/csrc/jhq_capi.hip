@@ -66,19 +66,22 @@ struct DBuf {
         p = nullptr;
         n = 0;
     }
+    // The new buffer is allocated before the old one is freed, so a failed
+    // allocation leaves the old buffer (and its contents) in place.
     int alloc(size_t count) {
-        release();
         if (count == 0) count = 1;
-        hipError_t e = hipMalloc(reinterpret_cast<void**>(&p), count * sizeof(T));
-        if (e != hipSuccess) {
-            p = nullptr;
+        T* np = nullptr;
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&np), count * sizeof(T));
+        if (e != hipSuccess)
             return fail(JHQ_ENOMEM, "hipMalloc of " + std::to_string(count * sizeof(T)) +
                                         " bytes: " + hipGetErrorString(e));
-        }
+        release();
+        p = np;
         n = count;
         return JHQ_OK;
     }
-    int ensure(size_t count) { return count <= n && p ? JHQ_OK : alloc(count); }
+    bool has(size_t count) const { return p && count <= n; }
+    int ensure(size_t count) { return has(count) ? JHQ_OK : alloc(count); }
     int upload(const T* h, size_t count) {
         JHQ_TRY(alloc(count));
         JHQ_HIP(hipMemcpy(p, h, count * sizeof(T), hipMemcpyHostToDevice));
@@ -116,7 +119,16 @@ struct jhq_index {
     int64_t ntotal = 0;
     bool trained = false;
     bool added = false;
+    // set while an insert rewrites the lists; a failed insert leaves it set
+    // and searches refuse the index (its device descriptors may be stale)
+    bool broken = false;
     int num_cu = 256;
+    // searches with k <= res_k (and the current nprobe, alpha, batch_size)
+    // run in the preallocated workspace; jhq_reserve raises it
+    int res_k = 10;
+    // largest per-query candidate count of the dump scan for dump_P probes
+    int dump_P = -1;
+    int64_t dump_perq = 0;
 
     float sigma = 1.f;
     std::vector<float> Pi_cm;  // JLTransform::pi_data() (column-major)
@@ -129,6 +141,10 @@ struct jhq_index {
     int64_t pool_cap = 0, pool_used = 0;
 
     hipStream_t stream = nullptr;
+    // recorded on the caller's stream after every device search; inserts,
+    // re-reservations and host searches wait on it
+    hipEvent_t done_ev = nullptr;
+    bool done_pending = false;
     DBuf<float> dP, dc1d, dres_c1d, dcent, dnorms;
     DBuf<int4> dldesc;
     DBuf<int32_t> dlist_ids;
@@ -171,6 +187,7 @@ struct jhq_index {
             if (e) (void)hipEventDestroy(e);
         for (auto& l : lane)
             if (l) (void)hipStreamDestroy(l);
+        if (done_ev) (void)hipEventDestroy(done_ev);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -192,6 +209,16 @@ struct jhq_index {
         JHQ_HIP(hipGetDeviceProperties(&prop, dev));
         num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
         JHQ_HIP(hipStreamCreate(&stream));
+        JHQ_HIP(hipEventCreateWithFlags(&done_ev, hipEventDisableTiming));
+        return JHQ_OK;
+    }
+
+    // Blocks until the last device search has finished with the lists and
+    // workspaces.
+    int quiesce() {
+        if (!done_pending) return JHQ_OK;
+        JHQ_HIP(hipEventSynchronize(done_ev));
+        done_pending = false;
         return JHQ_OK;
     }
 };
@@ -299,19 +326,31 @@ int train_ivf(jhq_index* ix, const float* d_y, int64_t n) {
     return JHQ_OK;
 }
 
-int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_segments) {
+// A workspace buffer of at least `count` elements: grown when `grow`, else
+// it must already be that large (a search outside the reserved shape).
+template <class T>
+int need(DBuf<T>& b, size_t count, bool grow) {
+    if (b.has(count)) return JHQ_OK;
+    if (grow) return b.alloc(count);
+    return fail(JHQ_ESTATE,
+                "the search needs a larger workspace than was reserved; call jhq_reserve() "
+                "with this k (after any set_nprobe / set_alpha) before a device search");
+}
+
+int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_segments,
+                     bool grow) {
     const size_t B = static_cast<size_t>(ix->batch_size);
-    JHQ_TRY(w.wq.ensure(B * ix->d));
-    JHQ_TRY(w.wqrot.ensure(B * ix->d));
-    JHQ_TRY(w.wscores.ensure(B * ix->nlist));
-    JHQ_TRY(w.wprobes.ensure(B * P));
-    JHQ_TRY(w.wgofs.ensure(B * (P + 1)));
-    JHQ_TRY(w.wqtot.ensure(B));
-    JHQ_TRY(w.wpartial.ensure(static_cast<size_t>(max_segments) * ck));
-    JHQ_TRY(w.wpslot.ensure(static_cast<size_t>(max_segments) * ck));
-    JHQ_TRY(w.wtopck.ensure(B * ck));
-    JHQ_TRY(w.wout_d.ensure(B * k));
-    JHQ_TRY(w.wout_i.ensure(B * k));
+    JHQ_TRY(need(w.wq, B * ix->d, grow));
+    JHQ_TRY(need(w.wqrot, B * ix->d, grow));
+    JHQ_TRY(need(w.wscores, B * ix->nlist, grow));
+    JHQ_TRY(need(w.wprobes, B * P, grow));
+    JHQ_TRY(need(w.wgofs, B * (P + 1), grow));
+    JHQ_TRY(need(w.wqtot, B, grow));
+    JHQ_TRY(need(w.wpartial, static_cast<size_t>(max_segments) * ck, grow));
+    JHQ_TRY(need(w.wpslot, static_cast<size_t>(max_segments) * ck, grow));
+    JHQ_TRY(need(w.wtopck, B * ck, grow));
+    JHQ_TRY(need(w.wout_d, B * k, grow));
+    JHQ_TRY(need(w.wout_i, B * k, grow));
     return JHQ_OK;
 }
 
@@ -354,7 +393,10 @@ struct BatchPlan {
     jhq::ScanShape sh;
 };
 
-int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws = 1) {
+// The plan of a search batch and the workspaces it needs on nws lanes.
+// grow = false (device searches): nothing is allocated or refreshed, and a
+// shape beyond the reservation fails with JHQ_ESTATE.
+int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) {
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
     if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
@@ -362,17 +404,27 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws = 1) {
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
-    if (bp->sh.skew) JHQ_TRY(refresh_skew(ix));
+    if (bp->sh.skew && ix->skew_stale) {
+        if (!grow) return fail(JHQ_ESTATE, "the skewed code copy is out of date");
+        JHQ_TRY(refresh_skew(ix));
+    }
     for (int i = 0; i < nws; i++)
-        JHQ_TRY(ensure_workspace(ix, ix->ws[i], bp->ck, k, bp->P, bp->sh.max_segments));
+        JHQ_TRY(ensure_workspace(ix, ix->ws[i], bp->ck, k, bp->P, bp->sh.max_segments, grow));
     if (bp->sh.dump) {
-        // a query's candidates are at most the padded sizes of the P largest lists
-        std::vector<int32_t> sz(ix->l_size);
-        std::partial_sort(sz.begin(), sz.begin() + bp->P, sz.end(), std::greater<int32_t>());
-        int64_t per_q = 0;
-        for (int i = 0; i < bp->P; i++) per_q += (sz[i] + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+        // a query's candidates are at most the padded sizes of the P largest
+        // lists (cached per P; inserts reset the cache)
+        if (ix->dump_P != bp->P) {
+            std::vector<int32_t> sz(ix->l_size);
+            std::partial_sort(sz.begin(), sz.begin() + bp->P, sz.end(), std::greater<int32_t>());
+            int64_t per_q = 0;
+            for (int i = 0; i < bp->P; i++)
+                per_q += (sz[i] + jhq::kGroup - 1) / jhq::kGroup * jhq::kGroup;
+            ix->dump_P = bp->P;
+            ix->dump_perq = per_q;
+        }
         for (int i = 0; i < nws; i++)
-            JHQ_TRY(ix->ws[i].wdump.ensure(static_cast<size_t>(Bq) * std::max<int64_t>(per_q, 1)));
+            JHQ_TRY(need(ix->ws[i].wdump,
+                         static_cast<size_t>(Bq) * std::max<int64_t>(ix->dump_perq, 1), grow));
     }
     return JHQ_OK;
 }
@@ -422,6 +474,8 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
 
 int check_searchable(jhq_index* ix, int64_t nq, int k) {
     if (!ix) return fail(JHQ_EINVAL, "null index");
+    if (ix->broken)
+        return fail(JHQ_ESTATE, "a failed add/append left the index's lists inconsistent");
     if (ix->ntotal == 0) return fail(JHQ_ESTATE, "index is empty");
     if (nq < 0) return fail(JHQ_EINVAL, "nq must be >= 0");
     if (k <= 0) return fail(JHQ_EINVAL, "k must be positive");
@@ -435,6 +489,23 @@ int ensure_host_staging(jhq_index* ix, int l, int Bmax, int k) {
     return JHQ_OK;
 }
 
+// Preallocates everything a search with k <= res_k needs (the reference's
+// alloc_workspace at the end of add(), v14/jhq_gpu_index.cu:166-206,531, and
+// realloc_ck_buffers, v14/search.cu:294-313): both lanes' workspaces, streams
+// and pinned staging, and an up-to-date skewed code copy.  Called after every
+// add / append / load and parameter change, so device searches allocate
+// nothing.
+int reserve_search(jhq_index* ix) {
+    if (ix->ntotal == 0 || !ix->trained) return JHQ_OK;
+    JHQ_TRY(ix->quiesce());
+    if (skew_eligible(ix) && ix->skew_stale) JHQ_TRY(refresh_skew(ix));
+    BatchPlan bp;
+    JHQ_TRY(plan_batch(ix, ix->batch_size, ix->res_k, &bp, kLanes, true));
+    JHQ_TRY(ix->ensure_lanes());
+    for (int l = 0; l < kLanes; l++) JHQ_TRY(ensure_host_staging(ix, l, ix->batch_size, ix->res_k));
+    return JHQ_OK;
+}
+
 // Host arrays over several batches: the batches alternate between two lanes
 // (workspace, pinned staging, stream).  While one lane's batch runs, the host
 // copies the other lane's finished results out and its next queries in.
@@ -443,7 +514,7 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
     const int d = ix->d;
     const int Bmax = ix->batch_size;
     BatchPlan bp;
-    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, kLanes));
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, kLanes, true));
     JHQ_TRY(ix->ensure_lanes());
     for (int l = 0; l < kLanes; l++) JHQ_TRY(ensure_host_staging(ix, l, Bmax, k));
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], ix->stream));
@@ -492,12 +563,14 @@ int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, 
                 float* q_rot, int32_t* probes, int32_t* topck_pos, float* topck_dist) {
     JHQ_TRY(check_searchable(ix, nq, k));
     if (nq == 0) return JHQ_OK;
+    // a device search may still use the workspaces, which a larger k regrows
+    JHQ_TRY(ix->quiesce());
     const int d = ix->d;
     const int Bmax = ix->batch_size;
     const bool dbg = (q_rot || probes || topck_pos || topck_dist);
     if (!dbg && !ix->timing && nq > Bmax) return search_host_pipelined(ix, q, nq, k, dists, ids);
     BatchPlan bp;
-    JHQ_TRY(plan_batch(ix, Bmax, k, &bp));
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, 1, true));
     JHQ_TRY(ensure_host_staging(ix, 0, Bmax, k));
     std::vector<unsigned long long> tk;
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
@@ -543,6 +616,9 @@ int search_host(jhq_index* ix, const float* q, int64_t nq, int k, float* dists, 
 }
 
 }  // namespace
+
+// Sets the thread-local error message (for entry points in other files).
+int jhq_set_error(int code, const char* msg) { return fail(code, msg ? msg : ""); }
 
 // ---------------------------------------------------------------------------
 // C-ABI
@@ -622,6 +698,7 @@ int jhq_create(int d, const jhq_params* p, jhq_index** out) {
 }
 
 int jhq_destroy(jhq_index* idx) {
+    if (idx) (void)idx->quiesce();
     delete idx;
     return JHQ_OK;
 }
@@ -632,15 +709,24 @@ int jhq_dim(const jhq_index* idx) { return idx ? idx->d : 0; }
 int jhq_set_nprobe(jhq_index* idx, int nprobe) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (nprobe <= 0) return fail(JHQ_EINVAL, "nprobe must be positive");
+    JHQ_TRY(idx->quiesce());
     idx->nprobe = std::min(nprobe, idx->nlist);
-    return JHQ_OK;
+    return reserve_search(idx);
 }
 
 int jhq_set_alpha(jhq_index* idx, float alpha) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (!(alpha > 0.0f)) return fail(JHQ_EINVAL, "alpha must be positive");
+    JHQ_TRY(idx->quiesce());
     idx->alpha = alpha;
-    return JHQ_OK;
+    return reserve_search(idx);
+}
+
+int jhq_reserve(jhq_index* idx, int k_max) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (k_max <= 0) return fail(JHQ_EINVAL, "k_max must be positive");
+    idx->res_k = std::max(idx->res_k, k_max);
+    return reserve_search(idx);
 }
 
 int jhq_get_dims(const jhq_index* idx, int* Ds, int* K1D, int* bpd, int* Kr, int* bpv) {
@@ -853,7 +939,10 @@ int repack_pool(jhq_index* ix, const std::vector<int64_t>& need) {
 // left for such moves every list is re-packed into a new pool instead.
 int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_fit) {
     JHQ_TRY(ix->ensure_stream());
+    // a device search still in flight reads the lists rewritten below
+    JHQ_TRY(ix->quiesce());
     ix->skew_stale = true;
+    ix->dump_P = -1;
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
     hipStream_t s = ix->stream;
     const int64_t id_base = ix->ntotal;
@@ -912,7 +1001,9 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         if (static_cast<int64_t>(ix->l_size[l]) + add[l + 1] > INT32_MAX)
             return fail(JHQ_EINVAL, "list size exceeds int32");
     }
-    // block placement
+    // block placement: from here until the descriptors are uploaded the
+    // device lists and the host mirror may disagree
+    ix->broken = true;
     std::vector<int4> moves;
     if (exact_fit) {
         int64_t pos = 0;
@@ -996,6 +1087,7 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     }
     JHQ_TRY(upload_ldesc(ix));
     ix->ntotal += n;
+    ix->broken = false;
     return JHQ_OK;
 }
 
@@ -1034,7 +1126,7 @@ int jhq_add_ex(jhq_index* ix, const void* x, int dtype, int64_t n) {
     if (ix->added || ix->ntotal > 0) return fail(JHQ_ESTATE, "only one add() call is supported");
     JHQ_TRY(insert_impl(ix, x, dtype, n, true));
     ix->added = true;
-    return JHQ_OK;
+    return reserve_search(ix);
 }
 
 int jhq_append(jhq_index* ix, const float* x, int64_t n) {
@@ -1047,7 +1139,7 @@ int jhq_append_ex(jhq_index* ix, const void* x, int dtype, int64_t n) {
         return fail(JHQ_EINVAL, "unknown dtype");
     JHQ_TRY(insert_impl(ix, x, dtype, n, false));
     ix->added = true;
-    return JHQ_OK;
+    return reserve_search(ix);
 }
 
 int jhq_search(jhq_index* idx, const float* q, int64_t nq, int k, float* dists, int32_t* ids) {
@@ -1072,17 +1164,25 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     // several batches: alternate two workspaces on two streams forked from s
     // and joined back into it (step timing keeps one stream)
     const bool pipe = nq > Bmax && !ix->timing;
+    // enqueue-only: the reserved workspace must cover this shape (no
+    // allocation, no host synchronisation)
     BatchPlan bp;
-    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, pipe ? kLanes : 1));
+    JHQ_TRY(plan_batch(ix, Bmax, k, &bp, pipe ? kLanes : 1, false));
+    if (pipe && !ix->lane[kLanes - 1])
+        return fail(JHQ_ESTATE, "search lanes are not set up; call jhq_reserve()");
+    // ordered after the previous device search (it shares the workspaces),
+    // whatever stream that one ran on
+    if (ix->done_pending) JHQ_HIP(hipStreamWaitEvent(s, ix->done_ev, 0));
     if (!pipe) {
         for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
             const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
             JHQ_TRY(run_batch(ix, ix->ws[0], d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k,
                               d_ids + q0 * k, false, s));
         }
+        JHQ_HIP(hipEventRecord(ix->done_ev, s));
+        ix->done_pending = true;
         return JHQ_OK;
     }
-    JHQ_TRY(ix->ensure_lanes());
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], s));
     for (int l = 0; l < kLanes; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
     int64_t bi = 0;
@@ -1096,6 +1196,8 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
         JHQ_HIP(hipEventRecord(ix->lane_ev[1 + l], ix->lane[l]));
         JHQ_HIP(hipStreamWaitEvent(s, ix->lane_ev[1 + l], 0));
     }
+    JHQ_HIP(hipEventRecord(ix->done_ev, s));
+    ix->done_pending = true;
     return JHQ_OK;
 }
 
@@ -1117,6 +1219,11 @@ int jhq_get_lists(const jhq_index* idx, int32_t* offsets, int32_t* ids, uint8_t*
                   uint8_t* res, float* corr) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (!idx->added) return fail(JHQ_ESTATE, "index is empty");
+    if (idx->broken)
+        return fail(JHQ_ESTATE, "a failed add/append left the index's lists inconsistent");
+    // the copies below run on the null stream; a device search may still be
+    // in flight on a caller's non-blocking stream
+    JHQ_TRY(const_cast<jhq_index*>(idx)->quiesce());
     const int M = idx->M, nlist = idx->nlist, bpv = idx->bpv;
     // canonical order: lists in list order, candidates in insertion order
     std::vector<int64_t> cbase(nlist + 1, 0);
@@ -1386,6 +1493,8 @@ int jhq_load(const char* path, jhq_index** out) {
     if (rc != JHQ_OK) return done(rc);
     ix->ntotal = n;
     ix->added = ad != 0;
+    rc = reserve_search(ix);
+    if (rc != JHQ_OK) return done(rc);
     *out = ix;
     return JHQ_OK;
 }

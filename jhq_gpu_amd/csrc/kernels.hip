@@ -1088,24 +1088,27 @@ __global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const int32_t*
                                   uint8_t* __restrict__ skew) {
     const int4 L = ldesc[blockIdx.x];
     const int q = threadIdx.x >> 4;
-    const int i = (from[blockIdx.x] & ~15) + blockIdx.y * 16 + (threadIdx.x & 15);
-    if (q >= M / 16 || i >= L.z) return;
-    const uint8_t* src = codes_t + (int64_t)L.x * M + i;
-    const int s = i & 31;
-    uint32_t w[4];
+    if (q >= M / 16) return;
+    // blocks of 16 slots; grid-y strides over the list's blocks
+    for (int64_t i = (int64_t)(from[blockIdx.x] & ~15) + (int64_t)blockIdx.y * 16 + (threadIdx.x & 15);
+         i < L.z; i += (int64_t)gridDim.y * 16) {
+        const uint8_t* src = codes_t + (int64_t)L.x * M + i;
+        const int s = (int)(i & 31);
+        uint32_t w[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        w[k] = 0u;
+        for (int k = 0; k < 4; k++) {
+            w[k] = 0u;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            int m = 16 * q + 4 * k + e - s;
-            // tail bytes (t < s) hold code + 1 (mod 256)
-            const uint32_t inc = m < 0 ? 1u : 0u;
-            if (m < 0) m += M;
-            w[k] |= ((src[(int64_t)m * L.y] + inc) & 0xffu) << (8 * e);
+            for (int e = 0; e < 4; e++) {
+                int m = 16 * q + 4 * k + e - s;
+                // tail bytes (t < s) hold code + 1 (mod 256)
+                const uint32_t inc = m < 0 ? 1u : 0u;
+                if (m < 0) m += M;
+                w[k] |= ((src[(int64_t)m * L.y] + inc) & 0xffu) << (8 * e);
+            }
         }
+        *(uint4*)(skew + skew_piece((int64_t)L.x + i, q, M)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    *(uint4*)(skew + skew_piece((int64_t)L.x + i, q, M)) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 int64_t skew_bytes(int64_t pool_cap, int M) { return (pool_cap + 15) / 16 * 16 * M; }
@@ -1114,8 +1117,9 @@ hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max
                       const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s) {
     if (nlist <= 0 || max_rows <= 0) return hipSuccess;
     // one block of threads per 16 slots; from[l] is rounded down to 16
-    const int64_t gy = ((int64_t)max_rows + 15 + 15) / 16;
-    if (M % 32 != 0 || M > 256 || gy > 65535) return hipErrorInvalidValue;
+    // (a list of any length: the kernel strides over grid-y)
+    const int64_t gy = std::min<int64_t>(((int64_t)max_rows + 15 + 15) / 16, 65535);
+    if (M % 32 != 0 || M > 256) return hipErrorInvalidValue;
     hipLaunchKernelGGL(skew_codes_kernel, dim3(nlist, (unsigned)gy), dim3(M), 0, s, ldesc, from,
                        codes_t, M, skew);
     return hipGetLastError();

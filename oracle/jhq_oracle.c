@@ -11,6 +11,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -20,6 +21,51 @@
 #ifndef M_SQRT2
 #define M_SQRT2 1.41421356237309504880
 #endif
+
+/* ------------------------------------------------------------------------ */
+/* Row-parallel loops.  Every row (vector, query) is computed by one thread   */
+/* exactly as in the serial loop, so results do not depend on the thread     */
+/* count; o_set_threads(1) (the default) runs everything on the caller.       */
+/* ------------------------------------------------------------------------ */
+static int g_threads = 1;
+
+void o_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 256 ? 256 : n); }
+int o_get_threads(void) { return g_threads; }
+
+typedef void (*o_range_fn)(void* ctx, int64_t lo, int64_t hi);
+typedef struct { o_range_fn fn; void* ctx; int64_t lo, hi; } o_job;
+
+static void* o_job_run(void* a) {
+    o_job* j = (o_job*)a;
+    j->fn(j->ctx, j->lo, j->hi);
+    return NULL;
+}
+
+/* fn(ctx, lo, hi) over [0, n) split into at most g_threads contiguous ranges. */
+static void o_parallel(int64_t n, o_range_fn fn, void* ctx) {
+    int T = g_threads;
+    if (T > n) T = (int)n;
+    if (T <= 1) {
+        if (n > 0) fn(ctx, 0, n);
+        return;
+    }
+    o_job jobs[256];
+    pthread_t th[256];
+    int started[256];
+    for (int t = 0; t < T; t++) {
+        jobs[t].fn = fn;
+        jobs[t].ctx = ctx;
+        jobs[t].lo = n * t / T;
+        jobs[t].hi = n * (t + 1) / T;
+        started[t] = 0;
+    }
+    for (int t = 1; t < T; t++) started[t] = pthread_create(&th[t], NULL, o_job_run, &jobs[t]) == 0;
+    o_job_run(&jobs[0]);
+    for (int t = 1; t < T; t++) {
+        if (started[t]) pthread_join(th[t], NULL);
+        else o_job_run(&jobs[t]); /* thread creation failed: run it here */
+    }
+}
 
 /* ------------------------------------------------------------------------ */
 /* std::mt19937 (C++ [rand.eng.mers] parameters), as used by                 */
@@ -253,16 +299,25 @@ void o_build_rotation(int d, int seed, float* Pi) {
 /* search.cu:338-339 use cuBLAS; this build pins the order to an fmaf chain   */
 /* over k ascending, the order the HIP rotation kernel uses).                */
 /* ------------------------------------------------------------------------ */
-void o_rotate(const float* P, const float* x, int64_t n, int d, float* y) {
-    for (int64_t i = 0; i < n; i++) {
-        const float* xi = x + i * d;
+typedef struct { const float *P, *x; int d; float* y; } o_rot_ctx;
+
+static void o_rotate_rows(void* c, int64_t lo, int64_t hi) {
+    const o_rot_ctx* a = (const o_rot_ctx*)c;
+    const int d = a->d;
+    for (int64_t i = lo; i < hi; i++) {
+        const float* xi = a->x + i * d;
         for (int j = 0; j < d; j++) {
-            const float* pj = P + (int64_t)j * d;
+            const float* pj = a->P + (int64_t)j * d;
             float acc = 0.0f;
             for (int k = 0; k < d; k++) acc = fmaf(xi[k], pj[k], acc);
-            y[i * d + j] = acc;
+            a->y[i * d + j] = acc;
         }
     }
+}
+
+void o_rotate(const float* P, const float* x, int64_t n, int d, float* y) {
+    o_rot_ctx a = {P, x, d, y};
+    o_parallel(n, o_rotate_rows, &a);
 }
 
 static int bits_per_dim(int d, int M, int K1D) {
@@ -273,10 +328,16 @@ static int bits_per_dim(int d, int M, int K1D) {
 }
 
 /* encode.cu:20-41 (primary_encode_kernel) == cpu/codebook.cpp:96-110. */
-void o_primary_encode(const float* y, int64_t n, int d, int M, const float* c1d,
-                      int K1D, uint8_t* codes) {
+typedef struct { const float* y; int d, M; const float* c1d; int K1D; uint8_t* codes; } o_penc_ctx;
+
+static void o_primary_encode_rows(void* c, int64_t lo, int64_t hi) {
+    const o_penc_ctx* a = (const o_penc_ctx*)c;
+    const float* y = a->y;
+    const float* c1d = a->c1d;
+    uint8_t* codes = a->codes;
+    const int d = a->d, M = a->M, K1D = a->K1D;
     const int Ds = d / M, bpd = bits_per_dim(d, M, K1D);
-    for (int64_t i = 0; i < n; i++) {
+    for (int64_t i = lo; i < hi; i++) {
         const float* yi = y + i * d;
         for (int m = 0; m < M; m++) {
             uint8_t cm = 0;
@@ -287,6 +348,12 @@ void o_primary_encode(const float* y, int64_t n, int d, int M, const float* c1d,
             codes[i * M + m] = cm;
         }
     }
+}
+
+void o_primary_encode(const float* y, int64_t n, int d, int M, const float* c1d,
+                      int K1D, uint8_t* codes) {
+    o_penc_ctx a = {y, d, M, c1d, K1D, codes};
+    o_parallel(n, o_primary_encode_rows, &a);
 }
 
 /* encode.cu:43-86 (residual_encode_kernel): nibble packing (even j low
@@ -300,13 +367,23 @@ void o_residual_encode(const float* y, const uint8_t* primary, int64_t n, int d,
 /* RC residual codebooks of Kr words: RC = 1 (every dimension, the
  * reference), or RC = M (dimension j uses codebook j / Ds; an extension with
  * no reference counterpart). */
-void o_residual_encode_rc(const float* y, const uint8_t* primary, int64_t n, int d,
-                          int M, const float* c1d, int K1D, const float* res_c1d,
-                          int Kr, int RC, int Br, uint8_t* res_codes, float* corr) {
+typedef struct {
+    const float* y; const uint8_t* primary; int d, M; const float* c1d; int K1D;
+    const float* res_c1d; int Kr, RC, Br; uint8_t* res_codes; float* corr;
+} o_renc_ctx;
+
+static void o_residual_encode_rows(void* c, int64_t lo, int64_t hi) {
+    const o_renc_ctx* a = (const o_renc_ctx*)c;
+    const float* y = a->y;
+    const uint8_t* primary = a->primary;
+    const float *c1d = a->c1d, *res_c1d = a->res_c1d;
+    uint8_t* res_codes = a->res_codes;
+    float* corr = a->corr;
+    const int d = a->d, M = a->M, K1D = a->K1D, Kr = a->Kr, RC = a->RC, Br = a->Br;
     const int Ds = d / M, bpd = bits_per_dim(d, M, K1D);
     const int bpv = (d * Br + 7) / 8;
     const int kmask = K1D - 1;
-    for (int64_t i = 0; i < n; i++) {
+    for (int64_t i = lo; i < hi; i++) {
         const float* yi = y + i * d;
         const uint8_t* pc = primary + i * M;
         uint8_t* rc = res_codes + i * bpv;
@@ -330,6 +407,13 @@ void o_residual_encode_rc(const float* y, const uint8_t* primary, int64_t n, int
         }
         corr[i] = 2.0f * dot;
     }
+}
+
+void o_residual_encode_rc(const float* y, const uint8_t* primary, int64_t n, int d,
+                          int M, const float* c1d, int K1D, const float* res_c1d,
+                          int Kr, int RC, int Br, uint8_t* res_codes, float* corr) {
+    o_renc_ctx a = {y, primary, d, M, c1d, K1D, res_c1d, Kr, RC, Br, res_codes, corr};
+    o_parallel(n, o_residual_encode_rows, &a);
 }
 
 /* cpu/codebook.cpp:161-171 */
@@ -412,9 +496,14 @@ static float dot_fma(const float* a, const float* b, int d) {
 
 /* jhq_gpu_index.cu:23-40 (assign_from_dots_kernel): argmin ||c||^2 - 2<c,y>,
  * strict < so ties keep the lowest c.  <c,y> is the fmaf chain. */
-void o_assign(const float* y, int64_t n, int d, const float* cent,
-              const float* norms, int nlist, int32_t* out) {
-    for (int64_t i = 0; i < n; i++) {
+typedef struct { const float *y, *cent, *norms; int d, nlist; int32_t* out; } o_asg_ctx;
+
+static void o_assign_rows(void* c, int64_t lo, int64_t hi) {
+    const o_asg_ctx* a = (const o_asg_ctx*)c;
+    const float *y = a->y, *cent = a->cent, *norms = a->norms;
+    const int d = a->d, nlist = a->nlist;
+    int32_t* out = a->out;
+    for (int64_t i = lo; i < hi; i++) {
         const float* yi = y + i * d;
         float best = fmaf(-2.0f, dot_fma(yi, cent, d), norms[0]);
         int bi = 0;
@@ -424,6 +513,12 @@ void o_assign(const float* y, int64_t n, int d, const float* cent,
         }
         out[i] = bi;
     }
+}
+
+void o_assign(const float* y, int64_t n, int d, const float* cent,
+              const float* norms, int nlist, int32_t* out) {
+    o_asg_ctx a = {y, cent, norms, d, nlist, out};
+    o_parallel(n, o_assign_rows, &a);
 }
 
 /* jhq_gpu_index.cu:228-299 (train_ivf_centroids). */
@@ -517,8 +612,90 @@ int o_ck(float alpha, int k) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* The approximate top-ck of the reference's IVF scan                         */
+/* (jhq_v14_streaming_add/search.cu:105-195, scan_ivf_coalesced_kernel, one   */
+/* 256-thread block per query).  Thread t visits candidates t, t+256, ... of   */
+/* the probed lists laid end to end in probe order and keeps its 4 smallest   */
+/* distances (insert at the last slot if strictly smaller, bubble up while    */
+/* strictly smaller: :153-161); the 4*256 survivors sit at s[t*4 + i]         */
+/* (:163-168).  Then ck rounds: every thread takes the first strict minimum   */
+/* over s[t], s[t+256], ... (:176-178), a tree reduction keeps the left entry */
+/* unless the right one is strictly smaller (:179-185), and the winner is     */
+/* emitted and set to +inf (:186-191); no winner -> (+inf, -1).               */
+/* ------------------------------------------------------------------------ */
+#define V14_BLOCK 256
+#define V14_KLOCAL 4
+
+/* v14 block argmin over vals[0..n) with the strided per-thread scan and the
+ * keep-left tree reduction; returns the winning index or -1. */
+static int v14_block_argmin(const float* vals, int n) {
+    float rv[V14_BLOCK];
+    int ri[V14_BLOCK];
+    for (int t = 0; t < V14_BLOCK; t++) {
+        float bv = INFINITY;
+        int bi = -1;
+        for (int c = t; c < n; c += V14_BLOCK)
+            if (vals[c] < bv) { bv = vals[c]; bi = c; }
+        rv[t] = bv;
+        ri[t] = bi;
+    }
+    for (int stride = V14_BLOCK >> 1; stride > 0; stride >>= 1)
+        for (int t = 0; t < stride; t++)
+            if (rv[t + stride] < rv[t]) { rv[t] = rv[t + stride]; ri[t] = ri[t + stride]; }
+    return ri[0];
+}
+
+/* dists/poss: the query's candidates in the order the scan visits them
+ * (local index = position in the probe-ordered concatenation). */
+static void v14_topck(const float* dists, const int32_t* poss, int64_t total, int ck,
+                      float* out_d, int32_t* out_p) {
+    float sd[V14_BLOCK * V14_KLOCAL];
+    int32_t sp[V14_BLOCK * V14_KLOCAL];
+    for (int t = 0; t < V14_BLOCK; t++) {
+        float ld[V14_KLOCAL];
+        int32_t lp[V14_KLOCAL];
+        for (int i = 0; i < V14_KLOCAL; i++) { ld[i] = INFINITY; lp[i] = -1; }
+        for (int64_t c = t; c < total; c += V14_BLOCK) {
+            const float dist = dists[c];
+            if (dist < ld[V14_KLOCAL - 1]) {
+                ld[V14_KLOCAL - 1] = dist;
+                lp[V14_KLOCAL - 1] = poss[c];
+                for (int i = V14_KLOCAL - 1; i > 0 && ld[i] < ld[i - 1]; --i) {
+                    const float td = ld[i - 1]; ld[i - 1] = ld[i]; ld[i] = td;
+                    const int32_t tp = lp[i - 1]; lp[i - 1] = lp[i]; lp[i] = tp;
+                }
+            }
+        }
+        for (int i = 0; i < V14_KLOCAL; i++) {
+            sd[t * V14_KLOCAL + i] = ld[i];
+            sp[t * V14_KLOCAL + i] = lp[i];
+        }
+    }
+    for (int c = 0; c < ck; c++) {
+        const int w = v14_block_argmin(sd, V14_BLOCK * V14_KLOCAL);
+        out_d[c] = w >= 0 ? sd[w] : INFINITY;
+        out_p[c] = w >= 0 ? sp[w] : -1;
+        if (w >= 0) sd[w] = INFINITY;
+    }
+}
+
+/* batched_topk_final_kernel (jhq_v14_streaming_add/search.cu:244-291): k
+ * rounds of the same block argmin over the ck composite distances; the id is
+ * list_ids[pos] of the winning slot, no winner -> (+inf, -1). */
+static void v14_final(float* comp, const int32_t* cid, int ck, int k, float* out_d,
+                      int32_t* out_i) {
+    for (int r = 0; r < k; r++) {
+        const int w = v14_block_argmin(comp, ck);
+        out_i[r] = (w >= 0) ? cid[w] : -1;
+        out_d[r] = (w >= 0) ? comp[w] : INFINITY;
+        if (w >= 0) comp[w] = INFINITY;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Whole search, one query at a time (jhq_v14_streaming_add/search.cu:315-386 */
-/* pipeline with jhq_v3_ivf exact selection).                                */
+/* pipeline).  mode 0: exact selection (jhq_v3_ivf/search.cu:22-25,189-279),  */
+/* mode 1: the reference's approximate selection above.                       */
 /* ------------------------------------------------------------------------ */
 int o_search(const o_index* ix, const float* q, int64_t nq, int k,
              float* out_dist, int32_t* out_ids,
@@ -531,6 +708,25 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
                 const int32_t* probes_in, int64_t nq, int k,
                 float* out_dist, int32_t* out_ids,
                 int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist) {
+    return o_search_mode(ix, q, q_rot_in, probes_in, nq, k, 0, out_dist, out_ids, dbg_probes,
+                         dbg_topck_pos, dbg_topck_dist);
+}
+
+typedef struct {
+    const o_index* ix;
+    const float *q, *q_rot_in;
+    const int32_t* probes_in;
+    int k, mode;
+    float* out_dist;
+    int32_t* out_ids;
+    int32_t *dbg_probes, *dbg_topck_pos;
+    float* dbg_topck_dist;
+} o_search_ctx;
+
+static void o_search_rows(void* cv, int64_t q0, int64_t q1) {
+    const o_search_ctx* a = (const o_search_ctx*)cv;
+    const o_index* ix = a->ix;
+    const int k = a->k, mode = a->mode;
     const int d = ix->d, M = ix->M, nlist = ix->nlist;
     const int nprobe = ix->nprobe < nlist ? ix->nprobe : nlist;
     const int ck = o_ck(ix->alpha, k);
@@ -547,11 +743,20 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
     int32_t* cid = (int32_t*)malloc((size_t)ck * sizeof(int32_t));
     for (int c = 0; c < nlist; c++) cids[c] = c;
 
-    for (int64_t qi = 0; qi < nq; qi++) {
-        if (q_rot_in) memcpy(q_rot, q_rot_in + qi * d, (size_t)d * sizeof(float));
-        else o_rotate(ix->P, q + qi * d, 1, d, q_rot);
-        if (probes_in) {
-            memcpy(probes, probes_in + qi * nprobe, (size_t)nprobe * sizeof(int32_t));
+    for (int64_t qi = q0; qi < q1; qi++) {
+        if (a->q_rot_in) memcpy(q_rot, a->q_rot_in + qi * d, (size_t)d * sizeof(float));
+        else {
+            /* y = Pi q, the fmaf chain of o_rotate */
+            const float* qq = a->q + qi * d;
+            for (int j = 0; j < d; j++) {
+                const float* pj = ix->P + (int64_t)j * d;
+                float acc = 0.0f;
+                for (int kk = 0; kk < d; kk++) acc = fmaf(qq[kk], pj[kk], acc);
+                q_rot[j] = acc;
+            }
+        }
+        if (a->probes_in) {
+            memcpy(probes, a->probes_in + qi * nprobe, (size_t)nprobe * sizeof(int32_t));
         } else {
             /* centroid scores: ||c||^2 - 2<c,q> (search.cu:31-32) */
             for (int c = 0; c < nlist; c++)
@@ -559,7 +764,8 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
                                  ix->cent_norms[c]);
             o_select_topk_pairs(scores, cids, nlist, nprobe, pd, probes);
         }
-        if (dbg_probes) memcpy(dbg_probes + qi * nprobe, probes, (size_t)nprobe * sizeof(int32_t));
+        if (a->dbg_probes)
+            memcpy(a->dbg_probes + qi * nprobe, probes, (size_t)nprobe * sizeof(int32_t));
 
         int64_t total = 0;
         for (int p = 0; p < nprobe; p++)
@@ -576,10 +782,11 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
                 t++;
             }
         }
-        o_select_topk_pairs(dists, poss, total, ck, cd, cp);
+        if (mode == 1) v14_topck(dists, poss, total, ck, cd, cp);
+        else o_select_topk_pairs(dists, poss, total, ck, cd, cp);
         free(dists); free(poss);
-        if (dbg_topck_pos) memcpy(dbg_topck_pos + qi * ck, cp, (size_t)ck * sizeof(int32_t));
-        if (dbg_topck_dist) memcpy(dbg_topck_dist + qi * ck, cd, (size_t)ck * sizeof(float));
+        if (a->dbg_topck_pos) memcpy(a->dbg_topck_pos + qi * ck, cp, (size_t)ck * sizeof(int32_t));
+        if (a->dbg_topck_dist) memcpy(a->dbg_topck_dist + qi * ck, cd, (size_t)ck * sizeof(float));
 
         /* residual refine: search.cu:198-242 */
         for (int c = 0; c < ck; c++) {
@@ -597,10 +804,24 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
             comp[c] = (cd[c] + d_res) + ix->list_corr[pos];
             cid[c] = ix->list_ids[pos];
         }
-        /* final top-k by (dist, id): jhq_v3_ivf/search.cu:242-279 */
-        o_select_topk_pairs(comp, cid, ck, k, out_dist + qi * k, out_ids + qi * k);
+        if (mode == 1) {
+            v14_final(comp, cid, ck, k, a->out_dist + qi * k, a->out_ids + qi * k);
+        } else {
+            /* final top-k by (dist, id): jhq_v3_ivf/search.cu:242-279 */
+            o_select_topk_pairs(comp, cid, ck, k, a->out_dist + qi * k, a->out_ids + qi * k);
+        }
     }
     free(q_rot); free(scores); free(cids); free(pd); free(probes); free(lut);
     free(cd); free(cp); free(comp); free(cid);
+}
+
+int o_search_mode(const o_index* ix, const float* q, const float* q_rot_in,
+                  const int32_t* probes_in, int64_t nq, int k, int mode,
+                  float* out_dist, int32_t* out_ids,
+                  int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist) {
+    if (mode != 0 && mode != 1) return -1;
+    o_search_ctx a = {ix, q, q_rot_in, probes_in, k, mode, out_dist, out_ids,
+                      dbg_probes, dbg_topck_pos, dbg_topck_dist};
+    o_parallel(nq, o_search_rows, &a);
     return 0;
 }

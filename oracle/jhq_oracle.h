@@ -38,6 +38,11 @@
  *   o_select_topk_pairs, o_search
  *                        numpy stable argsort brute force; composite distance
  *                        identity ||q - (yhat + rhat)||^2 + ||q||^2
+ *   o_search_mode(1)     (the reference's approximate selection) a
+ *                        pure-Python loop transcription of the 256-thread
+ *                        block on small cases, and the properties that fix
+ *                        it: exact whenever every thread holds at most 4
+ *                        candidates; a thread's 5th-best candidate is lost
  */
 #ifndef JHQ_ORACLE_H
 #define JHQ_ORACLE_H
@@ -47,6 +52,12 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Threads for the row-parallel loops (rotation, encode, assignment and
+ * search run one vector or query per thread, so results do not depend on
+ * the count).  Default 1. */
+void o_set_threads(int n);
+int  o_get_threads(void);
 
 /* ---- std::mt19937 and std::normal_distribution<float> (libstdc++) ---- */
 typedef struct {
@@ -143,6 +154,14 @@ int o_search_ex(const o_index* ix, const float* q, const float* q_rot_in,
                 const int32_t* probes_in, int64_t nq, int k,
                 float* out_dist, int32_t* out_ids,
                 int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist);
+/* mode 0: o_search_ex.  mode 1: the same pipeline with the reference's own
+ * approximate selection (jhq_v14_streaming_add/search.cu:105-195 per-thread
+ * top-4 + block argmin, and :244-291 final block argmin), to measure how
+ * often the reference's search differs from exact selection. */
+int o_search_mode(const o_index* ix, const float* q, const float* q_rot_in,
+                  const int32_t* probes_in, int64_t nq, int k, int mode,
+                  float* out_dist, int32_t* out_ids,
+                  int32_t* dbg_probes, int32_t* dbg_topck_pos, float* dbg_topck_dist);
 /* ck = max(k, ceil(alpha * k)) (jhq_v14_streaming_add/search.cu:408) */
 int o_ck(float alpha, int k);
 

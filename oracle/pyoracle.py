@@ -60,6 +60,10 @@ _SIGS = {
     "o_search": (_I, [ctypes.POINTER(_OIndex), _VP, _I64, _I, _VP, _VP, _VP, _VP, _VP]),
     "o_search_ex": (_I, [ctypes.POINTER(_OIndex), _VP, _VP, _VP, _I64, _I, _VP, _VP, _VP, _VP,
                          _VP]),
+    "o_search_mode": (_I, [ctypes.POINTER(_OIndex), _VP, _VP, _VP, _I64, _I, _I, _VP, _VP, _VP,
+                           _VP, _VP]),
+    "o_set_threads": (None, [_I]),
+    "o_get_threads": (_I, []),
 }
 
 _REF_SIGS = {
@@ -106,6 +110,20 @@ def ref():
         except OSError:
             _ref = None
     return _ref
+
+
+def set_threads(n):
+    """Threads of the oracle's row-parallel loops (results do not depend on it)."""
+    lib().o_set_threads(int(n))
+
+
+def get_threads():
+    return int(lib().o_get_threads())
+
+
+def default_threads():
+    """All host cores up to 16 (a one-GPU box's CPU share)."""
+    return max(1, min(os.cpu_count() or 1, 16))
 
 
 def _p(a):
@@ -392,9 +410,11 @@ class OracleIndex:
          s.list_codes, s.list_res, s.list_corr) = [_p(a) for a in self._keep]
         return s
 
-    def search(self, q, k, debug=False, q_rot=None, probes=None):
+    def search(self, q, k, debug=False, q_rot=None, probes=None, mode=0):
         """Reference pipeline per query.  Stage-wise parity: q_rot [nq, d] replaces
-        the rotation and probes [nq, nprobe] replaces the probe selection."""
+        the rotation and probes [nq, nprobe] replaces the probe selection.
+        mode 0: exact selection; mode 1: the reference's approximate per-thread
+        top-4 selection (jhq_v14_streaming_add/search.cu:105-195, 244-291)."""
         q = _c(q, np.float32)
         nq = q.shape[0]
         if q_rot is not None:
@@ -410,10 +430,10 @@ class OracleIndex:
         tdist = np.empty((nq, ck), np.float32) if debug else None
         s = self._struct()
         pr_out = np.empty((nq, self.nprobe), np.int32) if debug else None
-        lib().o_search_ex(ctypes.byref(s), _p(q), _p(q_rot) if q_rot is not None else None,
-                          _p(probes) if probes is not None else None, nq, k, _p(dists),
-                          _p(ids), _p(pr_out) if debug else None, _p(tpos) if debug else None,
-                          _p(tdist) if debug else None)
+        lib().o_search_mode(ctypes.byref(s), _p(q), _p(q_rot) if q_rot is not None else None,
+                            _p(probes) if probes is not None else None, nq, k, int(mode),
+                            _p(dists), _p(ids), _p(pr_out) if debug else None,
+                            _p(tpos) if debug else None, _p(tdist) if debug else None)
         if debug:
             return dict(dists=dists, ids=ids, probes=pr_out, topck_pos=tpos, topck_dist=tdist)
         return dists, ids

@@ -13,6 +13,18 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X); runs the HIP product")
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _oracle_threads():
+    """The checker's row loops on all host cores (at most 16); its results do
+    not depend on the thread count."""
+    import pyoracle as po
+    try:
+        po.set_threads(po.default_threads())
+    except ImportError:
+        pass  # oracle not built: the tests that need it fail on their own
+    yield
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """torch on the HIP device; GPU tests fail loudly when none is visible."""

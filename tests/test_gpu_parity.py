@@ -191,6 +191,7 @@ def test_search_device_pipelined_batches(gpu, name):
     case = CASES[IDS.index(name)]
     g, o, base, q, k = _build(case)
     batch = case[-1]
+    g.reserve(k)  # device searches run in the reserved workspace only
     qq = np.ascontiguousarray(np.tile(q, (1 + 5 * batch // q.shape[0], 1))[:5 * batch + 3])
     d1, i1 = g.search(qq, k)
     qt = torch.from_numpy(qq).to(gpu)

@@ -178,9 +178,13 @@ def test_rotation_known_seed_is_stable():
 
 
 # -- the reference code itself on fresh inputs (when oracle/_ref is built) ---
-@pytest.mark.skipif(po.ref() is None, reason="oracle/_ref/libjhq_ref.so not built")
 def test_fresh_inputs_vs_reference_build():
+    # checked at run time, so collecting this module never loads the library
+    if not os.path.exists(po.REF_LIB):
+        pytest.skip("oracle/_ref/libjhq_ref.so not built")
     r = po.ref()
+    if r is None:
+        pytest.skip("oracle/_ref/libjhq_ref.so does not load")
     rng = np.random.default_rng(99)
     for (d, M, B) in CB_SHAPES:
         sigma = 0.05
