@@ -259,6 +259,17 @@ int jhq_k_select_probes(const float* d_scores, int B, int nlist, int P,
                         const int32_t* d_list_sizes, int32_t* d_probes,
                         int32_t* d_gofs, int32_t* d_qtot, void* stream);
 
+/* jhq_k_assign without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  Same arguments
+ * and results as jhq_k_assign, but the per-row keys live in a fixed device
+ * array of 2^20 entries (8 MiB per device, held until the process ends), so
+ * n is at most 1048576 (larger n fails with JHQ_EINVAL).  Calls that overlap
+ * on one device share that array and race. */
+int jhq_k_assign_noalloc(const float* d_y, int64_t n, int d, const float* d_cent,
+                         const float* d_cent_norms, int nlist, int32_t* d_assign,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

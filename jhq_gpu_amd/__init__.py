@@ -19,6 +19,7 @@ import numpy as np
 __all__ = [
     "Params", "JHQGpuIndex", "JHQError", "JHQDeviceError", "JHQNotBuiltError",
     "lib", "lib_path", "k_rotate", "k_primary_encode", "k_residual_encode", "k_assign",
+    "k_assign_noalloc",
     "STEP_NAMES",
 ]
 
@@ -112,6 +113,7 @@ _SIGS = {
     "jhq_k_residual_encode": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _I,
                                    _I, _I, _I, _VP]),
     "jhq_k_assign": (_I, [_VP, _I64, _I, _VP, _VP, _I, _VP, _VP]),
+    "jhq_k_assign_noalloc": (_I, [_VP, _I64, _I, _VP, _VP, _I, _VP, _VP]),
     "jhq_k_select_probes": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
 }
 
@@ -401,6 +403,13 @@ def k_assign(y, cent, norms, assign, stream=None):
     n, d = y.shape
     _check(lib().jhq_k_assign(_dptr(y), int(n), int(d), _dptr(cent), _dptr(norms),
                               int(cent.shape[0]), _dptr(assign), _stream(stream)))
+
+
+def k_assign_noalloc(y, cent, norms, assign, stream=None):
+    """k_assign with no allocation (keys in a fixed 2^20-row device array)."""
+    n, d = y.shape
+    _check(lib().jhq_k_assign_noalloc(_dptr(y), int(n), int(d), _dptr(cent), _dptr(norms),
+                                      int(cent.shape[0]), _dptr(assign), _stream(stream)))
 
 
 def k_select_probes(scores, list_sizes, P, probes, gofs, qtot, stream=None):

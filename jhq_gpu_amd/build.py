@@ -34,7 +34,8 @@ def _run(cmd):
 
 
 def build_engine(verbose=False):
-    """Compile kernels.hip, jhq_capi.hip, kmeans.hip and host_train.cpp into libjhq_amd.so."""
+    """Compile kernels.hip, jhq_capi.hip, kmeans.hip, noalloc.hip and host_train.cpp into
+    libjhq_amd.so."""
     os.makedirs(BUILD, exist_ok=True)
     jobs = [
         ([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, "kernels.hip"),
@@ -43,6 +44,8 @@ def build_engine(verbose=False):
                                 "-o", os.path.join(BUILD, "jhq_capi.o")]),
         ([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, "kmeans.hip"),
                                 "-o", os.path.join(BUILD, "kmeans.o")]),
+        ([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, "noalloc.hip"),
+                                "-o", os.path.join(BUILD, "noalloc.o")]),
         (["g++"] + CXX_FLAGS + ["-c", os.path.join(CSRC, "host_train.cpp"),
                                 "-o", os.path.join(BUILD, "host_train.o")]),
     ]
@@ -61,7 +64,8 @@ def build_engine(verbose=False):
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-pthread", "-o", tmp,
           os.path.join(BUILD, "kernels.o"), os.path.join(BUILD, "jhq_capi.o"),
-          os.path.join(BUILD, "kmeans.o"), os.path.join(BUILD, "host_train.o")])
+          os.path.join(BUILD, "kmeans.o"), os.path.join(BUILD, "noalloc.o"),
+          os.path.join(BUILD, "host_train.o")])
     os.replace(tmp, LIB)
     return LIB
 
