@@ -259,6 +259,43 @@ int jhq_k_select_probes(const float* d_scores, int B, int nlist, int P,
                         const int32_t* d_list_sizes, int32_t* d_probes,
                         int32_t* d_gofs, int32_t* d_qtot, void* stream);
 
+/* build_byte_lut_kernel — v14/search.cu:65-91: d_byte_lut[b][m][v] =
+ * sum_{k<Ds} (q_rot[b][m*Ds+k] - c1d[(v >> k*bits_per_dim) & (K1D-1)])^2,
+ * one fma per k, k ascending ([B][M][256] floats).  The search pipeline
+ * builds the same entries in LDS inside its scan. */
+int jhq_k_build_lut(const float* d_q_rot, const float* d_c1d, float* d_byte_lut, int B, int d,
+                    int M, int Ds, int K1D, int bits_per_dim, void* stream);
+
+/* scan_ivf_coalesced_kernel — v14/search.cu:105-195, same inputs: the byte
+ * LUT [B][M][256], probe_ids [B][nprobe], probe_offsets [B][nprobe+1] (the
+ * probed lists' sizes as a prefix), list_offsets [nlist+1], the primary codes
+ * transposed to [M][N] (v14/jhq_gpu_index.cu:512-517) and query_total [B].
+ * dist = sum over m ascending of lut[m][code_m]; per query the ck smallest
+ * (dist, position) pairs, ascending, exact (the reference keeps 4 candidates
+ * per thread and is approximate, :116,153-161); unfilled = (+inf, -1). */
+int jhq_k_scan_topck(const float* d_byte_lut, const int32_t* d_probe_ids,
+                     const int32_t* d_probe_offsets, const int32_t* d_list_offsets,
+                     const uint8_t* d_list_primary_t, const int32_t* d_query_total,
+                     float* d_topck_primary, int32_t* d_topck_pos, int B, int nprobe, int M,
+                     int64_t N, int ck, void* stream);
+
+/* build_residual_lut_batched_kernel + residual_refine_batched_kernel —
+ * v14/search.cu:198-242: comp[b][c] = (topck_primary + sum over j ascending of
+ * (q_rot[b][j] - res_c1d[r_j])^2) + list_corr[pos], r_j the Br-bit residual
+ * code of dimension j (Br = 4: even j in the low nibble); pos < 0 -> +inf.
+ * The reference's summation order (the search pipeline's fused refine adds 16
+ * partial sums instead). */
+int jhq_k_refine(const float* d_q_rot, const float* d_res_c1d, const int32_t* d_topck_pos,
+                 const float* d_topck_primary, const uint8_t* d_list_res, const float* d_list_corr,
+                 float* d_comp_dists, int B, int ck, int d, int Kr, int Br, int bpv, void* stream);
+
+/* batched_topk_final_kernel — v14/search.cu:244-291: per query the k smallest
+ * (comp, id) pairs, id = list_ids[pos], ascending by (dist, id)
+ * (jhq_v3_ivf/search.cu:242-279); unfilled = (+inf, -1). */
+int jhq_k_final_topk(const float* d_comp_dists, const int32_t* d_topck_pos,
+                     const int32_t* d_list_ids, float* d_final_dists, int32_t* d_final_ids, int B,
+                     int ck, int k, void* stream);
+
 /* jhq_k_assign without any allocation.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops, harnesses that forbid hipMalloc).  Same arguments

@@ -19,7 +19,7 @@ import numpy as np
 __all__ = [
     "Params", "JHQGpuIndex", "JHQError", "JHQDeviceError", "JHQNotBuiltError",
     "lib", "lib_path", "k_rotate", "k_primary_encode", "k_residual_encode", "k_assign",
-    "k_assign_noalloc",
+    "k_assign_noalloc", "k_build_lut", "k_scan_topck", "k_refine", "k_final_topk",
     "STEP_NAMES",
 ]
 
@@ -115,6 +115,10 @@ _SIGS = {
     "jhq_k_assign": (_I, [_VP, _I64, _I, _VP, _VP, _I, _VP, _VP]),
     "jhq_k_assign_noalloc": (_I, [_VP, _I64, _I, _VP, _VP, _I, _VP, _VP]),
     "jhq_k_select_probes": (_I, [_VP, _I, _I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "jhq_k_build_lut": (_I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP]),
+    "jhq_k_scan_topck": (_I, [_VP] * 8 + [_I, _I, _I, _I64, _I, _VP]),
+    "jhq_k_refine": (_I, [_VP] * 7 + [_I] * 6 + [_VP]),
+    "jhq_k_final_topk": (_I, [_VP] * 5 + [_I, _I, _I, _VP]),
 }
 
 
@@ -418,3 +422,44 @@ def k_select_probes(scores, list_sizes, P, probes, gofs, qtot, stream=None):
     _check(lib().jhq_k_select_probes(_dptr(scores), int(B), int(nlist), int(P),
                                      _dptr(list_sizes), _dptr(probes), _dptr(gofs), _dptr(qtot),
                                      _stream(stream)))
+
+
+def k_build_lut(q_rot, c1d, lut, M, stream=None):
+    """q_rot [B, d], c1d [K1D] -> lut [B, M, 256] (device tensors)."""
+    B, d = q_rot.shape
+    K1D = int(c1d.shape[0])
+    _check(lib().jhq_k_build_lut(_dptr(q_rot), _dptr(c1d), _dptr(lut), int(B), int(d), int(M),
+                                 int(d // M), K1D, K1D.bit_length() - 1, _stream(stream)))
+
+
+def k_scan_topck(lut, probe_ids, probe_offsets, list_offsets, primary_t, query_total,
+                 topck_primary, topck_pos, stream=None):
+    """Reference-layout scan: lut [B, M, 256], probe_ids [B, P], probe_offsets
+    [B, P+1], list_offsets [nlist+1], primary_t [M, N], query_total [B] ->
+    topck_primary / topck_pos [B, ck]."""
+    B, M = int(lut.shape[0]), int(lut.shape[1])
+    P = int(probe_ids.shape[1])
+    N = int(primary_t.shape[1])
+    ck = int(topck_pos.shape[1])
+    _check(lib().jhq_k_scan_topck(_dptr(lut), _dptr(probe_ids), _dptr(probe_offsets),
+                                  _dptr(list_offsets), _dptr(primary_t), _dptr(query_total),
+                                  _dptr(topck_primary), _dptr(topck_pos), B, P, M, N, ck,
+                                  _stream(stream)))
+
+
+def k_refine(q_rot, res_c1d, topck_pos, topck_primary, list_res, list_corr, comp, Br,
+             stream=None):
+    B, d = q_rot.shape
+    ck = int(topck_pos.shape[1])
+    _check(lib().jhq_k_refine(_dptr(q_rot), _dptr(res_c1d), _dptr(topck_pos),
+                              _dptr(topck_primary), _dptr(list_res), _dptr(list_corr),
+                              _dptr(comp), int(B), ck, int(d), int(res_c1d.shape[0]), int(Br),
+                              int(list_res.shape[1]), _stream(stream)))
+
+
+def k_final_topk(comp, topck_pos, list_ids, final_dists, final_ids, stream=None):
+    B, ck = comp.shape
+    k = int(final_ids.shape[1])
+    _check(lib().jhq_k_final_topk(_dptr(comp), _dptr(topck_pos), _dptr(list_ids),
+                                  _dptr(final_dists), _dptr(final_ids), int(B), int(ck), k,
+                                  _stream(stream)))

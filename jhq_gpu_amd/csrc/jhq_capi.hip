@@ -1592,6 +1592,64 @@ int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent, const 
     return JHQ_OK;
 }
 
+int jhq_k_build_lut(const float* d_q_rot, const float* d_c1d, float* d_byte_lut, int B, int d,
+                    int M, int Ds, int K1D, int bits_per_dim, void* stream) {
+    if (!d_q_rot || !d_c1d || !d_byte_lut || B < 0 || M <= 0 || Ds <= 0 || Ds * M != d ||
+        bits_per_dim < 0 || bits_per_dim > 8 || (1 << bits_per_dim) != K1D)
+        return fail(JHQ_EINVAL, "bad argument");
+    JHQ_HIP(jhq::stage_byte_lut(d_q_rot, d_c1d, d_byte_lut, B, d, M, Ds, K1D, bits_per_dim,
+                                static_cast<hipStream_t>(stream)));
+    return JHQ_OK;
+}
+
+int jhq_k_scan_topck(const float* d_byte_lut, const int32_t* d_probe_ids,
+                     const int32_t* d_probe_offsets, const int32_t* d_list_offsets,
+                     const uint8_t* d_list_primary_t, const int32_t* d_query_total,
+                     float* d_topck_primary, int32_t* d_topck_pos, int B, int nprobe, int M,
+                     int64_t N, int ck, void* stream) {
+    if (!d_byte_lut || !d_probe_ids || !d_probe_offsets || !d_list_offsets || !d_list_primary_t ||
+        !d_query_total || !d_topck_primary || !d_topck_pos || B < 0 || nprobe <= 0 || M <= 0 ||
+        N < 0 || N > INT32_MAX || ck <= 0)
+        return fail(JHQ_EINVAL, "bad argument");
+    hipError_t e = jhq::stage_scan_topck(d_byte_lut, d_probe_ids, d_probe_offsets, d_list_offsets,
+                                         d_list_primary_t, d_query_total, d_topck_primary,
+                                         d_topck_pos, B, nprobe, M, N, ck,
+                                         static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue)
+        return fail(JHQ_EINVAL, "nprobe=" + std::to_string(nprobe) + ", ck=" + std::to_string(ck) +
+                                    ": the selection state does not fit in LDS");
+    JHQ_HIP(e);
+    return JHQ_OK;
+}
+
+int jhq_k_refine(const float* d_q_rot, const float* d_res_c1d, const int32_t* d_topck_pos,
+                 const float* d_topck_primary, const uint8_t* d_list_res, const float* d_list_corr,
+                 float* d_comp_dists, int B, int ck, int d, int Kr, int Br, int bpv, void* stream) {
+    if (!d_q_rot || !d_res_c1d || !d_topck_pos || !d_topck_primary || !d_list_res ||
+        !d_list_corr || !d_comp_dists || B < 0 || ck <= 0 || d <= 0 || (Br != 4 && Br != 8) ||
+        Kr <= 0 || Kr > (1 << Br) || bpv != (d * Br + 7) / 8)
+        return fail(JHQ_EINVAL, "bad argument");
+    JHQ_HIP(jhq::stage_refine(d_q_rot, d_res_c1d, d_topck_pos, d_topck_primary, d_list_res,
+                              d_list_corr, d_comp_dists, B, ck, d, Br, bpv,
+                              static_cast<hipStream_t>(stream)));
+    return JHQ_OK;
+}
+
+int jhq_k_final_topk(const float* d_comp_dists, const int32_t* d_topck_pos,
+                     const int32_t* d_list_ids, float* d_final_dists, int32_t* d_final_ids, int B,
+                     int ck, int k, void* stream) {
+    if (!d_comp_dists || !d_topck_pos || !d_list_ids || !d_final_dists || !d_final_ids || B < 0 ||
+        ck <= 0 || k <= 0)
+        return fail(JHQ_EINVAL, "bad argument");
+    hipError_t e = jhq::stage_final_topk(d_comp_dists, d_topck_pos, d_list_ids, d_final_dists,
+                                         d_final_ids, B, ck, k, static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue)
+        return fail(JHQ_EINVAL, "ck=" + std::to_string(ck) + ", k=" + std::to_string(k) +
+                                    ": the selection state does not fit in LDS");
+    JHQ_HIP(e);
+    return JHQ_OK;
+}
+
 int jhq_k_select_probes(const float* d_scores, int B, int nlist, int P,
                         const int32_t* d_list_sizes, int32_t* d_probes, int32_t* d_gofs,
                         int32_t* d_qtot, void* stream) {

@@ -138,4 +138,23 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
                        const float* list_corr, const int32_t* list_ids, float* out_d,
                        int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s);
 
+// Search stages in the reference's data layout (kernel-granular C-ABI):
+// byte LUT [B][M][256] (v14/search.cu:65-91); exact top-ck per query over
+// [M][N] transposed codes and list_offsets (v14/search.cu:105-195); residual
+// refine in the reference's order (v14/search.cu:198-242); exact final top-k
+// by (dist, id) (v14/search.cu:244-291).
+hipError_t stage_byte_lut(const float* q_rot, const float* c1d, float* lut, int B, int d, int M,
+                          int Ds, int K1D, int bpd, hipStream_t s);
+hipError_t stage_scan_topck(const float* byte_lut, const int32_t* probe_ids,
+                            const int32_t* probe_offsets, const int32_t* list_offsets,
+                            const uint8_t* primary_t, const int32_t* query_total, float* out_d,
+                            int32_t* out_p, int B, int nprobe, int M, int64_t N, int ck,
+                            hipStream_t s);
+hipError_t stage_refine(const float* q_rot, const float* res_c1d, const int32_t* topck_pos,
+                        const float* topck_primary, const uint8_t* list_res,
+                        const float* list_corr, float* comp, int B, int ck, int d, int Br,
+                        int bpv, hipStream_t s);
+hipError_t stage_final_topk(const float* comp, const int32_t* topck_pos, const int32_t* list_ids,
+                            float* out_d, int32_t* out_i, int B, int ck, int k, hipStream_t s);
+
 }  // namespace jhq

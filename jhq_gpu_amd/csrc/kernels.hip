@@ -3543,6 +3543,231 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Search stages in the reference's own data layout, for the kernel-granular
+// C-ABI (stage-wise parity and callers of the reference's kernels): a global
+// byte LUT [B][M][256], primary codes transposed to [M][N] with list_offsets
+// (v14/jhq_gpu_index.cu:488-517), per-query probe ids and prefix offsets.
+// Every stage follows the reference's arithmetic order; selection is exact
+// by (dist, position) and (dist, id) (jhq_v3_ivf/search.cu:22-25).
+// ---------------------------------------------------------------------------
+
+// build_byte_lut_kernel (v14/search.cu:65-91): lut[b][m][v] = sum over
+// k < Ds of (q[b][m*Ds+k] - c1d[digit_k(v)])^2, one fma per k, k ascending.
+__global__ void stage_lut_kernel(const float* __restrict__ q_rot, const float* __restrict__ c1d,
+                                 float* __restrict__ lut, int B, int d, int M, int Ds, int K1D,
+                                 int bpd) {
+    const int64_t total = (int64_t)B * M * 256;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = i / ((int64_t)M * 256);
+        const int loc = (int)(i - b * (int64_t)M * 256);
+        const int m = loc >> 8, v = loc & 255;
+        const float* qm = q_rot + b * d + (int64_t)m * Ds;
+        float acc = 0.0f;
+        for (int k = 0; k < Ds && k < 8; k++) {
+            const float df = qm[k] - c1d[(v >> (k * bpd)) & (K1D - 1)];
+            acc = fmaf(df, df, acc);
+        }
+        lut[i] = acc;
+    }
+}
+
+// scan_ivf_coalesced_kernel (v14/search.cu:105-195) with exact selection: one
+// workgroup per query; candidate t of the probed lists laid end to end (probe
+// p holds t in [offs[p], offs[p+1])) is position list_offsets[probe] +
+// t - offs[p]; dist = sum over m ascending of lut[m][code_m], the codes read
+// from primary_t[m*N + pos] (consecutive threads, consecutive positions).
+// The query's top-ck by (dist, pos) goes to out_d / out_p ascending, unfilled
+// = (+inf, -1).  LUT_LDS: the query's LUT is copied to LDS first (M <= ~150).
+template <int NT, bool LUT_LDS>
+__global__ void __launch_bounds__(NT)
+stage_scan_kernel(const float* __restrict__ byte_lut, const int32_t* __restrict__ probe_ids,
+                  const int32_t* __restrict__ probe_offsets, const int32_t* __restrict__ list_offsets,
+                  const uint8_t* __restrict__ primary_t, const int32_t* __restrict__ query_total,
+                  float* __restrict__ out_d, int32_t* __restrict__ out_p, int nprobe, int M,
+                  int64_t N, int ck) {
+    constexpr int CPT = 4;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float* glut = byte_lut + (int64_t)b * M * 256;
+    float* llut = (float*)smem;
+    StreamSel S;
+    int32_t* soff = (int32_t*)stream_carve<NT>(smem + (LUT_LDS ? (size_t)M * 1024 : 0), ck, &S);
+    int32_t* sbase = soff + nprobe + 1;
+    if (LUT_LDS)
+        for (int i = tid; i < M * 256; i += NT) llut[i] = glut[i];
+    for (int i = tid; i <= nprobe; i += NT) soff[i] = probe_offsets[(int64_t)b * (nprobe + 1) + i];
+    for (int i = tid; i < nprobe; i += NT) sbase[i] = list_offsets[probe_ids[(int64_t)b * nprobe + i]];
+    stream_begin<NT>(S);
+    __syncthreads();
+    const float* L = LUT_LDS ? llut : glut;
+    const int total = query_total[b];
+    for (int base = 0; base < total; base += NT * CPT) {
+        uint32_t o[CPT], tg[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int t = base + j * NT + tid;
+            o[j] = ~0u;
+            tg[j] = 0u;
+            if (t < total) {
+                int lo = 0, hi = nprobe - 1;  // last probe with offs[p] <= t
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (soff[mid] <= t) lo = mid;
+                    else hi = mid - 1;
+                }
+                const int64_t pos = (int64_t)sbase[lo] + (t - soff[lo]);
+                float dist = 0.0f;
+                for (int m = 0; m < M; m++) dist += L[m * 256 + primary_t[(int64_t)m * N + pos]];
+                o[j] = f2ord(dist);
+                tg[j] = (uint32_t)pos;
+            }
+        }
+        stream_round<NT, CPT>(S, ck, o, tg);
+    }
+    const int kk = stream_end<NT>(S, ck);
+    for (int i = tid; i < ck; i += NT) {
+        const unsigned long long kv = i < kk ? S.kout[i] : ~0ull;
+        out_d[(int64_t)b * ck + i] = i < kk ? ord2f((uint32_t)(kv >> 32)) : __builtin_huge_valf();
+        out_p[(int64_t)b * ck + i] = i < kk ? (int32_t)(uint32_t)(kv & 0xffffffffull) : -1;
+    }
+}
+
+// build_residual_lut_batched_kernel + residual_refine_batched_kernel
+// (v14/search.cu:198-242), one thread per short-list entry:
+// comp = (primary + sum over j ascending of (q[j] - res_c1d[r_j])^2) + corr[pos]
+// with each square rounded before it is added (the reference stores them in a
+// LUT first); pos < 0 gives +inf.
+__global__ void stage_refine_kernel(const float* __restrict__ q_rot,
+                                    const float* __restrict__ res_c1d,
+                                    const int32_t* __restrict__ topck_pos,
+                                    const float* __restrict__ topck_primary,
+                                    const uint8_t* __restrict__ list_res,
+                                    const float* __restrict__ list_corr, float* __restrict__ comp,
+                                    int B, int ck, int d, int Br, int bpv) {
+    const int64_t total = (int64_t)B * ck;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t pos = topck_pos[i];
+        if (pos < 0) {
+            comp[i] = __builtin_huge_valf();
+            continue;
+        }
+        const float* q = q_rot + (i / ck) * d;
+        const uint8_t* rc = list_res + (int64_t)pos * bpv;
+        float dres = 0.0f;
+        for (int j = 0; j < d; j++) {
+            const int ri = (Br == 4) ? ((j & 1) ? (rc[j >> 1] >> 4) : (rc[j >> 1] & 0x0F)) : rc[j];
+            const float df = q[j] - res_c1d[ri];
+            const float sq = df * df;
+            dres = dres + sq;
+        }
+        comp[i] = (topck_primary[i] + dres) + list_corr[pos];
+    }
+}
+
+// batched_topk_final_kernel (v14/search.cu:244-291) with exact (dist, id)
+// order: per query the k smallest composite distances among entries with
+// pos >= 0 and a finite distance, id = list_ids[pos]; unfilled = (+inf, -1).
+// Positions within a row are distinct (as the scan emits them).
+template <int NT>
+__global__ void __launch_bounds__(NT)
+stage_final_kernel(const float* __restrict__ comp, const int32_t* __restrict__ topck_pos,
+                   const int32_t* __restrict__ list_ids, float* __restrict__ out_d,
+                   int32_t* __restrict__ out_i, int ck, int k) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned long long* keys = (unsigned long long*)smem;  // [ck]
+    unsigned long long* kout = keys + ck;                  // [k]
+    unsigned long long* ktmp = kout + k;                   // [k]
+    SelState* st = (SelState*)(ktmp + k);
+    int* kidx = (int*)(st + 1);                            // [k]
+    int* cnt = kidx + k;
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (tid == 0) *cnt = 0;
+    __syncthreads();
+    for (int c = tid; c < ck; c += NT) {
+        const int32_t pos = topck_pos[(int64_t)b * ck + c];
+        const float dv = comp[(int64_t)b * ck + c];
+        if (pos >= 0 && dv < __builtin_huge_valf()) {
+            const int at = atomicAdd(cnt, 1);
+            keys[at] = ((unsigned long long)f2ord(dv) << 32) | (uint32_t)list_ids[pos];
+        }
+    }
+    __syncthreads();
+    const int n = *cnt;
+    const int kf = n < k ? n : k;
+    if (kf > 0) select_keys<NT>(keys, n, kf, kout, kidx, ktmp, st);
+    for (int r = tid; r < k; r += NT) {
+        out_d[(int64_t)b * k + r] = r < kf ? ord2f((uint32_t)(kout[r] >> 32)) : __builtin_huge_valf();
+        out_i[(int64_t)b * k + r] = r < kf ? (int32_t)(uint32_t)(kout[r] & 0xffffffffull) : -1;
+    }
+}
+
+static int grid_for(int64_t total, int nt) {
+    const int64_t g = (total + nt - 1) / nt;
+    return (int)(g < 65536 ? (g > 0 ? g : 1) : 65536);
+}
+
+hipError_t stage_byte_lut(const float* q_rot, const float* c1d, float* lut, int B, int d, int M,
+                          int Ds, int K1D, int bpd, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(stage_lut_kernel, dim3(grid_for((int64_t)B * M * 256, 256)), dim3(256), 0,
+                       s, q_rot, c1d, lut, B, d, M, Ds, K1D, bpd);
+    return hipGetLastError();
+}
+
+size_t stage_scan_lds(int M, int nprobe, int ck, bool lut_lds) {
+    return (lut_lds ? (size_t)M * 1024 : 0) + stream_lds_bytes(512, ck) + (size_t)(2 * nprobe + 1) * 4;
+}
+
+hipError_t stage_scan_topck(const float* byte_lut, const int32_t* probe_ids,
+                            const int32_t* probe_offsets, const int32_t* list_offsets,
+                            const uint8_t* primary_t, const int32_t* query_total, float* out_d,
+                            int32_t* out_p, int B, int nprobe, int M, int64_t N, int ck,
+                            hipStream_t s) {
+    constexpr int NT = 512;
+    if (B <= 0) return hipSuccess;
+    static const int mx1 = allow_max_lds((const void*)stage_scan_kernel<NT, true>);
+    static const int mx0 = allow_max_lds((const void*)stage_scan_kernel<NT, false>);
+    const size_t l1 = stage_scan_lds(M, nprobe, ck, true), l0 = stage_scan_lds(M, nprobe, ck, false);
+    if ((int)l1 <= mx1) {
+        hipLaunchKernelGGL((stage_scan_kernel<NT, true>), dim3(B), dim3(NT), l1, s, byte_lut,
+                           probe_ids, probe_offsets, list_offsets, primary_t, query_total, out_d,
+                           out_p, nprobe, M, N, ck);
+    } else if ((int)l0 <= mx0) {
+        hipLaunchKernelGGL((stage_scan_kernel<NT, false>), dim3(B), dim3(NT), l0, s, byte_lut,
+                           probe_ids, probe_offsets, list_offsets, primary_t, query_total, out_d,
+                           out_p, nprobe, M, N, ck);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t stage_refine(const float* q_rot, const float* res_c1d, const int32_t* topck_pos,
+                        const float* topck_primary, const uint8_t* list_res,
+                        const float* list_corr, float* comp, int B, int ck, int d, int Br,
+                        int bpv, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(stage_refine_kernel, dim3(grid_for((int64_t)B * ck, 256)), dim3(256), 0, s,
+                       q_rot, res_c1d, topck_pos, topck_primary, list_res, list_corr, comp, B, ck,
+                       d, Br, bpv);
+    return hipGetLastError();
+}
+
+hipError_t stage_final_topk(const float* comp, const int32_t* topck_pos, const int32_t* list_ids,
+                            float* out_d, int32_t* out_i, int B, int ck, int k, hipStream_t s) {
+    constexpr int NT = 256;
+    if (B <= 0) return hipSuccess;
+    const size_t lds = (size_t)ck * 8 + (size_t)k * 16 + sizeof(SelState) + (size_t)k * 4 + 16;
+    static const int mx = allow_max_lds((const void*)stage_final_kernel<NT>);
+    if ((int)lds > mx) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(stage_final_kernel<NT>, dim3(B), dim3(NT), lds, s, comp, topck_pos,
+                       list_ids, out_d, out_i, ck, k);
+    return hipGetLastError();
+}
+
 }  // namespace jhq
 
 #ifdef JHQ_PHASE_TIMING
