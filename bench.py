@@ -65,6 +65,9 @@ def parse():
                          "first --nprobe/--alpha plus one 256 MiB device copy (the counter "
                          "calibration kernel), print per-step times and exit")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--index", type=str, default=None,
+                    help="configs 3/4 with --profile-batches: load the index from this file "
+                         "(jhq_save format) if it exists, else build it and save it there")
     ap.add_argument("--seed", type=int, default=None,
                     help="data seed (default 0x4A48510000 + config)")
     return ap.parse_args()
@@ -567,6 +570,15 @@ def bench_bytes(args, cf):
     npb = int((args.nprobe or str(cf["NPROBE"])).split(",")[0])
     alpha = float((args.alpha or "4").split(",")[0])
 
+    if args.profile_batches > 0 and args.index and os.path.exists(args.index):
+        # counter runs over a saved index: only the queries are generated
+        _, means = gen_bytes(torch, dev, 0, D, NCOMP, seed, cf["kind"])
+        qb, _ = gen_bytes(torch, dev, NQ, D, NCOMP, seed + 0x100, cf["kind"], means)
+        t0 = time.time()
+        ix = jg.JHQGpuIndex.load(args.index)
+        log(f"loaded {args.index} ({ix.ntotal} vectors) in {time.time() - t0:.1f}s")
+        profile_mode(torch, dev, ix, qb.float(), K, BATCH, npb, alpha, args.profile_batches)
+        return
     t0 = time.time()
     base, means = gen_bytes(torch, dev, N, D, NCOMP, seed, cf["kind"])
     qb, _ = gen_bytes(torch, dev, NQ, D, NCOMP, seed + 0x100, cf["kind"], means)
@@ -580,10 +592,11 @@ def bench_bytes(args, cf):
     qf = qb.float()
     log(f"host copy {time.time() - t0:.1f}s")
 
-    t0 = time.time()
-    gt_i, gt_d = ground_truth_int(torch, base, qf)
-    torch.cuda.synchronize()
-    log(f"ground truth {time.time() - t0:.1f}s")
+    if args.profile_batches <= 0:
+        t0 = time.time()
+        gt_i, gt_d = ground_truth_int(torch, base, qf)
+        torch.cuda.synchronize()
+        log(f"ground truth {time.time() - t0:.1f}s")
 
     p = jg.Params(M=M, B=8, Br=4, alpha=alpha, nlist=NLIST, nprobe=npb, ivf_iters=8,
                   batch_size=BATCH, seed=42)
@@ -598,6 +611,15 @@ def bench_bytes(args, cf):
     t_add = time.time() - t0
     log(f"add {t_add:.1f}s ({N / t_add / 1e6:.2f} M vectors/s)")
     del hb
+    if args.profile_batches > 0:
+        del base
+        torch.cuda.empty_cache()
+        if args.index:
+            t0 = time.time()
+            ix.save(args.index)
+            log(f"saved {args.index} in {time.time() - t0:.1f}s")
+        profile_mode(torch, dev, ix, qf, K, BATCH, npb, alpha, args.profile_batches)
+        return
 
     out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
