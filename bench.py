@@ -610,6 +610,7 @@ def bench_bytes(args, cf):
     ix.add(hb)
     t_add = time.time() - t0
     log(f"add {t_add:.1f}s ({N / t_add / 1e6:.2f} M vectors/s)")
+    x_sample = np.ascontiguousarray(hb[:min(N, 1_000_000)])
     del hb
     if args.profile_batches > 0:
         del base
@@ -637,6 +638,10 @@ def bench_bytes(args, cf):
     log("per-batch us: " + " ".join(f"{k2}={v:.1f}" for k2, v in step_us.items()))
     roof = scan_roofline(ix, hq.astype(np.float32), K, BATCH, step_us, cf["name"], npb, alpha)
     used, cap = ix.pool()
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(ix, npb, alpha, hq.astype(np.float32), K, ids, args.cpu_seconds,
+                           x_sample=x_sample)
     line = {
         "metric": f"QPS ({N // 1_000_000}Mx{D} {cf['kind']} IVF, nprobe {npb}, batch {BATCH}); "
                   "ADC-scan HBM GB/s vs peak",
@@ -658,7 +663,7 @@ def bench_bytes(args, cf):
             "step_us_per_batch": {k2: round(v, 2) for k2, v in step_us.items()},
         },
         "roofline": roof,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
@@ -862,7 +867,41 @@ def cpu_info():
     return model, threads
 
 
-def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds, train_x, nlist, n_train):
+def verify_sample(po, ix, L, cb, x_sample, n_assign, T):
+    """The GPU-built lists against the oracle on the first len(x_sample) vectors
+    (ids 0 ..): primary codes, residual codes and corrections bit for bit, and
+    the IVF list of the first n_assign of them (the oracle's assignment is the
+    expensive part at 65 536 lists)."""
+    t0 = time.time()
+    po.set_threads(T)
+    pp = ix.params
+    ids = L["ids"]
+    pos = np.empty(ids.size, np.int64)
+    pos[ids] = np.arange(ids.size, dtype=np.int64)
+    ns = x_sample.shape[0]
+    p = pos[:ns]
+    y = po.rotate(cb["P"], np.ascontiguousarray(x_sample, np.float32))
+    codes = po.primary_encode(y, pp.M, cb["c1d"])
+    res, corr = po.residual_encode(y, codes, pp.M, cb["c1d"], cb["res_c1d"], pp.Br)
+    bad_codes = int((L["codes"][p] != codes).any(1).sum())
+    bad_res = int((L["res"][p] != res).any(1).sum())
+    bad_corr = int((L["corr"][p].view(np.uint32) != corr.view(np.uint32)).sum())
+    na = min(n_assign, ns)
+    asg = po.assign(y[:na], cb["centroids"], cb["cent_norms"])
+    lst = np.searchsorted(L["offsets"], p[:na], side="right") - 1
+    bad_asg = int((lst != asg).sum())
+    ok = bad_codes == 0 and bad_res == 0 and bad_corr == 0 and bad_asg == 0
+    log(f"build check: {ns} vectors, codes/res/corr mismatches {bad_codes}/{bad_res}/{bad_corr}, "
+        f"list mismatches {bad_asg} of {na} ({time.time() - t0:.1f}s)")
+    return {"vectors_checked": ns, "assignments_checked": na, "bit_exact": ok,
+            "mismatched_codes": bad_codes, "mismatched_residual_codes": bad_res,
+            "mismatched_corrections": bad_corr, "mismatched_lists": bad_asg,
+            "note": "ids 0.. of the GPU-built index against the oracle's rotation, encode and "
+                    "assignment of the same input rows"}
+
+
+def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds, train_x=None, nlist=None,
+                 n_train=None, x_sample=None, n_assign=10_000):
     """The reference's CPU path as the oracle restates it (scalar C, test
     infrastructure): host train on a bounded sample, then search on the
     GPU-built index, one query at a time on one thread and over all host
@@ -881,6 +920,9 @@ def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds, train_x, nlist, n_t
     o = po.OracleIndex.from_state(ix.dim, pp, cb["P"], cb["c1d"], cb["res_c1d"], cb["centroids"],
                                   cb["cent_norms"], L["offsets"], L["ids"], L["codes"], L["res"],
                                   L["corr"])
+    check = None
+    if x_sample is not None:
+        check = verify_sample(po, ix, L, cb, x_sample, n_assign, T)
     budget = max(1.0, seconds / 3.0)
     # 1. search, one query at a time on one thread
     po.set_threads(1)
@@ -907,18 +949,22 @@ def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds, train_x, nlist, n_t
     # 4. host train (the oracle's restatement of the reference's train) on a
     # bounded sample: rotation QR, sigma, Lloyd-Max codebook, rotation of the
     # sample, IVF k-means with the lists scaled to the sample, residual 1-D k-means
-    ns = min(train_x.shape[0], 10_000)
-    nl_s = max(1, int(round(nlist * ns / max(n_train, 1))))
-    t0 = time.time()
-    ot = po.OracleIndex(ix.dim, M=pp.M, B=pp.B, Br=pp.Br, alpha=alpha, nlist=nl_s,
-                        nprobe=min(nprobe, nl_s), ivf_iters=pp.ivf_iters, seed=pp.seed)
-    ot.train(np.ascontiguousarray(train_x[:ns], np.float32))
-    t_train = time.time() - t0
+    ns = nl_s = 0
+    t_train = None
+    if train_x is not None:
+        ns = min(train_x.shape[0], 10_000)
+        nl_s = max(1, int(round(nlist * ns / max(n_train, 1))))
+        t0 = time.time()
+        ot = po.OracleIndex(ix.dim, M=pp.M, B=pp.B, Br=pp.Br, alpha=alpha, nlist=nl_s,
+                            nprobe=min(nprobe, nl_s), ivf_iters=pp.ivf_iters, seed=pp.seed)
+        ot.train(np.ascontiguousarray(train_x[:ns], np.float32))
+        t_train = time.time() - t0
     po.set_threads(1)
     log(f"cpu baseline: 1 thread {qps1:.1f} q/s ({n1} queries), {T} threads {qpsT:.1f} q/s "
         f"({nT} queries), id overlap with GPU {same:.4f}; reference approximate top-ck "
-        f"differs on {q_diff:.4f} of queries ({id_diff:.5f} of ids); train sample "
-        f"n={ns} nlist={nl_s}: {t_train:.1f}s on {T} threads; cpu {model}")
+        f"differs on {q_diff:.4f} of queries ({id_diff:.5f} of ids); "
+        + (f"train sample n={ns} nlist={nl_s}: {t_train:.1f}s on {T} threads; "
+           if t_train is not None else "") + f"cpu {model}")
     return {
         "value": round(qpsT, 2),
         "unit": "queries/s",
@@ -930,8 +976,10 @@ def cpu_baseline(ix, nprobe, alpha, hq, k, gpu_ids, seconds, train_x, nlist, n_t
         "single_thread_qps": round(qps1, 2),
         "cpu_model": model,
         "host_threads": T,
-        "train_s": round(t_train, 2),
-        "train_sample": f"n_train={ns}, nlist={nl_s}, ivf_iters={pp.ivf_iters}, {T} threads",
+        "train_s": None if t_train is None else round(t_train, 2),
+        "train_sample": (f"n_train={ns}, nlist={nl_s}, ivf_iters={pp.ivf_iters}, {T} threads"
+                         if t_train is not None else None),
+        "build_check": check,
         "reference_approx_topck": {
             "queries_with_other_ids": round(q_diff, 5),
             "ids_differing": round(id_diff, 6),
