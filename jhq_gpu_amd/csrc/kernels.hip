@@ -1954,6 +1954,9 @@ __device__ __forceinline__ uint32_t wave_kth_u32(const uint32_t (&v)[C], int r) 
     return res;
 }
 
+// lgkmcnt field of an s_waitcnt immediate (4 bits at bit 8)
+__host__ __device__ constexpr int lgkm_imm(int n) { return (n < 15 ? n : 15) << 8; }
+
 template <int CPT> struct CodeWord;
 template <> struct CodeWord<1> { using type = uint8_t; };
 template <> struct CodeWord<2> { using type = uint16_t; };
@@ -2158,24 +2161,56 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
 #pragma unroll
                     for (int u = 0; u < SU; u++) wc[u] = *(const word_t*)(base + (int64_t)u * npad);
                 }
+                using lds_f = const __attribute__((address_space(3))) float;
+                lds_f* lutl = (lds_f*)lut;
                 for (int m = 0; m < MS; m += SU) {
                     if (m + SU < MS) {
 #pragma unroll
                         for (int u = 0; u < SU; u++)
                             wn[u] = *(const word_t*)(base + (int64_t)(m + SU + u) * npad);
                     }
+                    // the block's gathers, one subspace (C reads) per group;
+                    // the reads of the next LA groups are issued before a
+                    // group's adds, so up to (LA + 1) * C reads stay in flight
+                    // (the LDS counter tracks 15) instead of one wait per read
+                    constexpr int GR = C, LA = C == 4 ? 2 : (C == 2 ? 6 : 14), NGR = SU;
+                    static_assert((LA + 1) * GR <= 15, "LDS reads in flight");
+                    float rv[LA + 1][GR];
+                    auto fetchg = [&](int k, float (&dst)[GR]) {
+                        lds_f* lm = lutl + (m + k) * 256;
 #pragma unroll
-                    for (int u = 0; u < SU; u++) {
-                        const float* lm = lut + (m + u) * 256;
+                        for (int j = 0; j < C; j++) dst[j] = lm[(wc[k] >> (8 * j)) & 0xffu];
+                    };
 #pragma unroll
-                        for (int j = 0; j < C; j++) a[j] += lm[(wc[u] >> (8 * j)) & 0xffu];
+                    for (int k = 0; k < LA && k < NGR; k++) fetchg(k, rv[k]);
+#pragma unroll
+                    for (int k = 0; k < NGR; k++) {
+                        if (k + LA < NGR) fetchg(k + LA, rv[(k + LA) % (LA + 1)]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        // groups k + 1 .. k + LA may still be in flight
+                        switch (k + LA < NGR ? LA : NGR - 1 - k) {
+                            // (immediates clamped to the counter's 4 bits; only
+                            // cases up to LA are reached)
+                            case 14: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(14 * GR)); break;
+                            case 6: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(6 * GR)); break;
+                            case 5: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(5 * GR)); break;
+                            case 4: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(4 * GR)); break;
+                            case 3: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(3 * GR)); break;
+                            case 2: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(2 * GR)); break;
+                            case 1: __builtin_amdgcn_s_waitcnt(0xc07f | lgkm_imm(1 * GR)); break;
+                            default: __builtin_amdgcn_s_waitcnt(0xc07f); break;
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int j = 0; j < C; j++) a[j] += rv[k % (LA + 1)][j];
+                        __builtin_amdgcn_sched_barrier(0);
                     }
 #pragma unroll
                     for (int u = 0; u < SU; u++) wc[u] = wn[u];
                 }
                 for (int m = MS; m < M; m++) {
                     const uint32_t ww = *(const word_t*)(base + (int64_t)m * npad);
-                    const float* lm = lut + m * 256;
+                    lds_f* lm = lutl + m * 256;
 #pragma unroll
                     for (int j = 0; j < C; j++) a[j] += lm[(ww >> (8 * j)) & 0xffu];
                 }

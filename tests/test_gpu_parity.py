@@ -46,6 +46,13 @@ CASES = [
     ("m32_p80", 64, 32, 8, 4, 96, 80, 4.0, 4000, 12, 10, 16),
     # skewed scan at M=128 (parity LUT) with exactly 64 probes (lookup in registers)
     ("m128_p64", 256, 128, 8, 4, 64, 64, 4.0, 3000, 10, 10, 16),
+    # M=16 (config 3's code size): the wave scan with ck=100 (three 64-key wave
+    # buffers) and many segments
+    ("m16_ck100", 128, 16, 8, 4, 32, 8, 10.0, 6000, 40, 10, 32),
+    # M=16 with Ds=4 (K1D=4) and more probes than a wave has lanes
+    ("m16_p80", 64, 16, 8, 4, 96, 80, 4.0, 5000, 12, 10, 16),
+    # M=24 (not a multiple of 16): the wave scan
+    ("m24_wave", 96, 24, 8, 4, 16, 5, 4.0, 3000, 20, 10, 32),
 ]
 IDS = [c[0] for c in CASES]
 
@@ -216,6 +223,13 @@ def test_skewed_scan_taken(gpu, name):
     """The M % 32 == 0 cases above exercise the skewed scan (not a fallback)."""
     g, _, _, _, k = _build(CASES[IDS.index(name)])
     assert g.scan_plan(k)[0] == "scan_skew_kernel"
+
+
+@pytest.mark.parametrize("name", ["ds8_k1d2", "ds4_k1d4_d100", "m24_wave", "m16_ck100", "m16_p80",
+                                  "flat_nlist1"])
+def test_wave_scan_taken(gpu, name):
+    g, _, _, _, k = _build(CASES[IDS.index(name)])
+    assert g.scan_plan(k)[0] == "scan_wave_kernel"
 
 
 def test_k_larger_than_candidates(gpu):

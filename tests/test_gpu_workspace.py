@@ -55,13 +55,14 @@ def test_device_search_within_reservation(gpu):
     assert np.array_equal(oi.cpu().numpy(), i1)
 
 
-@pytest.mark.parametrize("M", [32, 16], ids=["skewed_scan", "wave_scan"])
-def test_append_after_outstanding_device_search(gpu, M):
+@pytest.mark.parametrize("d,M", [(128, 32), (128, 16), (96, 24)],
+                         ids=["skewed_scan", "wave_scan_m16", "wave_scan_m24"])
+def test_append_after_outstanding_device_search(gpu, d, M):
     """Device search on a side stream, then append() with no host sync, then
     another device search: the first search sees the old lists, the second
     the new ones, both stage-wise exact against the oracle."""
     import torch
-    d, k = 128, 10
+    k = 10
     base, q = queries_and_base(9000, 48, d, 40, seed=901 + M)
     g, o = _pair(d=d, M=M)
     g.train(base[:2000])
