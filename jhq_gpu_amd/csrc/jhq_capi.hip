@@ -106,6 +106,8 @@ struct Workspace {
     DBuf<float> wq, wqrot, wscores, wout_d;
     DBuf<int32_t> wprobes, wgofs, wqtot, wout_i, wpslot;
     DBuf<unsigned long long> wpartial, wtopck, wdump;
+    // split sums of the query product
+    DBuf<float> wqpart;
 };
 
 }  // namespace
@@ -351,6 +353,10 @@ int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_
     JHQ_TRY(need(w.wtopck, B * ck, grow));
     JHQ_TRY(need(w.wout_d, B * k, grow));
     JHQ_TRY(need(w.wout_i, B * k, grow));
+    if (ix->dqmat.p) {
+        const size_t pf = jhq::mfma_qb_space(ix->batch_size, ix->d + ix->nlist, ix->d);
+        if (pf) JHQ_TRY(need(w.wqpart, pf, grow));
+    }
     return JHQ_OK;
 }
 
@@ -437,8 +443,9 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
     if (ix->dqmat.p) {
         // rotation and centroid dots in one tiled product
-        JHQ_HIP(jhq::mfma_q(d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, w.wqrot.p, d,
-                            w.wscores.p, ix->nlist, ix->dnorms.p, s));
+        const jhq::QbPlan qp = jhq::mfma_qb_plan(Bq, d + ix->nlist, d);
+        JHQ_HIP(jhq::mfma_qb(qp, d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, w.wqrot.p, d,
+                             w.wscores.p, ix->nlist, ix->dnorms.p, w.wqpart.p, w.wqpart.n, s));
     } else {
         // d not a multiple of 64: the 16-row kernels
         JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, w.wqrot.p, d, s));

@@ -30,12 +30,22 @@ hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t 
 // choices depend on it, never the stored codes.
 // Query product against Bm (N rows of K): columns < nrot are stored to C1,
 // the others become scores norms[c] - 2 * dot in C2 (column c - nrot).
-// fp32 MFMA, 64 rows x 16 columns per wave.  mfma_q_ok: K % 64 == 0 and
-// lda, ldb multiples of 4 (A and Bm must also be 16-byte aligned).
+// fp32 MFMA, 64 rows x 16*C columns x K/nsplit per workgroup, the launch
+// sized to the chip.  mfma_q_ok: K % 64 == 0 and lda, ldb multiples of 4 (A
+// and Bm must also be 16-byte aligned).  With nsplit > 1 the split sums pass
+// through part (part_floats floats) and a second kernel adds them in split
+// order; launches sharing part must not overlap.
 bool mfma_q_ok(int K, int64_t lda, int64_t ldb);
-hipError_t mfma_q(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N, int K,
-                  int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2, const float* norms,
-                  hipStream_t s);
+struct QbPlan {
+    int C, NI, nsplit, ncg, R;
+    size_t part_floats;
+};
+QbPlan mfma_qb_plan(int nb, int N, int K);
+// part floats that cover the plan of every nb <= nb_max
+size_t mfma_qb_space(int nb_max, int N, int K);
+hipError_t mfma_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm, int64_t ldb,
+                   int nb, int N, int K, int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2,
+                   const float* norms, float* part, size_t part_floats, hipStream_t s);
 hipError_t mfma_nt_store(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
                          int K, float* C, int64_t ldc, hipStream_t s);
 hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,

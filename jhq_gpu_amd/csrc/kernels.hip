@@ -666,164 +666,240 @@ mfma_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
 // back to the unrotated space, so the scores need not wait for the rotation):
 // C[row][col] = sum_k A[row][k] * Bm[col][k]; columns below nrot are the
 // rotated query (stored to C1), the rest centroid scores norms[c] - 2 * dot
-// (stored to C2 at column c - nrot).  Like mfma_nt_kernel (each lane streams
-// its own rows' k-runs as float4, S waves split K and add in a fixed order
-// through LDS), but a wave covers 64 rows x 16 columns (four 16x16 MFMA
-// tiles sharing each B fragment), so Bm is read once per 64 rows.
-// Requires K % (64 * S) == 0, lda and ldb multiples of 4, aligned A and Bm.
+// (stored to C2 at column c - nrot).  Requires K % 64 == 0, lda and ldb
+// multiples of 4, 16-byte aligned A and Bm.
 // ---------------------------------------------------------------------------
-template <int S, int CT>
-__global__ void __launch_bounds__(64 * S, CT > 1 ? 1 : 4)  // CT = 1: two 8-wave groups per CU
-mfma_q_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
-              int64_t ldb, int nb, int N, int K, int nrot, float* __restrict__ C1, int64_t ld1,
-              float* __restrict__ C2, int64_t ld2, const float* __restrict__ norms) {
-    constexpr int RT = 4, D = 2;
-    __shared__ v4f red[S > 1 ? (S - 1) * 64 * RT * CT : 1];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int b0 = blockIdx.y * 64, n0 = blockIdx.x * 16 * CT;
-    // lane (r, g) reads the float4 at k = wv*Ks + 16t + 4g of its rows, so
-    // the four k-groups of a row read 64 contiguous bytes per load; every
-    // k of the wave's range is summed once whatever its MFMA k-slot.  The
-    // wave's CT column tiles share each A fragment.
-    const int Ks = K / S;
-    const int ka = wv * Ks + 4 * g;
-    const float4* a4[RT];
-#pragma unroll
-    for (int i = 0; i < RT; i++) {
-        const int row = b0 + 16 * i + r;
-        a4[i] = (const float4*)(A + (int64_t)(row < nb ? row : 0) * lda + ka);
-    }
-    const float4* b4[CT];
-#pragma unroll
-    for (int c = 0; c < CT; c++) {
-        const int col = n0 + 16 * c + r;
-        b4[c] = (const float4*)(Bm + (int64_t)(col < N ? col : 0) * ldb + ka);
-    }
-    v4f acc0[CT][RT], acc1[CT][RT];
-#pragma unroll
-    for (int c = 0; c < CT; c++)
-#pragma unroll
-        for (int i = 0; i < RT; i++) {
-            acc0[c][i] = v4f{0.f, 0.f, 0.f, 0.f};
-            acc1[c][i] = v4f{0.f, 0.f, 0.f, 0.f};
-        }
-    const int n4 = Ks / 16;
-    float4 an[D][RT], bn[D][CT];
-#pragma unroll
-    for (int u = 0; u < D; u++) {
-#pragma unroll
-        for (int c = 0; c < CT; c++) bn[u][c] = b4[c][4 * u];
-#pragma unroll
-        for (int i = 0; i < RT; i++) an[u][i] = a4[i][4 * u];
-    }
-    for (int it = 0; it < n4; it += D) {
-        float4 ac[D][RT], bc[D][CT];
-#pragma unroll
-        for (int u = 0; u < D; u++) {
-#pragma unroll
-            for (int c = 0; c < CT; c++) bc[u][c] = bn[u][c];
-#pragma unroll
-            for (int i = 0; i < RT; i++) ac[u][i] = an[u][i];
-        }
-        if (it + D < n4) {
-#pragma unroll
-            for (int u = 0; u < D; u++) {
-#pragma unroll
-                for (int c = 0; c < CT; c++) bn[u][c] = b4[c][4 * (it + D + u)];
-#pragma unroll
-                for (int i = 0; i < RT; i++) an[u][i] = a4[i][4 * (it + D + u)];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < D; u++) {
-#pragma unroll
-            for (int c = 0; c < CT; c++) {
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    acc0[c][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].x, bc[u][c].x, acc0[c][i], 0, 0, 0);
-                    acc1[c][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].y, bc[u][c].y, acc1[c][i], 0, 0, 0);
-                    acc0[c][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].z, bc[u][c].z, acc0[c][i], 0, 0, 0);
-                    acc1[c][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(ac[u][i].w, bc[u][c].w, acc1[c][i], 0, 0, 0);
-                }
-            }
-        }
-    }
-    v4f acc[CT][RT];
-#pragma unroll
-    for (int c = 0; c < CT; c++)
-#pragma unroll
-        for (int i = 0; i < RT; i++) acc[c][i] = acc0[c][i] + acc1[c][i];
-    if (S > 1) {
-        if (wv > 0)
-#pragma unroll
-            for (int c = 0; c < CT; c++)
-#pragma unroll
-                for (int i = 0; i < RT; i++) red[(((wv - 1) * CT + c) * RT + i) * 64 + lane] = acc[c][i];
-        __syncthreads();
-        if (wv > 0) return;
-#pragma unroll
-        for (int w2 = 0; w2 < S - 1; w2++)
-#pragma unroll
-            for (int c = 0; c < CT; c++)
-#pragma unroll
-                for (int i = 0; i < RT; i++) acc[c][i] += red[((w2 * CT + c) * RT + i) * 64 + lane];
-    }
-#pragma unroll
-    for (int c = 0; c < CT; c++) {
-        const int col = n0 + 16 * c + r;
-        if (col >= N) continue;
-#pragma unroll
-        for (int i = 0; i < RT; i++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int row = b0 + 16 * i + 4 * g + j;
-                if (row < nb) {
-                    const float v = acc[c][i][j];
-                    if (col < nrot) C1[(int64_t)row * ld1 + col] = v;
-                    else C2[(int64_t)row * ld2 + (col - nrot)] = fmaf(-2.0f, v, norms[col - nrot]);
-                }
-            }
-        }
-    }
-}
-
-// column tiles per wave of the 8-wave query product: 2 halves the re-reads of
-// the queries' k-slices (29 -> 25 us per batch of 64 at D = 1024, nlist 4096;
-// 4 spills)
-#ifndef JHQ_Q_CT
-#define JHQ_Q_CT 2
-#endif
 bool mfma_q_ok(int K, int64_t lda, int64_t ldb) {
     return K % 64 == 0 && lda % 4 == 0 && ldb % 4 == 0;
 }
 
-hipError_t mfma_q(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N, int K,
-                  int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2, const float* norms,
-                  hipStream_t s) {
-    if (nb <= 0 || N <= 0) return hipSuccess;
-    if (!mfma_q_ok(K, lda, ldb) || ((uintptr_t)A & 15) || ((uintptr_t)Bm & 15) ||
-        (nb + 63) / 64 > 65535)
-        return hipErrorInvalidValue;
-    const int64_t tiles = (int64_t)((N + 15) / 16) * ((nb + 63) / 64);
-    int S = 1;
-    while (S < 8 && tiles * S < 2048 && K % (64 * S * 2) == 0 && K / (S * 2) >= 64) S *= 2;
-    dim3 grid((N + 15) / 16, (nb + 63) / 64);
-    switch (S) {
-        case 1: hipLaunchKernelGGL((mfma_q_kernel<1, 1>), grid, dim3(64), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
-        case 2: hipLaunchKernelGGL((mfma_q_kernel<2, 1>), grid, dim3(128), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
-        case 4: hipLaunchKernelGGL((mfma_q_kernel<4, 1>), grid, dim3(256), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms); break;
-        default:
-            if (JHQ_Q_CT > 1) {
-                // each wave covers JHQ_Q_CT column tiles
-                dim3 g2((N + 16 * JHQ_Q_CT - 1) / (16 * JHQ_Q_CT), (nb + 63) / 64);
-                hipLaunchKernelGGL((mfma_q_kernel<8, JHQ_Q_CT>), g2, dim3(512), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms);
-            } else {
-                hipLaunchKernelGGL((mfma_q_kernel<8, 1>), grid, dim3(512), 0, s, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms);
+// The launch is sized to the chip (mfma_qb_plan: about one workgroup per CU
+// at D = 1024, nlist 4096, batch 64: C = 5, nsplit = 4, 256 workgroups).
+// Workgroup (cg, sp, rb) covers rows 64*rb .. +63, column tiles cg*C .. +C-1
+// (16 columns each) and its share sp of K.  Its 4 waves split that share
+// again (K in steps of 16, 4 * nsplit * NI = K / 16: wave w of split sp takes
+// steps (4*sp + w)*NI .. +NI-1); each wave puts all of its A and Bm float4
+// loads in flight up front (NI <= 4 steps) and runs 4*C*4 MFMAs per step
+// (4 row tiles x C column tiles, every tile an independent accumulator).
+// Lane (r, g) supplies row / column r of a tile and k = 16*step + 4g .. +3,
+// one k per MFMA.  The 4 wave sums meet in LDS and are added in wave order.
+// With nsplit > 1 the workgroup stores its sums to part[sp] and
+// mfma_qb_reduce_kernel adds the nsplit partial tiles in split order, so the
+// sum order is fixed.  (A last-arriving-workgroup reduction inside this
+// kernel needs device-scope fences, whose L2 write-backs cost more than the
+// second launch: 49 against 19 us per batch of 64 at D = 1024, nlist 4096;
+// the 8-wave kernel this replaces, 64 rows x 32 columns per wave with K split
+// over the waves, took 24 us on 160 workgroups.)
+// ---------------------------------------------------------------------------
+template <int C, int NI>
+__global__ void __launch_bounds__(256)
+mfma_qb_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
+               int64_t ldb, int nb, int N, int K, int nrot, float* __restrict__ C1, int64_t ld1,
+               float* __restrict__ C2, int64_t ld2, const float* __restrict__ norms, int nsplit,
+               v4f* __restrict__ part) {
+    constexpr int RT = 4, NT = C * RT;
+    extern __shared__ __align__(16) unsigned char smem[];
+    v4f* red = reinterpret_cast<v4f*>(smem);  // [4 waves][NT tiles][64 lanes]
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int cg = blockIdx.x, sp = blockIdx.y, rb = blockIdx.z;
+    const int b0 = rb * 64, n0 = cg * 16 * C;
+    // lane (r, g) reads the float4 at k = 16*step + 4g of its rows: the four
+    // k-groups of a row read 64 contiguous bytes per load
+    const int ka = (sp * 4 + wv) * NI * 16 + 4 * g;
+    float4 av[NI][RT], bv[NI][C];
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+        const int uu = u;
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const int row = b0 + 16 * i + r;
+            av[u][i] = ((const float4*)(A + (int64_t)(row < nb ? row : 0) * lda + ka))[4 * uu];
+        }
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            const int col = n0 + 16 * c + r;
+            bv[u][c] = ((const float4*)(Bm + (int64_t)(col < N ? col : 0) * ldb + ka))[4 * uu];
+        }
+    }
+    // every load is in flight before the first MFMA (the scheduler would
+    // otherwise sink each load to its first use and wait for it there)
+    __builtin_amdgcn_sched_barrier(0);
+    v4f acc[C][RT];
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+        for (int i = 0; i < RT; i++) acc[c][i] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int c = 0; c < C; c++)
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const float a = e == 0 ? av[u][i].x : e == 1 ? av[u][i].y : e == 2 ? av[u][i].z : av[u][i].w;
+                    const float b = e == 0 ? bv[u][c].x : e == 1 ? bv[u][c].y : e == 2 ? bv[u][c].z : bv[u][c].w;
+                    acc[c][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[c][i], 0, 0, 0);
+                }
+    }
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+        for (int i = 0; i < RT; i++) red[(wv * NT + c * RT + i) * 64 + lane] = acc[c][i];
+    __syncthreads();
+    // wave w finishes tiles w, w + 4, ...: the four wave sums in wave order
+    v4f sum[(NT + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < (NT + 3) / 4; j++) {
+        const int t = wv + 4 * j;
+        if (t < NT) {
+            v4f v = red[t * 64 + lane];
+#pragma unroll
+            for (int w2 = 1; w2 < 4; w2++) v += red[(w2 * NT + t) * 64 + lane];
+            sum[j] = v;
+        }
+    }
+    if (nsplit > 1) {
+        // part[sp][rb][cg][tile][lane]; mfma_qb_reduce_kernel finishes
+        v4f* mine = part + ((int64_t)(sp * gridDim.z + rb) * gridDim.x + cg) * NT * 64;
+#pragma unroll
+        for (int j = 0; j < (NT + 3) / 4; j++) {
+            const int t = wv + 4 * j;
+            if (t < NT) mine[t * 64 + lane] = sum[j];
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < (NT + 3) / 4; j++) {
+        const int t = wv + 4 * j;
+        if (t >= NT) continue;
+        const int c = t / RT, i = t % RT;
+        const int col = n0 + 16 * c + r;
+        if (col >= N) continue;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int row = b0 + 16 * i + 4 * g + e;
+            if (row < nb) {
+                const float v = sum[j][e];
+                if (col < nrot) C1[(int64_t)row * ld1 + col] = v;
+                else C2[(int64_t)row * ld2 + (col - nrot)] = fmaf(-2.0f, v, norms[col - nrot]);
             }
-            break;
+        }
+    }
+}
+
+// part[sp][rb][cg][tile][lane] summed over sp in order, then stored like
+// mfma_qb_kernel's epilogue; one thread per (rb, cg, tile, lane).
+__global__ void __launch_bounds__(256)
+mfma_qb_reduce_kernel(const v4f* __restrict__ part, int nsplit, int C, int ncg, int R, int nb,
+                      int N, int nrot, float* __restrict__ C1, int64_t ld1, float* __restrict__ C2,
+                      int64_t ld2, const float* __restrict__ norms) {
+    const int NT = 4 * C;
+    const int64_t per = (int64_t)R * ncg * NT * 64;
+    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (x >= per) return;
+    const int lane = (int)(x % 64);
+    const int64_t tt = x / 64;
+    const int t = (int)(tt % NT);
+    const int64_t rc = tt / NT;
+    const int cg = (int)(rc % ncg), rb = (int)(rc / ncg);
+    v4f v = part[x];
+    for (int s2 = 1; s2 < nsplit; s2++) v += part[s2 * per + x];
+    const int r = lane & 15, g = lane >> 4;
+    const int c = t / 4, i = t % 4;
+    const int col = cg * 16 * C + 16 * c + r;
+    if (col >= N) return;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int row = rb * 64 + 16 * i + 4 * g + e;
+        if (row < nb) {
+            if (col < nrot) C1[(int64_t)row * ld1 + col] = v[e];
+            else C2[(int64_t)row * ld2 + (col - nrot)] = fmaf(-2.0f, v[e], norms[col - nrot]);
+        }
+    }
+}
+
+QbPlan mfma_qb_plan(int nb, int N, int K) {
+    QbPlan p{};
+    if (nb <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return p;
+    // K / 16 = 4m steps of 16; nsplit = the least divisor of m that leaves
+    // at most 4 steps per wave
+    const int m = K / 64;
+    int s = (m + 3) / 4;
+    while (m % s) s++;
+    const int T = (N + 15) / 16, R = (nb + 63) / 64;
+    int best = 0;
+    int64_t best_cost = 0;
+    for (int c = 1; c <= 5; c++) {
+        // MFMA steps of the busiest CU with one workgroup per CU per round
+        const int64_t wg = (int64_t)((T + c - 1) / c) * s * R;
+        const int64_t cost = (wg + 255) / 256 * c;
+        if (best == 0 || cost <= best_cost) {
+            best = c;
+            best_cost = cost;
+        }
+    }
+    p.C = best;
+    p.nsplit = s;
+    p.NI = m / s;
+    p.ncg = (T + best - 1) / best;
+    p.R = R;
+    p.part_floats = s > 1 ? (size_t)s * R * p.ncg * best * 4 * 64 * 4 : 0;
+    return p;
+}
+
+size_t mfma_qb_space(int nb_max, int N, int K) {
+    // any plan for nb <= nb_max: ncg * C <= T + 4 column tiles, R <= R_max
+    const QbPlan p = mfma_qb_plan(nb_max, N, K);
+    const size_t T = (N + 15) / 16;
+    return p.nsplit > 1 ? (size_t)p.nsplit * p.R * (T + 4) * 4 * 64 * 4 : 0;
+}
+
+template <int C, int NI>
+static hipError_t launch_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm,
+                            int64_t ldb, int nb, int N, int K, int nrot, float* C1, int64_t ld1,
+                            float* C2, int64_t ld2, const float* norms, float* part,
+                            hipStream_t s) {
+    const void* fn = (const void*)mfma_qb_kernel<C, NI>;
+    const int lds = 4 * C * 4 * 64 * 16;
+    static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((mfma_qb_kernel<C, NI>), dim3(p.ncg, p.nsplit, p.R), dim3(256), lds, s, A, lda,
+                       Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, p.nsplit,
+                       reinterpret_cast<v4f*>(part));
+    if (p.nsplit > 1) {
+        const int64_t per = (int64_t)p.R * p.ncg * 4 * C * 64;
+        hipLaunchKernelGGL(mfma_qb_reduce_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
+                           s, reinterpret_cast<const v4f*>(part), p.nsplit, C, p.ncg, p.R, nb, N,
+                           nrot, C1, ld1, C2, ld2, norms);
     }
     return hipGetLastError();
+}
+
+hipError_t mfma_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm, int64_t ldb,
+                   int nb, int N, int K, int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2,
+                   const float* norms, float* part, size_t part_floats, hipStream_t s) {
+    if (nb <= 0 || N <= 0) return hipSuccess;
+    if (!mfma_q_ok(K, lda, ldb) || ((uintptr_t)A & 15) || ((uintptr_t)Bm & 15) ||
+        ((uintptr_t)part & 15) || p.C < 1 || p.C > 5 || p.NI < 1 || p.NI > 4 || p.R > 65535 ||
+        p.nsplit > 65535 || p.part_floats > part_floats || (p.nsplit > 1 && !part))
+        return hipErrorInvalidValue;
+#define JHQ_QB(CC)                                                                              \
+    switch (p.NI) {                                                                             \
+        case 1: return launch_qb<CC, 1>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
+        case 2: return launch_qb<CC, 2>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
+        case 3: return launch_qb<CC, 3>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
+        default: return launch_qb<CC, 4>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
+    }
+    switch (p.C) {
+        case 1: JHQ_QB(1)
+        case 2: JHQ_QB(2)
+        case 3: JHQ_QB(3)
+        case 4: JHQ_QB(4)
+        default: JHQ_QB(5)
+    }
+#undef JHQ_QB
 }
 
 template <int EPI>

@@ -53,6 +53,11 @@ CASES = [
     ("m16_p80", 64, 16, 8, 4, 96, 80, 4.0, 5000, 12, 10, 16),
     # M=24 (not a multiple of 16): the wave scan
     ("m24_wave", 96, 24, 8, 4, 16, 5, 4.0, 3000, 20, 10, 32),
+    # query product with K split over 5 workgroups of one step per wave
+    ("qprod_d320_split5", 320, 40, 8, 4, 24, 5, 4.0, 2500, 70, 10, 64),
+    # query product over 3 row blocks (batch 130) with a 20-row last batch,
+    # K split over 3 workgroups of three steps per wave
+    ("qprod_d576_b130", 576, 72, 8, 4, 40, 6, 4.0, 3000, 150, 10, 130),
 ]
 IDS = [c[0] for c in CASES]
 
@@ -173,6 +178,21 @@ def test_search_parity(gpu, case):
     d2, i2 = g.search(q, k)
     assert np.array_equal(i2, gr["ids"])
     assert np.array_equal(_bits(d2), _bits(gr["dists"]))
+
+
+@pytest.mark.parametrize("name", ["d1024_m128", "qprod_d320_split5", "qprod_d576_b130"])
+def test_query_product_repeatable(gpu, name):
+    """The query product adds its split sums in a fixed order: repeated
+    searches give bit-identical rotated queries, probes and results."""
+    case = CASES[IDS.index(name)]
+    g, o, base, q, k = _build(case)
+    a = g.search_debug(q, k)
+    for _ in range(2):
+        b = g.search_debug(q, k)
+        assert np.array_equal(_bits(a["q_rot"]), _bits(b["q_rot"]))
+        assert np.array_equal(a["probes"], b["probes"])
+        assert np.array_equal(a["ids"], b["ids"])
+        assert np.array_equal(_bits(a["dists"]), _bits(b["dists"]))
 
 
 @pytest.mark.parametrize("case", CASES[:2], ids=IDS[:2])
