@@ -2038,6 +2038,26 @@ template <> struct CodeWord<1> { using type = uint8_t; };
 template <> struct CodeWord<2> { using type = uint16_t; };
 template <> struct CodeWord<4> { using type = uint32_t; };
 
+// LDS byte address 4 * (byte J of w): one SDWA shift (src1 selects the byte)
+// instead of a bit-field extract and a shift-add.
+template <int J>
+__device__ __forceinline__ uint32_t byte_x4(uint32_t w) {
+    uint32_t a;
+    if (J == 0)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(a) : "v"(w));
+    else if (J == 1)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(a) : "v"(w));
+    else if (J == 2)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(a) : "v"(w));
+    else
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(a) : "v"(w));
+    return a;
+}
+
 // ---------------------------------------------------------------------------
 // Wave-level exact selection.  buf[0..n) holds distinct keys
 // (value << 32 | tag), n <= 64 * J; keeps the k smallest (k < n), compacted
@@ -2231,37 +2251,23 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                 float a[C];
 #pragma unroll
                 for (int j = 0; j < C; j++) a[j] = 0.0f;
-                const int MS = M - M % SU;
-                uint32_t wc[SU], wn[SU];
-                if (MS > 0) {
-#pragma unroll
-                    for (int u = 0; u < SU; u++) wc[u] = *(const word_t*)(base + (int64_t)u * npad);
-                }
                 using lds_f = const __attribute__((address_space(3))) float;
-                lds_f* lutl = (lds_f*)lut;
-                for (int m = 0; m < MS; m += SU) {
-                    if (m + SU < MS) {
-#pragma unroll
-                        for (int u = 0; u < SU; u++)
-                            wn[u] = *(const word_t*)(base + (int64_t)(m + SU + u) * npad);
-                    }
-                    // the block's gathers, one subspace (C reads) per group;
-                    // the reads of the next LA groups are issued before a
-                    // group's adds, so up to (LA + 1) * C reads stay in flight
-                    // (the LDS counter tracks 15) instead of one wait per read
-                    constexpr int GR = C, LA = C == 4 ? 2 : (C == 2 ? 6 : 14), NGR = SU;
-                    static_assert((LA + 1) * GR <= 15, "LDS reads in flight");
+                using lds_b = const __attribute__((address_space(3))) char;
+                // the pipelined gathers of NGR subspaces (one group of C
+                // reads each) from code words cw[]: the reads of the next
+                // LA groups are issued before a group's adds, so up to
+                // (LA + 1) * C reads stay in flight (the LDS counter tracks
+                // 15) instead of one wait per read
+                constexpr int GR = C, LA = C == 4 ? 2 : (C == 2 ? 6 : 14);
+                static_assert((LA + 1) * GR <= 15, "LDS reads in flight");
+                auto gathers = [&](auto ngr, const uint32_t* cw, auto fetchg) {
+                    constexpr int NGR = decltype(ngr)::value;
                     float rv[LA + 1][GR];
-                    auto fetchg = [&](int k, float (&dst)[GR]) {
-                        lds_f* lm = lutl + (m + k) * 256;
 #pragma unroll
-                        for (int j = 0; j < C; j++) dst[j] = lm[(wc[k] >> (8 * j)) & 0xffu];
-                    };
-#pragma unroll
-                    for (int k = 0; k < LA && k < NGR; k++) fetchg(k, rv[k]);
+                    for (int k = 0; k < LA && k < NGR; k++) fetchg(k, cw[k], rv[k]);
 #pragma unroll
                     for (int k = 0; k < NGR; k++) {
-                        if (k + LA < NGR) fetchg(k + LA, rv[(k + LA) % (LA + 1)]);
+                        if (k + LA < NGR) fetchg(k + LA, cw[k + LA], rv[(k + LA) % (LA + 1)]);
                         __builtin_amdgcn_sched_barrier(0);
                         // groups k + 1 .. k + LA may still be in flight
                         switch (k + LA < NGR ? LA : NGR - 1 - k) {
@@ -2281,6 +2287,47 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                         for (int j = 0; j < C; j++) a[j] += rv[k % (LA + 1)][j];
                         __builtin_amdgcn_sched_barrier(0);
                     }
+                };
+                if (M == 16) {
+                    // config 3's code size: all 16 code words in flight at once,
+                    // the subspace offsets immediates, the LUT at LDS address 0
+                    // (this kernel has no static LDS; the launch checks it), so
+                    // a read's address is one SDWA shift of its code byte
+                    uint32_t cw[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) cw[u] = *(const word_t*)(base + (int64_t)u * npad);
+                    gathers(std::integral_constant<int, 16>(), cw,
+                            [&](int k, uint32_t w, float (&dst)[GR]) {
+#pragma unroll
+                                for (int j = 0; j < C; j++) {
+                                    const uint32_t ad = j == 0 ? byte_x4<0>(w)
+                                                      : j == 1 ? byte_x4<1>(w)
+                                                      : j == 2 ? byte_x4<2>(w) : byte_x4<3>(w);
+                                    dst[j] = *(lds_f*)((lds_b*)(uintptr_t)ad + k * 1024);
+                                }
+                            });
+                } else {
+                const int MS = M - M % SU;
+                uint32_t wc[SU], wn[SU];
+                if (MS > 0) {
+#pragma unroll
+                    for (int u = 0; u < SU; u++) wc[u] = *(const word_t*)(base + (int64_t)u * npad);
+                }
+                lds_f* lutl = (lds_f*)lut;
+                for (int m = 0; m < MS; m += SU) {
+                    if (m + SU < MS) {
+#pragma unroll
+                        for (int u = 0; u < SU; u++)
+                            wn[u] = *(const word_t*)(base + (int64_t)(m + SU + u) * npad);
+                    }
+                    // the block's gathers, one subspace (C reads) per group
+                    lds_f* lb = lutl + m * 256;
+                    gathers(std::integral_constant<int, SU>(), wc,
+                            [&](int k, uint32_t w, float (&dst)[GR]) {
+                                lds_f* lm = lb + k * 256;
+#pragma unroll
+                                for (int j = 0; j < C; j++) dst[j] = lm[(w >> (8 * j)) & 0xffu];
+                            });
 #pragma unroll
                     for (int u = 0; u < SU; u++) wc[u] = wn[u];
                 }
@@ -2289,6 +2336,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
                     lds_f* lm = lutl + m * 256;
 #pragma unroll
                     for (int j = 0; j < C; j++) a[j] += lm[(ww >> (8 * j)) & 0xffu];
+                }
                 }
                 const uint32_t p0 = (uint32_t)(soff[plo] + c0);
 #pragma unroll
@@ -3327,7 +3375,11 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
         static int mx[2][5] = {{-1, -1, -1, -1, -1}, {-1, -1, -1, -1, -1}};
         const int ji = sh.wave == 2 ? 0 : sh.wave == 3 ? 1 : sh.wave == 4 ? 2 : sh.wave == 6 ? 3 : 4;
         const int ni = sh.nt == NT ? 0 : 1;
-        if (mx[ni][ji] < 0) mx[ni][ji] = allow_max_lds((const void*)kf[ni][ji]);
+        if (mx[ni][ji] < 0) {
+            mx[ni][ji] = allow_max_lds((const void*)kf[ni][ji]);
+            // M = 16 addresses its LUT from LDS address 0: no static LDS
+            if (static_lds((const void*)kf[ni][ji]) != 0) mx[ni][ji] = 0;
+        }
         if (sh.lds > mx[ni][ji]) return hipErrorInvalidValue;
         hipLaunchKernelGGL(kf[ni][ji], dim3(sh.G), dim3(sh.nt), sh.lds, s, q_rot, d, Ds, K1D, bpd,
                            c1d, M, probes, gofs, qtot, B, P, ldesc, codes_t, ck, sh.region,
