@@ -34,8 +34,8 @@ def _run(cmd):
 
 
 def build_engine(verbose=False):
-    """Compile kernels.hip, jhq_capi.hip, kmeans.hip, noalloc.hip and host_train.cpp into
-    libjhq_amd.so."""
+    """Compile kernels.hip, jhq_capi.hip, kmeans.hip, noalloc.hip, assign_mfma.hip and
+    host_train.cpp into libjhq_amd.so."""
     os.makedirs(BUILD, exist_ok=True)
     jobs = [
         ([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, "kernels.hip"),
@@ -46,6 +46,8 @@ def build_engine(verbose=False):
                                 "-o", os.path.join(BUILD, "kmeans.o")]),
         ([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, "noalloc.hip"),
                                 "-o", os.path.join(BUILD, "noalloc.o")]),
+        ([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, "assign_mfma.hip"),
+                                "-o", os.path.join(BUILD, "assign_mfma.o")]),
         (["g++"] + CXX_FLAGS + ["-c", os.path.join(CSRC, "host_train.cpp"),
                                 "-o", os.path.join(BUILD, "host_train.o")]),
     ]
@@ -65,7 +67,7 @@ def build_engine(verbose=False):
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-pthread", "-o", tmp,
           os.path.join(BUILD, "kernels.o"), os.path.join(BUILD, "jhq_capi.o"),
           os.path.join(BUILD, "kmeans.o"), os.path.join(BUILD, "noalloc.o"),
-          os.path.join(BUILD, "host_train.o")])
+          os.path.join(BUILD, "assign_mfma.o"), os.path.join(BUILD, "host_train.o")])
     os.replace(tmp, LIB)
     return LIB
 

@@ -162,6 +162,9 @@ struct jhq_index {
     // query GEMM operand [Pi ; centroids * Pi] ((d + nlist) x d): one product
     // gives the rotated query and the centroid dots
     DBuf<float> dqmat;
+    // IVF assignment scratch (assign_mfma) and rows the last insert re-checked
+    DBuf<float> dascr;
+    int64_t rechecked = 0;
 
     // search workspaces; ws[1] and the lane streams serve pipelined batches
     Workspace ws[kLanes];
@@ -246,9 +249,24 @@ int ensure_pinned(T*& p, size_t& cap, size_t n) {
 }
 
 // assign rows of d_y (device, [n x d]) to the nearest of the index's centroids.
+// The list of each row of d_y: on MFMA with the fixed-order re-check where it
+// applies (d % 4 == 0), else the fixed-order kernel alone; the same result.
 int assign_rows(jhq_index* ix, const float* d_y, int64_t n, int32_t* d_assign,
                 DBuf<unsigned long long>& keys) {
     JHQ_TRY(keys.ensure(static_cast<size_t>(n)));
+    if (jhq::assign_mfma_ok(ix->d, d_y, ix->dcent.p) && (n + 127) / 128 <= 65535) {
+        JHQ_TRY(ix->dascr.ensure(jhq::assign_mfma_scratch_floats(n)));
+        JHQ_HIP(jhq::assign_mfma(d_y, n, ix->d, ix->dcent.p, ix->nlist, ix->dnorms.p, d_assign,
+                                 ix->dascr.p, ix->dascr.n, keys.p, ix->stream));
+        if (verbose()) {
+            int32_t m = 0;
+            JHQ_HIP(hipMemcpyAsync(&m, jhq::assign_mfma_rechecked(ix->dascr.p, n), sizeof(m),
+                                   hipMemcpyDeviceToHost, ix->stream));
+            JHQ_HIP(hipStreamSynchronize(ix->stream));
+            ix->rechecked += m;
+        }
+        return JHQ_OK;
+    }
     JHQ_HIP(jhq::fill_u64(keys.p, n, ~0ull, ix->stream));
     JHQ_HIP(jhq::gemm_nt_argmin(d_y, ix->d, ix->dcent.p, ix->d, n, ix->nlist, ix->d, ix->dnorms.p,
                                 keys.p, ix->stream));
@@ -953,6 +971,7 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
     hipStream_t s = ix->stream;
     const int64_t id_base = ix->ntotal;
+    ix->rechecked = 0;
 
     DBuf<uint8_t> dpc, drc;
     DBuf<float> dco;
@@ -994,6 +1013,9 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
                              static_cast<long long>(start + nb), static_cast<long long>(n));
         }
     }
+    if (verbose())
+        std::fprintf(stderr, "[jhq] add: %lld of %lld rows re-checked by the fixed-order argmin\n",
+                     static_cast<long long>(ix->rechecked), static_cast<long long>(n));
     // stable order by (list, id) of the new vectors (the reference's
     // thrust::sort_by_key, v14/jhq_gpu_index.cu:468-486)
     std::vector<int32_t> asg(static_cast<size_t>(n));
@@ -1591,9 +1613,21 @@ int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent, const 
     hipStream_t s = static_cast<hipStream_t>(stream);
     unsigned long long* keys = nullptr;
     JHQ_HIP(hipMallocAsync(reinterpret_cast<void**>(&keys), std::max<int64_t>(n, 1) * 8, s));
-    hipError_t e = jhq::fill_u64(keys, n, ~0ull, s);
-    if (e == hipSuccess) e = jhq::gemm_nt_argmin(d_y, d, d_cent, d, n, nlist, d, d_cent_norms, keys, s);
-    if (e == hipSuccess) e = jhq::keys_to_assign(keys, n, d_assign, s);
+    hipError_t e = hipSuccess;
+    if (jhq::assign_mfma_ok(d, d_y, d_cent) && (n + 127) / 128 <= 65535) {
+        // MFMA scores, fixed-order re-check of near ties: the same lists
+        const size_t sf = jhq::assign_mfma_scratch_floats(std::max<int64_t>(n, 1));
+        float* scr = nullptr;
+        e = hipMallocAsync(reinterpret_cast<void**>(&scr), sf * sizeof(float), s);
+        if (e == hipSuccess) {
+            e = jhq::assign_mfma(d_y, n, d, d_cent, nlist, d_cent_norms, d_assign, scr, sf, keys, s);
+            (void)hipFreeAsync(scr, s);
+        }
+    } else {
+        e = jhq::fill_u64(keys, n, ~0ull, s);
+        if (e == hipSuccess) e = jhq::gemm_nt_argmin(d_y, d, d_cent, d, n, nlist, d, d_cent_norms, keys, s);
+        if (e == hipSuccess) e = jhq::keys_to_assign(keys, n, d_assign, s);
+    }
     (void)hipFreeAsync(keys, s);
     if (e != hipSuccess) return fail(JHQ_EDEVICE, std::string("assign: ") + hipGetErrorString(e));
     return JHQ_OK;

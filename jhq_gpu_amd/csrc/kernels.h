@@ -25,6 +25,24 @@ hipError_t gemm_nt_score(const float* A, int64_t lda, const float* Bm, int64_t l
 hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t ldb,
                           int64_t n, int m, int d, const float* norms,
                           unsigned long long* keys, hipStream_t s);
+// EPI argmin over the rows rowidx[0 .. min(n_max, *ndev)) of A (ndev read on
+// the device); keys[i] belongs to row rowidx[i].  n_max <= 65535 * 128.
+hipError_t gemm_nt_argmin_rows(const float* A, int64_t lda, const int32_t* rowidx,
+                               const int32_t* ndev, int64_t n_max, const float* Bm, int64_t ldb,
+                               int m, int d, const float* norms, unsigned long long* keys,
+                               hipStream_t s);
+// IVF assignment on fp32 MFMA with the fixed-order argmin re-checking every
+// row whose two best approximate scores are closer than the error bound
+// (assign_mfma.hip); the result equals gemm_nt_argmin's bit for bit.
+// scratch: assign_mfma_scratch_floats(n) floats; keys: n u64.  Enqueue only.
+bool assign_mfma_ok(int d, const float* Y, const float* Cm);
+size_t assign_mfma_scratch_floats(int64_t n);
+hipError_t assign_mfma(const float* Y, int64_t n, int d, const float* Cm, int nlist,
+                       const float* norms, int32_t* assign, float* scratch,
+                       size_t scratch_floats, unsigned long long* keys, hipStream_t s);
+// The number of rows the last assign_mfma on this scratch re-checked
+// (device int).
+const int32_t* assign_mfma_rechecked(const float* scratch, int64_t n);
 // The same products on fp32 MFMA for the query side (rotation, centroid
 // scores); not a fixed summation order, so only distances and near-tie probe
 // choices depend on it, never the stored codes.

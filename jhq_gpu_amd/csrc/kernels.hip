@@ -297,13 +297,16 @@ __device__ __forceinline__ int block_topk(GetV getv, GetT gett, int n, int k, in
 // ---------------------------------------------------------------------------
 // Fixed-order SIMT GEMM  C = A * Bm^T  (both operands k-contiguous rows)
 // ---------------------------------------------------------------------------
-enum { EPI_STORE = 0, EPI_SCORE = 1, EPI_ARGMIN = 2 };
+// EPI_ARGMIN_IDX: EPI_ARGMIN over the rows rowidx[0 .. min(n, *ndev)) of A
+// (row i of the product is A's row rowidx[i]; keys indexed by i)
+enum { EPI_STORE = 0, EPI_SCORE = 1, EPI_ARGMIN = 2, EPI_ARGMIN_IDX = 3 };
 
 template <int BM, int BN, int BK, int TM, int TN, int EPI>
 __global__ void __launch_bounds__((BM / TM) * (BN / TN))
 gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
                int64_t ldb, int64_t n, int m, int d, float* __restrict__ C, int64_t ldc,
-               const float* __restrict__ norms, unsigned long long* __restrict__ amin) {
+               const float* __restrict__ norms, unsigned long long* __restrict__ amin,
+               const int32_t* __restrict__ rowidx, const int32_t* __restrict__ ndev) {
     constexpr int TX = BN / TN, TY = BM / TM, NT = TX * TY;
     constexpr int AL = BM * BK / NT, BL = BN * BK / NT;
     static_assert((BM * BK) % NT == 0 && (BN * BK) % NT == 0, "tile/threads mismatch");
@@ -314,6 +317,11 @@ gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
     const int tx = tid % TX, ty = tid / TX;
     const int64_t row0 = (int64_t)blockIdx.y * BM;
     const int col0 = blockIdx.x * BN;
+    if constexpr (EPI == EPI_ARGMIN_IDX) {
+        const int64_t c = *ndev;
+        if (c < n) n = c;
+        if (row0 >= n) return;
+    }
 
     float ra[AL], rb[BL];
     auto gload = [&](int k0) {
@@ -322,7 +330,10 @@ gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
             const int e = tid + i * NT, r = e / BK, kk = e % BK;
             const int64_t gr = row0 + r;
             const int gk = k0 + kk;
-            ra[i] = (gr < n && gk < d) ? A[gr * lda + gk] : 0.0f;
+            if constexpr (EPI == EPI_ARGMIN_IDX)
+                ra[i] = (gr < n && gk < d) ? A[(int64_t)rowidx[gr] * lda + gk] : 0.0f;
+            else
+                ra[i] = (gr < n && gk < d) ? A[gr * lda + gk] : 0.0f;
         }
 #pragma unroll
         for (int i = 0; i < BL; i++) {
@@ -381,7 +392,7 @@ gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
         __syncthreads();
     }
 
-    if constexpr (EPI == EPI_ARGMIN) {
+    if constexpr (EPI == EPI_ARGMIN || EPI == EPI_ARGMIN_IDX) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
             const int64_t gr = row0 + row_of(i);
@@ -433,7 +444,8 @@ static hipError_t launch_gemm(const float* A, int64_t lda, const float* Bm, int6
         dim3 grid((m + BN - 1) / BN, (unsigned)((nr + BM - 1) / BM));
         hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, TM, TN, EPI>), grid, dim3(NT), 0, s,
                            A + r0 * lda, lda, Bm, ldb, nr, m, d,
-                           C ? C + r0 * ldc : nullptr, ldc, norms, amin ? amin + r0 : nullptr);
+                           C ? C + r0 * ldc : nullptr, ldc, norms, amin ? amin + r0 : nullptr,
+                           nullptr, nullptr);
     }
     return hipGetLastError();
 }
@@ -560,6 +572,18 @@ hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t 
                           hipStream_t s) {
     return launch_gemm<128, 128, 16, 8, 8, EPI_ARGMIN>(A, lda, Bm, ldb, n, m, d, nullptr, 0,
                                                         norms, keys, s);
+}
+
+hipError_t gemm_nt_argmin_rows(const float* A, int64_t lda, const int32_t* rowidx,
+                               const int32_t* ndev, int64_t n_max, const float* Bm, int64_t ldb,
+                               int m, int d, const float* norms, unsigned long long* keys,
+                               hipStream_t s) {
+    if (n_max <= 0 || m <= 0) return hipSuccess;
+    if ((n_max + 127) / 128 > 65535) return hipErrorInvalidValue;
+    dim3 grid((m + 127) / 128, (unsigned)((n_max + 127) / 128));
+    hipLaunchKernelGGL((gemm_nt_kernel<128, 128, 16, 8, 8, EPI_ARGMIN_IDX>), grid, dim3(256), 0, s,
+                       A, lda, Bm, ldb, n_max, m, d, nullptr, 0, norms, keys, rowidx, ndev);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

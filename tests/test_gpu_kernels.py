@@ -69,6 +69,36 @@ def test_assign_bit_exact_with_ties(gpu, n, d, nlist):
     assert np.array_equal(a.cpu().numpy(), po.assign(y, cent, norms))
 
 
+@pytest.mark.parametrize("n,d,nlist", [(4096, 128, 1000), (5000, 1024, 4000), (300, 96, 129)])
+def test_assign_near_ties_bit_exact(gpu, n, d, nlist):
+    """The MFMA assignment with its fixed-order re-check against the oracle on
+    rows built to sit on or next to decision boundaries: midpoints of two
+    centroids (the fixed-order rounding decides), rows a hair off a midpoint,
+    copies of centroids, duplicate centroids (ties to the lower list), plus
+    ragged tiles (nlist not a multiple of 128)."""
+    import torch
+    rng = np.random.default_rng(7 * n + d)
+    cent = rng.standard_normal((nlist, d)).astype(np.float32)
+    cent[nlist - 1] = cent[0]
+    cent[nlist // 2] = cent[nlist // 5]
+    y = rng.standard_normal((n, d)).astype(np.float32)
+    a_i = rng.integers(0, nlist, n)
+    b_i = rng.integers(0, nlist, n)
+    q = n // 4
+    y[:q] = 0.5 * (cent[a_i[:q]] + cent[b_i[:q]])
+    y[q:2 * q] = 0.5 * (cent[a_i[q:2 * q]] + cent[b_i[q:2 * q]]) + \
+        rng.standard_normal((q, d)).astype(np.float32) * 1e-6
+    y[2 * q:2 * q + 16] = cent[a_i[2 * q:2 * q + 16]]
+    y[2 * q + 16] = 0.0
+    norms = po.cent_norms(cent)
+    a = torch.empty((n,), dtype=torch.int32, device=gpu)
+    jg.k_assign(_t(y, gpu), _t(cent, gpu), _t(norms, gpu), a)
+    torch.cuda.synchronize()
+    want = po.assign(y, cent, norms)
+    got = a.cpu().numpy()
+    assert np.array_equal(got, want), np.argwhere(got != want)[:5]
+
+
 @pytest.mark.parametrize("B,nlist,P", [(5, 100, 7), (4, 4096, 16), (3, 5000, 64), (2, 8191, 512),
                                        (64, 65536, 64), (2, 65536, 1)])
 def test_select_probes_exact_with_ties(gpu, B, nlist, P):
