@@ -982,50 +982,85 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     JHQ_TRY(dasg.alloc(static_cast<size_t>(n)));
     {
         const int64_t AB = std::min<int64_t>(ix->add_batch, n);
-        DBuf<float> dxb, dyb;
-        DBuf<uint8_t> draw;
+        DBuf<float> dxb[2], dyb;
+        DBuf<uint8_t> draw[2];
         DBuf<unsigned long long> keys;
-        JHQ_TRY(dxb.alloc(static_cast<size_t>(AB) * d));
+        for (int i = 0; i < 2 && i * AB < n; i++) {
+            JHQ_TRY(dxb[i].alloc(static_cast<size_t>(AB) * d));
+            if (dtype != JHQ_F32) JHQ_TRY(draw[i].alloc(static_cast<size_t>(AB) * d));
+        }
         JHQ_TRY(dyb.alloc(static_cast<size_t>(AB) * d));
-        if (dtype != JHQ_F32) JHQ_TRY(draw.alloc(static_cast<size_t>(AB) * d));
+        // the copies run on their own stream a batch ahead of the kernels; an
+        // input buffer is refilled once the kernels that read it (two batches
+        // back) are done
+        struct Sync {
+            hipStream_t cs = nullptr;
+            hipEvent_t copied[2] = {nullptr, nullptr}, consumed[2] = {nullptr, nullptr};
+            ~Sync() {
+                if (cs) {
+                    (void)hipStreamSynchronize(cs);
+                    (void)hipStreamDestroy(cs);
+                }
+                for (int i = 0; i < 2; i++) {
+                    if (copied[i]) (void)hipEventDestroy(copied[i]);
+                    if (consumed[i]) (void)hipEventDestroy(consumed[i]);
+                }
+            }
+        } sy;
+        JHQ_HIP(hipStreamCreate(&sy.cs));
+        for (int i = 0; i < 2; i++) {
+            JHQ_HIP(hipEventCreateWithFlags(&sy.copied[i], hipEventDisableTiming));
+            JHQ_HIP(hipEventCreateWithFlags(&sy.consumed[i], hipEventDisableTiming));
+        }
         const uint8_t* xb = static_cast<const uint8_t*>(x);
         const size_t es = dtype_size(dtype);
-        for (int64_t start = 0; start < n; start += AB) {
+        for (int64_t start = 0, bi = 0; start < n; start += AB, bi++) {
+            const int i = static_cast<int>(bi & 1);
             const int64_t nb = std::min(AB, n - start);
             const size_t cnt = static_cast<size_t>(nb) * d;
+            if (bi >= 2) JHQ_HIP(hipStreamWaitEvent(sy.cs, sy.consumed[i], 0));
             if (dtype == JHQ_F32) {
-                JHQ_HIP(hipMemcpyAsync(dxb.p, xb + static_cast<size_t>(start) * d * es,
-                                       cnt * sizeof(float), hipMemcpyHostToDevice, s));
+                JHQ_HIP(hipMemcpyAsync(dxb[i].p, xb + static_cast<size_t>(start) * d * es,
+                                       cnt * sizeof(float), hipMemcpyHostToDevice, sy.cs));
             } else {
                 // bytes cross PCIe; float32 conversion on the device
-                JHQ_HIP(hipMemcpyAsync(draw.p, xb + static_cast<size_t>(start) * d, cnt,
-                                       hipMemcpyHostToDevice, s));
-                JHQ_HIP(jhq::convert_to_f32(draw.p, dtype, static_cast<int64_t>(cnt), dxb.p, s));
+                JHQ_HIP(hipMemcpyAsync(draw[i].p, xb + static_cast<size_t>(start) * d, cnt,
+                                       hipMemcpyHostToDevice, sy.cs));
             }
-            JHQ_HIP(jhq::gemm_nt_store(dxb.p, d, ix->dP.p, d, nb, d, d, dyb.p, d, false, s));
+            JHQ_HIP(hipEventRecord(sy.copied[i], sy.cs));
+            JHQ_HIP(hipStreamWaitEvent(s, sy.copied[i], 0));
+            if (dtype != JHQ_F32)
+                JHQ_HIP(jhq::convert_to_f32(draw[i].p, dtype, static_cast<int64_t>(cnt), dxb[i].p, s));
+            JHQ_HIP(jhq::gemm_nt_store(dxb[i].p, d, ix->dP.p, d, nb, d, d, dyb.p, d, false, s));
+            JHQ_HIP(hipEventRecord(sy.consumed[i], s));
             JHQ_HIP(jhq::encode(dyb.p, nb, d, M, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, ix->Kr, ix->RC,
                                 ix->Br, bpv, ix->dres_c1d.p, dpc.p + start * M,
                                 drc.p + start * bpv, dco.p + start, 3, s));
             JHQ_TRY(assign_rows(ix, dyb.p, nb, dasg.p + start, keys));
-            JHQ_HIP(hipStreamSynchronize(s));
-            if (verbose() && (start / AB + 1) % 128 == 0)
-                std::fprintf(stderr, "[jhq] add: %lld / %lld vectors encoded and assigned\n",
+            if (verbose() && (bi + 1) % 128 == 0)
+                std::fprintf(stderr, "[jhq] add: %lld / %lld vectors enqueued\n",
                              static_cast<long long>(start + nb), static_cast<long long>(n));
         }
+        JHQ_HIP(hipStreamSynchronize(s));
     }
     if (verbose())
         std::fprintf(stderr, "[jhq] add: %lld of %lld rows re-checked by the fixed-order argmin\n",
                      static_cast<long long>(ix->rechecked), static_cast<long long>(n));
     // stable order by (list, id) of the new vectors (the reference's
-    // thrust::sort_by_key, v14/jhq_gpu_index.cu:468-486)
-    std::vector<int32_t> asg(static_cast<size_t>(n));
-    JHQ_HIP(hipMemcpy(asg.data(), dasg.p, asg.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+    // thrust::sort_by_key, v14/jhq_gpu_index.cu:468-486): keys (list << 32 |
+    // vector) radix-sorted on the device; the host reads the list counts only
+    DBuf<unsigned char> oscr;
+    JHQ_TRY(oscr.alloc(jhq::kmeans_scratch_bytes(n, nlist)));
+    const unsigned long long* sorted = nullptr;
+    const int64_t* first = nullptr;
+    JHQ_HIP(jhq::list_order(dasg.p, n, nlist, oscr.p, oscr.n, &sorted, &first, s));
+    std::vector<int64_t> firsth(static_cast<size_t>(nlist) + 1);
+    JHQ_HIP(hipMemcpyAsync(firsth.data(), first, firsth.size() * sizeof(int64_t),
+                           hipMemcpyDeviceToHost, s));
+    JHQ_HIP(hipStreamSynchronize(s));
+    if (firsth[0] != 0 || firsth[nlist] != n) return fail(JHQ_EDEVICE, "invalid IVF assignment");
     std::vector<int64_t> add(nlist + 1, 0);
-    for (int64_t i = 0; i < n; i++) {
-        const int a = asg[i];
-        if (a < 0 || a >= nlist) return fail(JHQ_EDEVICE, "invalid IVF assignment");
-        add[a + 1]++;
-    }
+    for (int l = 0; l < nlist; l++) add[l + 1] = firsth[l + 1] - firsth[l];
     for (int l = 0; l < nlist; l++) {
         if (static_cast<int64_t>(ix->l_size[l]) + add[l + 1] > INT32_MAX)
             return fail(JHQ_EINVAL, "list size exceeds int32");
@@ -1087,32 +1122,20 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         ix->l_cap = ncap;
         ix->pool_used = used;
     }
-    // scatter the new vectors behind each list's current candidates
-    std::vector<int32_t> order(static_cast<size_t>(n)), slist(static_cast<size_t>(n)),
-        sidx(static_cast<size_t>(n));
+    // scatter the new vectors behind each list's current candidates (the
+    // descriptors still hold the sizes before the insert)
     {
-        std::vector<int64_t> fill(nlist);
-        for (int l = 0; l < nlist; l++) fill[l] = add[l];
-        for (int l = 0; l < nlist; l++) add[l + 1] += add[l];
-        for (int l = 0; l < nlist; l++) fill[l] = add[l];
-        std::vector<int32_t> rank(nlist, 0);
-        for (int64_t i = 0; i < n; i++) {
-            const int a = asg[i];
-            const int64_t p = fill[a]++;
-            order[p] = static_cast<int32_t>(i);
-            slist[p] = a;
-            sidx[p] = ix->l_size[a] + rank[a]++;
-        }
         JHQ_TRY(upload_ldesc(ix));
         DBuf<int32_t> dorder, dslist, dsidx;
-        JHQ_TRY(dorder.upload(order.data(), order.size()));
-        JHQ_TRY(dslist.upload(slist.data(), slist.size()));
-        JHQ_TRY(dsidx.upload(sidx.data(), sidx.size()));
+        JHQ_TRY(dorder.alloc(static_cast<size_t>(n)));
+        JHQ_TRY(dslist.alloc(static_cast<size_t>(n)));
+        JHQ_TRY(dsidx.alloc(static_cast<size_t>(n)));
+        JHQ_HIP(jhq::scatter_plan(sorted, first, ix->dldesc.p, n, dorder.p, dslist.p, dsidx.p, s));
         JHQ_HIP(jhq::scatter_lists(dorder.p, dslist.p, dsidx.p, n, id_base, ix->dldesc.p, dpc.p,
                                    drc.p, dco.p, M, bpv, ix->dlist_ids.p, ix->dcodes_t.p, ix->dres.p,
                                    ix->dcorr.p, s));
         JHQ_HIP(hipStreamSynchronize(s));
-        for (int l = 0; l < nlist; l++) ix->l_size[l] += rank[l];
+        for (int l = 0; l < nlist; l++) ix->l_size[l] += static_cast<int32_t>(add[l + 1]);
     }
     JHQ_TRY(upload_ldesc(ix));
     ix->ntotal += n;

@@ -93,6 +93,15 @@ size_t kmeans_scratch_bytes(int64_t n, int nlist);
 hipError_t kmeans_update(const int32_t* asg, const float* y, int d, int64_t n, int nlist, int iter,
                          float* cent, void* scratch, size_t scratch_bytes, hipStream_t s);
 hipError_t kmeans_norms(const float* cent, int d, int nlist, float* norms, hipStream_t s);
+// keys (asg[i] << 32 | i) sorted ascending into the scratch (same size as
+// kmeans_scratch_bytes), and first[l] = index of list l's first sorted key
+// (first[nlist] = n); the two pointers point into the scratch.
+hipError_t list_order(const int32_t* asg, int64_t n, int nlist, void* scratch, size_t scratch_bytes,
+                      const unsigned long long** sorted, const int64_t** first, hipStream_t s);
+// From list_order's output: order[p] = vector, slist[p] = its list, sidx[p] =
+// ldesc[list].z + its rank in the list (the scatter_lists inputs).
+hipError_t scatter_plan(const unsigned long long* sorted, const int64_t* first, const int4* ldesc,
+                        int64_t n, int32_t* order, int32_t* slist, int32_t* sidx, hipStream_t s);
 
 // List storage: one pool of padded candidate slots; list l is described by
 // int4 {start, cap, size, cbase}: slots [start, start + cap) with cap a

@@ -1,6 +1,10 @@
 // kmeans.hip — Lloyd iterations of the coarse (IVF) quantizer on the device
 // (v14/jhq_gpu_index.cu:228-299, whose means are computed on the host).
 //
+// The first two steps also order an insert's new vectors by (list, vector)
+// (list_order, scatter_plan: the reference's stable sort by list,
+// v14/jhq_gpu_index.cu:468-486).
+//
 // One iteration after the assignment (gemm_nt_argmin):
 //   1. keys (list << 32 | sample) sorted ascending: every list's members
 //      end up contiguous and in ascending sample order;
@@ -109,8 +113,9 @@ size_t kmeans_scratch_bytes(int64_t n, int nlist) {
            (sort_bytes + 255) / 256 * 256;
 }
 
-hipError_t kmeans_update(const int32_t* asg, const float* y, int d, int64_t n, int nlist, int iter,
-                         float* cent, void* scratch, size_t scratch_bytes, hipStream_t s) {
+hipError_t list_order(const int32_t* asg, int64_t n, int nlist, void* scratch, size_t scratch_bytes,
+                      const unsigned long long** sorted_out, const int64_t** first_out,
+                      hipStream_t s) {
     if (nlist <= 0 || n <= 0 || n > 0x7fffffffll) return hipErrorInvalidValue;
     int bits = 1;
     while ((1ll << bits) < (int64_t)nlist) bits++;
@@ -133,8 +138,44 @@ hipError_t kmeans_update(const int32_t* asg, const float* y, int d, int64_t n, i
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kmeans_bounds_kernel, dim3((nlist + 1 + 255) / 256), dim3(256), 0, s,
                        sorted, n, nlist, first);
+    *sorted_out = sorted;
+    *first_out = first;
+    return hipGetLastError();
+}
+
+hipError_t kmeans_update(const int32_t* asg, const float* y, int d, int64_t n, int nlist, int iter,
+                         float* cent, void* scratch, size_t scratch_bytes, hipStream_t s) {
+    const unsigned long long* sorted = nullptr;
+    const int64_t* first = nullptr;
+    hipError_t e = list_order(asg, n, nlist, scratch, scratch_bytes, &sorted, &first, s);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kmeans_means_kernel, dim3(nlist), dim3(256), 0, s, y, d, n, sorted, first,
                        iter, cent);
+    return hipGetLastError();
+}
+
+// Sorted position p of an insert's new vectors (keys (list << 32 | vector),
+// ascending): vector order[p] goes to list slist[p] at index
+// ldesc[list].size (the list's size before the insert) + p - first[list].
+__global__ void scatter_plan_kernel(const unsigned long long* __restrict__ sorted,
+                                    const int64_t* __restrict__ first,
+                                    const int4* __restrict__ ldesc, int64_t n,
+                                    int32_t* __restrict__ order, int32_t* __restrict__ slist,
+                                    int32_t* __restrict__ sidx) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const unsigned long long k = sorted[p];
+    const int l = (int)(k >> 32);
+    order[p] = (int32_t)(uint32_t)k;
+    slist[p] = l;
+    sidx[p] = (int32_t)(ldesc[l].z + (p - first[l]));
+}
+
+hipError_t scatter_plan(const unsigned long long* sorted, const int64_t* first, const int4* ldesc,
+                        int64_t n, int32_t* order, int32_t* slist, int32_t* sidx, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(scatter_plan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       sorted, first, ldesc, n, order, slist, sidx);
     return hipGetLastError();
 }
 
