@@ -250,6 +250,17 @@ recheck_scatter_kernel(const unsigned long long* __restrict__ keys,
         assign[recheck[i]] = (int32_t)(uint32_t)(keys[i] & 0xffffffffull);
 }
 
+__global__ void tally_kernel(const int32_t* __restrict__ cnt, unsigned long long* __restrict__ total) {
+    if (threadIdx.x == 0) total[0] += (unsigned long long)cnt[0];
+}
+
+hipError_t assign_mfma_tally(const float* scratch, int64_t n, unsigned long long* total,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(tally_kernel, dim3(1), dim3(64), 0, s, assign_mfma_rechecked(scratch, n),
+                       total);
+    return hipGetLastError();
+}
+
 bool assign_mfma_ok(int d, const float* Y, const float* Cm) {
     return d > 0 && d % 4 == 0 && ((uintptr_t)Y & 15) == 0 && ((uintptr_t)Cm & 15) == 0;
 }

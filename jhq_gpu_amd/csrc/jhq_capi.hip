@@ -162,9 +162,10 @@ struct jhq_index {
     // query GEMM operand [Pi ; centroids * Pi] ((d + nlist) x d): one product
     // gives the rotated query and the centroid dots
     DBuf<float> dqmat;
-    // IVF assignment scratch (assign_mfma) and rows the last insert re-checked
+    // IVF assignment scratch (assign_mfma) and, with JHQ_VERBOSE, the count of
+    // rows it re-checked since the insert began (device)
     DBuf<float> dascr;
-    int64_t rechecked = 0;
+    DBuf<unsigned long long> drecheck;
 
     // search workspaces; ws[1] and the lane streams serve pipelined batches
     Workspace ws[kLanes];
@@ -258,13 +259,8 @@ int assign_rows(jhq_index* ix, const float* d_y, int64_t n, int32_t* d_assign,
         JHQ_TRY(ix->dascr.ensure(jhq::assign_mfma_scratch_floats(n)));
         JHQ_HIP(jhq::assign_mfma(d_y, n, ix->d, ix->dcent.p, ix->nlist, ix->dnorms.p, d_assign,
                                  ix->dascr.p, ix->dascr.n, keys.p, ix->stream));
-        if (verbose()) {
-            int32_t m = 0;
-            JHQ_HIP(hipMemcpyAsync(&m, jhq::assign_mfma_rechecked(ix->dascr.p, n), sizeof(m),
-                                   hipMemcpyDeviceToHost, ix->stream));
-            JHQ_HIP(hipStreamSynchronize(ix->stream));
-            ix->rechecked += m;
-        }
+        if (verbose() && ix->drecheck.p)
+            JHQ_HIP(jhq::assign_mfma_tally(ix->dascr.p, n, ix->drecheck.p, ix->stream));
         return JHQ_OK;
     }
     JHQ_HIP(jhq::fill_u64(keys.p, n, ~0ull, ix->stream));
@@ -971,7 +967,10 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
     hipStream_t s = ix->stream;
     const int64_t id_base = ix->ntotal;
-    ix->rechecked = 0;
+    if (verbose()) {
+        JHQ_TRY(ix->drecheck.ensure(1));
+        JHQ_HIP(jhq::fill_u64(ix->drecheck.p, 1, 0ull, s));
+    }
 
     DBuf<uint8_t> dpc, drc;
     DBuf<float> dco;
@@ -1043,9 +1042,12 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         }
         JHQ_HIP(hipStreamSynchronize(s));
     }
-    if (verbose())
-        std::fprintf(stderr, "[jhq] add: %lld of %lld rows re-checked by the fixed-order argmin\n",
-                     static_cast<long long>(ix->rechecked), static_cast<long long>(n));
+    if (verbose() && ix->drecheck.p) {
+        unsigned long long rc = 0;
+        JHQ_HIP(hipMemcpy(&rc, ix->drecheck.p, sizeof(rc), hipMemcpyDeviceToHost));
+        std::fprintf(stderr, "[jhq] add: %llu of %lld rows re-checked by the fixed-order argmin\n",
+                     rc, static_cast<long long>(n));
+    }
     // stable order by (list, id) of the new vectors (the reference's
     // thrust::sort_by_key, v14/jhq_gpu_index.cu:468-486): keys (list << 32 |
     // vector) radix-sorted on the device; the host reads the list counts only

@@ -43,6 +43,9 @@ hipError_t assign_mfma(const float* Y, int64_t n, int d, const float* Cm, int nl
 // The number of rows the last assign_mfma on this scratch re-checked
 // (device int).
 const int32_t* assign_mfma_rechecked(const float* scratch, int64_t n);
+// *total += that count (on the stream)
+hipError_t assign_mfma_tally(const float* scratch, int64_t n, unsigned long long* total,
+                             hipStream_t s);
 // The same products on fp32 MFMA for the query side (rotation, centroid
 // scores); not a fixed summation order, so only distances and near-tie probe
 // choices depend on it, never the stored codes.
