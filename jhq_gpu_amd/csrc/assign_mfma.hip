@@ -26,7 +26,10 @@ typedef float v4f_a __attribute__((ext_vector_type(4)));
 
 constexpr int kTopBM = 128, kTopBN = 128, kTopBK = 16, kTopLd = kTopBK + 4;
 
-// One workgroup (4 waves) per 128 rows; it walks every 128-list tile.  Wave w
+// One workgroup (4 waves) per 128 rows and share of the 128-list tiles
+// (blockIdx.y of gridDim.y shares; with more than one, each share's best and
+// second best go to their own slots and top2_merge_kernel combines them in
+// share order, so a few rows still fill the chip).  Wave w
 // covers rows 64*(w>>1) .. +63 and tile columns 64*(w&1) .. +63 as 4 x 4
 // tiles of v_mfma_f32_16x16x4_f32.  K advances in chunks of 16 staged in LDS
 // (double-buffered, the next chunk's global loads issued before the current
@@ -48,7 +51,13 @@ mfma_top2_kernel(const float* __restrict__ Y, int64_t n, int d, const float* __r
     const int r = lane & 15, g = lane >> 4, rh = wv >> 1, ch = wv & 1;
     const int64_t r0 = (int64_t)blockIdx.x * kTopBM;
     const int nchunk = (d + kTopBK - 1) / kTopBK;
-    const int ntile = (nlist + kTopBN - 1) / kTopBN;
+    const int ntall = (nlist + kTopBN - 1) / kTopBN;
+    const int per = (ntall + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int tb = (int)blockIdx.y * per, te = min(ntall, tb + per);
+    const int ntile = te > tb ? te - tb : 0;
+    best += (int64_t)blockIdx.y * n;
+    s1 += (int64_t)blockIdx.y * n;
+    s2 += (int64_t)blockIdx.y * n;
     // staging: thread t moves rows (t >> 2) and 64 + (t >> 2), k4 = 4 * (t & 3)
     const int lrow = tid >> 2, lk = 4 * (tid & 3);
     float bv[16], sv[16];
@@ -86,13 +95,15 @@ mfma_top2_kernel(const float* __restrict__ Y, int64_t n, int d, const float* __r
     };
     const int nsteps = ntile * nchunk;
     float4 ra[2], rb[2];
-    load_a(0, ra);
-    load_b(0, 0, rb);
-    store(0, ra, rb);
+    if (nsteps > 0) {
+        load_a(0, ra);
+        load_b(tb, 0, rb);
+        store(0, ra, rb);
+    }
     __syncthreads();
     v4f_a acc[4][4];
     int step = 0;
-    for (int t = 0; t < ntile; t++) {
+    for (int t = tb; t < te; t++) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -187,6 +198,31 @@ mfma_top2_kernel(const float* __restrict__ Y, int64_t n, int d, const float* __r
     }
 }
 
+// Combines the S shares' (best, list, second) per row in share order (ties to
+// the lower list), into share 0's slots.
+__global__ void __launch_bounds__(256)
+top2_merge_kernel(int64_t n, int S, int32_t* __restrict__ best, float* __restrict__ s1,
+                  float* __restrict__ s2) {
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= n) return;
+    float b = s1[row], sc = s2[row];
+    int c = best[row];
+    for (int y = 1; y < S; y++) {
+        const float ob = s1[y * n + row], os = s2[y * n + row];
+        const int oc = best[y * n + row];
+        if (b < ob || (b == ob && c < oc)) {
+            sc = fminf(sc, ob);
+        } else {
+            sc = fminf(os, b);
+            b = ob;
+            c = oc;
+        }
+    }
+    best[row] = c;
+    s1[row] = b;
+    s2[row] = sc;
+}
+
 // Nmax = max ||c||^2 over the lists (one workgroup); also zeroes the
 // re-check count
 __global__ void __launch_bounds__(256) max_norm_kernel(const float* __restrict__ norms, int nlist,
@@ -265,13 +301,21 @@ bool assign_mfma_ok(int d, const float* Y, const float* Cm) {
     return d > 0 && d % 4 == 0 && ((uintptr_t)Y & 15) == 0 && ((uintptr_t)Cm & 15) == 0;
 }
 
+// shares of the list tiles: about 512 workgroups when the rows are few
+static int top2_shares(int64_t n) {
+    const int64_t rb = (n + kTopBM - 1) / kTopBM;
+    int64_t s = (512 + rb - 1) / rb;
+    return (int)(s < 1 ? 1 : (s > 8 ? 8 : s));
+}
+
 size_t assign_mfma_scratch_floats(int64_t n) {
-    // best, s1, s2, re-check rows (one word per row each), the re-check count, Nmax
-    return (size_t)n * 4 + 64;
+    // best, s1, s2 (one word per row and share), re-check rows, the re-check
+    // count, Nmax
+    return (size_t)n * (3 * top2_shares(n) + 1) + 64;
 }
 
 const int32_t* assign_mfma_rechecked(const float* scratch, int64_t n) {
-    return (const int32_t*)(scratch + 4 * n);
+    return (const int32_t*)(scratch + (size_t)n * (3 * top2_shares(n) + 1));
 }
 
 hipError_t assign_mfma(const float* Y, int64_t n, int d, const float* Cm, int nlist,
@@ -281,15 +325,19 @@ hipError_t assign_mfma(const float* Y, int64_t n, int d, const float* Cm, int nl
     if (!assign_mfma_ok(d, Y, Cm) || nlist <= 0 || !scratch || !keys ||
         scratch_floats < assign_mfma_scratch_floats(n) || (n + 127) / 128 > 65535)
         return hipErrorInvalidValue;
+    const int S = top2_shares(n);
     int32_t* best = (int32_t*)scratch;
-    float* s1 = scratch + n;
-    float* s2 = scratch + 2 * n;
-    int32_t* recheck = (int32_t*)(scratch + 3 * n);
-    int32_t* cnt = (int32_t*)(scratch + 4 * n);
-    float* nmax = scratch + 4 * n + 16;
+    float* s1 = scratch + (size_t)S * n;
+    float* s2 = scratch + (size_t)2 * S * n;
+    int32_t* recheck = (int32_t*)(scratch + (size_t)3 * S * n);
+    int32_t* cnt = (int32_t*)(scratch + (size_t)n * (3 * S + 1));
+    float* nmax = (float*)cnt + 16;
     hipLaunchKernelGGL(max_norm_kernel, dim3(1), dim3(256), 0, s, norms, nlist, nmax, cnt);
-    hipLaunchKernelGGL(mfma_top2_kernel, dim3((unsigned)((n + kTopBM - 1) / kTopBM)), dim3(256), 0,
-                       s, Y, n, d, Cm, nlist, norms, best, s1, s2);
+    hipLaunchKernelGGL(mfma_top2_kernel, dim3((unsigned)((n + kTopBM - 1) / kTopBM), (unsigned)S),
+                       dim3(256), 0, s, Y, n, d, Cm, nlist, norms, best, s1, s2);
+    if (S > 1)
+        hipLaunchKernelGGL(top2_merge_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, n,
+                           S, best, s1, s2);
     hipLaunchKernelGGL(top2_accept_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, Y, n, d,
                        best, s1, s2, nmax, assign, recheck, cnt);
     // the fixed-order argmin over the listed rows (their count read on the device)

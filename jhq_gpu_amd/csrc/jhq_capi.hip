@@ -171,6 +171,9 @@ struct jhq_index {
     Workspace ws[kLanes];
     hipStream_t lane[kLanes] = {};
     hipEvent_t lane_ev[kLanes + 1] = {};  // fork, then each lane's last batch done
+    // inserts: the input copy stream and its two buffers' copied / consumed events
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t copy_ev[4] = {};
     float* h_q[kLanes] = {};  // pinned staging, one set per lane
     float* h_d[kLanes] = {};
     int32_t* h_i[kLanes] = {};
@@ -194,7 +197,17 @@ struct jhq_index {
         for (auto& l : lane)
             if (l) (void)hipStreamDestroy(l);
         if (done_ev) (void)hipEventDestroy(done_ev);
+        for (auto& e : copy_ev)
+            if (e) (void)hipEventDestroy(e);
+        if (copy_stream) (void)hipStreamDestroy(copy_stream);
         if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    int ensure_copy_stream() {
+        if (copy_stream) return JHQ_OK;
+        for (auto& e : copy_ev) JHQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        JHQ_HIP(hipStreamCreate(&copy_stream));
+        return JHQ_OK;
     }
 
     int ensure_lanes() {
@@ -992,25 +1005,17 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         // the copies run on their own stream a batch ahead of the kernels; an
         // input buffer is refilled once the kernels that read it (two batches
         // back) are done
-        struct Sync {
-            hipStream_t cs = nullptr;
-            hipEvent_t copied[2] = {nullptr, nullptr}, consumed[2] = {nullptr, nullptr};
-            ~Sync() {
-                if (cs) {
-                    (void)hipStreamSynchronize(cs);
-                    (void)hipStreamDestroy(cs);
-                }
-                for (int i = 0; i < 2; i++) {
-                    if (copied[i]) (void)hipEventDestroy(copied[i]);
-                    if (consumed[i]) (void)hipEventDestroy(consumed[i]);
-                }
-            }
-        } sy;
-        JHQ_HIP(hipStreamCreate(&sy.cs));
-        for (int i = 0; i < 2; i++) {
-            JHQ_HIP(hipEventCreateWithFlags(&sy.copied[i], hipEventDisableTiming));
-            JHQ_HIP(hipEventCreateWithFlags(&sy.consumed[i], hipEventDisableTiming));
-        }
+        JHQ_TRY(ix->ensure_copy_stream());
+        // on every exit the copy stream is drained before the buffers go
+        struct Drain {
+            hipStream_t cs;
+            ~Drain() { (void)hipStreamSynchronize(cs); }
+        } drain{ix->copy_stream};
+        struct {
+            hipStream_t cs;
+            hipEvent_t* copied;
+            hipEvent_t* consumed;
+        } sy{ix->copy_stream, ix->copy_ev, ix->copy_ev + 2};
         const uint8_t* xb = static_cast<const uint8_t*>(x);
         const size_t es = dtype_size(dtype);
         for (int64_t start = 0, bi = 0; start < n; start += AB, bi++) {
