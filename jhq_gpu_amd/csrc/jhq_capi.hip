@@ -171,8 +171,10 @@ struct jhq_index {
     Workspace ws[kLanes];
     hipStream_t lane[kLanes] = {};
     hipEvent_t lane_ev[kLanes + 1] = {};  // fork, then each lane's last batch done
-    // inserts: the input copy stream and its two buffers' copied / consumed events
-    hipStream_t copy_stream = nullptr;
+    // inserts: the two input buffers' copied / consumed events (the copies run
+    // on the last lane's stream, idle while an insert runs: a stream of its
+    // own would share one of the process's 4 hardware queues with a lane and
+    // serialise the lanes' batches)
     hipEvent_t copy_ev[4] = {};
     float* h_q[kLanes] = {};  // pinned staging, one set per lane
     float* h_d[kLanes] = {};
@@ -199,14 +201,13 @@ struct jhq_index {
         if (done_ev) (void)hipEventDestroy(done_ev);
         for (auto& e : copy_ev)
             if (e) (void)hipEventDestroy(e);
-        if (copy_stream) (void)hipStreamDestroy(copy_stream);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
     int ensure_copy_stream() {
-        if (copy_stream) return JHQ_OK;
+        JHQ_TRY(ensure_lanes());
+        if (copy_ev[0]) return JHQ_OK;
         for (auto& e : copy_ev) JHQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-        JHQ_HIP(hipStreamCreate(&copy_stream));
         return JHQ_OK;
     }
 
@@ -1006,16 +1007,18 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         // input buffer is refilled once the kernels that read it (two batches
         // back) are done
         JHQ_TRY(ix->ensure_copy_stream());
+        // one batch has nothing to overlap: its copy stays on the kernels' stream
+        hipStream_t cst = n > AB ? ix->lane[kLanes - 1] : s;
         // on every exit the copy stream is drained before the buffers go
         struct Drain {
             hipStream_t cs;
             ~Drain() { (void)hipStreamSynchronize(cs); }
-        } drain{ix->copy_stream};
+        } drain{cst};
         struct {
             hipStream_t cs;
             hipEvent_t* copied;
             hipEvent_t* consumed;
-        } sy{ix->copy_stream, ix->copy_ev, ix->copy_ev + 2};
+        } sy{cst, ix->copy_ev, ix->copy_ev + 2};
         const uint8_t* xb = static_cast<const uint8_t*>(x);
         const size_t es = dtype_size(dtype);
         for (int64_t start = 0, bi = 0; start < n; start += AB, bi++) {
