@@ -2089,6 +2089,44 @@ __device__ __forceinline__ uint32_t byte_x4(uint32_t w) {
 // value.  The value is found bit by bit with ballots; among keys equal to it,
 // the needed number of smallest tags is found the same way.
 // ---------------------------------------------------------------------------
+// End of a segment: a bound on its ck-th smallest key value tighter than the
+// largest wave bound.  Candidates are the waves' bounds wsum[c] (each wave's
+// r-th smallest value, ~0 when it holds fewer than r keys); every wave counts
+// its own keys at or below each candidate with ballots, and the smallest
+// candidate with at least ck keys of the segment at or below it is returned
+// (~0 if none).  cnt: NW + 1 ints of LDS, cnt[c] = 0 and cnt[NW] = ~0 since
+// the segment began.  All threads call it after the barrier that follows
+// every wave's last buffer write.  Segments with waves that hold fewer than r
+// keys otherwise merge every kept key (up to ~1000).
+// ---------------------------------------------------------------------------
+template <int NT, int J>
+__device__ __forceinline__ uint32_t tighter_bound(const unsigned long long* wb, int nw,
+                                                  const int* wsum, int ck, int* cnt) {
+    constexpr int NW = NT / 64;
+    const int lane = threadIdx.x & 63;
+    uint32_t v[J];
+    bool ok[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int i = j * 64 + lane;
+        ok[j] = i < nw;
+        v[j] = ok[j] ? (uint32_t)(wb[i] >> 32) : 0u;
+    }
+    for (int c = 0; c < NW; c++) {
+        const uint32_t t = (uint32_t)wsum[c];
+        int m = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) m += __popcll(__ballot(ok[j] && v[j] <= t));
+        if (lane == 0 && m) atomicAdd(&cnt[c], m);
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < NW && cnt[threadIdx.x] >= ck)
+        atomicMin((unsigned int*)&cnt[NW], (uint32_t)wsum[threadIdx.x]);
+    __syncthreads();
+    return (uint32_t)cnt[NW];
+}
+
+// ---------------------------------------------------------------------------
 template <int J>
 __device__ __forceinline__ uint32_t wave_prune(unsigned long long* buf, int n, int k) {
     const int lane = threadIdx.x & 63;
@@ -2244,6 +2282,9 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             ctl[1] = 0;         // merge count
             ctl[2] = 0;         // next task
         }
+        // the end-of-segment bound's counters (ktmp is free until the merge)
+        if (2 * ck >= NW + 1)
+            for (int i = tid; i <= NW; i += NT) ((int*)ktmp)[i] = i < NW ? 0 : (int)~0u;
         __syncthreads();
         build_lut_lds<NT>(sq, M, Ds, K1D, bpd, sc1d, lut);
         __syncthreads();
@@ -2437,6 +2478,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             for (int w2 = 0; w2 < NW; w2++) t3 = max(t3, (uint32_t)wsum[w2]);
             Tf = min(Tf, t3);
         }
+        if (2 * ck >= NW + 1) Tf = min(Tf, tighter_bound<NT, J>(wb, nw, wsum, ck, (int*)ktmp));
         for (int i0 = 0; i0 < nw; i0 += 64) {
             const int i = i0 + lane;
             const unsigned long long key = i < nw ? wb[i] : ~0ull;
@@ -2598,6 +2640,9 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             ctl[1] = 0;
             ctl[2] = 0;
         }
+        // the end-of-segment bound's counters (ktmp is free until the merge)
+        if (2 * ck >= NW + 1)
+            for (int i = tid; i <= NW; i += NT) ((int*)ktmp)[i] = i < NW ? 0 : (int)~0u;
         __syncthreads();
         // rows (32 candidates) of each probe that meet the segment's groups
         for (int i = tid; i < P; i += NT) {
@@ -2923,6 +2968,7 @@ scan_skew_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
             for (int w2 = 0; w2 < NW; w2++) t3 = max(t3, (uint32_t)wsum[w2]);
             Tf = min(Tf, t3);
         }
+        if (2 * ck >= NW + 1) Tf = min(Tf, tighter_bound<NT, J>(wb, nw, wsum, ck, (int*)ktmp));
         for (int i0 = 0; i0 < nw; i0 += 64) {
             const int i = i0 + lane;
             const unsigned long long key = i < nw ? wb[i] : ~0ull;
