@@ -289,3 +289,82 @@ def test_search_k_exceeds_candidates_pads():
         nfill = int(np.sum(ids[i] >= 0))
         assert nfill <= 64 and np.all(ids[i][nfill:] == -1)
         assert np.all(np.isinf(dist[i][nfill:])) and np.all(np.diff(dist[i][:nfill]) >= 0)
+
+
+# -- the reference's approximate top-ck (jhq_v14_streaming_add/search.cu:105-195) --
+class _P:
+    """Params of a hand-built flat index (one list)."""
+    M, B, Br, nlist, nprobe, ivf_iters, residual_per_subspace = 1, 8, 4, 1, 1, 1, 0
+
+    def __init__(self, alpha):
+        self.alpha = alpha
+
+
+def _hand_index(codes, alpha):
+    """d = 8, one subspace of 8 one-bit dimensions (code bit t picks
+    c1d[(v >> t) & 1] = -1 or +1), identity rotation, zero residual codebook
+    and corrections: a candidate's primary distance to q = (+1, ..., +1) is 4x
+    the number of zero bits of its code."""
+    n = len(codes)
+    d = 8
+    return po.OracleIndex.from_state(
+        d, _P(alpha), np.eye(d, dtype=np.float32), np.array([-1.0, 1.0], np.float32),
+        np.zeros(16, np.float32), np.zeros((1, d), np.float32), np.zeros(1, np.float32),
+        np.array([0, n], np.int32), np.arange(n, dtype=np.int32),
+        np.asarray(codes, np.uint8).reshape(n, 1), np.zeros((n, 4), np.uint8),
+        np.zeros(n, np.float32))
+
+
+def test_reference_selection_drops_a_threads_fifth_candidate():
+    """Known answer worked out by hand from the reference's selection: 256
+    threads stride the candidates, each keeps its 4 best (a candidate enters
+    only if strictly below the fourth), and each of the ck rounds takes a
+    block argmin: thread t scans slots t, t + 256, ... of the 1024 kept values
+    (slot 4 t + i = thread t's i-th), then a halving tree keeps the left value
+    on ties.  Five distance-0 candidates sit on thread 0's stride (positions
+    0, 256, 512, 768, 1024): exact selection returns the five; the reference's
+    keeps only the first four (slots 0-3).  Round 1 takes slot 0.  Round 2:
+    slots 1, 2, 3 tie; the tree pairs thread 0's side (now holding thread
+    2's 0 after the stride-2 step) against thread 1's, keeping the left:
+    slot 2 (position 512); round 3 slot 1 (256); round 4 slot 3 (768).  Round 5
+    among the distance-4 candidates at positions 1 (slot 4, scanned by thread
+    4), 2 (slot 8, thread 8) and 300 (thread 44's slot 176, thread 176): the
+    stride-128 step moves thread 176's 4 to thread 48, stride 32 to thread 16,
+    stride 16 to thread 0, which keeps it against thread 4's equal value at
+    stride 4: position 300."""
+    n = 1300
+    codes = np.full(n, 0x0F, np.uint8)          # four zero bits: distance 16
+    codes[[0, 256, 512, 768, 1024]] = 0xFF       # distance 0
+    codes[[1, 2, 300]] = 0xFE                    # one zero bit: distance 4
+    o = _hand_index(codes, alpha=1.0)
+    q = np.ones((1, 8), np.float32)
+    pr = np.zeros((1, 1), np.int32)
+    ex = o.search(q, 5, debug=True, q_rot=q, probes=pr, mode=0)
+    ap = o.search(q, 5, debug=True, q_rot=q, probes=pr, mode=1)
+    assert list(ex["topck_pos"][0]) == [0, 256, 512, 768, 1024]
+    assert list(ex["topck_dist"][0]) == [0.0] * 5
+    assert list(ap["topck_pos"][0]) == [0, 512, 256, 768, 300]
+    assert list(ap["topck_dist"][0]) == [0.0, 0.0, 0.0, 0.0, 4.0]
+
+
+def test_reference_selection_is_exact_with_one_candidate_per_thread():
+    """With at most 256 candidates every thread holds at most one, so the
+    reference's selection keeps all of them: its ck distances are exactly the
+    ck smallest (the same values as exact selection), and the two short lists
+    hold the same candidates below the ck-th distance (at that distance a tie
+    may be broken another way: the argmin tree, not the position, decides)."""
+    rng = np.random.default_rng(11)
+    codes = rng.integers(0, 256, 250).astype(np.uint8)
+    codes[rng.integers(0, 250, 40)] = 0xF0  # many equal distances
+    o = _hand_index(codes, alpha=4.0)
+    q = np.ones((1, 8), np.float32)
+    pr = np.zeros((1, 1), np.int32)
+    ex = o.search(q, 10, debug=True, q_rot=q, probes=pr, mode=0)
+    ap = o.search(q, 10, debug=True, q_rot=q, probes=pr, mode=1)
+    de, da = ex["topck_dist"][0], ap["topck_dist"][0]
+    assert np.array_equal(np.sort(de).view(np.uint32), np.sort(da).view(np.uint32))
+    last = de.max()
+    assert set(ex["topck_pos"][0][de < last]) == set(ap["topck_pos"][0][da < last])
+    # and the brute-force distances: 4 x the number of zero bits
+    zeros = np.array([8 - bin(int(c)).count("1") for c in codes])
+    assert np.array_equal(np.sort(de), np.sort(4.0 * zeros)[:de.size].astype(np.float32))
