@@ -246,7 +246,12 @@ int jhq_k_residual_encode(const float* d_y, const uint8_t* d_primary,
                           int Br, int bpv, int bits_per_dim, void* stream);
 
 /* assign_on_gpu + assign_from_dots_kernel — v14/jhq_gpu_index.cu:367-393,
- * 23-40: argmin_c ||c||^2 - 2<c,y>, ties to the lowest c. */
+ * 23-40: argmin_c ||c||^2 - 2<c,y>, ties to the lowest c, each score the
+ * fixed-order fmaf chain (k ascending).  When d % 4 == 0 (and the arrays are
+ * 16-byte aligned) the scores are computed on MFMA and every row whose two
+ * best scores lie within the summation-order error bound is re-assigned by
+ * the fixed-order kernel, so the result is the same bit for bit.  Temporary
+ * device memory comes from the stream-ordered allocator on `stream`. */
 int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent,
                  const float* d_cent_norms, int nlist, int32_t* d_assign,
                  void* stream);
