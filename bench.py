@@ -70,6 +70,9 @@ def parse():
                          "(jhq_save format) if it exists, else build it and save it there")
     ap.add_argument("--seed", type=int, default=None,
                     help="data seed (default 0x4A48510000 + config)")
+    ap.add_argument("--scan-kind", type=int, default=0, choices=(0, 1),
+                    help="0 (default): the integer-MFMA pre-scan with exact re-check where it "
+                         "applies; 1: the byte-LUT scans only (same results)")
     return ap.parse_args()
 
 
@@ -195,6 +198,7 @@ def bench_float(args, cf):
                   ivf_iters=8, batch_size=BATCH, seed=42)
     t0 = time.time()
     ix = jg.JHQGpuIndex(D, p)
+    ix.set_scan_kind(args.scan_kind)
     t_create = time.time() - t0
     n_train = min(N, 100_000)
     t0 = time.time()
@@ -576,6 +580,7 @@ def bench_bytes(args, cf):
         qb, _ = gen_bytes(torch, dev, NQ, D, NCOMP, seed + 0x100, cf["kind"], means)
         t0 = time.time()
         ix = jg.JHQGpuIndex.load(args.index)
+        ix.set_scan_kind(args.scan_kind)
         log(f"loaded {args.index} ({ix.ntotal} vectors) in {time.time() - t0:.1f}s")
         profile_mode(torch, dev, ix, qb.float(), K, BATCH, npb, alpha, args.profile_batches)
         return
@@ -601,6 +606,7 @@ def bench_bytes(args, cf):
     p = jg.Params(M=M, B=8, Br=4, alpha=alpha, nlist=NLIST, nprobe=npb, ivf_iters=8,
                   batch_size=BATCH, seed=42)
     ix = jg.JHQGpuIndex(D, p)
+    ix.set_scan_kind(args.scan_kind)
     n_train = min(N, max(100_000, 16 * NLIST))
     t0 = time.time()
     ix.train(hb[:n_train])
@@ -732,6 +738,7 @@ def bench_streaming(args):
     p = jg.Params(M=M, B=8, Br=4, alpha=alpha, nlist=NLIST, nprobe=npb, ivf_iters=8,
                   batch_size=BATCH, seed=42, residual_per_subspace=1)
     ix = jg.JHQGpuIndex(D, p)
+    ix.set_scan_kind(args.scan_kind)
     n_train = min(N0, max(100_000, 16 * NLIST))
     t0 = time.time()
     ix.train(hb[:n_train])

@@ -199,8 +199,19 @@ int jhq_load(const char* path, jhq_index** out);
  * (scan_topck_kernel), 1 wave-level selection (scan_wave_kernel), 2 every
  * distance to a buffer then one selection per query (scan_dump_kernel +
  * select_query_kernel), 3 wave-level selection with lanes skewed across
- * subspaces (scan_skew_kernel); and the short-list length ck. */
+ * subspaces (scan_skew_kernel), 4 integer-MFMA pre-scan with an exact
+ * re-check (mfma_scan_kernel + mfma_recheck_kernel); and the short-list
+ * length ck. */
 int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list);
+
+/* Scan choice (no counterpart in the reference, whose search always runs its
+ * byte-LUT scan): 0 (default) the integer-MFMA pre-scan wherever it applies
+ * (one-bit digits: K1D = 2 with Ds = 8, M a multiple of 16 up to 128, at most
+ * 2048 probes per batch), else the byte-LUT scans; 1 the byte-LUT scans only.
+ * Results are identical either way: the pre-scan only decides which
+ * candidates get their distance recomputed in the reference's order.
+ * Re-reserves the search workspace like jhq_set_nprobe. */
+int jhq_set_scan_kind(jhq_index* idx, int kind);
 
 /* List pool occupancy: slots in use (including padding, headroom and blocks
  * left behind by moves since the last re-pack) and allocated slots. */

@@ -97,6 +97,7 @@ _SIGS = {
     "jhq_get_plan": (_I, [_VP, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "jhq_search_device": (_I, [_VP, _VP, _I64, _I, _VP, _VP, _VP]),
     "jhq_reserve": (_I, [_VP, _I]),
+    "jhq_set_scan_kind": (_I, [_VP, _I]),
     "jhq_ntotal": (_I64, [_VP]),
     "jhq_dim": (_I, [_VP]),
     "jhq_set_nprobe": (_I, [_VP, _I]),
@@ -265,6 +266,12 @@ class JHQGpuIndex:
         with a larger k raise RuntimeError)."""
         _check(lib().jhq_reserve(self._h, int(k_max)))
 
+    def set_scan_kind(self, kind):
+        """0: the integer-MFMA pre-scan with exact re-check where it applies
+        (one-bit digits), else the byte-LUT scans; 1: the byte-LUT scans only.
+        Results are identical; only the speed differs."""
+        _check(lib().jhq_set_scan_kind(self._h, int(kind)))
+
     def search_device(self, q, k, out_dists, out_ids, stream=None):
         """q, out_dists, out_ids: torch device tensors (or int addresses).
         Enqueue-only: k must be within the reserved workspace (reserve())."""
@@ -307,7 +314,8 @@ class JHQGpuIndex:
         """(scan kernel name, short-list length ck) a search with this k uses."""
         kind, ck = _I(), _I()
         _check(lib().jhq_get_plan(self._h, int(k), ctypes.byref(kind), ctypes.byref(ck)))
-        names = ("scan_topck_kernel", "scan_wave_kernel", "scan_dump_kernel", "scan_skew_kernel")
+        names = ("scan_topck_kernel", "scan_wave_kernel", "scan_dump_kernel", "scan_skew_kernel",
+                 "mfma_scan_kernel")
         return names[kind.value], int(ck.value)
 
     def pool(self):

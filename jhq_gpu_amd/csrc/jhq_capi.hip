@@ -108,6 +108,8 @@ struct Workspace {
     DBuf<unsigned long long> wpartial, wtopck, wdump;
     // split sums of the query product
     DBuf<float> wqpart;
+    // integer-MFMA pre-scan: quantized queries, work list, counters
+    DBuf<unsigned char> wmfma;
 };
 
 }  // namespace
@@ -128,6 +130,9 @@ struct jhq_index {
     // searches with k <= res_k (and the current nprobe, alpha, batch_size)
     // run in the preallocated workspace; jhq_reserve raises it
     int res_k = 10;
+    // 0: the integer-MFMA pre-scan where it applies (one-bit digits), else the
+    // byte-LUT scans; 1: the byte-LUT scans only
+    int scan_kind = 0;
     // largest per-query candidate count of the dump scan for dump_P probes
     int dump_P = -1;
     int64_t dump_perq = 0;
@@ -390,6 +395,11 @@ int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_
 
 bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128; }
 
+bool mfma_eligible(const jhq_index* ix, int Bq, int P, int ck) {
+    return ix->scan_kind == 0 &&
+           jhq::mfma_scan_ok(ix->M, ix->d, ix->Ds, ix->K1D, ix->bpd, Bq, P, ck);
+}
+
 // Brings the skewed copy up to date: rows appended since the last refresh,
 // and every row of a list whose block moved (or of every list when the copy
 // had to grow).  Synchronous, so any stream may read the copy afterwards.
@@ -434,7 +444,7 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
     if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
-                        skew_eligible(ix)))
+                        skew_eligible(ix), mfma_eligible(ix, Bq, bp->P, bp->ck)))
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
@@ -444,7 +454,7 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
     }
     for (int i = 0; i < nws; i++)
         JHQ_TRY(ensure_workspace(ix, ix->ws[i], bp->ck, k, bp->P, bp->sh.max_segments, grow));
-    if (bp->sh.dump) {
+    if (bp->sh.dump || bp->sh.mfma) {
         // a query's candidates are at most the padded sizes of the P largest
         // lists (cached per P; inserts reset the cache)
         if (ix->dump_P != bp->P) {
@@ -456,9 +466,14 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
             ix->dump_P = bp->P;
             ix->dump_perq = per_q;
         }
+        // keys (dump scan) or biased integer distances (MFMA pre-scan)
+        const size_t slots = static_cast<size_t>(Bq) * std::max<int64_t>(ix->dump_perq, 1);
         for (int i = 0; i < nws; i++)
-            JHQ_TRY(need(ix->ws[i].wdump,
-                         static_cast<size_t>(Bq) * std::max<int64_t>(ix->dump_perq, 1), grow));
+            JHQ_TRY(need(ix->ws[i].wdump, bp->sh.mfma ? (slots + 1) / 2 : slots, grow));
+        if (bp->sh.mfma)
+            for (int i = 0; i < nws; i++)
+                JHQ_TRY(need(ix->ws[i].wmfma, jhq::mfma_scan_bytes(Bq, bp->P, ix->M, ix->num_cu),
+                             grow));
     }
     return JHQ_OK;
 }
@@ -484,10 +499,17 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
     JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
                                w.wgofs.p, w.wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
-    JHQ_HIP(jhq::scan_topck(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
-                            w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
-                            ix->dcodes_t.p, bp.ck, bp.sh, w.wpartial.p, w.wpslot.p,
-                            w.wdump.p, ix->dcodes_s.p, s));
+    if (bp.sh.mfma)
+        JHQ_HIP(jhq::mfma_scan(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
+                               w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
+                               ix->dcodes_t.p, bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
+                               w.wmfma.p, w.wmfma.n,
+                               w.wpartial.p, w.wpslot.p, ix->num_cu, s));
+    else
+        JHQ_HIP(jhq::scan_topck(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
+                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
+                                ix->dcodes_t.p, bp.ck, bp.sh, w.wpartial.p, w.wpslot.p,
+                                w.wdump.p, ix->dcodes_s.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
     JHQ_HIP(jhq::refine_topk(w.wpartial.p, w.wpslot.p, w.wqtot.p, Bq, bp.sh, bp.ck, k,
                              w.wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
@@ -761,6 +783,14 @@ int jhq_reserve(jhq_index* idx, int k_max) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (k_max <= 0) return fail(JHQ_EINVAL, "k_max must be positive");
     idx->res_k = std::max(idx->res_k, k_max);
+    return reserve_search(idx);
+}
+
+int jhq_set_scan_kind(jhq_index* idx, int kind) {
+    if (!idx) return fail(JHQ_EINVAL, "null index");
+    if (kind != 0 && kind != 1) return fail(JHQ_EINVAL, "scan kind must be 0 or 1");
+    JHQ_TRY(idx->quiesce());
+    idx->scan_kind = kind;
     return reserve_search(idx);
 }
 
@@ -1567,9 +1597,9 @@ int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list) {
     const int P = std::min(idx->nprobe, idx->nlist);
     jhq::ScanShape sh{};
     if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh,
-                        skew_eligible(idx)))
+                        skew_eligible(idx), mfma_eligible(idx, idx->batch_size, P, ck)))
         return fail(JHQ_EINVAL, "no scan plan fits in LDS");
-    if (scan_kind) *scan_kind = sh.dump ? 2 : sh.skew ? 3 : sh.wave ? 1 : 0;
+    if (scan_kind) *scan_kind = sh.mfma ? 4 : sh.dump ? 2 : sh.skew ? 3 : sh.wave ? 1 : 0;
     if (short_list) *short_list = ck;
     return JHQ_OK;
 }

@@ -153,11 +153,29 @@ struct ScanShape {
                        // lists) * 16 keys
     int region;        // wave selection: bytes of the LUT / merge region
     int ov;            // work plan: virtual groups per query (the cost of a segment)
+    int mfma;          // 1: integer-MFMA pre-scan + exact re-check, one segment per query
+                       // (B * (groups of the P largest lists) * 16 u32 values in the dump
+                       // buffer and mfma_scan_bytes of workspace)
 };
 // LDS plan of the scan kernel; returns false if the byte LUT and the
 // selection buffers do not fit.
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
-               bool skew = false);
+               bool skew = false, bool mfma = false);
+
+// Integer-MFMA pre-scan for one-bit digits (K1D = 2, Ds = 8, M a multiple of
+// 16 up to 128): per query the distances C + s * I(x) with I exact from int8
+// MFMA products over the batch's shared lists, then every candidate that the
+// error bound cannot exclude from the exact top-ck is re-checked with the
+// reference's arithmetic; partial[query's segment][ck] as scan_topck writes
+// it.  dump holds one u32 per candidate slot of the batch (the sum of qtot
+// times 16); ws (256-byte aligned) holds mfma_scan_bytes for this num_cu.
+bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck);
+size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
+hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
+                     int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
+                     const int4* ldesc, const uint8_t* codes_t, int ck, uint32_t* dump,
+                     unsigned char* ws, size_t ws_bytes, unsigned long long* partial,
+                     int32_t* partial_slot, int num_cu, hipStream_t s);
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from
 // q_rot (v14/search.cu:65-195); partial[segment][ck] keys

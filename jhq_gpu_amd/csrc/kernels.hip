@@ -3282,8 +3282,26 @@ static size_t scan_wave_lds(int NT, int M, int d, int P, int ck, int K1D, int B,
            (size_t)K1D * 4 + NW * 4 + 64;
 }
 
+static size_t mfma_plan_lds(int B, int P);
+static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B);
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
-               bool skew) {
+               bool skew, bool mfma) {
+    out->mfma = 0;
+    if (mfma) {
+        // integer-MFMA pre-scan and one exact re-check per query: one
+        // segment per query (the caller checked mfma_scan_ok)
+        out->G = 1;
+        out->ov = 0;
+        out->max_segments = B;
+        out->wave = 0;
+        out->skew = 0;
+        out->dump = 0;
+        out->mfma = 1;
+        out->nt = 1024;
+        out->lds = (int)mfma_recheck_lds(M, d, P, ck, K1D, B);
+        out->region = (int)mfma_plan_lds(B, P);
+        return true;
+    }
     out->G = target_wg;
     out->max_segments = target_wg + B;
     // a segment (its LUT build, merge and first loads of a new query's lists)
@@ -3773,6 +3791,743 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
                        qtot, B, sh.G, ck, k, q_rot, d, Ds, res_c1d, Kr, RC, Br, bpv, ldesc, nlist,
                        list_res, list_corr, list_ids, out_d, out_i, topck_dbg, stage_cap,
                        sh.ov);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Integer-MFMA pre-scan for one-bit digits (K1D = 2, Ds = 8), with an exact
+// re-check.  With one bit per dimension a subspace's LUT entry is affine in
+// the bits b_k of its code (v14/search.cu:65-91 computes it as a sum of
+// squares over the subspace's dimensions):
+//   lut[m][v] = sum_k (q_k - c[b_k])^2 = sum_k (q_k - c0)^2 + sum_k b_k dl_k,
+//   dl_k = (q_k - c1)^2 - (q_k - c0)^2,
+// so a candidate's ADC distance is a(x) = C + <dl, bits(x)> with
+// C = ||q - c0||^2.  Per query, dl is rounded to multiples of a step s
+// (|round(dl/s)| <= 32000, split into two int8 halves hi * 256 + lo), and
+// I(x) = sum_k b_k round(dl_k / s) is exact in int32: two int8 MFMA products
+// per 64 dimensions, for up to 16 queries that probe the same list at once
+// (the queries of a batch share most of their probed candidates).
+//
+// Bound: |C + s I(x) - a(x)| <= e_q = s D / 2 (plus rounding slack), and the
+// reference's fp32 distance a_ref(x), a sum of nonnegative rounded terms, is
+// within g = (M + 16) 2^-23 of a(x) relatively.  With T the ck-th smallest I
+// of the query, at least ck candidates have a_ref <= U = (1 + g)(C + s T +
+// e_q), so every candidate in the exact top-ck has
+//   I(x) <= ((U / (1 - g)) + e_q - C) / s.
+// Those candidates are re-checked: their distances are recomputed in the
+// reference's order (each LUT entry's fma chain, then the M entries added in
+// m order from 0.0f) and the exact top-ck by (dist, stored position) is
+// selected from them, so the result does not depend on the MFMA values.
+// Queries with non-finite or huge values re-check every candidate.
+// ---------------------------------------------------------------------------
+constexpr int kMfmaPlanNT = 1024;
+constexpr int kMfmaWavesPerCU = 8;  // scan waves: two 4-wave workgroups per CU
+constexpr int kRecheckNT = 1024;
+constexpr int kRecheckCap = 2048;   // survivors / members held in LDS
+constexpr int kRecheckCHM = 128;    // members per exact-distance round
+constexpr int kRecheckLPT = 16;     // 16-byte row loads in flight per re-check thread
+constexpr int kMfmaPairsPT = 4;     // probes per work-list thread
+constexpr int kMfmaMaxBP = kMfmaPairsPT * kMfmaPlanNT;  // probes per batch
+
+struct MfmaQS {
+    double s, C, e;
+    int all, pad;  // all = 1: re-check every candidate
+};
+
+typedef int mfma_v4i __attribute__((ext_vector_type(4)));
+
+// hash slots for BP probes: load factor at most 2/3
+static int mfma_hash_size(int BP) { return (3 * BP / 2 + 127) / 64 * 64; }
+
+// A group is one probed list and up to 16 of the queries that probe it: the
+// MFMA tiles of 16 candidates over the list's slots (a probed list of nl
+// vectors fills ceil(nl / 16) 16-slot groups of each probing query's
+// candidate row).  The batch's tiles are numbered group by group, and scan
+// wave v takes tiles [v T / W, (v + 1) T / W).  Workspace pieces, 256-byte
+// aligned, in this order.
+struct MfmaWs {
+    int8_t* qa;      // [B][2][D]: hi then lo bytes in the lanes' register order
+    MfmaQS* qs;      // [B]
+    int2* pairs;     // [B*P]: (query, dump offset of the list's first slot)
+    int4* grp;       // [B*P][2]: (block start, row stride, size, first pair),
+                     //           (queries, tiles, 0, 0)
+    int2* wstart;    // [waves]: (group, tile in the group) where a wave starts
+    int* ctl;        // [16]: tiles of the batch, groups
+};
+
+static size_t mfma_carve(int B, int P, int M, int nwaves, unsigned char* base, MfmaWs* w) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    size_t off = 0;
+    const size_t o_qa = off;
+    off += al((size_t)B * 2 * 8 * M);
+    const size_t o_qs = off;
+    off += al((size_t)B * sizeof(MfmaQS));
+    const size_t o_pairs = off;
+    off += al((size_t)B * P * sizeof(int2));
+    const size_t o_g = off;
+    off += al((size_t)B * P * 2 * sizeof(int4));
+    const size_t o_ws = off;
+    off += al((size_t)nwaves * sizeof(int2));
+    const size_t o_ctl = off;
+    off += al(16 * sizeof(int));
+    if (w) {
+        w->qa = (int8_t*)(base + o_qa);
+        w->qs = (MfmaQS*)(base + o_qs);
+        w->pairs = (int2*)(base + o_pairs);
+        w->grp = (int4*)(base + o_g);
+        w->wstart = (int2*)(base + o_ws);
+        w->ctl = (int*)(base + o_ctl);
+    }
+    return off;
+}
+
+// Block sums / max of three doubles (every thread gets the result).
+template <int NT>
+__device__ __forceinline__ void block_reduce3(double& a, double& b, double& c, double* red) {
+    constexpr int NW = NT / 64;
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off);
+        b += __shfl_xor(b, off);
+        c = fmax(c, __shfl_xor(c, off));
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        red[3 * wv] = a;
+        red[3 * wv + 1] = b;
+        red[3 * wv + 2] = c;
+    }
+    __syncthreads();
+    a = 0.0;
+    b = 0.0;
+    c = 0.0;
+    for (int w2 = 0; w2 < NW; w2++) {
+        a += red[3 * w2];
+        b += red[3 * w2 + 1];
+        c = fmax(c, red[3 * w2 + 2]);
+    }
+}
+
+// Workgroups 0..B-1 quantize one query each; workgroup B builds the batch's
+// work list: the distinct probed lists (a hash in LDS), the queries of each
+// (in arrival order; the order does not change any result), the groups and
+// where each of the nwaves scan waves starts.
+template <int NT>
+__global__ void __launch_bounds__(NT)
+mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __restrict__ c1d,
+                 const int32_t* __restrict__ probes, const int32_t* __restrict__ gofs,
+                 const int32_t* __restrict__ qtot, int B, int P, const int4* __restrict__ ldesc,
+                 MfmaWs w, int H, int nwaves) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x;
+    if ((int)blockIdx.x < B) {
+        const int b = blockIdx.x, D = d, NK = M / 8, GS = M / 4;
+        double* red = (double*)smem;
+        const double c0 = c1d[0], c1 = c1d[1];
+        double sC = 0.0, sA = 0.0, mx = 0.0;
+        for (int i = tid; i < D; i += NT) {
+            const double q = q_rot[(int64_t)b * d + i];
+            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
+            sC += t0 * t0;
+            sA += fabs(dl);
+            mx = fmax(mx, fabs(dl));
+        }
+        block_reduce3<NT>(sC, sA, mx, red);
+        const bool fin = isfinite(sC) && isfinite(sA) && sC + sA < 1e36;
+        const double s = fin && mx > 0.0 ? mx / 32000.0 : 1.0;
+        int8_t* qa = w.qa + (int64_t)b * 2 * D;
+        for (int i = tid; i < D; i += NT) {
+            const double q = q_rot[(int64_t)b * d + i];
+            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
+            const int iq = fin ? (int)rint(dl / s) : 0;
+            const int hi = (iq + 128) >> 8, lo = iq - hi * 256;
+            // dimension i = 8 m + k: lane group h = m / GS, dword t and byte
+            // e of that group's subspaces, K-step 2t + k / 4, register k % 4
+            const int m = i >> 3, k = i & 7, h = m / GS, mm = m % GS;
+            const int off = h * NK * 16 + (2 * (mm >> 2) + (k >> 2)) * 16 + (k & 3) * 4 + (mm & 3);
+            qa[off] = (int8_t)hi;
+            qa[D + off] = (int8_t)lo;
+        }
+        if (tid == 0) {
+            MfmaQS Q;
+            Q.s = s;
+            Q.C = sC;
+            Q.e = 0.5000001 * s * D + 1e-12 * (sC + sA);
+            Q.all = fin ? 0 : 1;
+            Q.pad = 0;
+            w.qs[b] = Q;
+        }
+        return;
+    }
+    // ---- work list ----
+    // a pair e = (query b, probe p) of the batch is taken by thread e % NT;
+    // its hash slot and rank stay in that thread's registers
+    const int BP = B * P;
+    int* hk = (int*)smem;       // [H] list id or -1
+    int* hc = hk + H;           // [H] queries of the slot
+    int* hg = hc + H;           // [H + 1] group prefix
+    int* hst = hg + H + 1;      // [H + 1] first pair prefix
+    int* htl = hst + H + 1;     // [H + 1] tile prefix
+    int* qpre = htl + H + 1;    // [B + 1]
+    int* wsum = qpre + B + 1;   // [NT / 64]
+    for (int i = tid; i < H; i += NT) {
+        hk[i] = -1;
+        hc[i] = 0;
+    }
+    block_exclusive_scan<NT>([&](int b) { return (int)qtot[b]; }, B, qpre, wsum);
+    int ps[kMfmaPairsPT], pr[kMfmaPairsPT];
+#pragma unroll
+    for (int i = 0; i < kMfmaPairsPT; i++) {
+        const int e = tid + i * NT;
+        ps[i] = -1;
+        pr[i] = 0;
+        if (e >= BP) continue;
+        const int l = probes[e];
+        if (ldesc[l].z == 0) continue;  // empty list: no slots
+        int h = (int)(((uint64_t)((uint32_t)l * 2654435761u) * (uint32_t)H) >> 32);
+        for (;;) {
+            const int old = atomicCAS(&hk[h], -1, l);
+            if (old == -1 || old == l) break;
+            h = h + 1 == H ? 0 : h + 1;
+        }
+        pr[i] = atomicAdd(&hc[h], 1);
+        ps[i] = h;
+    }
+    __syncthreads();
+    // slot h holds ceil(hc / 16) groups of ceil(size / 16) tiles each
+    auto ntl = [&](int h) { return (ldesc[hk[h]].z + kGroup - 1) / kGroup; };
+    block_exclusive_scan<NT>([&](int h) { return hk[h] >= 0 ? (hc[h] + 15) / 16 : 0; }, H, hg,
+                             wsum);
+    block_exclusive_scan<NT>([&](int h) { return hc[h]; }, H, hst, wsum);
+    block_exclusive_scan<NT>(
+        [&](int h) { return hk[h] >= 0 ? ((hc[h] + 15) / 16) * ntl(h) : 0; }, H, htl, wsum);
+    const int T = htl[H];
+    for (int h = tid; h < H; h += NT) {
+        if (hk[h] < 0) continue;
+        const int4 L = ldesc[hk[h]];
+        const int nt = (L.z + kGroup - 1) / kGroup;
+        for (int t = 0; t < (hc[h] + 15) / 16; t++) {
+            const int g = hg[h] + t;
+            w.grp[2 * g] = make_int4(L.x, L.y, L.z, hst[h] + 16 * t);
+            w.grp[2 * g + 1] = make_int4(min(16, hc[h] - 16 * t), nt, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kMfmaPairsPT; i++) {
+        if (ps[i] < 0) continue;
+        const int e = tid + i * NT, b = e / P, p = e - b * P;
+        w.pairs[hst[ps[i]] + pr[i]] =
+            make_int2(b, (qpre[b] + gofs[(int64_t)b * (P + 1) + p]) * kGroup);
+    }
+    // wave v starts at tile a = v T / W: in slot h with htl[h] <= a <
+    // htl[h + 1] (the largest h with htl[h] <= a is occupied when a < T)
+    for (int v = tid; v < nwaves; v += NT) {
+        const int a = (int)((int64_t)v * T / nwaves);
+        int2 st = make_int2(0, 0);
+        if (a < T) {
+            int lo = 0, hi = H - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (htl[mid] <= a) lo = mid;
+                else hi = mid - 1;
+            }
+            const int nt = ntl(lo), r = a - htl[lo];
+            st = make_int2(hg[lo] + r / nt, r - (r / nt) * nt);
+        }
+        w.wstart[v] = st;
+    }
+    if (tid == 0) {
+        w.ctl[0] = T;
+        w.ctl[1] = hg[H];
+    }
+}
+
+constexpr int kMfmaPD = 4;  // tiles in flight per wave
+// One 16-candidate tile from its LDS copy: the lane's four code dwords, the
+// bit planes, two int8 MFMA chains (hi and lo halves of the query steps),
+// and the biased integer distances of rows 4h..4h+3 (rows without a query
+// have d < 0).
+template <int M>
+__device__ __forceinline__ void mfma_tile(const unsigned char* tb, int h, int j, uint32_t qsel,
+                                          const mfma_v4i (&ahi)[M / 8],
+                                          const mfma_v4i (&alo)[M / 8], int cand, int nl,
+                                          uint32_t* out, int d0, int d1, int d2, int d3) {
+    constexpr int NK = M / 8, ND = M / 16, GS = M / 4;
+    uint32_t cw[ND];
+#pragma unroll
+    for (int tt = 0; tt < ND; tt++) {
+        const int m0 = GS * h + 4 * tt;
+        const unsigned char* rp = tb + (m0 + h) * 16 + (j & 12);
+        const uint32_t r0 = *(const uint32_t*)rp;
+        const uint32_t r1 = *(const uint32_t*)(rp + 16);
+        const uint32_t r2 = *(const uint32_t*)(rp + 32);
+        const uint32_t r3 = *(const uint32_t*)(rp + 48);
+        const uint32_t x01 = __builtin_amdgcn_perm(r1, r0, qsel);
+        const uint32_t x23 = __builtin_amdgcn_perm(r3, r2, qsel);
+        cw[tt] = __builtin_amdgcn_perm(x23, x01, 0x05040100u);
+    }
+    mfma_v4i ah = {0, 0, 0, 0}, alw = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NK; s++) {
+        const uint32_t x = cw[s >> 1];
+        const int k0 = 4 * (s & 1);
+        mfma_v4i bv;
+        bv[0] = (int)((x >> k0) & 0x01010101u);
+        bv[1] = (int)((x >> (k0 + 1)) & 0x01010101u);
+        bv[2] = (int)((x >> (k0 + 2)) & 0x01010101u);
+        bv[3] = (int)((x >> (k0 + 3)) & 0x01010101u);
+        ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[s], bv, ah, 0, 0, 0);
+        alw = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[s], bv, alw, 0, 0, 0);
+    }
+    const bool ok = cand < nl;
+    if (d0 >= 0) out[d0] = ok ? (uint32_t)(ah[0] * 256 + alw[0]) + 0x80000000u : 0xffffffffu;
+    if (d1 >= 0) out[d1] = ok ? (uint32_t)(ah[1] * 256 + alw[1]) + 0x80000000u : 0xffffffffu;
+    if (d2 >= 0) out[d2] = ok ? (uint32_t)(ah[2] * 256 + alw[2]) + 0x80000000u : 0xffffffffu;
+    if (d3 >= 0) out[d3] = ok ? (uint32_t)(ah[3] * 256 + alw[3]) + 0x80000000u : 0xffffffffu;
+}
+
+// Lane l: query row / candidate column l % 16, K group l / 16 (the lane
+// layout of v_mfma_i32_16x16x64_i8: A and B bytes of one lane cover the same
+// 16 dimensions; result register v of lane l is query row 4 (l / 16) + v,
+// candidate l % 16).  Each wave walks its share of the batch's tiles group by
+// group (no shared counter).  A tile of 16 candidates is M rows of 16 code
+// bytes; each row arrives with one 16-byte load, kMfmaPD tiles ahead, and is
+// written to the wave's LDS ring (rows of lane group h start one row apart,
+// so the 16 addresses a read touches sit in distinct banks).  A lane's code
+// bytes for its candidate are four LDS dwords and a 4x4 byte transpose
+// (v_perm_b32); bit plane k of a code dword is (w >> k) & 0x01010101.
+template <int M>
+__global__ void __launch_bounds__(256)
+mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __restrict__ dump) {
+    constexpr int NK = M / 8, GS = M / 4, D = 8 * M;
+    constexpr int RL = (M + 63) / 64;          // rows a lane loads per tile (1 or 2)
+    static_assert(RL <= 2, "at most 128 subspaces");
+    constexpr int TB = (M + 4) * 16;           // LDS bytes of one tile
+    __shared__ __align__(16) unsigned char ring[4][kMfmaPD * TB];
+    const int lane = threadIdx.x & 63, j = lane & 15, h = lane >> 4;
+    unsigned char* my = ring[threadIdx.x >> 6];
+    const int W = gridDim.x * 4, wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int T = w.ctl[0];
+    const int a0 = (int)((int64_t)wid * T / W), a1 = (int)((int64_t)(wid + 1) * T / W);
+    int left = a1 - a0;
+    if (left <= 0) return;
+    const uint32_t qsel = (uint32_t)(j & 3) | ((uint32_t)(4 + (j & 3)) << 8) | 0x0c0c0000u;
+    const int2 st = w.wstart[wid];
+    int g = st.x, off = st.y;
+    while (left > 0) {
+        const int4 ga = w.grp[2 * g], gb = w.grp[2 * g + 1];
+        const int nq = gb.x, q0 = ga.w;
+        const int n = min(gb.y - off, left);
+        // row stride: the list's capacity; slots: its size rounded up to 16
+        const int npad = ga.y, nl = ga.z;
+        const uint8_t* base = codes_t + (int64_t)ga.x * M + 16 * off;
+        // tiles past the run's last reload its last tile (kept in bounds,
+        // never used); rows past M - 1 reload row M - 1.  The ring is four
+        // named registers (no array), so it stays out of private memory.
+        const uint8_t* rowa = base + (int64_t)min(lane, M - 1) * npad;
+        const uint8_t* rowb = base + (int64_t)min(lane + 64, M - 1) * npad;
+        uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+#define JHQ_MFMA_FETCH(U, K)                                                     \
+    do {                                                                         \
+        const int c_ = 16 * min((K), n - 1);                                     \
+        ra##U = *(const uint4*)(rowa + c_);                                      \
+        if (RL > 1) rb##U = *(const uint4*)(rowb + c_);                          \
+    } while (0)
+        JHQ_MFMA_FETCH(0, 0);
+        JHQ_MFMA_FETCH(1, 1);
+        JHQ_MFMA_FETCH(2, 2);
+        JHQ_MFMA_FETCH(3, 3);
+        mfma_v4i ahi[NK], alo[NK];
+        if (j < nq) {
+            const int b = w.pairs[q0 + j].x;
+            const mfma_v4i* src = (const mfma_v4i*)(w.qa + (int64_t)b * 2 * D + h * NK * 16);
+#pragma unroll
+            for (int s = 0; s < NK; s++) {
+                ahi[s] = src[s];
+                alo[s] = src[D / 16 + s];
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < NK; s++) {
+                ahi[s] = mfma_v4i{0, 0, 0, 0};
+                alo[s] = mfma_v4i{0, 0, 0, 0};
+            }
+        }
+        // dump offsets of the run's first slot for query rows 4h .. 4h+3
+        const int d0 = 4 * h + 0 < nq ? w.pairs[q0 + 4 * h + 0].y + 16 * off : -1;
+        const int d1 = 4 * h + 1 < nq ? w.pairs[q0 + 4 * h + 1].y + 16 * off : -1;
+        const int d2 = 4 * h + 2 < nq ? w.pairs[q0 + 4 * h + 2].y + 16 * off : -1;
+        const int d3 = 4 * h + 3 < nq ? w.pairs[q0 + 4 * h + 3].y + 16 * off : -1;
+        const int cbase = 16 * off + j;
+        // every pass issues the same loads (tiles past the last are clamped),
+        // so the wait for a ring slot leaves the later slots' loads in flight
+#define JHQ_MFMA_TILE(U)                                                                    \
+    {                                                                                       \
+        const int k = k0 + U;                                                               \
+        unsigned char* tb = my + U * TB;                                                    \
+        const bool live = k < n;                                                            \
+        if (live) {                                                                         \
+            if (lane < M) *(uint4*)(tb + (lane + lane / GS) * 16) = ra##U;                  \
+            if (RL > 1 && lane + 64 < M)                                                    \
+                *(uint4*)(tb + (lane + 64 + (lane + 64) / GS) * 16) = rb##U;                \
+        }                                                                                   \
+        JHQ_MFMA_FETCH(U, k + kMfmaPD);                                                     \
+        if (live) {                                                                         \
+            __builtin_amdgcn_s_waitcnt(0xc07f); /* this wave's LDS writes done */           \
+            mfma_tile<M>(tb, h, j, qsel, ahi, alo, cbase + 16 * k, nl, dump + 16 * k + j, d0, \
+                         d1, d2, d3);                                                       \
+        }                                                                                   \
+    }
+        for (int k0 = 0; k0 < n; k0 += kMfmaPD) {
+            JHQ_MFMA_TILE(0)
+            JHQ_MFMA_TILE(1)
+            JHQ_MFMA_TILE(2)
+            JHQ_MFMA_TILE(3)
+        }
+#undef JHQ_MFMA_TILE
+#undef JHQ_MFMA_FETCH
+        left -= n;
+        g++;
+        off = 0;
+    }
+}
+
+// Largest biased I (I + 2^31) a member of the exact top-ck can have, given
+// the biased ck-th smallest I of the query (see the bound above).
+__device__ __forceinline__ uint32_t mfma_member_bound(const MfmaQS& Q, uint32_t Tb, int M) {
+    if (Q.all) return 0xfffffffeu;
+    const double g = (double)(M + 16) * 0x1p-23, ab = 1e-30;
+    const double I = (double)((int64_t)Tb - 2147483648ll);
+    const double U = (1.0 + g) * (Q.C + Q.s * I + Q.e) + ab;
+    double R = ((U + ab) / (1.0 - g) + Q.e - Q.C) / Q.s;
+    R = R + 1e-9 * fabs(R) + 1.0;
+    if (!(R < 2147483646.0)) return 0xfffffffeu;
+    if (R < -2147483647.0) return 0u;
+    return (uint32_t)((int64_t)floor(R) + 2147483648ll);
+}
+
+// One workgroup per query: the ck-th smallest I bounds the members (two
+// passes over the query's I values), the members' distances are recomputed
+// in the reference's order, and the exact top-ck by (dist, position) goes
+// to partial[segment][ck] (one segment per query).
+template <int NT>
+__global__ void __launch_bounds__(NT)
+mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict__ qs,
+                    const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
+                    const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
+                    const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B,
+                    int P, const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t,
+                    int ck, unsigned long long* __restrict__ partial,
+                    int32_t* __restrict__ partial_slot) {
+    constexpr int NW = NT / 64;
+    extern __shared__ __align__(16) unsigned char smem[];
+    StreamSel S;
+    unsigned char* p0 = stream_carve<NT>(smem, ck, &S);
+    unsigned long long* surv = (unsigned long long*)p0;        // [kRecheckCap]
+    int* mp = (int*)(surv + kRecheckCap);                      // [kRecheckCap] member probe
+    int* mc = mp + kRecheckCap;                                // [kRecheckCap] member column
+    float* ebuf = (float*)(mc + kRecheckCap);                  // [CHM][M + 1]
+    float* sq = ebuf + kRecheckCHM * (M + 1);                  // [d]
+    float* sc1d = sq + d;                                      // [K1D]
+    int* meta = (int*)(sc1d + K1D);                            // [P][4]
+    int* sg = meta + 4 * P;                                    // [P + 1]
+    int* qpre = sg + P + 1;                                    // [B + 1]
+    int* spre = qpre + B + 1;                                  // [B + 1]
+    int* wsum = spre + B + 1;                                  // [NW]
+    int* ctl = wsum + NW;                                      // [4]
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    work_plan<NT>(qtot, B, 1, 0, qpre, spre, wsum);
+    const int s0 = spre[b], s1 = spre[b + 1];
+    if (s1 == s0) return;  // no candidates: refine sees no segment
+    for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
+    for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
+    for (int i = tid; i < P; i += NT) {
+        const int4 L = ldesc[probes[(int64_t)b * P + i]];
+        meta[4 * i] = L.x;
+        meta[4 * i + 1] = L.y;
+        meta[4 * i + 2] = L.z;
+        meta[4 * i + 3] = L.w;
+    }
+    for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
+    if (tid == 0) ctl[0] = 0;
+    stream_begin<NT>(S);
+    __syncthreads();
+    const MfmaQS Q = qs[b];
+    const int64_t n = (int64_t)(qpre[b + 1] - qpre[b]) * kGroup;
+    const uint32_t* row = dump + (int64_t)qpre[b] * kGroup;
+    // pass 1: an upper bound of the ck-th smallest I (each wave's r-th
+    // smallest thread minimum; NW * r >= ck values are at or below the max)
+    // (rows are whole 16-slot groups: 16-byte loads, kRecheckLPT of them in
+    // flight per thread)
+    const uint4* row4 = (const uint4*)row;
+    const int64_t n4 = n / 4;
+    uint32_t mn = ~0u;
+    for (int64_t i0 = tid; i0 < n4; i0 += kRecheckLPT * NT) {
+        uint4 v[kRecheckLPT];
+#pragma unroll
+        for (int u = 0; u < kRecheckLPT; u++)
+            v[u] = i0 + u * NT < n4 ? row4[i0 + u * NT] : make_uint4(~0u, ~0u, ~0u, ~0u);
+#pragma unroll
+        for (int u = 0; u < kRecheckLPT; u++)
+            mn = min(mn, min(min(v[u].x, v[u].y), min(v[u].z, v[u].w)));
+    }
+    const int r = (ck + NW - 1) / NW;
+    const uint32_t tw = r <= 64 ? wave_kth_u32(mn, r) : ~0u;
+    if (lane == 0) wsum[wv] = (int)tw;
+    __syncthreads();
+    uint32_t That = 0u;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; w2++) That = max(That, (uint32_t)wsum[w2]);
+    const uint32_t thr1 = That == ~0u ? 0xfffffffeu : mfma_member_bound(Q, That, M);
+    // pass 2: the candidates at or below thr1 (they include the ck smallest
+    // I values and every member)
+    for (int64_t i0 = 0; i0 < n4; i0 += kRecheckLPT * NT) {
+        uint4 v4[kRecheckLPT];
+#pragma unroll
+        for (int u = 0; u < kRecheckLPT; u++) {
+            const int64_t i = i0 + u * NT + tid;
+            v4[u] = i < n4 ? row4[i] : make_uint4(~0u, ~0u, ~0u, ~0u);
+        }
+#pragma unroll
+        for (int u = 0; u < kRecheckLPT; u++) {
+            const uint32_t vv[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+            const bool any = __ballot(vv[0] <= thr1 || vv[1] <= thr1 || vv[2] <= thr1 ||
+                                      vv[3] <= thr1) != 0ull;
+            if (!any) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bool keep = vv[e] <= thr1;
+                const unsigned long long mk = __ballot(keep);
+                if (!mk) continue;
+                int at = 0;
+                if (lane == 0) at = atomicAdd(&ctl[0], __popcll(mk));
+                at = __shfl(at, 0);
+                const int pos = at + __popcll(mk & lt);
+                const int64_t i = 4 * (i0 + u * NT + tid) + e;
+                if (keep && pos < kRecheckCap)
+                    surv[pos] = ((unsigned long long)vv[e] << 32) | (uint32_t)i;
+            }
+        }
+    }
+    __syncthreads();
+    const int ns = ctl[0];
+    // the exact distance of the candidate in slot i of the query's row
+    auto locate = [&](int i, int& pp, int& cc) {
+        const int g = i / kGroup;
+        int lo = 0, hi = P - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (sg[mid] <= g) lo = mid;
+            else hi = mid - 1;
+        }
+        pp = lo;
+        cc = i - sg[lo] * kGroup;
+    };
+    const int kmask = K1D - 1;
+    auto entry = [&](int pp, int cc, int m) {
+        const uint8_t v = codes_t[(int64_t)meta[4 * pp] * M + (int64_t)m * meta[4 * pp + 1] + cc];
+        float e = 0.0f;
+        for (int k = 0; k < Ds; k++) {
+            const float df = sq[m * Ds + k] - sc1d[(v >> (k * bpd)) & kmask];
+            e = fmaf(df, df, e);
+        }
+        return e;
+    };
+    int kk = 0;
+    if (ns <= kRecheckCap) {
+        // the ck-th smallest I among the survivors, then the members
+        uint32_t thr2 = thr1;
+        if (ns >= ck) {
+            // radix select of the ck-th smallest survivor value, 8 bits a
+            // round (the histogram in the member arrays, free until below)
+            int* hist = mp;
+            uint32_t pre = 0u, msk = 0u;
+            int kr = ck;
+            for (int sh = 24; sh >= 0; sh -= 8) {
+                for (int i = tid; i < 256; i += NT) hist[i] = 0;
+                __syncthreads();
+                for (int i = tid; i < ns; i += NT) {
+                    const uint32_t v = (uint32_t)(surv[i] >> 32);
+                    if ((v & msk) == pre) atomicAdd(&hist[(v >> sh) & 255u], 1);
+                }
+                __syncthreads();
+                if (wv == 0) {
+                    // lane l holds bins 4l .. 4l+3: inclusive prefix over lanes
+                    int c[4], t = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        c[e] = hist[4 * lane + e];
+                        t += c[e];
+                    }
+                    int inc = t;
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const int x = __shfl_up(inc, o);
+                        if (lane >= o) inc += x;
+                    }
+                    int below = inc - t;
+                    // the lane whose bins cross kr picks the bin
+                    if (below < kr && kr <= inc) {
+                        int e = 0;
+                        while (below + c[e] < kr) below += c[e++];
+                        ctl[2] = 4 * lane + e;
+                        ctl[3] = below;
+                    }
+                }
+                __syncthreads();
+                pre |= (uint32_t)ctl[2] << sh;
+                msk |= 255u << sh;
+                kr -= ctl[3];
+                __syncthreads();
+            }
+            thr2 = min(thr1, mfma_member_bound(Q, pre, M));
+        }
+        if (tid == 0) ctl[1] = 0;
+        __syncthreads();
+        for (int i0 = 0; i0 < ns; i0 += NT) {
+            const int i = i0 + tid;
+            const bool keep = i < ns && (uint32_t)(surv[i] >> 32) <= thr2;
+            const unsigned long long mk = __ballot(keep);
+            int at = 0;
+            if (lane == 0 && mk) at = atomicAdd(&ctl[1], __popcll(mk));
+            at = __shfl(at, 0);
+            if (keep) {
+                int pp, cc;
+                locate((int)(uint32_t)surv[i], pp, cc);
+                mp[at + __popcll(mk & lt)] = pp;
+                mc[at + __popcll(mk & lt)] = cc;
+            }
+        }
+        __syncthreads();
+        const int nm = ctl[1];
+        // member keys replace the survivors in surv; per round every code
+        // byte is requested before the first is used
+        constexpr int EPT = kRecheckCHM * 128 / NT;  // (member, subspace) pairs per thread
+        for (int c0 = 0; c0 < nm; c0 += kRecheckCHM) {
+            const int nc = min(kRecheckCHM, nm - c0);
+            uint8_t cb[EPT];
+#pragma unroll
+            for (int u = 0; u < EPT; u++) {
+                const int x = tid + u * NT, jj = x / M, m = x - jj * M;
+                cb[u] = 0;
+                if (jj < nc) {
+                    const int pp = mp[c0 + jj];
+                    cb[u] = codes_t[(int64_t)meta[4 * pp] * M + (int64_t)m * meta[4 * pp + 1] +
+                                    mc[c0 + jj]];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < EPT; u++) {
+                const int x = tid + u * NT, jj = x / M, m = x - jj * M;
+                if (jj < nc) {
+                    float e = 0.0f;
+                    for (int k = 0; k < Ds; k++) {
+                        const float df = sq[m * Ds + k] - sc1d[(cb[u] >> (k * bpd)) & kmask];
+                        e = fmaf(df, df, e);
+                    }
+                    ebuf[jj * (M + 1) + m] = e;
+                }
+            }
+            __syncthreads();
+            if (tid < nc) {
+                float acc = 0.0f;
+                for (int m = 0; m < M; m++) acc += ebuf[tid * (M + 1) + m];
+                const int pp = mp[c0 + tid], cc = mc[c0 + tid];
+                surv[c0 + tid] = ((unsigned long long)f2ord(acc) << 32) |
+                                 (uint32_t)(meta[4 * pp + 3] + cc);
+            }
+            __syncthreads();
+        }
+        kk = min(ck, nm);
+        if (kk > 0) select_keys<NT>(surv, nm, kk, S.kout, S.kidx, S.ktmp, S.st);
+    } else {
+        // more survivors than fit: every candidate at or below thr1, exact
+        // distances one per thread, streamed through the selection
+        for (int64_t r0 = 0; r0 < n; r0 += NT) {
+            const int64_t i = r0 + tid;
+            uint32_t o[1] = {~0u}, tg[1] = {~0u};
+            if (i < n && row[i] <= thr1) {
+                int pp, cc;
+                locate((int)i, pp, cc);
+                float acc = 0.0f;
+                for (int m = 0; m < M; m++) acc += entry(pp, cc, m);
+                o[0] = f2ord(acc);
+                tg[0] = (uint32_t)(meta[4 * pp + 3] + cc);
+            }
+            stream_round<NT, 1>(S, ck, o, tg);
+        }
+        kk = stream_end<NT>(S, ck);
+    }
+    __syncthreads();
+    for (int i = tid; i < ck; i += NT) {
+        int32_t slot = -1;
+        if (i < kk) {
+            const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
+            for (int q = 0; q < P; q++)
+                if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
+                    slot = meta[4 * q] + (tag - meta[4 * q + 3]);
+        }
+        partial[(int64_t)s0 * ck + i] = i < kk ? S.kout[i] : ~0ull;
+        partial_slot[(int64_t)s0 * ck + i] = slot;
+    }
+}
+
+static size_t mfma_plan_lds(int B, int P) {
+    const int H = mfma_hash_size(B * P);
+    const size_t work = (size_t)(5 * (H + 1) + B + 1 + kMfmaPlanNT / 64) * 4 + 64;
+    const size_t quant = (size_t)3 * (kMfmaPlanNT / 64) * 8 + 64;
+    return std::max(work, quant);
+}
+
+static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B) {
+    return stream_lds_bytes(kRecheckNT, ck) + (size_t)kRecheckCap * (8 + 4 + 4) +
+           (size_t)kRecheckCHM * (M + 1) * 4 + (size_t)d * 4 + (size_t)K1D * 4 +
+           (size_t)(4 * P + P + 1) * 4 + (size_t)(2 * (B + 1)) * 4 + (kRecheckNT / 64) * 4 + 16 +
+           64;
+}
+
+bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck) {
+    if (K1D != 2 || bpd != 1 || Ds != 8 || d != 8 * M) return false;
+    if (M % 16 != 0 || M < 16 || M > 128) return false;
+    if (B < 1 || P < 1 || (int64_t)B * P > kMfmaMaxBP || ck < 1 || ck > kRecheckCap) return false;
+    return mfma_plan_lds(B, P) <= (size_t)kLdsBytes - 1024 &&
+           mfma_recheck_lds(M, d, P, ck, K1D, B) <= (size_t)kLdsBytes - 1024;
+}
+
+static int mfma_scan_waves(int num_cu) { return std::max(1, num_cu) * kMfmaWavesPerCU; }
+
+size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
+    return mfma_carve(B, P, M, mfma_scan_waves(num_cu), nullptr, nullptr);
+}
+
+hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
+                     int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
+                     const int4* ldesc, const uint8_t* codes_t, int ck, uint32_t* dump,
+                     unsigned char* ws, size_t ws_bytes, unsigned long long* partial,
+                     int32_t* partial_slot, int num_cu, hipStream_t s) {
+    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck) || !ws || ((uintptr_t)ws & 255) || !dump)
+        return hipErrorInvalidValue;
+    MfmaWs w;
+    const int nwaves = mfma_scan_waves(num_cu);
+    if (mfma_carve(B, P, M, nwaves, ws, &w) > ws_bytes) return hipErrorInvalidValue;
+    const int H = mfma_hash_size(B * P);
+    const size_t lp = mfma_plan_lds(B, P);
+    static const int mxp = allow_max_lds((const void*)mfma_plan_kernel<kMfmaPlanNT>);
+    if ((int)lp > mxp) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mfma_plan_kernel<kMfmaPlanNT>, dim3(B + 1), dim3(kMfmaPlanNT), lp, s, q_rot,
+                       d, M, c1d, probes, gofs, qtot, B, P, ldesc, w, H, nwaves);
+    using SFn = void (*)(MfmaWs, const uint8_t*, uint32_t*);
+    SFn f = M == 16 ? mfma_scan_kernel<16> : M == 32 ? mfma_scan_kernel<32>
+          : M == 48 ? mfma_scan_kernel<48> : M == 64 ? mfma_scan_kernel<64>
+          : M == 80 ? mfma_scan_kernel<80> : M == 96 ? mfma_scan_kernel<96>
+          : M == 112 ? mfma_scan_kernel<112> : mfma_scan_kernel<128>;
+    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, codes_t, dump);
+    const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B);
+    static const int mxr = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT>);
+    if ((int)lr > mxr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mfma_recheck_kernel<kRecheckNT>, dim3(B), dim3(kRecheckNT), lr, s, dump,
+                       w.qs, q_rot, d, Ds, K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc,
+                       codes_t, ck, partial, partial_slot);
     return hipGetLastError();
 }
 

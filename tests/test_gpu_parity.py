@@ -238,18 +238,35 @@ def test_search_device_pipelined_batches(gpu, name):
     assert np.array_equal(_bits(od2.cpu().numpy()), _bits(d1))
 
 
-@pytest.mark.parametrize("name", ["m64_ds4_ck100", "m96_d768", "m32_p80", "m128_p64"])
+@pytest.mark.parametrize("name", ["m64_ds4_ck100", "m32_p80", "m128_p64"])
 def test_skewed_scan_taken(gpu, name):
     """The M % 32 == 0 cases above exercise the skewed scan (not a fallback)."""
     g, _, _, _, k = _build(CASES[IDS.index(name)])
     assert g.scan_plan(k)[0] == "scan_skew_kernel"
 
 
-@pytest.mark.parametrize("name", ["ds8_k1d2", "ds4_k1d4_d100", "m24_wave", "m16_ck100", "m16_p80",
+@pytest.mark.parametrize("name", ["ds8_k1d2", "ds4_k1d4_d100", "m24_wave", "m16_p80",
                                   "flat_nlist1"])
 def test_wave_scan_taken(gpu, name):
     g, _, _, _, k = _build(CASES[IDS.index(name)])
     assert g.scan_plan(k)[0] == "scan_wave_kernel"
+
+
+# one-bit digits with M a multiple of 16 take the integer-MFMA pre-scan by
+# default; the byte-LUT scans they would otherwise run are checked here with
+# scan kind 1
+@pytest.mark.parametrize("name,lut_scan", [("d1024_m128", "scan_skew_kernel"),
+                                           ("m96_d768", "scan_skew_kernel"),
+                                           ("m16_ck100", "scan_wave_kernel")])
+def test_lut_scans_of_mfma_cases(gpu, name, lut_scan):
+    g, o, base, q, k = _build(CASES[IDS.index(name)])
+    assert g.scan_plan(k)[0] == "mfma_scan_kernel"
+    g.set_scan_kind(1)
+    try:
+        assert g.scan_plan(k)[0] == lut_scan
+        _stagewise(g, o, q, k)
+    finally:
+        g.set_scan_kind(0)
 
 
 def test_k_larger_than_candidates(gpu):

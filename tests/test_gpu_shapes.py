@@ -1,9 +1,13 @@
 """GPU parity at the shapes the benchmark runs, smaller N.
 
-* The benchmarked scan instance of config 2: D=1024, M=128 (the skewed scan
-  with the subspace-parity LUT), alpha=10 -> ck=100 (three 64-key wave buffers),
-  nlist 256, nprobe 16 and 64, batch 64 — many queries split over many
-  workgroups (multi-segment work plan, the segment merge).
+Every shape here has one-bit digits, so it runs the integer-MFMA pre-scan with
+exact re-check by default (scan kind 0) and the byte-LUT scans with scan kind
+1; both are checked.
+
+* Config 2: D=1024, M=128 (the skewed scan with the subspace-parity LUT),
+  alpha=10 -> ck=100 (three 64-key wave buffers), nlist 256, nprobe 16 and
+  64, batch 64 — many queries split over many workgroups (multi-segment work
+  plan, the segment merge); the pre-scan's lists shared by many queries.
 * Config 1's shape: the flat index (nlist = 1) at D=1024, M=128, one query
   per batch, so each query's single list is split across the chip and merged
   from ~256 segments (jhq_v1_plain/search.cu:126-228).
@@ -75,15 +79,18 @@ def test_cfg2_shape_lists_bit_exact(gpu):
     _lists_equal(g, o)
 
 
+@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
 @pytest.mark.parametrize("nprobe", [16, 64])
-def test_cfg2_shape_benchmarked_scan(gpu, nprobe):
-    """scan_skew_kernel at M=128 with ck=100 (the instance bench.py times)."""
+def test_cfg2_shape_benchmarked_scan(gpu, nprobe, kind, scan):
+    """M=128 with ck=100 (the instance bench.py times): the pre-scan and the
+    skewed scan."""
     g, o, q = _cfg2()
     g.set_nprobe(nprobe)
+    g.set_scan_kind(kind)
     o.nprobe = nprobe
     try:
-        assert g.scan_plan(10) == ("scan_skew_kernel", 100)
-        _say(f"cfg2_shape nprobe={nprobe}: stage-wise search")
+        assert g.scan_plan(10) == (scan, 100)
+        _say(f"cfg2_shape nprobe={nprobe} kind={kind}: stage-wise search")
         gr, _ = _stagewise(g, o, q, 10)
         # queries really span several workgroups: the probed candidates of
         # one query exceed a workgroup's share of the batch
@@ -92,41 +99,55 @@ def test_cfg2_shape_benchmarked_scan(gpu, nprobe):
         assert per_q.sum() / 256 < per_q.max()
     finally:
         g.set_nprobe(16)
+        g.set_scan_kind(0)
         o.nprobe = 16
 
 
-def test_cfg2_shape_alpha4(gpu):
+@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
+def test_cfg2_shape_alpha4(gpu, kind, scan):
     """The same index at alpha=4 (ck=40, two 64-key wave buffers)."""
     g, o, q = _cfg2()
     g.set_alpha(4.0)
+    g.set_scan_kind(kind)
     o.alpha = np.float32(4.0)
     try:
-        assert g.scan_plan(10) == ("scan_skew_kernel", 40)
+        assert g.scan_plan(10) == (scan, 40)
         _stagewise(g, o, q, 10)
     finally:
         g.set_alpha(10.0)
+        g.set_scan_kind(0)
         o.alpha = np.float32(10.0)
 
 
-def test_cfg1_shape_flat(gpu):
+@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
+def test_cfg1_shape_flat(gpu, kind, scan):
     """Flat index (nlist = 1) at D=1024, M=128, one query per batch
     (jhq_v1_plain/search.cu:126-228; v1's ck = min(ceil(alpha k), N) equals
     the short list here since N > ck)."""
     base, q = queries_and_base(20_000, 12, 1024, 64, seed=zlib.crc32(b"cfg1_flat") % 10000)
     g, o = _pair("cfg1_flat", 1024, 128, 1, 1, 4.0, 1, base, 5000)
-    assert g.scan_plan(10) == ("scan_skew_kernel", 40)
-    _lists_equal(g, o)
-    _say("cfg1_flat: stage-wise search")
-    _stagewise(g, o, q, 10)
+    g.set_scan_kind(kind)
+    try:
+        assert g.scan_plan(10) == (scan, 40)
+        _lists_equal(g, o)
+        _say(f"cfg1_flat kind={kind}: stage-wise search")
+        _stagewise(g, o, q, 10)
+    finally:
+        g.set_scan_kind(0)
 
 
-def test_cfg3_shape_uint8(gpu):
+@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_wave_kernel")])
+def test_cfg3_shape_uint8(gpu, kind, scan):
     """uint8 rows at D=128, M=16 (wave scan), nlist 1024, nprobe 64, batch 64."""
     seed = zlib.crc32(b"cfg3_shape") % 10000
     base = byte_mixture(100_000, 128, 2048, seed, "uint8", comp_seed=seed + 1)
     qb = byte_mixture(64, 128, 2048, seed + 100, "uint8", comp_seed=seed + 1)
     g, o = _pair("cfg3_shape", 128, 16, 1024, 64, 4.0, 64, base, 16_384)
-    assert g.scan_plan(10)[0] == "scan_wave_kernel"
-    _lists_equal(g, o)
-    _say("cfg3_shape: stage-wise search")
-    _stagewise(g, o, qb.astype(np.float32), 10)
+    g.set_scan_kind(kind)
+    try:
+        assert g.scan_plan(10)[0] == scan
+        _lists_equal(g, o)
+        _say(f"cfg3_shape kind={kind}: stage-wise search")
+        _stagewise(g, o, qb.astype(np.float32), 10)
+    finally:
+        g.set_scan_kind(0)
