@@ -39,7 +39,7 @@ namespace jhq {
 // probe-selection and refine kernels; jhq_debug_phase_ticks() reads them.
 #ifdef JHQ_PHASE_TIMING
 constexpr int kPhaseBlocks = 4096, kPhases = 8;
-__device__ unsigned long long g_phase[3][kPhaseBlocks][kPhases];
+__device__ unsigned long long g_phase[4][kPhaseBlocks][kPhases];
 #define JHQ_PHASE_DECL unsigned long long ph_t = wall_clock64(), ph_acc[kPhases] = {0};
 #define JHQ_PHASE(i)                                              \
     do {                                                          \
@@ -3848,9 +3848,9 @@ static int mfma_hash_size(int BP) { return (3 * BP / 2 + 127) / 64 * 64; }
 struct MfmaWs {
     int8_t* qa;      // [B][2][D]: hi then lo bytes in the lanes' register order
     MfmaQS* qs;      // [B]
-    int2* pairs;     // [B*P]: (query, dump offset of the list's first slot)
-    int4* grp;       // [B*P][2]: (block start, row stride, size, first pair),
-                     //           (queries, tiles, 0, 0)
+    int2* gq;        // [B*P][16]: a group's queries (query, dump offset of the
+                     //            list's first slot); entries past its count unused
+    int4* grp;       // [B*P]: (block start, row stride, size, queries)
     int2* wstart;    // [waves]: (group, tile in the group) where a wave starts
     int* ctl;        // [16]: tiles of the batch, groups
 };
@@ -3862,10 +3862,10 @@ static size_t mfma_carve(int B, int P, int M, int nwaves, unsigned char* base, M
     off += al((size_t)B * 2 * 8 * M);
     const size_t o_qs = off;
     off += al((size_t)B * sizeof(MfmaQS));
-    const size_t o_pairs = off;
-    off += al((size_t)B * P * sizeof(int2));
+    const size_t o_gq = off;
+    off += al((size_t)B * P * 16 * sizeof(int2));
     const size_t o_g = off;
-    off += al((size_t)B * P * 2 * sizeof(int4));
+    off += al((size_t)B * P * sizeof(int4));
     const size_t o_ws = off;
     off += al((size_t)nwaves * sizeof(int2));
     const size_t o_ctl = off;
@@ -3873,7 +3873,7 @@ static size_t mfma_carve(int B, int P, int M, int nwaves, unsigned char* base, M
     if (w) {
         w->qa = (int8_t*)(base + o_qa);
         w->qs = (MfmaQS*)(base + o_qs);
-        w->pairs = (int2*)(base + o_pairs);
+        w->gq = (int2*)(base + o_gq);
         w->grp = (int4*)(base + o_g);
         w->wstart = (int2*)(base + o_ws);
         w->ctl = (int*)(base + o_ctl);
@@ -3966,8 +3966,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     int* hk = (int*)smem;       // [H] list id or -1
     int* hc = hk + H;           // [H] queries of the slot
     int* hg = hc + H;           // [H + 1] group prefix
-    int* hst = hg + H + 1;      // [H + 1] first pair prefix
-    int* htl = hst + H + 1;     // [H + 1] tile prefix
+    int* htl = hg + H + 1;      // [H + 1] tile prefix
     int* qpre = htl + H + 1;    // [B + 1]
     int* wsum = qpre + B + 1;   // [NT / 64]
     for (int i = tid; i < H; i += NT) {
@@ -3998,25 +3997,21 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     auto ntl = [&](int h) { return (ldesc[hk[h]].z + kGroup - 1) / kGroup; };
     block_exclusive_scan<NT>([&](int h) { return hk[h] >= 0 ? (hc[h] + 15) / 16 : 0; }, H, hg,
                              wsum);
-    block_exclusive_scan<NT>([&](int h) { return hc[h]; }, H, hst, wsum);
     block_exclusive_scan<NT>(
         [&](int h) { return hk[h] >= 0 ? ((hc[h] + 15) / 16) * ntl(h) : 0; }, H, htl, wsum);
     const int T = htl[H];
     for (int h = tid; h < H; h += NT) {
         if (hk[h] < 0) continue;
         const int4 L = ldesc[hk[h]];
-        const int nt = (L.z + kGroup - 1) / kGroup;
-        for (int t = 0; t < (hc[h] + 15) / 16; t++) {
-            const int g = hg[h] + t;
-            w.grp[2 * g] = make_int4(L.x, L.y, L.z, hst[h] + 16 * t);
-            w.grp[2 * g + 1] = make_int4(min(16, hc[h] - 16 * t), nt, 0, 0);
-        }
+        for (int t = 0; t < (hc[h] + 15) / 16; t++)
+            w.grp[hg[h] + t] = make_int4(L.x, L.y, L.z, min(16, hc[h] - 16 * t));
     }
+    // the query of rank r in slot h is entry r % 16 of the slot's group r / 16
 #pragma unroll
     for (int i = 0; i < kMfmaPairsPT; i++) {
         if (ps[i] < 0) continue;
         const int e = tid + i * NT, b = e / P, p = e - b * P;
-        w.pairs[hst[ps[i]] + pr[i]] =
+        w.gq[(hg[ps[i]] + pr[i] / 16) * 16 + (pr[i] & 15)] =
             make_int2(b, (qpre[b] + gofs[(int64_t)b * (P + 1) + p]) * kGroup);
     }
     // wave v starts at tile a = v T / W: in slot h with htl[h] <= a <
@@ -4114,10 +4109,13 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
     const uint32_t qsel = (uint32_t)(j & 3) | ((uint32_t)(4 + (j & 3)) << 8) | 0x0c0c0000u;
     const int2 st = w.wstart[wid];
     int g = st.x, off = st.y;
+    JHQ_PHASE_DECL
     while (left > 0) {
-        const int4 ga = w.grp[2 * g], gb = w.grp[2 * g + 1];
-        const int nq = gb.x, q0 = ga.w;
-        const int n = min(gb.y - off, left);
+        // the group record and its 16 query entries are loaded side by side
+        const int4 ga = w.grp[g];
+        const int2 gqv = w.gq[g * 16 + j];
+        const int nq = ga.w;
+        const int n = min((ga.z + kGroup - 1) / kGroup - off, left);
         // row stride: the list's capacity; slots: its size rounded up to 16
         const int npad = ga.y, nl = ga.z;
         const uint8_t* base = codes_t + (int64_t)ga.x * M + 16 * off;
@@ -4139,7 +4137,7 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
         JHQ_MFMA_FETCH(3, 3);
         mfma_v4i ahi[NK], alo[NK];
         if (j < nq) {
-            const int b = w.pairs[q0 + j].x;
+            const int b = gqv.x;
             const mfma_v4i* src = (const mfma_v4i*)(w.qa + (int64_t)b * 2 * D + h * NK * 16);
 #pragma unroll
             for (int s = 0; s < NK; s++) {
@@ -4154,11 +4152,19 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
             }
         }
         // dump offsets of the run's first slot for query rows 4h .. 4h+3
-        const int d0 = 4 * h + 0 < nq ? w.pairs[q0 + 4 * h + 0].y + 16 * off : -1;
-        const int d1 = 4 * h + 1 < nq ? w.pairs[q0 + 4 * h + 1].y + 16 * off : -1;
-        const int d2 = 4 * h + 2 < nq ? w.pairs[q0 + 4 * h + 2].y + 16 * off : -1;
-        const int d3 = 4 * h + 3 < nq ? w.pairs[q0 + 4 * h + 3].y + 16 * off : -1;
+        // (lane r of the wave's first 16 holds row r's entry)
+        const int e0 = __shfl(gqv.y, 4 * h + 0), e1 = __shfl(gqv.y, 4 * h + 1);
+        const int e2 = __shfl(gqv.y, 4 * h + 2), e3 = __shfl(gqv.y, 4 * h + 3);
+        const int d0 = 4 * h + 0 < nq ? e0 + 16 * off : -1;
+        const int d1 = 4 * h + 1 < nq ? e1 + 16 * off : -1;
+        const int d2 = 4 * h + 2 < nq ? e2 + 16 * off : -1;
+        const int d3 = 4 * h + 3 < nq ? e3 + 16 * off : -1;
         const int cbase = 16 * off + j;
+        JHQ_PHASE(0);
+#ifdef JHQ_PHASE_TIMING
+        ph_acc[6] += 1;
+        ph_acc[7] += n;
+#endif
         // every pass issues the same loads (tiles past the last are clamped),
         // so the wait for a ring slot leaves the later slots' loads in flight
 #define JHQ_MFMA_TILE(U)                                                                    \
@@ -4189,7 +4195,9 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
         left -= n;
         g++;
         off = 0;
+        JHQ_PHASE(1);
     }
+    JHQ_PHASE_FLUSH(0);
 }
 
 // Largest biased I (I + 2^31) a member of the exact top-ck can have, given
@@ -4237,22 +4245,16 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
     int* ctl = wsum + NW;                                      // [4]
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const unsigned long long lt = (1ull << lane) - 1ull;
+    JHQ_PHASE_DECL
     work_plan<NT>(qtot, B, 1, 0, qpre, spre, wsum);
     const int s0 = spre[b], s1 = spre[b + 1];
     if (s1 == s0) return;  // no candidates: refine sees no segment
-    for (int i = tid; i < d; i += NT) sq[i] = q_rot[(int64_t)b * d + i];
-    for (int i = tid; i < K1D; i += NT) sc1d[i] = c1d[i];
-    for (int i = tid; i < P; i += NT) {
-        const int4 L = ldesc[probes[(int64_t)b * P + i]];
-        meta[4 * i] = L.x;
-        meta[4 * i + 1] = L.y;
-        meta[4 * i + 2] = L.z;
-        meta[4 * i + 3] = L.w;
-    }
-    for (int i = tid; i <= P; i += NT) sg[i] = gofs[(int64_t)b * (P + 1) + i];
-    if (tid == 0) ctl[0] = 0;
-    stream_begin<NT>(S);
-    __syncthreads();
+    // the query, codebook and probe table are requested now and stored in
+    // LDS after pass 1, whose loads do not wait for them (d <= NT, P < NT)
+    const float qv = tid < d ? q_rot[(int64_t)b * d + tid] : 0.0f;
+    const float cv = tid < K1D ? c1d[tid] : 0.0f;
+    const int4 Lv = tid < P ? ldesc[probes[(int64_t)b * P + tid]] : make_int4(0, 0, 0, 0);
+    const int gv = tid <= P ? gofs[(int64_t)b * (P + 1) + tid] : 0;
     const MfmaQS Q = qs[b];
     const int64_t n = (int64_t)(qpre[b + 1] - qpre[b]) * kGroup;
     const uint32_t* row = dump + (int64_t)qpre[b] * kGroup;
@@ -4272,6 +4274,17 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
         for (int u = 0; u < kRecheckLPT; u++)
             mn = min(mn, min(min(v[u].x, v[u].y), min(v[u].z, v[u].w)));
     }
+    if (tid < d) sq[tid] = qv;
+    if (tid < K1D) sc1d[tid] = cv;
+    if (tid < P) {
+        meta[4 * tid] = Lv.x;
+        meta[4 * tid + 1] = Lv.y;
+        meta[4 * tid + 2] = Lv.z;
+        meta[4 * tid + 3] = Lv.w;
+    }
+    if (tid <= P) sg[tid] = gv;
+    if (tid == 0) ctl[0] = 0;
+    stream_begin<NT>(S);
     const int r = (ck + NW - 1) / NW;
     const uint32_t tw = r <= 64 ? wave_kth_u32(mn, r) : ~0u;
     if (lane == 0) wsum[wv] = (int)tw;
@@ -4280,6 +4293,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
 #pragma unroll
     for (int w2 = 0; w2 < NW; w2++) That = max(That, (uint32_t)wsum[w2]);
     const uint32_t thr1 = That == ~0u ? 0xfffffffeu : mfma_member_bound(Q, That, M);
+    JHQ_PHASE(1);
     // pass 2: the candidates at or below thr1 (they include the ck smallest
     // I values and every member)
     for (int64_t i0 = 0; i0 < n4; i0 += kRecheckLPT * NT) {
@@ -4312,6 +4326,10 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
     }
     __syncthreads();
     const int ns = ctl[0];
+    JHQ_PHASE(2);
+#ifdef JHQ_PHASE_TIMING
+    ph_acc[7] += (unsigned long long)ns;
+#endif
     // the exact distance of the candidate in slot i of the query's row
     auto locate = [&](int i, int& pp, int& cc) {
         const int g = i / kGroup;
@@ -4382,6 +4400,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
             }
             thr2 = min(thr1, mfma_member_bound(Q, pre, M));
         }
+        JHQ_PHASE(3);
         if (tid == 0) ctl[1] = 0;
         __syncthreads();
         for (int i0 = 0; i0 < ns; i0 += NT) {
@@ -4400,32 +4419,47 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
         }
         __syncthreads();
         const int nm = ctl[1];
-        // member keys replace the survivors in surv; per round every code
-        // byte is requested before the first is used
-        constexpr int EPT = kRecheckCHM * 128 / NT;  // (member, subspace) pairs per thread
+        JHQ_PHASE(4);
+#ifdef JHQ_PHASE_TIMING
+        ph_acc[6] += (unsigned long long)nm;
+#endif
+        // member keys replace the survivors in surv.  Thread t computes
+        // subspace t % M of members t / M, t / M + NT / M, ... (its query
+        // values in registers); every code byte of a round is requested
+        // before the first is used; member rows of the entries are padded
+        // to M + 1 words, so both the writes and the in-order sums of a
+        // member row are free of bank conflicts
+        constexpr int EPT = kRecheckCHM * 128 / NT;  // entries per thread (M <= 128)
+        const int me = tid % M, mstep = NT / M;
+        float qm[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) qm[k] = k < Ds ? sq[me * Ds + k] : 0.0f;
         for (int c0 = 0; c0 < nm; c0 += kRecheckCHM) {
             const int nc = min(kRecheckCHM, nm - c0);
             uint8_t cb[EPT];
 #pragma unroll
             for (int u = 0; u < EPT; u++) {
-                const int x = tid + u * NT, jj = x / M, m = x - jj * M;
+                const int jj = tid / M + u * mstep;
                 cb[u] = 0;
                 if (jj < nc) {
                     const int pp = mp[c0 + jj];
-                    cb[u] = codes_t[(int64_t)meta[4 * pp] * M + (int64_t)m * meta[4 * pp + 1] +
+                    cb[u] = codes_t[(int64_t)meta[4 * pp] * M + (int64_t)me * meta[4 * pp + 1] +
                                     mc[c0 + jj]];
                 }
             }
 #pragma unroll
             for (int u = 0; u < EPT; u++) {
-                const int x = tid + u * NT, jj = x / M, m = x - jj * M;
+                const int jj = tid / M + u * mstep;
                 if (jj < nc) {
                     float e = 0.0f;
-                    for (int k = 0; k < Ds; k++) {
-                        const float df = sq[m * Ds + k] - sc1d[(cb[u] >> (k * bpd)) & kmask];
-                        e = fmaf(df, df, e);
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        if (k < Ds) {
+                            const float df = qm[k] - sc1d[(cb[u] >> (k * bpd)) & kmask];
+                            e = fmaf(df, df, e);
+                        }
                     }
-                    ebuf[jj * (M + 1) + m] = e;
+                    ebuf[jj * (M + 1) + me] = e;
                 }
             }
             __syncthreads();
@@ -4438,6 +4472,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
             }
             __syncthreads();
         }
+        JHQ_PHASE(5);
         kk = min(ck, nm);
         if (kk > 0) select_keys<NT>(surv, nm, kk, S.kout, S.kidx, S.ktmp, S.st);
     } else {
@@ -4470,11 +4505,13 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
         partial[(int64_t)s0 * ck + i] = i < kk ? S.kout[i] : ~0ull;
         partial_slot[(int64_t)s0 * ck + i] = slot;
     }
+    JHQ_PHASE(0);
+    JHQ_PHASE_FLUSH(3);
 }
 
 static size_t mfma_plan_lds(int B, int P) {
     const int H = mfma_hash_size(B * P);
-    const size_t work = (size_t)(5 * (H + 1) + B + 1 + kMfmaPlanNT / 64) * 4 + 64;
+    const size_t work = (size_t)(4 * (H + 1) + B + 1 + kMfmaPlanNT / 64) * 4 + 64;
     const size_t quant = (size_t)3 * (kMfmaPlanNT / 64) * 8 + 64;
     return std::max(work, quant);
 }
@@ -4488,7 +4525,7 @@ static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B) {
 
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck) {
     if (K1D != 2 || bpd != 1 || Ds != 8 || d != 8 * M) return false;
-    if (M % 16 != 0 || M < 16 || M > 128) return false;
+    if (M % 16 != 0 || M < 16 || M > 128 || d > kRecheckNT || P >= kRecheckNT) return false;
     if (B < 1 || P < 1 || (int64_t)B * P > kMfmaMaxBP || ck < 1 || ck > kRecheckCap) return false;
     return mfma_plan_lds(B, P) <= (size_t)kLdsBytes - 1024 &&
            mfma_recheck_lds(M, d, P, ck, K1D, B) <= (size_t)kLdsBytes - 1024;
@@ -4759,7 +4796,7 @@ hipError_t stage_final_topk(const float* comp, const int32_t* topck_pos, const i
 }  // namespace jhq
 
 #ifdef JHQ_PHASE_TIMING
-// Copies the phase accumulators [3][4096][8] (ticks of the 100 MHz clock).
+// Copies the phase accumulators [4][4096][8] (ticks of the 100 MHz clock).
 extern "C" int jhq_debug_phase_ticks(unsigned long long* out) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(jhq::g_phase), sizeof(jhq::g_phase), 0,
                                     hipMemcpyDeviceToHost);
