@@ -70,9 +70,10 @@ def parse():
                          "(jhq_save format) if it exists, else build it and save it there")
     ap.add_argument("--seed", type=int, default=None,
                     help="data seed (default 0x4A48510000 + config)")
-    ap.add_argument("--scan-kind", type=int, default=0, choices=(0, 1),
+    ap.add_argument("--scan-kind", type=int, default=0, choices=(0, 1, 2),
                     help="0 (default): the integer-MFMA pre-scan with exact re-check where it "
-                         "applies; 1: the byte-LUT scans only (same results)")
+                         "applies and pays off; 1: the byte-LUT scans only; 2: the pre-scan "
+                         "wherever it applies (same results)")
     return ap.parse_args()
 
 

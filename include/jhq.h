@@ -205,12 +205,15 @@ int jhq_load(const char* path, jhq_index** out);
 int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list);
 
 /* Scan choice (no counterpart in the reference, whose search always runs its
- * byte-LUT scan): 0 (default) the integer-MFMA pre-scan wherever it applies
- * (one-bit digits: K1D = 2 with Ds = 8, M a multiple of 16 up to 128, at most
- * 2048 probes per batch), else the byte-LUT scans; 1 the byte-LUT scans only.
- * Results are identical either way: the pre-scan only decides which
- * candidates get their distance recomputed in the reference's order.
- * Re-reserves the search workspace like jhq_set_nprobe. */
+ * byte-LUT scan).  The integer-MFMA pre-scan applies to one-bit digits (K1D =
+ * 2 with Ds = 8), M a multiple of 16 up to 128 and at most 4096 probes per
+ * batch.  0 (default): the pre-scan where it applies and the list sizes
+ * predict that the queries of a batch share their probed lists (its 16-query
+ * tiles mostly full), else the byte-LUT scans; 1: the byte-LUT scans only;
+ * 2: the pre-scan wherever it applies.  Results are identical in every
+ * case: the pre-scan only decides which candidates get their distance
+ * recomputed in the reference's order.  Re-reserves the search workspace
+ * like jhq_set_nprobe. */
 int jhq_set_scan_kind(jhq_index* idx, int kind);
 
 /* List pool occupancy: slots in use (including padding, headroom and blocks

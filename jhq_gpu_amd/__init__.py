@@ -268,8 +268,9 @@ class JHQGpuIndex:
 
     def set_scan_kind(self, kind):
         """0: the integer-MFMA pre-scan with exact re-check where it applies
-        (one-bit digits), else the byte-LUT scans; 1: the byte-LUT scans only.
-        Results are identical; only the speed differs."""
+        (one-bit digits) and the list sizes predict shared probed lists, else
+        the byte-LUT scans; 1: the byte-LUT scans only; 2: the pre-scan
+        wherever it applies.  Results are identical; only the speed differs."""
         _check(lib().jhq_set_scan_kind(self._h, int(kind)))
 
     def search_device(self, q, k, out_dists, out_ids, stream=None):

@@ -130,9 +130,17 @@ struct jhq_index {
     // searches with k <= res_k (and the current nprobe, alpha, batch_size)
     // run in the preallocated workspace; jhq_reserve raises it
     int res_k = 10;
-    // 0: the integer-MFMA pre-scan where it applies (one-bit digits), else the
-    // byte-LUT scans; 1: the byte-LUT scans only
+    // 0: the integer-MFMA pre-scan where it applies (one-bit digits) and its
+    // tiles are expected to be mostly full, else the byte-LUT scans; 1: the
+    // byte-LUT scans only; 2: the pre-scan wherever it applies
     int scan_kind = 0;
+    // the default scan kind's choice of the pre-scan, measured on stored
+    // vectors taken as queries; valid for batches of mfma_dec_B queries with
+    // mfma_dec_P probes while the index holds 0.8 to 1.25 times mfma_dec_n
+    // vectors
+    int mfma_dec_B = 0, mfma_dec_P = 0;
+    int64_t mfma_dec_n = 0;
+    double mfma_dec_cost = 0.0, mfma_dec_cand = 0.0;
     // largest per-query candidate count of the dump scan for dump_P probes
     int dump_P = -1;
     int64_t dump_perq = 0;
@@ -395,9 +403,114 @@ int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_
 
 bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128; }
 
-bool mfma_eligible(const jhq_index* ix, int Bq, int P, int ck) {
-    return ix->scan_kind == 0 &&
-           jhq::mfma_scan_ok(ix->M, ix->d, ix->Ds, ix->K1D, ix->bpd, Bq, P, ck);
+// The pre-scan computes 16-query tiles over every probed list; it pays off
+// when the queries of a batch share their lists so that the tiles are mostly
+// full, when the byte-LUT scan's work per candidate (M lookups) is large
+// against the re-check's (one 4-byte value per candidate, read by the
+// query's one workgroup), and while that workgroup's exact top-ck is short.
+// Measured: 1M x 1024 (M 128, nlist 4096, batch 64, 1.2 rows per pair, 51 K
+// to 200 K candidates per query): 1.4x the byte-LUT scan's QPS at nprobe 16
+// to 64 and ck 100 to 400; 10M x 128 uint8 (M 16, 420 K candidates per
+// query, 2.1 rows per pair): 11x slower; 11M x 768 (M 96) at ck 1000: 10x
+// slower; one query per batch: equal.
+constexpr double kMfmaMaxTileCost = 3.0;
+constexpr int kMfmaMinM = 64;
+constexpr int kMfmaMaxCk = 512;
+
+// Rows computed per real (query, candidate) pair for batches of B queries
+// with P probes, measured on stored vectors taken as queries: up to 8
+// batches of B vectors spread over the index, each decoded from its primary
+// code (the rotated-space levels of its digits), their P nearest lists
+// selected as a search selects them, and per batch
+//   rows = sum over distinct lists of 16 ceil(queries / 16) ceil(size / 16),
+//   pairs = sum over probes of ceil(size / 16),
+// and the mean candidates per query.
+int mfma_measure_cost(jhq_index* ix, int B, int P, double* cost, double* cand) {
+    const int64_t n = ix->ntotal;
+    const int nb = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(8, n / std::max(B, 1))));
+    const int S = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(nb) * B, n));
+    const int nlist = ix->nlist, d = ix->d;
+    std::vector<int64_t> cpre(nlist + 1, 0);
+    for (int l = 0; l < nlist; l++) cpre[l + 1] = cpre[l] + ix->l_size[l];
+    std::vector<int4> samp(S);
+    for (int i = 0; i < S; i++) {
+        // canonical positions spread by a multiplicative hash
+        const int64_t pos = static_cast<int64_t>((static_cast<uint64_t>(i) * 2654435761ull +
+                                                  12345ull) % static_cast<uint64_t>(n));
+        const int l = static_cast<int>(std::upper_bound(cpre.begin(), cpre.end(), pos) -
+                                       cpre.begin()) - 1;
+        samp[i] = make_int4(ix->l_start[l], ix->l_cap[l], static_cast<int>(pos - cpre[l]), 0);
+    }
+    DBuf<int4> dsamp;
+    DBuf<float> rows, scores;
+    DBuf<int32_t> probes, gofs, qtot;
+    JHQ_TRY(dsamp.upload(samp.data(), samp.size()));
+    JHQ_TRY(rows.alloc(static_cast<size_t>(S) * d));
+    JHQ_TRY(scores.alloc(static_cast<size_t>(S) * nlist));
+    JHQ_TRY(probes.alloc(static_cast<size_t>(S) * P));
+    JHQ_TRY(gofs.alloc(static_cast<size_t>(S) * (P + 1)));
+    JHQ_TRY(qtot.alloc(static_cast<size_t>(S)));
+    hipStream_t st = ix->stream;
+    JHQ_HIP(jhq::decode_rows(dsamp.p, S, ix->dcodes_t.p, ix->M, ix->Ds, ix->K1D, ix->bpd,
+                             ix->dc1d.p, rows.p, st));
+    JHQ_HIP(jhq::mfma_nt_score(rows.p, d, ix->dcent.p, d, S, nlist, d, ix->dnorms.p, scores.p,
+                               nlist, st));
+    JHQ_HIP(jhq::select_probes(scores.p, S, nlist, P, ix->dldesc.p, probes.p, gofs.p, qtot.p, st));
+    std::vector<int32_t> hp(static_cast<size_t>(S) * P);
+    JHQ_HIP(hipMemcpyAsync(hp.data(), probes.p, hp.size() * sizeof(int32_t),
+                           hipMemcpyDeviceToHost, st));
+    JHQ_HIP(hipStreamSynchronize(st));
+    double rows_sum = 0.0, pairs = 0.0, cands = 0.0;
+    std::vector<int> cnt(nlist, 0);
+    for (int b0 = 0; b0 < S; b0 += B) {
+        const int b1 = std::min(S, b0 + B);
+        for (int i = b0 * P; i < b1 * P; i++) cnt[hp[i]]++;
+        for (int i = b0 * P; i < b1 * P; i++) {
+            const int l = hp[i];
+            const double tiles = (ix->l_size[l] + jhq::kGroup - 1) / jhq::kGroup;
+            pairs += tiles;
+            cands += ix->l_size[l];
+            if (cnt[l] > 0) {
+                rows_sum += 16.0 * ((cnt[l] + 15) / 16) * tiles;
+                cnt[l] = 0;  // counted once per batch
+            }
+        }
+    }
+    *cost = pairs > 0.0 ? rows_sum / pairs : 1e30;
+    *cand = cands / S;
+    return JHQ_OK;
+}
+
+// Whether a batch of Bq queries (P probes, short list ck) runs the pre-scan.
+// measure = false (device searches, plan queries): the cached choice only.
+int mfma_choose(jhq_index* ix, int Bq, int P, int ck, bool measure, bool* use) {
+    *use = false;
+    if (ix->scan_kind == 1 ||
+        !jhq::mfma_scan_ok(ix->M, ix->d, ix->Ds, ix->K1D, ix->bpd, Bq, P, ck))
+        return JHQ_OK;
+    if (ix->scan_kind == 2) {
+        *use = true;
+        return JHQ_OK;
+    }
+    if (ck > kMfmaMaxCk || ix->M < kMfmaMinM)
+        return JHQ_OK;
+    const int B = ix->batch_size;
+    const bool cached = ix->mfma_dec_B == B && ix->mfma_dec_P == P && ix->mfma_dec_n > 0 &&
+                        ix->ntotal * 5 >= ix->mfma_dec_n * 4 && ix->ntotal * 4 <= ix->mfma_dec_n * 5;
+    if (!cached && measure && ix->ntotal > 0) {
+        JHQ_TRY(mfma_measure_cost(ix, B, P, &ix->mfma_dec_cost, &ix->mfma_dec_cand));
+        ix->mfma_dec_B = B;
+        ix->mfma_dec_P = P;
+        ix->mfma_dec_n = ix->ntotal;
+        if (verbose())
+            std::fprintf(stderr,
+                         "[jhq] plan: pre-scan %.2f rows per pair, %.0f candidates per query "
+                         "(batch %d, %d probes): %s\n",
+                         ix->mfma_dec_cost, ix->mfma_dec_cand, B, P,
+                         ix->mfma_dec_cost <= kMfmaMaxTileCost ? "pre-scan" : "byte-LUT scan");
+    }
+    *use = (cached || (measure && ix->ntotal > 0)) && ix->mfma_dec_cost <= kMfmaMaxTileCost;
+    return JHQ_OK;
 }
 
 // Brings the skewed copy up to date: rows appended since the last refresh,
@@ -443,8 +556,10 @@ struct BatchPlan {
 int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) {
     bp->ck = ceil_ck(ix->alpha, k);
     bp->P = std::min(ix->nprobe, ix->nlist);
+    bool use_mfma = false;
+    JHQ_TRY(mfma_choose(ix, Bq, bp->P, bp->ck, grow, &use_mfma));
     if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
-                        skew_eligible(ix), mfma_eligible(ix, Bq, bp->P, bp->ck)))
+                        skew_eligible(ix), use_mfma))
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
@@ -467,9 +582,11 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
             ix->dump_perq = per_q;
         }
         // keys (dump scan) or biased integer distances (MFMA pre-scan)
+        // (the pre-scan: u32 slots and one tile minimum per 16 after them)
         const size_t slots = static_cast<size_t>(Bq) * std::max<int64_t>(ix->dump_perq, 1);
         for (int i = 0; i < nws; i++)
-            JHQ_TRY(need(ix->ws[i].wdump, bp->sh.mfma ? (slots + 1) / 2 : slots, grow));
+            JHQ_TRY(need(ix->ws[i].wdump, bp->sh.mfma ? (slots + slots / 16 + 40) / 2 : slots,
+                         grow));
         if (bp->sh.mfma)
             for (int i = 0; i < nws; i++)
                 JHQ_TRY(need(ix->ws[i].wmfma, jhq::mfma_scan_bytes(Bq, bp->P, ix->M, ix->num_cu),
@@ -503,6 +620,7 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
         JHQ_HIP(jhq::mfma_scan(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                ix->dcodes_t.p, bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
+                               static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
                                w.wmfma.p, w.wmfma.n,
                                w.wpartial.p, w.wpslot.p, ix->num_cu, s));
     else
@@ -788,7 +906,7 @@ int jhq_reserve(jhq_index* idx, int k_max) {
 
 int jhq_set_scan_kind(jhq_index* idx, int kind) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
-    if (kind != 0 && kind != 1) return fail(JHQ_EINVAL, "scan kind must be 0 or 1");
+    if (kind < 0 || kind > 2) return fail(JHQ_EINVAL, "scan kind must be 0, 1 or 2");
     JHQ_TRY(idx->quiesce());
     idx->scan_kind = kind;
     return reserve_search(idx);
@@ -1596,8 +1714,10 @@ int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list) {
     const int ck = ceil_ck(idx->alpha, k);
     const int P = std::min(idx->nprobe, idx->nlist);
     jhq::ScanShape sh{};
+    bool use_mfma = false;
+    JHQ_TRY(mfma_choose(const_cast<jhq_index*>(idx), idx->batch_size, P, ck, false, &use_mfma));
     if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh,
-                        skew_eligible(idx), mfma_eligible(idx, idx->batch_size, P, ck)))
+                        skew_eligible(idx), use_mfma))
         return fail(JHQ_EINVAL, "no scan plan fits in LDS");
     if (scan_kind) *scan_kind = sh.mfma ? 4 : sh.dump ? 2 : sh.skew ? 3 : sh.wave ? 1 : 0;
     if (short_list) *short_list = ck;

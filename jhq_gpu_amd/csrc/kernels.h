@@ -141,6 +141,12 @@ hipError_t relocate_lists(const int4* moves, int nmoves, int M, int bpv, const u
 hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
                          int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s);
 
+// rows[i] = the stored vector at column samp[i].z of the list block (start
+// samp[i].x, row stride samp[i].y) decoded from its primary code (rotated
+// space, one Lloyd-Max level per coordinate)
+hipError_t decode_rows(const int4* samp, int S, const uint8_t* codes_t, int M, int Ds, int K1D,
+                       int bpd, const float* c1d, float* rows, hipStream_t s);
+
 struct ScanShape {
     int G;             // persistent scan workgroups
     int lds;           // dynamic LDS bytes of the scan kernel
@@ -167,15 +173,17 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 // MFMA products over the batch's shared lists, then every candidate that the
 // error bound cannot exclude from the exact top-ck is re-checked with the
 // reference's arithmetic; partial[query's segment][ck] as scan_topck writes
-// it.  dump holds one u32 per candidate slot of the batch (the sum of qtot
-// times 16); ws (256-byte aligned) holds mfma_scan_bytes for this num_cu.
+// it.  dump holds one u32 per candidate slot of the batch (dump_slots, a
+// multiple of 16, at least the sum of qtot times 16) and after them one per
+// 16 slots; ws (256-byte aligned) holds mfma_scan_bytes for this num_cu.
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck);
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
                      const int4* ldesc, const uint8_t* codes_t, int ck, uint32_t* dump,
-                     unsigned char* ws, size_t ws_bytes, unsigned long long* partial,
-                     int32_t* partial_slot, int num_cu, hipStream_t s);
+                     int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
+                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
+                     hipStream_t s);
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from
 // q_rot (v14/search.cu:65-195); partial[segment][ck] keys

@@ -965,6 +965,31 @@ hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t l
     return launch_mfma<EPI_SCORE>(A, lda, Bm, ldb, nb, N, K, C, ldc, norms, s);
 }
 
+// Stored vectors decoded from their primary codes (rotated space, each
+// coordinate its digit's Lloyd-Max level): rows[i] for the candidate at
+// column samp[i].z of the list block (start samp[i].x, row stride samp[i].y).
+// Used as stand-in queries when estimating how a batch's probes overlap.
+__global__ void decode_rows_kernel(const int4* __restrict__ samp, const uint8_t* __restrict__ codes_t,
+                                   int M, int Ds, int K1D, int bpd, const float* __restrict__ c1d,
+                                   float* __restrict__ rows) {
+    const int i = blockIdx.x;
+    const int4 sp = samp[i];
+    const int d = M * Ds;
+    for (int t = threadIdx.x; t < d; t += blockDim.x) {
+        const int m = t / Ds, k = t - m * Ds;
+        const uint8_t v = codes_t[(int64_t)sp.x * M + (int64_t)m * sp.y + sp.z];
+        rows[(int64_t)i * d + t] = c1d[(v >> (k * bpd)) & (K1D - 1)];
+    }
+}
+
+hipError_t decode_rows(const int4* samp, int S, const uint8_t* codes_t, int M, int Ds, int K1D,
+                       int bpd, const float* c1d, float* rows, hipStream_t s) {
+    if (S <= 0) return hipSuccess;
+    hipLaunchKernelGGL(decode_rows_kernel, dim3(S), dim3(256), 0, s, samp, codes_t, M, Ds, K1D,
+                       bpd, c1d, rows);
+    return hipGetLastError();
+}
+
 // uint8 / int8 vectors converted to float32 on the device (dtype 1 = uint8,
 // 2 = int8), 16 elements per thread iteration.
 __global__ void convert_kernel(const uint8_t* __restrict__ src, int dtype, int64_t n,
@@ -3852,6 +3877,7 @@ struct MfmaWs {
                      //            list's first slot); entries past its count unused
     int4* grp;       // [B*P]: (block start, row stride, size, queries)
     int2* wstart;    // [waves]: (group, tile in the group) where a wave starts
+    int4* qinfo;     // [B]: (first slot of the query's row, its segment, tiles, 0)
     int* ctl;        // [16]: tiles of the batch, groups
 };
 
@@ -3868,6 +3894,8 @@ static size_t mfma_carve(int B, int P, int M, int nwaves, unsigned char* base, M
     off += al((size_t)B * P * sizeof(int4));
     const size_t o_ws = off;
     off += al((size_t)nwaves * sizeof(int2));
+    const size_t o_qi = off;
+    off += al((size_t)B * sizeof(int4));
     const size_t o_ctl = off;
     off += al(16 * sizeof(int));
     if (w) {
@@ -3876,6 +3904,7 @@ static size_t mfma_carve(int B, int P, int M, int nwaves, unsigned char* base, M
         w->gq = (int2*)(base + o_gq);
         w->grp = (int4*)(base + o_g);
         w->wstart = (int2*)(base + o_ws);
+        w->qinfo = (int4*)(base + o_qi);
         w->ctl = (int*)(base + o_ctl);
     }
     return off;
@@ -4034,6 +4063,12 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     if (tid == 0) {
         w.ctl[0] = T;
         w.ctl[1] = hg[H];
+        int seg = 0;
+        for (int b = 0; b < B; b++) {
+            const int nt = qpre[b + 1] - qpre[b];
+            w.qinfo[b] = make_int4(qpre[b] * kGroup, seg, nt, 0);
+            seg += nt > 0 ? 1 : 0;
+        }
     }
 }
 
@@ -4046,7 +4081,8 @@ template <int M>
 __device__ __forceinline__ void mfma_tile(const unsigned char* tb, int h, int j, uint32_t qsel,
                                           const mfma_v4i (&ahi)[M / 8],
                                           const mfma_v4i (&alo)[M / 8], int cand, int nl,
-                                          uint32_t* out, int d0, int d1, int d2, int d3) {
+                                          uint32_t* dump, uint32_t* tmin, int d0, int d1, int d2,
+                                          int d3) {
     constexpr int NK = M / 8, ND = M / 16, GS = M / 4;
     uint32_t cw[ND];
 #pragma unroll
@@ -4075,10 +4111,31 @@ __device__ __forceinline__ void mfma_tile(const unsigned char* tb, int h, int j,
         alw = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[s], bv, alw, 0, 0, 0);
     }
     const bool ok = cand < nl;
-    if (d0 >= 0) out[d0] = ok ? (uint32_t)(ah[0] * 256 + alw[0]) + 0x80000000u : 0xffffffffu;
-    if (d1 >= 0) out[d1] = ok ? (uint32_t)(ah[1] * 256 + alw[1]) + 0x80000000u : 0xffffffffu;
-    if (d2 >= 0) out[d2] = ok ? (uint32_t)(ah[2] * 256 + alw[2]) + 0x80000000u : 0xffffffffu;
-    if (d3 >= 0) out[d3] = ok ? (uint32_t)(ah[3] * 256 + alw[3]) + 0x80000000u : 0xffffffffu;
+    const uint32_t v0 = ok ? (uint32_t)(ah[0] * 256 + alw[0]) + 0x80000000u : 0xffffffffu;
+    const uint32_t v1 = ok ? (uint32_t)(ah[1] * 256 + alw[1]) + 0x80000000u : 0xffffffffu;
+    const uint32_t v2 = ok ? (uint32_t)(ah[2] * 256 + alw[2]) + 0x80000000u : 0xffffffffu;
+    const uint32_t v3 = ok ? (uint32_t)(ah[3] * 256 + alw[3]) + 0x80000000u : 0xffffffffu;
+    // d0..d3: the rows' dump slots of the tile's first candidate (multiples of 16)
+    if (d0 >= 0) dump[d0 + j] = v0;
+    if (d1 >= 0) dump[d1 + j] = v1;
+    if (d2 >= 0) dump[d2 + j] = v2;
+    if (d3 >= 0) dump[d3 + j] = v3;
+    // each row's minimum over the tile's 16 candidates (the lanes of one
+    // group): the re-check bounds its ck-th smallest value from these
+    uint32_t m0 = v0, m1 = v1, m2 = v2, m3 = v3;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        m0 = min(m0, (uint32_t)__shfl_xor((int)m0, o));
+        m1 = min(m1, (uint32_t)__shfl_xor((int)m1, o));
+        m2 = min(m2, (uint32_t)__shfl_xor((int)m2, o));
+        m3 = min(m3, (uint32_t)__shfl_xor((int)m3, o));
+    }
+    if (j == 0) {
+        if (d0 >= 0) tmin[d0 / 16] = m0;
+        if (d1 >= 0) tmin[d1 / 16] = m1;
+        if (d2 >= 0) tmin[d2 / 16] = m2;
+        if (d3 >= 0) tmin[d3 / 16] = m3;
+    }
 }
 
 // Lane l: query row / candidate column l % 16, K group l / 16 (the lane
@@ -4093,7 +4150,8 @@ __device__ __forceinline__ void mfma_tile(const unsigned char* tb, int h, int j,
 // (v_perm_b32); bit plane k of a code dword is (w >> k) & 0x01010101.
 template <int M>
 __global__ void __launch_bounds__(256)
-mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __restrict__ dump) {
+mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __restrict__ dump,
+                 uint32_t* __restrict__ tmin) {
     constexpr int NK = M / 8, GS = M / 4, D = 8 * M;
     constexpr int RL = (M + 63) / 64;          // rows a lane loads per tile (1 or 2)
     static_assert(RL <= 2, "at most 128 subspaces");
@@ -4180,8 +4238,9 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
         JHQ_MFMA_FETCH(U, k + kMfmaPD);                                                     \
         if (live) {                                                                         \
             __builtin_amdgcn_s_waitcnt(0xc07f); /* this wave's LDS writes done */           \
-            mfma_tile<M>(tb, h, j, qsel, ahi, alo, cbase + 16 * k, nl, dump + 16 * k + j, d0, \
-                         d1, d2, d3);                                                       \
+            mfma_tile<M>(tb, h, j, qsel, ahi, alo, cbase + 16 * k, nl, dump, tmin,          \
+                         d0 < 0 ? -1 : d0 + 16 * k, d1 < 0 ? -1 : d1 + 16 * k,              \
+                         d2 < 0 ? -1 : d2 + 16 * k, d3 < 0 ? -1 : d3 + 16 * k);             \
         }                                                                                   \
     }
         for (int k0 = 0; k0 < n; k0 += kMfmaPD) {
@@ -4214,18 +4273,68 @@ __device__ __forceinline__ uint32_t mfma_member_bound(const MfmaQS& Q, uint32_t 
     return (uint32_t)((int64_t)floor(R) + 2147483648ll);
 }
 
-// One workgroup per query: the ck-th smallest I bounds the members (two
-// passes over the query's I values), the members' distances are recomputed
-// in the reference's order, and the exact top-ck by (dist, position) goes
-// to partial[segment][ck] (one segment per query).
+// The k-th smallest (1 <= k <= n) of n values get(0..n), 8 bits a round:
+// an LDS histogram of the values that match the bits found so far, and one
+// wave finds the bin that holds the k-th.  hist: 256 ints; c2: 2 ints.
+template <int NT, class Get>
+__device__ uint32_t block_radix_kth(Get get, int n, int k, int* hist, int* c2) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t pre = 0u, msk = 0u;
+    int kr = k;
+    for (int sh = 24; sh >= 0; sh -= 8) {
+        for (int i = tid; i < 256; i += NT) hist[i] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += NT) {
+            const uint32_t v = get(i);
+            if ((v & msk) == pre) atomicAdd(&hist[(v >> sh) & 255u], 1);
+        }
+        __syncthreads();
+        if (wv == 0) {
+            // lane l holds bins 4l .. 4l+3: inclusive prefix over lanes
+            int c[4], t = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                c[e] = hist[4 * lane + e];
+                t += c[e];
+            }
+            int inc = t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int x = __shfl_up(inc, o);
+                if (lane >= o) inc += x;
+            }
+            int below = inc - t;
+            // the lane whose bins cross kr picks the bin
+            if (below < kr && kr <= inc) {
+                int e = 0;
+                while (below + c[e] < kr) below += c[e++];
+                c2[0] = 4 * lane + e;
+                c2[1] = below;
+            }
+        }
+        __syncthreads();
+        pre |= (uint32_t)c2[0] << sh;
+        msk |= 255u << sh;
+        kr -= c2[1];
+        __syncthreads();
+    }
+    return pre;
+}
+
+// One workgroup per query: the ck-th smallest of the query's tile minima
+// (written by the scan) bounds the members, one pass over the query's I
+// values collects the candidates that can be members, the ck-th smallest I
+// among them tightens the bound, the members' distances are recomputed in
+// the reference's order, and the exact top-ck by (dist, position) goes to
+// partial[segment][ck] (one segment per query).
 template <int NT>
 __global__ void __launch_bounds__(NT)
-mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict__ qs,
+mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restrict__ tmin,
+                    const MfmaQS* __restrict__ qs, const int4* __restrict__ qinfo,
                     const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
                     const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
-                    const int32_t* __restrict__ gofs, const int32_t* __restrict__ qtot, int B,
-                    int P, const int4* __restrict__ ldesc, const uint8_t* __restrict__ codes_t,
-                    int ck, unsigned long long* __restrict__ partial,
+                    const int32_t* __restrict__ gofs, int P, const int4* __restrict__ ldesc,
+                    const uint8_t* __restrict__ codes_t, int ck,
+                    unsigned long long* __restrict__ partial,
                     int32_t* __restrict__ partial_slot) {
     constexpr int NW = NT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -4239,16 +4348,14 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
     float* sc1d = sq + d;                                      // [K1D]
     int* meta = (int*)(sc1d + K1D);                            // [P][4]
     int* sg = meta + 4 * P;                                    // [P + 1]
-    int* qpre = sg + P + 1;                                    // [B + 1]
-    int* spre = qpre + B + 1;                                  // [B + 1]
-    int* wsum = spre + B + 1;                                  // [NW]
+    int* wsum = sg + P + 1;                                    // [NW]
     int* ctl = wsum + NW;                                      // [4]
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const unsigned long long lt = (1ull << lane) - 1ull;
     JHQ_PHASE_DECL
-    work_plan<NT>(qtot, B, 1, 0, qpre, spre, wsum);
-    const int s0 = spre[b], s1 = spre[b + 1];
-    if (s1 == s0) return;  // no candidates: refine sees no segment
+    const int4 qi = qinfo[b];
+    if (qi.z == 0) return;  // no candidates: refine sees no segment
+    const int s0 = qi.y;
     // the query, codebook and probe table are requested now and stored in
     // LDS after pass 1, whose loads do not wait for them (d <= NT, P < NT)
     const float qv = tid < d ? q_rot[(int64_t)b * d + tid] : 0.0f;
@@ -4256,24 +4363,10 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
     const int4 Lv = tid < P ? ldesc[probes[(int64_t)b * P + tid]] : make_int4(0, 0, 0, 0);
     const int gv = tid <= P ? gofs[(int64_t)b * (P + 1) + tid] : 0;
     const MfmaQS Q = qs[b];
-    const int64_t n = (int64_t)(qpre[b + 1] - qpre[b]) * kGroup;
-    const uint32_t* row = dump + (int64_t)qpre[b] * kGroup;
-    // pass 1: an upper bound of the ck-th smallest I (each wave's r-th
-    // smallest thread minimum; NW * r >= ck values are at or below the max)
-    // (rows are whole 16-slot groups: 16-byte loads, kRecheckLPT of them in
-    // flight per thread)
+    const int64_t n = (int64_t)qi.z * kGroup;
+    const uint32_t* row = dump + qi.x;
     const uint4* row4 = (const uint4*)row;
     const int64_t n4 = n / 4;
-    uint32_t mn = ~0u;
-    for (int64_t i0 = tid; i0 < n4; i0 += kRecheckLPT * NT) {
-        uint4 v[kRecheckLPT];
-#pragma unroll
-        for (int u = 0; u < kRecheckLPT; u++)
-            v[u] = i0 + u * NT < n4 ? row4[i0 + u * NT] : make_uint4(~0u, ~0u, ~0u, ~0u);
-#pragma unroll
-        for (int u = 0; u < kRecheckLPT; u++)
-            mn = min(mn, min(min(v[u].x, v[u].y), min(v[u].z, v[u].w)));
-    }
     if (tid < d) sq[tid] = qv;
     if (tid < K1D) sc1d[tid] = cv;
     if (tid < P) {
@@ -4285,47 +4378,87 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
     if (tid <= P) sg[tid] = gv;
     if (tid == 0) ctl[0] = 0;
     stream_begin<NT>(S);
-    const int r = (ck + NW - 1) / NW;
-    const uint32_t tw = r <= 64 ? wave_kth_u32(mn, r) : ~0u;
-    if (lane == 0) wsum[wv] = (int)tw;
-    __syncthreads();
-    uint32_t That = 0u;
+    // pass 1: an upper bound of the ck-th smallest I from the tile minima
+    // (each is an I value of its own tile): their exact ck-th smallest when
+    // they fit in LDS, else each wave's r-th smallest thread minimum (NW * r
+    // >= ck values are at or below the largest)
+    const uint32_t* tm = tmin + qi.x / kGroup;
+    const int nt = qi.z;
+    uint32_t That = ~0u;
+    if (nt >= ck && nt <= 2 * kRecheckCap) {
+        uint32_t* tl = (uint32_t*)mp;  // mp and mc, free until the members
+        for (int i0 = tid; i0 < nt; i0 += 4 * NT) {
+            uint32_t v[4];
 #pragma unroll
-    for (int w2 = 0; w2 < NW; w2++) That = max(That, (uint32_t)wsum[w2]);
+            for (int u = 0; u < 4; u++) v[u] = i0 + u * NT < nt ? tm[i0 + u * NT] : 0u;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (i0 + u * NT < nt) tl[i0 + u * NT] = v[u];
+        }
+        __syncthreads();
+        That = block_radix_kth<NT>([&](int i) { return tl[i]; }, nt, ck, (int*)ebuf, ctl + 2);
+    } else if (nt >= ck) {
+        uint32_t mn = ~0u;
+        for (int i = tid; i < nt; i += NT) mn = min(mn, tm[i]);
+        const int r = (ck + NW - 1) / NW;
+        const uint32_t tw = r <= 64 ? wave_kth_u32(mn, r) : ~0u;
+        if (lane == 0) wsum[wv] = (int)tw;
+        __syncthreads();
+        That = 0u;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; w2++) That = max(That, (uint32_t)wsum[w2]);
+    } else {
+        __syncthreads();
+    }
     const uint32_t thr1 = That == ~0u ? 0xfffffffeu : mfma_member_bound(Q, That, M);
     JHQ_PHASE(1);
-    // pass 2: the candidates at or below thr1 (they include the ck smallest
-    // I values and every member)
-    for (int64_t i0 = 0; i0 < n4; i0 += kRecheckLPT * NT) {
-        uint4 v4[kRecheckLPT];
+    // pass 2: the candidates at or below a bound (they include the ck
+    // smallest I values and every member), into surv
+    auto collect = [&](uint32_t thr) {
+        if (tid == 0) ctl[0] = 0;
+        __syncthreads();
+        for (int64_t i0 = 0; i0 < n4; i0 += kRecheckLPT * NT) {
+            uint4 v4[kRecheckLPT];
 #pragma unroll
-        for (int u = 0; u < kRecheckLPT; u++) {
-            const int64_t i = i0 + u * NT + tid;
-            v4[u] = i < n4 ? row4[i] : make_uint4(~0u, ~0u, ~0u, ~0u);
-        }
+            for (int u = 0; u < kRecheckLPT; u++) {
+                const int64_t i = i0 + u * NT + tid;
+                v4[u] = i < n4 ? row4[i] : make_uint4(~0u, ~0u, ~0u, ~0u);
+            }
 #pragma unroll
-        for (int u = 0; u < kRecheckLPT; u++) {
-            const uint32_t vv[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
-            const bool any = __ballot(vv[0] <= thr1 || vv[1] <= thr1 || vv[2] <= thr1 ||
-                                      vv[3] <= thr1) != 0ull;
-            if (!any) continue;
+            for (int u = 0; u < kRecheckLPT; u++) {
+                const uint32_t vv[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+                const bool any = __ballot(vv[0] <= thr || vv[1] <= thr || vv[2] <= thr ||
+                                          vv[3] <= thr) != 0ull;
+                if (!any) continue;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const bool keep = vv[e] <= thr1;
-                const unsigned long long mk = __ballot(keep);
-                if (!mk) continue;
-                int at = 0;
-                if (lane == 0) at = atomicAdd(&ctl[0], __popcll(mk));
-                at = __shfl(at, 0);
-                const int pos = at + __popcll(mk & lt);
-                const int64_t i = 4 * (i0 + u * NT + tid) + e;
-                if (keep && pos < kRecheckCap)
-                    surv[pos] = ((unsigned long long)vv[e] << 32) | (uint32_t)i;
+                for (int e = 0; e < 4; e++) {
+                    const bool keep = vv[e] <= thr;
+                    const unsigned long long mk = __ballot(keep);
+                    if (!mk) continue;
+                    int at = 0;
+                    if (lane == 0) at = atomicAdd(&ctl[0], __popcll(mk));
+                    at = __shfl(at, 0);
+                    const int pos = at + __popcll(mk & lt);
+                    const int64_t i = 4 * (i0 + u * NT + tid) + e;
+                    if (keep && pos < kRecheckCap)
+                        surv[pos] = ((unsigned long long)vv[e] << 32) | (uint32_t)i;
+                }
             }
         }
+        __syncthreads();
+        return ctl[0];
+    };
+    int ns = collect(thr1);
+    uint32_t thr = thr1;
+    if (ns > kRecheckCap && n >= ck) {
+        // the tile minima left too many candidates: the exact ck-th smallest
+        // I of the row (padding slots hold the largest value) and again
+        thr = min(thr1, mfma_member_bound(
+                            Q, block_radix_kth<NT>([&](int i) { return row[i]; }, (int)n, ck,
+                                                   (int*)ebuf, ctl + 2),
+                            M));
+        ns = collect(thr);
     }
-    __syncthreads();
-    const int ns = ctl[0];
     JHQ_PHASE(2);
 #ifdef JHQ_PHASE_TIMING
     ph_acc[7] += (unsigned long long)ns;
@@ -4355,50 +4488,11 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
     int kk = 0;
     if (ns <= kRecheckCap) {
         // the ck-th smallest I among the survivors, then the members
-        uint32_t thr2 = thr1;
+        uint32_t thr2 = thr;
         if (ns >= ck) {
-            // radix select of the ck-th smallest survivor value, 8 bits a
-            // round (the histogram in the member arrays, free until below)
-            int* hist = mp;
-            uint32_t pre = 0u, msk = 0u;
-            int kr = ck;
-            for (int sh = 24; sh >= 0; sh -= 8) {
-                for (int i = tid; i < 256; i += NT) hist[i] = 0;
-                __syncthreads();
-                for (int i = tid; i < ns; i += NT) {
-                    const uint32_t v = (uint32_t)(surv[i] >> 32);
-                    if ((v & msk) == pre) atomicAdd(&hist[(v >> sh) & 255u], 1);
-                }
-                __syncthreads();
-                if (wv == 0) {
-                    // lane l holds bins 4l .. 4l+3: inclusive prefix over lanes
-                    int c[4], t = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        c[e] = hist[4 * lane + e];
-                        t += c[e];
-                    }
-                    int inc = t;
-                    for (int o = 1; o < 64; o <<= 1) {
-                        const int x = __shfl_up(inc, o);
-                        if (lane >= o) inc += x;
-                    }
-                    int below = inc - t;
-                    // the lane whose bins cross kr picks the bin
-                    if (below < kr && kr <= inc) {
-                        int e = 0;
-                        while (below + c[e] < kr) below += c[e++];
-                        ctl[2] = 4 * lane + e;
-                        ctl[3] = below;
-                    }
-                }
-                __syncthreads();
-                pre |= (uint32_t)ctl[2] << sh;
-                msk |= 255u << sh;
-                kr -= ctl[3];
-                __syncthreads();
-            }
-            thr2 = min(thr1, mfma_member_bound(Q, pre, M));
+            const uint32_t pre = block_radix_kth<NT>(
+                [&](int i) { return (uint32_t)(surv[i] >> 32); }, ns, ck, mp, ctl + 2);
+            thr2 = min(thr, mfma_member_bound(Q, pre, M));
         }
         JHQ_PHASE(3);
         if (tid == 0) ctl[1] = 0;
@@ -4476,12 +4570,13 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const MfmaQS* __restrict_
         kk = min(ck, nm);
         if (kk > 0) select_keys<NT>(surv, nm, kk, S.kout, S.kidx, S.ktmp, S.st);
     } else {
-        // more survivors than fit: every candidate at or below thr1, exact
-        // distances one per thread, streamed through the selection
+        // more survivors than fit (ties at the bound): every candidate at or
+        // below it, exact distances one per thread, streamed through the
+        // selection
         for (int64_t r0 = 0; r0 < n; r0 += NT) {
             const int64_t i = r0 + tid;
             uint32_t o[1] = {~0u}, tg[1] = {~0u};
-            if (i < n && row[i] <= thr1) {
+            if (i < n && row[i] <= thr) {
                 int pp, cc;
                 locate((int)i, pp, cc);
                 float acc = 0.0f;
@@ -4519,8 +4614,7 @@ static size_t mfma_plan_lds(int B, int P) {
 static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B) {
     return stream_lds_bytes(kRecheckNT, ck) + (size_t)kRecheckCap * (8 + 4 + 4) +
            (size_t)kRecheckCHM * (M + 1) * 4 + (size_t)d * 4 + (size_t)K1D * 4 +
-           (size_t)(4 * P + P + 1) * 4 + (size_t)(2 * (B + 1)) * 4 + (kRecheckNT / 64) * 4 + 16 +
-           64;
+           (size_t)(4 * P + P + 1) * 4 + (kRecheckNT / 64) * 4 + 16 + 64;
 }
 
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck) {
@@ -4540,10 +4634,14 @@ size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
                      const int4* ldesc, const uint8_t* codes_t, int ck, uint32_t* dump,
-                     unsigned char* ws, size_t ws_bytes, unsigned long long* partial,
-                     int32_t* partial_slot, int num_cu, hipStream_t s) {
-    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck) || !ws || ((uintptr_t)ws & 255) || !dump)
+                     int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
+                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
+                     hipStream_t s) {
+    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck) || !ws || ((uintptr_t)ws & 255) || !dump ||
+        dump_slots % 16 != 0)
         return hipErrorInvalidValue;
+    // tile minima after the candidate slots
+    uint32_t* tmin = dump + dump_slots;
     MfmaWs w;
     const int nwaves = mfma_scan_waves(num_cu);
     if (mfma_carve(B, P, M, nwaves, ws, &w) > ws_bytes) return hipErrorInvalidValue;
@@ -4553,17 +4651,17 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
     if ((int)lp > mxp) return hipErrorInvalidValue;
     hipLaunchKernelGGL(mfma_plan_kernel<kMfmaPlanNT>, dim3(B + 1), dim3(kMfmaPlanNT), lp, s, q_rot,
                        d, M, c1d, probes, gofs, qtot, B, P, ldesc, w, H, nwaves);
-    using SFn = void (*)(MfmaWs, const uint8_t*, uint32_t*);
+    using SFn = void (*)(MfmaWs, const uint8_t*, uint32_t*, uint32_t*);
     SFn f = M == 16 ? mfma_scan_kernel<16> : M == 32 ? mfma_scan_kernel<32>
           : M == 48 ? mfma_scan_kernel<48> : M == 64 ? mfma_scan_kernel<64>
           : M == 80 ? mfma_scan_kernel<80> : M == 96 ? mfma_scan_kernel<96>
           : M == 112 ? mfma_scan_kernel<112> : mfma_scan_kernel<128>;
-    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, codes_t, dump);
+    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, codes_t, dump, tmin);
     const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B);
     static const int mxr = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT>);
     if ((int)lr > mxr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(mfma_recheck_kernel<kRecheckNT>, dim3(B), dim3(kRecheckNT), lr, s, dump,
-                       w.qs, q_rot, d, Ds, K1D, bpd, c1d, M, probes, gofs, qtot, B, P, ldesc,
+                       tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes, gofs, P, ldesc,
                        codes_t, ck, partial, partial_slot);
     return hipGetLastError();
 }

@@ -9,7 +9,8 @@ give the oracle's short list bit for bit, and the same results as the
 byte-LUT scans (scan kind 1) bit for bit.  Cases cover every M the kernel is
 built for up to 128, ck from 10 to 400, lists whose capacity exceeds their
 size (after appends), duplicates that overflow the re-check buffer (the
-streamed fallback), and pipelined device searches."""
+streamed fallback), and pipelined device searches.  The cases force the
+pre-scan (scan kind 2); test_default_choice checks when the default takes it."""
 import sys
 import zlib
 
@@ -35,6 +36,9 @@ CASES = [
     ("m112_a4", 896, 112, 8, 3, 4.0, 2500, 12, 10, 12),
     ("m128_a10", 1024, 128, 32, 6, 10.0, 3000, 20, 10, 64),
     ("m32_ck400", 256, 32, 8, 4, 4.0, 6000, 12, 100, 16),
+    # 80 K candidates per query: more tiles than the re-check holds in LDS,
+    # so its first bound comes from per-wave minima
+    ("m32_wide", 256, 32, 2, 2, 10.0, 80000, 8, 10, 8),
 ]
 IDS = [c[0] for c in CASES]
 _BUILT = {}
@@ -60,6 +64,7 @@ def _build(case):
     o.train(base[:ntrain])
     g.add(base)
     o.add(base)
+    g.set_scan_kind(2)
     _BUILT[name] = (g, o, q, k)
     return _BUILT[name]
 
@@ -82,7 +87,7 @@ def test_mfma_scan_matches_oracle_and_lut_scans(gpu, case):
         assert g.scan_plan(k)[0] != "mfma_scan_kernel"
         lr = g.search_debug(q, k)
     finally:
-        g.set_scan_kind(0)
+        g.set_scan_kind(2)
     _same(gr, lr)
     # repeated searches are bit-identical (the work list's order varies)
     _same(gr, g.search_debug(q, k))
@@ -105,13 +110,14 @@ def test_mfma_duplicates_overflow_recheck(gpu):
     o.train(base[:4000])
     g.add(base)
     o.add(base)
+    g.set_scan_kind(2)
     assert g.scan_plan(k)[0] == "mfma_scan_kernel"
     gr, _ = _stagewise(g, o, q, k)
     g.set_scan_kind(1)
     try:
         lr = g.search_debug(q, k)
     finally:
-        g.set_scan_kind(0)
+        g.set_scan_kind(2)
     _same(gr, lr)
 
 
@@ -127,6 +133,7 @@ def test_mfma_after_appends(gpu):
                        seed=42)
     g.train(base[:2000])
     o.train(base[:2000])
+    g.set_scan_kind(2)
     g.add(base[:1000])
     upto = 1000
     for n in (3, 600, 1, 2500, 31, 1865):
@@ -139,7 +146,7 @@ def test_mfma_after_appends(gpu):
         try:
             lr = g.search_debug(q, k)
         finally:
-            g.set_scan_kind(0)
+            g.set_scan_kind(2)
         _same(gr, lr)
 
 
@@ -160,3 +167,23 @@ def test_mfma_device_search_pipelined(gpu):
         g.search_device(qt, k, od, oi, stream=s)
         assert np.array_equal(oi.cpu().numpy(), i1), rep
         assert np.array_equal(_bits(od.cpu().numpy()), _bits(d1)), rep
+
+
+def test_default_choice(gpu):
+    """Scan kind 0 takes the pre-scan when the queries of a batch share their
+    lists (large batch, few lists) and the byte-LUT scan when each probed
+    list serves about one query (one query per batch) or the short list is
+    long."""
+    g, o, q, k = _build(CASES[IDS.index("m128_a10")])
+    g96, _, _, k96 = _build(CASES[IDS.index("m96_flat")])
+    try:
+        g.set_scan_kind(0)
+        g96.set_scan_kind(0)
+        assert g.scan_plan(k)[0] == "mfma_scan_kernel"
+        assert g96.scan_plan(k96)[0] == "scan_skew_kernel"
+        # a short list of 600 (k = 60, alpha = 10) is beyond what one
+        # workgroup per query re-checks quickly
+        assert g.scan_plan(60)[0] != "mfma_scan_kernel"
+    finally:
+        g.set_scan_kind(2)
+        g96.set_scan_kind(2)

@@ -252,18 +252,23 @@ def test_wave_scan_taken(gpu, name):
     assert g.scan_plan(k)[0] == "scan_wave_kernel"
 
 
-# one-bit digits with M a multiple of 16 take the integer-MFMA pre-scan by
-# default; the byte-LUT scans they would otherwise run are checked here with
-# scan kind 1
-@pytest.mark.parametrize("name,lut_scan", [("d1024_m128", "scan_skew_kernel"),
-                                           ("m96_d768", "scan_skew_kernel"),
-                                           ("m16_ck100", "scan_wave_kernel")])
-def test_lut_scans_of_mfma_cases(gpu, name, lut_scan):
+# one-bit digits with M a multiple of 16 can take the integer-MFMA pre-scan;
+# the default takes it for M >= 64 when a batch's queries share their lists.
+# The byte-LUT scans these cases would otherwise run are checked here with
+# scan kind 1, the pre-scan with scan kind 2
+@pytest.mark.parametrize("name,default,lut_scan", [
+    ("d1024_m128", "mfma_scan_kernel", "scan_skew_kernel"),
+    ("m96_d768", "mfma_scan_kernel", "scan_skew_kernel"),
+    ("m16_ck100", "scan_wave_kernel", "scan_wave_kernel")])
+def test_lut_scans_of_mfma_cases(gpu, name, default, lut_scan):
     g, o, base, q, k = _build(CASES[IDS.index(name)])
-    assert g.scan_plan(k)[0] == "mfma_scan_kernel"
-    g.set_scan_kind(1)
+    assert g.scan_plan(k)[0] == default
     try:
+        g.set_scan_kind(1)
         assert g.scan_plan(k)[0] == lut_scan
+        _stagewise(g, o, q, k)
+        g.set_scan_kind(2)
+        assert g.scan_plan(k)[0] == "mfma_scan_kernel"
         _stagewise(g, o, q, k)
     finally:
         g.set_scan_kind(0)

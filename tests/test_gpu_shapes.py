@@ -1,8 +1,8 @@
 """GPU parity at the shapes the benchmark runs, smaller N.
 
-Every shape here has one-bit digits, so it runs the integer-MFMA pre-scan with
-exact re-check by default (scan kind 0) and the byte-LUT scans with scan kind
-1; both are checked.
+Every shape here has one-bit digits, so it can run the integer-MFMA pre-scan
+with exact re-check (forced with scan kind 2) or the byte-LUT scans (scan kind
+1); both are checked.
 
 * Config 2: D=1024, M=128 (the skewed scan with the subspace-parity LUT),
   alpha=10 -> ck=100 (three 64-key wave buffers), nlist 256, nprobe 16 and
@@ -79,7 +79,7 @@ def test_cfg2_shape_lists_bit_exact(gpu):
     _lists_equal(g, o)
 
 
-@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
+@pytest.mark.parametrize("kind,scan", [(2, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
 @pytest.mark.parametrize("nprobe", [16, 64])
 def test_cfg2_shape_benchmarked_scan(gpu, nprobe, kind, scan):
     """M=128 with ck=100 (the instance bench.py times): the pre-scan and the
@@ -103,7 +103,7 @@ def test_cfg2_shape_benchmarked_scan(gpu, nprobe, kind, scan):
         o.nprobe = 16
 
 
-@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
+@pytest.mark.parametrize("kind,scan", [(2, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
 def test_cfg2_shape_alpha4(gpu, kind, scan):
     """The same index at alpha=4 (ck=40, two 64-key wave buffers)."""
     g, o, q = _cfg2()
@@ -119,7 +119,7 @@ def test_cfg2_shape_alpha4(gpu, kind, scan):
         o.alpha = np.float32(10.0)
 
 
-@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
+@pytest.mark.parametrize("kind,scan", [(2, "mfma_scan_kernel"), (1, "scan_skew_kernel")])
 def test_cfg1_shape_flat(gpu, kind, scan):
     """Flat index (nlist = 1) at D=1024, M=128, one query per batch
     (jhq_v1_plain/search.cu:126-228; v1's ck = min(ceil(alpha k), N) equals
@@ -136,7 +136,7 @@ def test_cfg1_shape_flat(gpu, kind, scan):
         g.set_scan_kind(0)
 
 
-@pytest.mark.parametrize("kind,scan", [(0, "mfma_scan_kernel"), (1, "scan_wave_kernel")])
+@pytest.mark.parametrize("kind,scan", [(2, "mfma_scan_kernel"), (1, "scan_wave_kernel")])
 def test_cfg3_shape_uint8(gpu, kind, scan):
     """uint8 rows at D=128, M=16 (wave scan), nlist 1024, nprobe 64, batch 64."""
     seed = zlib.crc32(b"cfg3_shape") % 10000
