@@ -35,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "QPS@recall@10>=0.95 (1Mx1024 IVF, batch 64); ADC-scan HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA
 
 
 def log(*a):
@@ -535,8 +536,28 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
             traffic_note = ("bytes per launch from %s (FETCH_SIZE x %.2f + WRITE_SIZE x %.2f)"
                             % (tj["source"], tj["fetch_scale"], tj["write_scale"]))
             limiter = tj.get("limiter")
+    names = {"scan_dump_kernel": "scan_dump_kernel + select_query_kernel",
+             "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel"}
+    extra = {}
+    if kernel == "mfma_scan_kernel":
+        # the pre-scan's integer products: per batch, each probed list's
+        # queries in 16-query tiles against its 16-row groups, two int8
+        # halves of K = d per tile (2 ops per multiply-add)
+        tiles = 0
+        for b in range(nb):
+            lists, cnt = np.unique(dbg["probes"][b * batch:(b + 1) * batch], return_counts=True)
+            tiles += int((((cnt + 15) // 16) * ((sizes[lists] + 15) // 16)).sum())
+        ops = tiles / nb * 16 * 16 * hq.shape[1] * 2 * 2
+        extra["int8_mfma"] = {
+            "tiles_per_launch": round(tiles / nb, 1),
+            "ops_per_launch": int(ops),
+            "achieved_tops": round(ops / (us * 1e-6) / 1e12, 2),
+            "peak_tops": INT8_PEAK_TOPS,
+            "frac": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 5),
+            "note": "ops over the scan step's time (plan + tiles + re-check)",
+        }
     return {
-        "kernel": kernel + (" + select_query_kernel" if kernel == "scan_dump_kernel" else ""),
+        "kernel": names.get(kernel, kernel),
         "dominant_step": max(step_us, key=step_us.get),
         # the roofline the scan is measured against: it streams each probed
         # code once per query (HBM-bound by design); the counter run, where
@@ -559,6 +580,7 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
             "definition": "(sum_q sum_probed |l| * M + sum_q ck * (bpv + 8)) / (scan + refine "
                           "kernel time)",
         },
+        **extra,
     }
 
 

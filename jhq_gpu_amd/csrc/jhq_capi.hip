@@ -619,7 +619,9 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
     if (bp.sh.mfma)
         JHQ_HIP(jhq::mfma_scan(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
-                               ix->dcodes_t.p, bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
+                               ix->dcodes_t.p,
+                               skew_eligible(ix) && !ix->skew_stale ? ix->dcodes_s.p : nullptr,
+                               bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
                                static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
                                w.wmfma.p, w.wmfma.n,
                                w.wpartial.p, w.wpslot.p, ix->num_cu, s));

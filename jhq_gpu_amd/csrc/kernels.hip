@@ -38,7 +38,7 @@ namespace jhq {
 // workgroup accumulates wall-clock ticks (100 MHz) per phase of the scan,
 // probe-selection and refine kernels; jhq_debug_phase_ticks() reads them.
 #ifdef JHQ_PHASE_TIMING
-constexpr int kPhaseBlocks = 4096, kPhases = 8;
+constexpr int kPhaseBlocks = 4096, kPhases = 10;
 __device__ unsigned long long g_phase[4][kPhaseBlocks][kPhases];
 #define JHQ_PHASE_DECL unsigned long long ph_t = wall_clock64(), ph_acc[kPhases] = {0};
 #define JHQ_PHASE(i)                                              \
@@ -4333,7 +4333,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
                     const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                     const int32_t* __restrict__ gofs, int P, const int4* __restrict__ ldesc,
-                    const uint8_t* __restrict__ codes_t, int ck,
+                    const uint8_t* __restrict__ codes_t, const uint8_t* __restrict__ skew, int ck,
                     unsigned long long* __restrict__ partial,
                     int32_t* __restrict__ partial_slot) {
     constexpr int NW = NT / 64;
@@ -4520,9 +4520,11 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         // member keys replace the survivors in surv.  Thread t computes
         // subspace t % M of members t / M, t / M + NT / M, ... (its query
         // values in registers); every code byte of a round is requested
-        // before the first is used; member rows of the entries are padded
-        // to M + 1 words, so both the writes and the in-order sums of a
-        // member row are free of bank conflicts
+        // before the first is used, from the lane-skewed copy when there is
+        // one (a member's M bytes in M / 16 runs of 16, against M cache
+        // lines of the code-major blocks); member rows of the entries are
+        // padded to M + 1 words, so both the writes and the in-order sums
+        // of a member row are free of bank conflicts
         constexpr int EPT = kRecheckCHM * 128 / NT;  // entries per thread (M <= 128)
         const int me = tid % M, mstep = NT / M;
         float qm[8];
@@ -4530,17 +4532,35 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         for (int k = 0; k < 8; k++) qm[k] = k < Ds ? sq[me * Ds + k] : 0.0f;
         for (int c0 = 0; c0 < nm; c0 += kRecheckCHM) {
             const int nc = min(kRecheckCHM, nm - c0);
-            uint8_t cb[EPT];
+            // every lane loads (rows past the chunk's end repeat its last
+            // member) into a register of its own, so that all EPT loads are
+            // in flight before the first wait
+            uint32_t cb[EPT];
+            uint32_t wrapm = 0u;
+            if (skew) {
 #pragma unroll
-            for (int u = 0; u < EPT; u++) {
-                const int jj = tid / M + u * mstep;
-                cb[u] = 0;
-                if (jj < nc) {
+                for (int u = 0; u < EPT; u++) {
+                    const int jj = min(tid / M + u * mstep, nc - 1);
+                    const int pp = mp[c0 + jj], cc = mc[c0 + jj];
+                    // subspace me of candidate cc sits at row position
+                    // me + cc % 32, wrapped positions holding code + 1
+                    int t = me + (cc & 31);
+                    const int wrap = t >= M ? 1 : 0;
+                    t -= wrap * M;
+                    wrapm |= (uint32_t)wrap << u;
+                    cb[u] = skew[skew_piece((int64_t)meta[4 * pp] + cc, t >> 4, M) + (t & 15)];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < EPT; u++) {
+                    const int jj = min(tid / M + u * mstep, nc - 1);
                     const int pp = mp[c0 + jj];
                     cb[u] = codes_t[(int64_t)meta[4 * pp] * M + (int64_t)me * meta[4 * pp + 1] +
                                     mc[c0 + jj]];
                 }
             }
+#pragma unroll
+            for (int u = 0; u < EPT; u++) cb[u] = (cb[u] - ((wrapm >> u) & 1u)) & 0xffu;
 #pragma unroll
             for (int u = 0; u < EPT; u++) {
                 const int jj = tid / M + u * mstep;
@@ -4556,7 +4576,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     ebuf[jj * (M + 1) + me] = e;
                 }
             }
+            JHQ_PHASE(8);
             __syncthreads();
+            JHQ_PHASE(9);
             if (tid < nc) {
                 float acc = 0.0f;
                 for (int m = 0; m < M; m++) acc += ebuf[tid * (M + 1) + m];
@@ -4633,12 +4655,12 @@ size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
 
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
-                     const int4* ldesc, const uint8_t* codes_t, int ck, uint32_t* dump,
-                     int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
+                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew, int ck,
+                     uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      unsigned long long* partial, int32_t* partial_slot, int num_cu,
                      hipStream_t s) {
     if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck) || !ws || ((uintptr_t)ws & 255) || !dump ||
-        dump_slots % 16 != 0)
+        dump_slots % 16 != 0 || (skew && M % 32 != 0))
         return hipErrorInvalidValue;
     // tile minima after the candidate slots
     uint32_t* tmin = dump + dump_slots;
@@ -4662,7 +4684,7 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
     if ((int)lr > mxr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(mfma_recheck_kernel<kRecheckNT>, dim3(B), dim3(kRecheckNT), lr, s, dump,
                        tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes, gofs, P, ldesc,
-                       codes_t, ck, partial, partial_slot);
+                       codes_t, skew, ck, partial, partial_slot);
     return hipGetLastError();
 }
 
