@@ -486,7 +486,7 @@ int mfma_measure_cost(jhq_index* ix, int B, int P, double* cost, double* cand) {
 int mfma_choose(jhq_index* ix, int Bq, int P, int ck, bool measure, bool* use) {
     *use = false;
     if (ix->scan_kind == 1 ||
-        !jhq::mfma_scan_ok(ix->M, ix->d, ix->Ds, ix->K1D, ix->bpd, Bq, P, ck))
+        !jhq::mfma_scan_ok(ix->M, ix->d, ix->Ds, ix->K1D, ix->bpd, Bq, P, ck, ix->RC * ix->Kr))
         return JHQ_OK;
     if (ix->scan_kind == 2) {
         *use = true;
@@ -559,7 +559,7 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
     bool use_mfma = false;
     JHQ_TRY(mfma_choose(ix, Bq, bp->P, bp->ck, grow, &use_mfma));
     if (!jhq::scan_plan(ix->M, ix->d, bp->P, bp->ck, ix->K1D, Bq, ix->num_cu, &bp->sh,
-                        skew_eligible(ix), use_mfma))
+                        skew_eligible(ix), use_mfma, ix->RC * ix->Kr))
         return fail(JHQ_EINVAL, "M=" + std::to_string(ix->M) + ", ck=" + std::to_string(bp->ck) +
                                     ", batch=" + std::to_string(Bq) +
                                     ": the byte LUT and selection buffers do not fit in LDS");
@@ -616,26 +616,30 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
     JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
                                w.wgofs.p, w.wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
-    if (bp.sh.mfma)
+    if (bp.sh.mfma) {
+        // the re-check refines each query's short list itself
         JHQ_HIP(jhq::mfma_scan(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                ix->dcodes_t.p,
                                skew_eligible(ix) && !ix->skew_stale ? ix->dcodes_s.p : nullptr,
                                bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
                                static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
-                               w.wmfma.p, w.wmfma.n,
-                               w.wpartial.p, w.wpslot.p, ix->num_cu, s));
-    else
+                               w.wmfma.p, w.wmfma.n, k, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
+                               ix->bpv, ix->dres.p, ix->dcorr.p, ix->dlist_ids.p, d_out, d_ids,
+                               want_topck ? w.wtopck.p : nullptr, ix->num_cu, s));
+        if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
+    } else {
         JHQ_HIP(jhq::scan_topck(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                 w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                 ix->dcodes_t.p, bp.ck, bp.sh, w.wpartial.p, w.wpslot.p,
                                 w.wdump.p, ix->dcodes_s.p, s));
-    if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
-    JHQ_HIP(jhq::refine_topk(w.wpartial.p, w.wpslot.p, w.wqtot.p, Bq, bp.sh, bp.ck, k,
-                             w.wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
-                             ix->bpv, ix->dldesc.p, ix->nlist, ix->dres.p, ix->dcorr.p,
-                             ix->dlist_ids.p, d_out, d_ids, want_topck ? w.wtopck.p : nullptr,
-                             s));
+        if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
+        JHQ_HIP(jhq::refine_topk(w.wpartial.p, w.wpslot.p, w.wqtot.p, Bq, bp.sh, bp.ck, k,
+                                 w.wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
+                                 ix->bpv, ix->dldesc.p, ix->nlist, ix->dres.p, ix->dcorr.p,
+                                 ix->dlist_ids.p, d_out, d_ids, want_topck ? w.wtopck.p : nullptr,
+                                 s));
+    }
     if (ix->timing) {
         JHQ_HIP(hipEventRecord(ix->ev[kSteps], s));
         JHQ_HIP(hipEventSynchronize(ix->ev[kSteps]));
@@ -1719,7 +1723,7 @@ int jhq_get_plan(const jhq_index* idx, int k, int* scan_kind, int* short_list) {
     bool use_mfma = false;
     JHQ_TRY(mfma_choose(const_cast<jhq_index*>(idx), idx->batch_size, P, ck, false, &use_mfma));
     if (!jhq::scan_plan(idx->M, idx->d, P, ck, idx->K1D, idx->batch_size, idx->num_cu, &sh,
-                        skew_eligible(idx), use_mfma))
+                        skew_eligible(idx), use_mfma, idx->RC * idx->Kr))
         return fail(JHQ_EINVAL, "no scan plan fits in LDS");
     if (scan_kind) *scan_kind = sh.mfma ? 4 : sh.dump ? 2 : sh.skew ? 3 : sh.wave ? 1 : 0;
     if (short_list) *short_list = ck;

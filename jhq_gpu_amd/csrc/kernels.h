@@ -164,27 +164,32 @@ struct ScanShape {
                        // buffer and mfma_scan_bytes of workspace)
 };
 // LDS plan of the scan kernel; returns false if the byte LUT and the
-// selection buffers do not fit.
+// selection buffers do not fit.  rck: residual codebook floats (RC * Kr),
+// which the pre-scan's re-check holds for its refine.
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
-               bool skew = false, bool mfma = false);
+               bool skew = false, bool mfma = false, int rck = 0);
 
 // Integer-MFMA pre-scan for one-bit digits (K1D = 2, Ds = 8, M a multiple of
 // 16 up to 128): per query the distances C + s * I(x) with I exact from int8
 // MFMA products over the batch's shared lists, then every candidate that the
 // error bound cannot exclude from the exact top-ck is re-checked with the
-// reference's arithmetic; partial[query's segment][ck] as scan_topck writes
-// it.  dump holds one u32 per candidate slot of the batch (dump_slots, a
-// multiple of 16, at least the sum of qtot times 16) and after them one per
-// 16 slots; ws (256-byte aligned) holds mfma_scan_bytes for this num_cu.
-// skew: the current lane-skewed copy of the codes (M % 32 == 0), or null; the
-// re-check reads members' codes from it when given.
-bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck);
+// reference's arithmetic, and the exact top-ck is refined in the same
+// workgroup as refine_topk refines a merged one: out_d / out_i [B][k] and
+// (optional) topck_dbg [B][ck] as refine_topk writes them.  dump holds one
+// u32 per candidate slot of the batch (dump_slots, a multiple of 16, at
+// least the sum of qtot times 16) and after them one per 16 slots; ws
+// (256-byte aligned) holds mfma_scan_bytes for this num_cu.  skew: the
+// current lane-skewed copy of the codes (M % 32 == 0), or null; the re-check
+// reads members' codes from it when given.  rck = RC * Kr.
+bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, int rck);
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
                      const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew, int ck,
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
-                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
+                     int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
+                     const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
+                     float* out_d, int32_t* out_i, unsigned long long* topck_dbg, int num_cu,
                      hipStream_t s);
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from

@@ -3308,9 +3308,9 @@ static size_t scan_wave_lds(int NT, int M, int d, int P, int ck, int K1D, int B,
 }
 
 static size_t mfma_plan_lds(int B, int P);
-static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B);
+static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B, int rck);
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
-               bool skew, bool mfma) {
+               bool skew, bool mfma, int rck) {
     out->mfma = 0;
     if (mfma) {
         // integer-MFMA pre-scan and one exact re-check per query: one
@@ -3323,7 +3323,7 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
         out->dump = 0;
         out->mfma = 1;
         out->nt = 1024;
-        out->lds = (int)mfma_recheck_lds(M, d, P, ck, K1D, B);
+        out->lds = (int)mfma_recheck_lds(M, d, P, ck, K1D, B, rck);
         out->region = (int)mfma_plan_lds(B, P);
         return true;
     }
@@ -3507,125 +3507,20 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
     return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------
-// Merge + residual refine + final top-k, one workgroup per query
-// (v14/search.cu:198-291 with the exact selection of jhq_v3_ivf).
-// The query's segment lists are merged by the streaming selection; the
-// residual distance of a candidate is summed by 16 lanes over 16 contiguous
-// dimension ranges, then added across the lanes in a fixed xor tree.
-// ---------------------------------------------------------------------------
+// Residual refine and final top-k of one query's exact short list (the
+// ksel keys in S.kout, ascending, with their pool slots in kslot):
+// topck_dbg (optional) gets the short list, out_d / out_i the k best by
+// (refined dist, id), (+inf, -1) past ksel.  Called by the whole workgroup;
+// cpos, cprim and fkeys are LDS scratch of ck entries, sq the query (one pad
+// word per 32), rc the residual codebooks.
 template <int NT>
-__global__ void __launch_bounds__(NT)
-refine_topk_kernel(const unsigned long long* __restrict__ partial,
-                   const int32_t* __restrict__ partial_slot, const int32_t* __restrict__ qtot,
-                   int B, int Gmax, int ck, int k, const float* __restrict__ q_rot, int d, int Ds,
-                   const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
-                   const int4* __restrict__ ldesc, int nlist, const uint8_t* __restrict__ list_res,
-                   const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
-                   float* __restrict__ out_d, int32_t* __restrict__ out_i,
-                   unsigned long long* __restrict__ topck_dbg, int stage_cap, int ov) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    StreamSel S;
-    unsigned char* p = stream_carve<NT>(smem, ck, &S);
-    unsigned long long* fkeys = (unsigned long long*)p;  // [ck] final-candidate keys
-    unsigned long long* stage = fkeys + ck;              // [stage_cap] segment lists
-    int* sslot = (int*)(stage + stage_cap);              // [stage_cap] their pool slots
-    int* kslot = sslot + stage_cap;                      // [ck] slots of the short list
-    float* rc = (float*)(kslot + ck);                    // [RC*Kr] residual codebooks
-    int* qpre = (int*)(rc + RC * Kr);
-    int* spre = qpre + B + 1;
-    int* cpos = spre + B + 1;
-    float* cprim = (float*)(cpos + ck);
-    int* wsum = (int*)(cprim + ck);
-    // query staged with one pad word per 32 so that lanes reading 32-dim
-    // ranges at a 32-word stride hit distinct banks
-    float* sq = (float*)(wsum + NT / 64);
-
-    const int b = blockIdx.x, tid = threadIdx.x;
-    JHQ_PHASE_DECL
-    work_plan<NT>(qtot, B, Gmax, ov, qpre, spre, wsum);
-    for (int i = tid; i < d; i += NT) sq[i + (i >> 5)] = q_rot[(int64_t)b * d + i];
-    for (int i = tid; i < RC * Kr; i += NT) rc[i] = res_c1d[i];
-    const int s0 = spre[b], s1 = spre[b + 1];
-    stream_begin<NT>(S);
-    __syncthreads();
-    JHQ_PHASE(0);
-
-    // merge the query's segment lists into the exact top-ck
-    const int nseg = s1 - s0;
-    const int nkeys = nseg * ck;
-    const unsigned long long* src = partial + (int64_t)s0 * ck;
-    int ksel;
-    if (nkeys <= stage_cap) {
-        // each list is sorted ascending (~0 padded): the rank of key x from
-        // list a at index i in the union is i + sum over the other lists of
-        // the number of keys below x (keys are distinct)
-        const int32_t* srcs = partial_slot + (int64_t)s0 * ck;
-        for (int i = tid; i < nkeys; i += NT) {
-            stage[i] = src[i];
-            sslot[i] = srcs[i];
-        }
-        if (tid == 0) S.ctl[0] = 0;
-        __syncthreads();
-        int nv = 0;
-        for (int i = tid; i < nkeys; i += NT) nv += stage[i] != ~0ull ? 1 : 0;
-        for (int off = 32; off > 0; off >>= 1) nv += __shfl_xor(nv, off);
-        if ((tid & 63) == 0 && nv) atomicAdd(&S.ctl[0], nv);
-        __syncthreads();
-        ksel = min(ck, S.ctl[0]);
-        for (int idx = tid; idx < nkeys; idx += NT) {
-            const unsigned long long x = stage[idx];
-            if (x == ~0ull) continue;
-            const int a = idx / ck;
-            int r = idx - a * ck;
-            for (int bl = 0; bl < nseg && r < ksel; bl++) {
-                if (bl == a) continue;
-                const unsigned long long* L = stage + bl * ck;
-                int lo = 0, hi = ck;  // first index with L[i] >= x
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (L[mid] < x) lo = mid + 1;
-                    else hi = mid;
-                }
-                r += lo;
-            }
-            if (r < ksel) {
-                S.kout[r] = x;
-                kslot[r] = sslot[idx];
-            }
-        }
-        __syncthreads();
-    } else {
-        // many segments: streaming selection, 4 keys per thread per round
-        const int rounds = (nkeys + NT * 4 - 1) / (NT * 4);
-        for (int r = 0; r < rounds; r++) {
-            uint32_t o[4], tg[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = r * NT * 4 + threadIdx.x * 4 + j;
-                const unsigned long long kk = i < nkeys ? src[i] : ~0ull;
-                o[j] = (uint32_t)(kk >> 32);
-                tg[j] = (uint32_t)(kk & 0xffffffffull);
-            }
-            stream_round<NT, 4>(S, ck, o, tg);
-        }
-        ksel = stream_end<NT>(S, ck);
-        // pool slots of the short list: the list whose canonical range holds
-        // the tag (binary search over the list descriptors)
-        for (int r = tid; r < ksel; r += NT) {
-            const int tag = (int)(uint32_t)(S.kout[r] & 0xffffffffull);
-            int lo = 0, hi = nlist - 1;  // last list with cbase <= tag
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (ldesc[mid].w <= tag) lo = mid;
-                else hi = mid - 1;
-            }
-            const int4 L = ldesc[lo];
-            kslot[r] = L.x + (tag - L.w);
-        }
-        __syncthreads();
-    }
-    JHQ_PHASE(1);
+__device__ __forceinline__ void refine_short_list(
+    StreamSel& S, int ksel, int ck, int k, int b, const int* kslot, int* cpos, float* cprim,
+    unsigned long long* fkeys, const float* sq, const float* rc, int d, int Ds, int Kr, int RC,
+    int Br, int bpv, const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
+    const int32_t* __restrict__ list_ids, float* __restrict__ out_d, int32_t* __restrict__ out_i,
+    unsigned long long* __restrict__ topck_dbg) {
+    const int tid = threadIdx.x;
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
             const unsigned long long kk = S.kout[r];
@@ -3779,7 +3674,6 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
         }
     }
     __syncthreads();
-    JHQ_PHASE(2);
 
     // final top-k by (dist, id)
     const int kf = ksel < k ? ksel : k;
@@ -3794,6 +3688,129 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
             out_i[(int64_t)b * k + r] = -1;
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Merge + residual refine + final top-k, one workgroup per query
+// (v14/search.cu:198-291 with the exact selection of jhq_v3_ivf).
+// The query's segment lists are merged by the streaming selection; the
+// residual distance of a candidate is summed by 16 lanes over 16 contiguous
+// dimension ranges, then added across the lanes in a fixed xor tree.
+// ---------------------------------------------------------------------------
+template <int NT>
+__global__ void __launch_bounds__(NT)
+refine_topk_kernel(const unsigned long long* __restrict__ partial,
+                   const int32_t* __restrict__ partial_slot, const int32_t* __restrict__ qtot,
+                   int B, int Gmax, int ck, int k, const float* __restrict__ q_rot, int d, int Ds,
+                   const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
+                   const int4* __restrict__ ldesc, int nlist, const uint8_t* __restrict__ list_res,
+                   const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
+                   float* __restrict__ out_d, int32_t* __restrict__ out_i,
+                   unsigned long long* __restrict__ topck_dbg, int stage_cap, int ov) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    StreamSel S;
+    unsigned char* p = stream_carve<NT>(smem, ck, &S);
+    unsigned long long* fkeys = (unsigned long long*)p;  // [ck] final-candidate keys
+    unsigned long long* stage = fkeys + ck;              // [stage_cap] segment lists
+    int* sslot = (int*)(stage + stage_cap);              // [stage_cap] their pool slots
+    int* kslot = sslot + stage_cap;                      // [ck] slots of the short list
+    float* rc = (float*)(kslot + ck);                    // [RC*Kr] residual codebooks
+    int* qpre = (int*)(rc + RC * Kr);
+    int* spre = qpre + B + 1;
+    int* cpos = spre + B + 1;
+    float* cprim = (float*)(cpos + ck);
+    int* wsum = (int*)(cprim + ck);
+    // query staged with one pad word per 32 so that lanes reading 32-dim
+    // ranges at a 32-word stride hit distinct banks
+    float* sq = (float*)(wsum + NT / 64);
+
+    const int b = blockIdx.x, tid = threadIdx.x;
+    JHQ_PHASE_DECL
+    work_plan<NT>(qtot, B, Gmax, ov, qpre, spre, wsum);
+    for (int i = tid; i < d; i += NT) sq[i + (i >> 5)] = q_rot[(int64_t)b * d + i];
+    for (int i = tid; i < RC * Kr; i += NT) rc[i] = res_c1d[i];
+    const int s0 = spre[b], s1 = spre[b + 1];
+    stream_begin<NT>(S);
+    __syncthreads();
+    JHQ_PHASE(0);
+
+    // merge the query's segment lists into the exact top-ck
+    const int nseg = s1 - s0;
+    const int nkeys = nseg * ck;
+    const unsigned long long* src = partial + (int64_t)s0 * ck;
+    int ksel;
+    if (nkeys <= stage_cap) {
+        // each list is sorted ascending (~0 padded): the rank of key x from
+        // list a at index i in the union is i + sum over the other lists of
+        // the number of keys below x (keys are distinct)
+        const int32_t* srcs = partial_slot + (int64_t)s0 * ck;
+        for (int i = tid; i < nkeys; i += NT) {
+            stage[i] = src[i];
+            sslot[i] = srcs[i];
+        }
+        if (tid == 0) S.ctl[0] = 0;
+        __syncthreads();
+        int nv = 0;
+        for (int i = tid; i < nkeys; i += NT) nv += stage[i] != ~0ull ? 1 : 0;
+        for (int off = 32; off > 0; off >>= 1) nv += __shfl_xor(nv, off);
+        if ((tid & 63) == 0 && nv) atomicAdd(&S.ctl[0], nv);
+        __syncthreads();
+        ksel = min(ck, S.ctl[0]);
+        for (int idx = tid; idx < nkeys; idx += NT) {
+            const unsigned long long x = stage[idx];
+            if (x == ~0ull) continue;
+            const int a = idx / ck;
+            int r = idx - a * ck;
+            for (int bl = 0; bl < nseg && r < ksel; bl++) {
+                if (bl == a) continue;
+                const unsigned long long* L = stage + bl * ck;
+                int lo = 0, hi = ck;  // first index with L[i] >= x
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (L[mid] < x) lo = mid + 1;
+                    else hi = mid;
+                }
+                r += lo;
+            }
+            if (r < ksel) {
+                S.kout[r] = x;
+                kslot[r] = sslot[idx];
+            }
+        }
+        __syncthreads();
+    } else {
+        // many segments: streaming selection, 4 keys per thread per round
+        const int rounds = (nkeys + NT * 4 - 1) / (NT * 4);
+        for (int r = 0; r < rounds; r++) {
+            uint32_t o[4], tg[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = r * NT * 4 + threadIdx.x * 4 + j;
+                const unsigned long long kk = i < nkeys ? src[i] : ~0ull;
+                o[j] = (uint32_t)(kk >> 32);
+                tg[j] = (uint32_t)(kk & 0xffffffffull);
+            }
+            stream_round<NT, 4>(S, ck, o, tg);
+        }
+        ksel = stream_end<NT>(S, ck);
+        // pool slots of the short list: the list whose canonical range holds
+        // the tag (binary search over the list descriptors)
+        for (int r = tid; r < ksel; r += NT) {
+            const int tag = (int)(uint32_t)(S.kout[r] & 0xffffffffull);
+            int lo = 0, hi = nlist - 1;  // last list with cbase <= tag
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (ldesc[mid].w <= tag) lo = mid;
+                else hi = mid - 1;
+            }
+            const int4 L = ldesc[lo];
+            kslot[r] = L.x + (tag - L.w);
+        }
+        __syncthreads();
+    }
+    JHQ_PHASE(1);
+    refine_short_list<NT>(S, ksel, ck, k, b, kslot, cpos, cprim, fkeys, sq, rc, d, Ds, Kr, RC, Br,
+                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg);
     JHQ_PHASE(3);
     JHQ_PHASE_FLUSH(2);
 }
@@ -4320,12 +4337,25 @@ __device__ uint32_t block_radix_kth(Get get, int n, int k, int* hist, int* c2) {
     return pre;
 }
 
+// Words of the re-check's entry buffer: its [kRecheckCHM][M + 1] entries, or
+// more when the refine's short-list arrays (keys, slots, positions and
+// primary distances of ck candidates), residual codebooks (rck floats) and
+// padded query, which take the place of the survivor buffers and the entry
+// buffer once the short list is selected, need the room.
+__host__ __device__ inline int recheck_ebuf_words(int M, int ck, int rck, int d) {
+    const int refine = 5 * ck + rck + d + d / 32 + 1;   // words, keys counted twice
+    const int spare = kRecheckCap * 4;                   // surv, mp and mc, in words
+    const int own = kRecheckCHM * (M + 1);
+    return refine - spare > own ? refine - spare : own;
+}
+
 // One workgroup per query: the ck-th smallest of the query's tile minima
 // (written by the scan) bounds the members, one pass over the query's I
 // values collects the candidates that can be members, the ck-th smallest I
 // among them tightens the bound, the members' distances are recomputed in
 // the reference's order, and the exact top-ck by (dist, position) goes to
-// partial[segment][ck] (one segment per query).
+// short list is refined in place (refine_short_list, as refine_topk_kernel
+// refines a merged one): out_d / out_i get the query's k best.
 template <int NT>
 __global__ void __launch_bounds__(NT)
 mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restrict__ tmin,
@@ -4334,8 +4364,10 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                     const int32_t* __restrict__ gofs, int P, const int4* __restrict__ ldesc,
                     const uint8_t* __restrict__ codes_t, const uint8_t* __restrict__ skew, int ck,
-                    unsigned long long* __restrict__ partial,
-                    int32_t* __restrict__ partial_slot) {
+                    int k, const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
+                    const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
+                    const int32_t* __restrict__ list_ids, float* __restrict__ out_d,
+                    int32_t* __restrict__ out_i, unsigned long long* __restrict__ topck_dbg) {
     constexpr int NW = NT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
@@ -4343,8 +4375,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     unsigned long long* surv = (unsigned long long*)p0;        // [kRecheckCap]
     int* mp = (int*)(surv + kRecheckCap);                      // [kRecheckCap] member probe
     int* mc = mp + kRecheckCap;                                // [kRecheckCap] member column
-    float* ebuf = (float*)(mc + kRecheckCap);                  // [CHM][M + 1]
-    float* sq = ebuf + kRecheckCHM * (M + 1);                  // [d]
+    float* ebuf = (float*)(mc + kRecheckCap);                  // [CHM][M + 1] (or more)
+    float* sq = ebuf + recheck_ebuf_words(M, ck, RC * Kr, d);  // [d]
     float* sc1d = sq + d;                                      // [K1D]
     int* meta = (int*)(sc1d + K1D);                            // [P][4]
     int* sg = meta + 4 * P;                                    // [P + 1]
@@ -4354,8 +4386,16 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     const unsigned long long lt = (1ull << lane) - 1ull;
     JHQ_PHASE_DECL
     const int4 qi = qinfo[b];
-    if (qi.z == 0) return;  // no candidates: refine sees no segment
-    const int s0 = qi.y;
+    if (qi.z == 0) {
+        // no candidates: no neighbours
+        for (int r = tid; r < k; r += NT) {
+            out_d[(int64_t)b * k + r] = __builtin_huge_valf();
+            out_i[(int64_t)b * k + r] = -1;
+        }
+        if (topck_dbg)
+            for (int r = tid; r < ck; r += NT) topck_dbg[(int64_t)b * ck + r] = ~0ull;
+        return;
+    }
     // the query, codebook and probe table are requested now and stored in
     // LDS after pass 1, whose loads do not wait for them (d <= NT, P < NT)
     const float qv = tid < d ? q_rot[(int64_t)b * d + tid] : 0.0f;
@@ -4611,17 +4651,28 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         kk = stream_end<NT>(S, ck);
     }
     __syncthreads();
-    for (int i = tid; i < ck; i += NT) {
+    // the refine's arrays replace the survivor and entry buffers: pool slots
+    // of the short list (the probe whose canonical range holds the tag), the
+    // residual codebooks, the query with one pad word per 32
+    unsigned long long* fkeys = (unsigned long long*)p0;
+    int* kslot = (int*)(fkeys + ck);
+    int* cpos = kslot + ck;
+    float* cprim = (float*)(cpos + ck);
+    float* rcb = cprim + ck;
+    float* sqp = rcb + RC * Kr;
+    for (int i = tid; i < kk; i += NT) {
+        const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
         int32_t slot = -1;
-        if (i < kk) {
-            const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
-            for (int q = 0; q < P; q++)
-                if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
-                    slot = meta[4 * q] + (tag - meta[4 * q + 3]);
-        }
-        partial[(int64_t)s0 * ck + i] = i < kk ? S.kout[i] : ~0ull;
-        partial_slot[(int64_t)s0 * ck + i] = slot;
+        for (int q = 0; q < P; q++)
+            if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
+                slot = meta[4 * q] + (tag - meta[4 * q + 3]);
+        kslot[i] = slot;
     }
+    for (int i = tid; i < RC * Kr; i += NT) rcb[i] = res_c1d[i];
+    for (int i = tid; i < d; i += NT) sqp[i + (i >> 5)] = sq[i];
+    __syncthreads();
+    refine_short_list<NT>(S, kk, ck, k, b, kslot, cpos, cprim, fkeys, sqp, rcb, d, Ds, Kr, RC, Br,
+                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg);
     JHQ_PHASE(0);
     JHQ_PHASE_FLUSH(3);
 }
@@ -4633,18 +4684,18 @@ static size_t mfma_plan_lds(int B, int P) {
     return std::max(work, quant);
 }
 
-static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B) {
+static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B, int rck) {
     return stream_lds_bytes(kRecheckNT, ck) + (size_t)kRecheckCap * (8 + 4 + 4) +
-           (size_t)kRecheckCHM * (M + 1) * 4 + (size_t)d * 4 + (size_t)K1D * 4 +
+           (size_t)recheck_ebuf_words(M, ck, rck, d) * 4 + (size_t)d * 4 + (size_t)K1D * 4 +
            (size_t)(4 * P + P + 1) * 4 + (kRecheckNT / 64) * 4 + 16 + 64;
 }
 
-bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck) {
+bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, int rck) {
     if (K1D != 2 || bpd != 1 || Ds != 8 || d != 8 * M) return false;
     if (M % 16 != 0 || M < 16 || M > 128 || d > kRecheckNT || P >= kRecheckNT) return false;
     if (B < 1 || P < 1 || (int64_t)B * P > kMfmaMaxBP || ck < 1 || ck > kRecheckCap) return false;
     return mfma_plan_lds(B, P) <= (size_t)kLdsBytes - 1024 &&
-           mfma_recheck_lds(M, d, P, ck, K1D, B) <= (size_t)kLdsBytes - 1024;
+           mfma_recheck_lds(M, d, P, ck, K1D, B, rck) <= (size_t)kLdsBytes - 1024;
 }
 
 static int mfma_scan_waves(int num_cu) { return std::max(1, num_cu) * kMfmaWavesPerCU; }
@@ -4657,10 +4708,12 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
                      const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew, int ck,
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
-                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
+                     int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
+                     const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
+                     float* out_d, int32_t* out_i, unsigned long long* topck_dbg, int num_cu,
                      hipStream_t s) {
-    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck) || !ws || ((uintptr_t)ws & 255) || !dump ||
-        dump_slots % 16 != 0 || (skew && M % 32 != 0))
+    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck, RC * Kr) || !ws || ((uintptr_t)ws & 255) ||
+        !dump || dump_slots % 16 != 0 || (skew && M % 32 != 0) || k < 1 || k > ck)
         return hipErrorInvalidValue;
     // tile minima after the candidate slots
     uint32_t* tmin = dump + dump_slots;
@@ -4679,12 +4732,13 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
           : M == 80 ? mfma_scan_kernel<80> : M == 96 ? mfma_scan_kernel<96>
           : M == 112 ? mfma_scan_kernel<112> : mfma_scan_kernel<128>;
     hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, codes_t, dump, tmin);
-    const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B);
+    const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B, RC * Kr);
     static const int mxr = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT>);
     if ((int)lr > mxr) return hipErrorInvalidValue;
     hipLaunchKernelGGL(mfma_recheck_kernel<kRecheckNT>, dim3(B), dim3(kRecheckNT), lr, s, dump,
                        tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes, gofs, P, ldesc,
-                       codes_t, skew, ck, partial, partial_slot);
+                       codes_t, skew, ck, k, res_c1d, Kr, RC, Br, bpv, list_res, list_corr,
+                       list_ids, out_d, out_i, topck_dbg);
     return hipGetLastError();
 }
 
