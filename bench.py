@@ -504,7 +504,9 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
     """The scan's roofline figures at the current operating point.
 
     achieved = algorithmic code bytes per launch (sum over the batch's queries
-    of probed list sizes x M) / the scan's HIP-event time per launch; also the
+    of probed list sizes x M; for the pre-scan, whose re-check refines the
+    short lists in place, plus the refine's bytes) / the scan's HIP-event time
+    per launch; also the
     scan + refine figure (codes + ck * (bpv + 4 + 4) per query over both
     kernels' time) and, when a committed counter run matches this operating
     point, the HBM traffic per launch and the measured limiter."""
@@ -515,12 +517,16 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
     nb = (nq + batch - 1) // batch
     per_launch = float(sizes[dbg["probes"]].sum()) * ix.params.M / nb
     us = step_us["scan_topck"]
-    ach = per_launch / (us * 1e-6) / 1e9
     kernel, ck = ix.scan_plan(k)
     bpv = ix.dims()["bpv"]
     # refine reads ck residual codes + correction + id per query
     refine_bytes = float(nq) / nb * ck * (bpv + 4 + 4)
-    sr_us = us + step_us["refine_topk"]
+    # the pre-scan's re-check refines its short lists in place: its scan step
+    # holds the refine's bytes and time (the refine step is empty)
+    fused = kernel == "mfma_scan_kernel"
+    step_bytes = per_launch + (refine_bytes if fused else 0.0)
+    ach = step_bytes / (us * 1e-6) / 1e9
+    sr_us = us + (0.0 if fused else step_us["refine_topk"])
     sr_ach = (per_launch + refine_bytes) / (sr_us * 1e-6) / 1e9
     traffic, traffic_note, limiter = None, "no counter run at this operating point", None
     pdir = os.path.join(ROOT, "profiles")
@@ -537,7 +543,8 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
                             % (tj["source"], tj["fetch_scale"], tj["write_scale"]))
             limiter = tj.get("limiter")
     names = {"scan_dump_kernel": "scan_dump_kernel + select_query_kernel",
-             "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel"}
+             "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel "
+                                 "(re-check and refine)"}
     extra = {}
     if kernel == "mfma_scan_kernel":
         # the pre-scan's integer products: per batch, each probed list's
@@ -570,7 +577,7 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
         "traffic": traffic,
         "traffic_note": traffic_note,
         "measured_limiter": limiter,
-        "algorithmic_bytes_per_launch": int(per_launch),
+        "algorithmic_bytes_per_launch": int(step_bytes),
         "avg_launch_us": round(us, 2),
         "scan_plus_refine": {
             "bytes_per_batch": int(per_launch + refine_bytes),
