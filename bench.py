@@ -521,9 +521,10 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
     bpv = ix.dims()["bpv"]
     # refine reads ck residual codes + correction + id per query
     refine_bytes = float(nq) / nb * ck * (bpv + 4 + 4)
-    # the pre-scan's re-check refines its short lists in place: its scan step
-    # holds the refine's bytes and time (the refine step is empty)
-    fused = kernel == "mfma_scan_kernel"
+    # the pre-scan's re-check refines short lists (ck <= 128) in place: its
+    # scan step then holds the refine's bytes and time (the refine step is
+    # empty)
+    fused = kernel == "mfma_scan_kernel" and ck <= 128
     step_bytes = per_launch + (refine_bytes if fused else 0.0)
     ach = step_bytes / (us * 1e-6) / 1e9
     sr_us = us + (0.0 if fused else step_us["refine_topk"])
@@ -543,8 +544,8 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
                             % (tj["source"], tj["fetch_scale"], tj["write_scale"]))
             limiter = tj.get("limiter")
     names = {"scan_dump_kernel": "scan_dump_kernel + select_query_kernel",
-             "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel "
-                                 "(re-check and refine)"}
+             "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel"
+                                 + (" (re-check and refine)" if fused else "")}
     extra = {}
     if kernel == "mfma_scan_kernel":
         # the pre-scan's integer products: per batch, each probed list's

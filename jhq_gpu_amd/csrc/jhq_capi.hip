@@ -617,7 +617,7 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
                                w.wgofs.p, w.wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     if (bp.sh.mfma) {
-        // the re-check refines each query's short list itself
+        // the re-check refines short short lists itself
         JHQ_HIP(jhq::mfma_scan(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                ix->dcodes_t.p,
@@ -626,8 +626,15 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
                                static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
                                w.wmfma.p, w.wmfma.n, k, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
                                ix->bpv, ix->dres.p, ix->dcorr.p, ix->dlist_ids.p, d_out, d_ids,
-                               want_topck ? w.wtopck.p : nullptr, ix->num_cu, s));
+                               want_topck ? w.wtopck.p : nullptr, w.wpartial.p, w.wpslot.p,
+                               ix->num_cu, s));
         if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
+        if (!jhq::mfma_fuses_refine(bp.ck))
+            JHQ_HIP(jhq::refine_topk(w.wpartial.p, w.wpslot.p, w.wqtot.p, Bq, bp.sh, bp.ck, k,
+                                     w.wqrot.p, d, ix->Ds, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
+                                     ix->bpv, ix->dldesc.p, ix->nlist, ix->dres.p, ix->dcorr.p,
+                                     ix->dlist_ids.p, d_out, d_ids,
+                                     want_topck ? w.wtopck.p : nullptr, s));
     } else {
         JHQ_HIP(jhq::scan_topck(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                 w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,

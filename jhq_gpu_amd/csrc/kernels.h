@@ -173,15 +173,18 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 // 16 up to 128): per query the distances C + s * I(x) with I exact from int8
 // MFMA products over the batch's shared lists, then every candidate that the
 // error bound cannot exclude from the exact top-ck is re-checked with the
-// reference's arithmetic, and the exact top-ck is refined in the same
-// workgroup as refine_topk refines a merged one: out_d / out_i [B][k] and
-// (optional) topck_dbg [B][ck] as refine_topk writes them.  dump holds one
+// reference's arithmetic.  When mfma_fuses_refine(ck), the exact top-ck is
+// refined in the same workgroup as refine_topk refines a merged one: out_d /
+// out_i [B][k] and (optional) topck_dbg [B][ck] as refine_topk writes them;
+// otherwise it goes to partial[query's segment][ck] (one segment per query)
+// and the caller runs refine_topk.  dump holds one
 // u32 per candidate slot of the batch (dump_slots, a multiple of 16, at
 // least the sum of qtot times 16) and after them one per 16 slots; ws
 // (256-byte aligned) holds mfma_scan_bytes for this num_cu.  skew: the
 // current lane-skewed copy of the codes (M % 32 == 0), or null; the re-check
 // reads members' codes from it when given.  rck = RC * Kr.
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, int rck);
+bool mfma_fuses_refine(int ck);
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
@@ -189,7 +192,8 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
-                     float* out_d, int32_t* out_i, unsigned long long* topck_dbg, int num_cu,
+                     float* out_d, int32_t* out_i, unsigned long long* topck_dbg,
+                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
                      hipStream_t s);
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from

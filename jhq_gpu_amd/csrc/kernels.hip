@@ -3863,7 +3863,15 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
 // Queries with non-finite or huge values re-check every candidate.
 // ---------------------------------------------------------------------------
 constexpr int kMfmaPlanNT = 1024;
-constexpr int kMfmaWavesPerCU = 8;  // scan waves: two 4-wave workgroups per CU
+// Tile-kernel waves per CU: one 4-wave workgroup.  The waves are bound by
+// issue and by their start-up load chain, and with the CU's other slots free
+// the other pipeline lane's kernels run beside them (config 2: 886 k queries/s
+// against 847 k with two workgroups per CU, 859 k with three waves, 790 k
+// with two).
+#ifndef JHQ_MFMA_WPC
+#define JHQ_MFMA_WPC 4
+#endif
+constexpr int kMfmaWavesPerCU = JHQ_MFMA_WPC;
 constexpr int kRecheckNT = 1024;
 constexpr int kRecheckCap = 2048;   // survivors / members held in LDS
 constexpr int kRecheckCHM = 128;    // members per exact-distance round
@@ -4015,6 +4023,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     int* htl = hg + H + 1;      // [H + 1] tile prefix
     int* qpre = htl + H + 1;    // [B + 1]
     int* wsum = qpre + B + 1;   // [NT / 64]
+    JHQ_PHASE_DECL
     for (int i = tid; i < H; i += NT) {
         hk[i] = -1;
         hc[i] = 0;
@@ -4039,6 +4048,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
         ps[i] = h;
     }
     __syncthreads();
+    JHQ_PHASE(0);
     // slot h holds ceil(hc / 16) groups of ceil(size / 16) tiles each
     auto ntl = [&](int h) { return (ldesc[hk[h]].z + kGroup - 1) / kGroup; };
     block_exclusive_scan<NT>([&](int h) { return hk[h] >= 0 ? (hc[h] + 15) / 16 : 0; }, H, hg,
@@ -4046,6 +4056,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     block_exclusive_scan<NT>(
         [&](int h) { return hk[h] >= 0 ? ((hc[h] + 15) / 16) * ntl(h) : 0; }, H, htl, wsum);
     const int T = htl[H];
+    JHQ_PHASE(1);
     for (int h = tid; h < H; h += NT) {
         if (hk[h] < 0) continue;
         const int4 L = ldesc[hk[h]];
@@ -4060,6 +4071,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
         w.gq[(hg[ps[i]] + pr[i] / 16) * 16 + (pr[i] & 15)] =
             make_int2(b, (qpre[b] + gofs[(int64_t)b * (P + 1) + p]) * kGroup);
     }
+    JHQ_PHASE(2);
     // wave v starts at tile a = v T / W: in slot h with htl[h] <= a <
     // htl[h + 1] (the largest h with htl[h] <= a is occupied when a < T)
     for (int v = tid; v < nwaves; v += NT) {
@@ -4077,6 +4089,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
         }
         w.wstart[v] = st;
     }
+    JHQ_PHASE(3);
     if (tid == 0) {
         w.ctl[0] = T;
         w.ctl[1] = hg[H];
@@ -4087,6 +4100,8 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
             seg += nt > 0 ? 1 : 0;
         }
     }
+    JHQ_PHASE(4);
+    JHQ_PHASE_FLUSH(2);
 }
 
 constexpr int kMfmaPD = 4;  // tiles in flight per wave
@@ -4342,21 +4357,29 @@ __device__ uint32_t block_radix_kth(Get get, int n, int k, int* hist, int* c2) {
 // primary distances of ck candidates), residual codebooks (rck floats) and
 // padded query, which take the place of the survivor buffers and the entry
 // buffer once the short list is selected, need the room.
-__host__ __device__ inline int recheck_ebuf_words(int M, int ck, int rck, int d) {
+__host__ __device__ inline int recheck_ebuf_words(int M, int ck, int rck, int d, bool fuse) {
     const int refine = 5 * ck + rck + d + d / 32 + 1;   // words, keys counted twice
     const int spare = kRecheckCap * 4;                   // surv, mp and mc, in words
     const int own = kRecheckCHM * (M + 1);
-    return refine - spare > own ? refine - spare : own;
+    return fuse && refine - spare > own ? refine - spare : own;
 }
+
+// Short lists up to this length are refined inside the re-check; longer ones
+// go to refine_topk_kernel (config 2, ck 100: 847 k queries/s with the refine
+// inside against 827 k; config 5, ck 400: 193 k with it against 217 k).
+constexpr int kMfmaFuseMaxCk = 128;
+bool mfma_fuses_refine(int ck) { return ck <= kMfmaFuseMaxCk; }
 
 // One workgroup per query: the ck-th smallest of the query's tile minima
 // (written by the scan) bounds the members, one pass over the query's I
 // values collects the candidates that can be members, the ck-th smallest I
 // among them tightens the bound, the members' distances are recomputed in
-// the reference's order, and the exact top-ck by (dist, position) goes to
-// short list is refined in place (refine_short_list, as refine_topk_kernel
-// refines a merged one): out_d / out_i get the query's k best.
-template <int NT>
+// the reference's order, and the exact top-ck by (dist, position) is
+// selected.  FUSE: the short list is refined in place (refine_short_list, as
+// refine_topk_kernel refines a merged one) and out_d / out_i get the query's
+// k best; else it goes to partial[segment][ck] (one segment per query) for
+// refine_topk_kernel.
+template <int NT, bool FUSE>
 __global__ void __launch_bounds__(NT)
 mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restrict__ tmin,
                     const MfmaQS* __restrict__ qs, const int4* __restrict__ qinfo,
@@ -4367,7 +4390,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     int k, const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
                     const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
                     const int32_t* __restrict__ list_ids, float* __restrict__ out_d,
-                    int32_t* __restrict__ out_i, unsigned long long* __restrict__ topck_dbg) {
+                    int32_t* __restrict__ out_i, unsigned long long* __restrict__ topck_dbg,
+                    unsigned long long* __restrict__ partial,
+                    int32_t* __restrict__ partial_slot) {
     constexpr int NW = NT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
@@ -4376,7 +4401,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     int* mp = (int*)(surv + kRecheckCap);                      // [kRecheckCap] member probe
     int* mc = mp + kRecheckCap;                                // [kRecheckCap] member column
     float* ebuf = (float*)(mc + kRecheckCap);                  // [CHM][M + 1] (or more)
-    float* sq = ebuf + recheck_ebuf_words(M, ck, RC * Kr, d);  // [d]
+    float* sq = ebuf + recheck_ebuf_words(M, ck, RC * Kr, d, FUSE);  // [d]
     float* sc1d = sq + d;                                      // [K1D]
     int* meta = (int*)(sc1d + K1D);                            // [P][4]
     int* sg = meta + 4 * P;                                    // [P + 1]
@@ -4387,7 +4412,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     JHQ_PHASE_DECL
     const int4 qi = qinfo[b];
     if (qi.z == 0) {
-        // no candidates: no neighbours
+        // no candidates: no neighbours (without FUSE, refine sees no segment)
+        if (!FUSE) return;
         for (int r = tid; r < k; r += NT) {
             out_d[(int64_t)b * k + r] = __builtin_huge_valf();
             out_i[(int64_t)b * k + r] = -1;
@@ -4651,6 +4677,24 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         kk = stream_end<NT>(S, ck);
     }
     __syncthreads();
+    if (!FUSE) {
+        // the short list and its pool slots (the probe whose canonical
+        // range holds the tag) as the query's one segment
+        for (int i = tid; i < ck; i += NT) {
+            int32_t slot = -1;
+            if (i < kk) {
+                const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
+                for (int q = 0; q < P; q++)
+                    if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
+                        slot = meta[4 * q] + (tag - meta[4 * q + 3]);
+            }
+            partial[(int64_t)qi.y * ck + i] = i < kk ? S.kout[i] : ~0ull;
+            partial_slot[(int64_t)qi.y * ck + i] = slot;
+        }
+        JHQ_PHASE(0);
+        JHQ_PHASE_FLUSH(3);
+        return;
+    }
     // the refine's arrays replace the survivor and entry buffers: pool slots
     // of the short list (the probe whose canonical range holds the tag), the
     // residual codebooks, the query with one pad word per 32
@@ -4686,7 +4730,8 @@ static size_t mfma_plan_lds(int B, int P) {
 
 static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B, int rck) {
     return stream_lds_bytes(kRecheckNT, ck) + (size_t)kRecheckCap * (8 + 4 + 4) +
-           (size_t)recheck_ebuf_words(M, ck, rck, d) * 4 + (size_t)d * 4 + (size_t)K1D * 4 +
+           (size_t)recheck_ebuf_words(M, ck, rck, d, mfma_fuses_refine(ck)) * 4 +
+           (size_t)d * 4 + (size_t)K1D * 4 +
            (size_t)(4 * P + P + 1) * 4 + (kRecheckNT / 64) * 4 + 16 + 64;
 }
 
@@ -4710,10 +4755,13 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
-                     float* out_d, int32_t* out_i, unsigned long long* topck_dbg, int num_cu,
+                     float* out_d, int32_t* out_i, unsigned long long* topck_dbg,
+                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
                      hipStream_t s) {
+    const bool fuse = mfma_fuses_refine(ck);
     if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck, RC * Kr) || !ws || ((uintptr_t)ws & 255) ||
-        !dump || dump_slots % 16 != 0 || (skew && M % 32 != 0) || k < 1 || k > ck)
+        !dump || dump_slots % 16 != 0 || (skew && M % 32 != 0) || k < 1 || k > ck ||
+        (!fuse && (!partial || !partial_slot)))
         return hipErrorInvalidValue;
     // tile minima after the candidate slots
     uint32_t* tmin = dump + dump_slots;
@@ -4733,12 +4781,21 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
           : M == 112 ? mfma_scan_kernel<112> : mfma_scan_kernel<128>;
     hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, codes_t, dump, tmin);
     const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B, RC * Kr);
-    static const int mxr = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT>);
-    if ((int)lr > mxr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mfma_recheck_kernel<kRecheckNT>, dim3(B), dim3(kRecheckNT), lr, s, dump,
-                       tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes, gofs, P, ldesc,
-                       codes_t, skew, ck, k, res_c1d, Kr, RC, Br, bpv, list_res, list_corr,
-                       list_ids, out_d, out_i, topck_dbg);
+    static const int mxf = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT, true>);
+    static const int mxs = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT, false>);
+    if ((int)lr > (fuse ? mxf : mxs)) return hipErrorInvalidValue;
+    if (fuse)
+        hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, true>), dim3(B), dim3(kRecheckNT), lr,
+                           s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
+                           gofs, P, ldesc, codes_t, skew, ck, k, res_c1d, Kr, RC, Br, bpv,
+                           list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
+                           partial_slot);
+    else
+        hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, false>), dim3(B), dim3(kRecheckNT), lr,
+                           s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
+                           gofs, P, ldesc, codes_t, skew, ck, k, res_c1d, Kr, RC, Br, bpv,
+                           list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
+                           partial_slot);
     return hipGetLastError();
 }
 
