@@ -1722,7 +1722,7 @@ __device__ __forceinline__ int wg_of_group(int64_t x, int64_t T, int G) {
 
 // Exclusive prefix over B values f(b) into out[0..B] (out[B] = total).
 template <int NT, class F>
-__device__ void block_exclusive_scan(F f, int B, int* out, int* wsum) {
+__device__ __forceinline__ void block_exclusive_scan(F f, int B, int* out, int* wsum) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int per = (B + NT - 1) / NT;
     const int s0 = min(B, tid * per), s1 = min(B, s0 + per);
@@ -4023,6 +4023,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     int* htl = hg + H + 1;      // [H + 1] tile prefix
     int* qpre = htl + H + 1;    // [B + 1]
     int* wsum = qpre + B + 1;   // [NT / 64]
+    int* hz = wsum + NT / 64;   // [H] list size of the slot
     JHQ_PHASE_DECL
     for (int i = tid; i < H; i += NT) {
         hk[i] = -1;
@@ -4037,10 +4038,12 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
         pr[i] = 0;
         if (e >= BP) continue;
         const int l = probes[e];
-        if (ldesc[l].z == 0) continue;  // empty list: no slots
+        const int sz = ldesc[l].z;
+        if (sz == 0) continue;  // empty list: no slots
         int h = (int)(((uint64_t)((uint32_t)l * 2654435761u) * (uint32_t)H) >> 32);
         for (;;) {
             const int old = atomicCAS(&hk[h], -1, l);
+            if (old == -1) hz[h] = sz;  // the slot's first pair records the size
             if (old == -1 || old == l) break;
             h = h + 1 == H ? 0 : h + 1;
         }
@@ -4050,7 +4053,7 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     __syncthreads();
     JHQ_PHASE(0);
     // slot h holds ceil(hc / 16) groups of ceil(size / 16) tiles each
-    auto ntl = [&](int h) { return (ldesc[hk[h]].z + kGroup - 1) / kGroup; };
+    auto ntl = [&](int h) { return (hz[h] + kGroup - 1) / kGroup; };
     block_exclusive_scan<NT>([&](int h) { return hk[h] >= 0 ? (hc[h] + 15) / 16 : 0; }, H, hg,
                              wsum);
     block_exclusive_scan<NT>(
@@ -4090,16 +4093,16 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
         w.wstart[v] = st;
     }
     JHQ_PHASE(3);
+    // segment of query b: the queries before it that have candidates (a
+    // prefix into hc, whose counts are no longer read)
     if (tid == 0) {
         w.ctl[0] = T;
         w.ctl[1] = hg[H];
-        int seg = 0;
-        for (int b = 0; b < B; b++) {
-            const int nt = qpre[b + 1] - qpre[b];
-            w.qinfo[b] = make_int4(qpre[b] * kGroup, seg, nt, 0);
-            seg += nt > 0 ? 1 : 0;
-        }
     }
+    __syncthreads();
+    block_exclusive_scan<NT>([&](int b) { return qpre[b + 1] > qpre[b] ? 1 : 0; }, B, hc, wsum);
+    for (int b = tid; b < B; b += NT)
+        w.qinfo[b] = make_int4(qpre[b] * kGroup, hc[b], qpre[b + 1] - qpre[b], 0);
     JHQ_PHASE(4);
     JHQ_PHASE_FLUSH(2);
 }
@@ -4725,7 +4728,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
 
 static size_t mfma_plan_lds(int B, int P) {
     const int H = mfma_hash_size(B * P);
-    const size_t work = (size_t)(4 * (H + 1) + B + 1 + kMfmaPlanNT / 64) * 4 + 64;
+    const size_t work = (size_t)(5 * H + 4 + B + 1 + kMfmaPlanNT / 64) * 4 + 64;
     const size_t quant = (size_t)3 * (kMfmaPlanNT / 64) * 8 + 64;
     return std::max(work, quant);
 }
