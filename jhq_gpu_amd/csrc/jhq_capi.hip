@@ -405,17 +405,18 @@ bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128
 
 // The pre-scan computes 16-query tiles over every probed list; it pays off
 // when the queries of a batch share their lists so that the tiles are mostly
-// full, when the byte-LUT scan's work per candidate (M lookups) is large
+// full, and when the byte-LUT scan's work per candidate (M gathers) is large
 // against the re-check's (one 4-byte value per candidate, read by the
-// query's one workgroup), and while that workgroup's exact top-ck is short.
-// Measured: 1M x 1024 (M 128, nlist 4096, batch 64, 1.2 rows per pair, 51 K
-// to 200 K candidates per query): 1.4x the byte-LUT scan's QPS at nprobe 16
-// to 64 and ck 100 to 400; 10M x 128 uint8 (M 16, 420 K candidates per
-// query, 2.1 rows per pair): 11x slower; 11M x 768 (M 96) at ck 1000: 10x
-// slower; one query per batch: equal.
+// query's one workgroup).  Measured: 1M x 1024 (M 128, nlist 4096, batch 64,
+// 1.2 rows per pair, 51 K to 200 K candidates per query): 1.5-1.6x the
+// byte-LUT scan's QPS at nprobe 16 to 64 and ck 100 to 400; 11M x 768 (M 96,
+// batch 128, 237 K candidates per query): 1.39x at ck 400 and 1.30x at
+// ck 1000; 10M x 128 uint8 (M 16, 420 K candidates per query, 2.1 rows per
+// pair): 11x slower; one query per batch: equal.  Longer short lists than
+// 1024 were not measured.
 constexpr double kMfmaMaxTileCost = 3.0;
 constexpr int kMfmaMinM = 64;
-constexpr int kMfmaMaxCk = 512;
+constexpr int kMfmaMaxCk = 1024;
 
 // Rows computed per real (query, candidate) pair for batches of B queries
 // with P probes, measured on stored vectors taken as queries: up to 8

@@ -3823,12 +3823,18 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
                        int32_t* out_i, unsigned long long* topck_dbg, hipStream_t s) {
     constexpr int NT = kRefineNT;
     if (k > ck) return hipErrorInvalidValue;
-    const int stage_cap = std::max(4096, 8 * ck);
-    const size_t lds = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)stage_cap * (8 + 4) +
-                       (size_t)ck * 4 + (size_t)RC * Kr * 4 + (size_t)(2 * (B + 1)) * 4 +
-                       (size_t)ck * 4 * 2 + (NT / 64) * 4 + (size_t)(d + d / 32 + 1) * 4 + 32;
+    // the segment lists are staged in LDS for the rank merge when they fit
+    // (up to max(4096, 8 ck) keys); more go through the streaming selection,
+    // so the stage shrinks to the LDS the rest leaves (long short lists with
+    // per-subspace codebooks)
+    const size_t rest = stream_lds_bytes(NT, ck) + (size_t)ck * 8 + (size_t)ck * 4 +
+                        (size_t)RC * Kr * 4 + (size_t)(2 * (B + 1)) * 4 + (size_t)ck * 4 * 2 +
+                        (NT / 64) * 4 + (size_t)(d + d / 32 + 1) * 4 + 32;
     static const int max_dyn = allow_max_lds((const void*)refine_topk_kernel<NT>);
-    if ((int)lds > max_dyn) return hipErrorInvalidValue;
+    if ((int)rest > max_dyn) return hipErrorInvalidValue;
+    const int stage_cap =
+        (int)std::min<size_t>((size_t)std::max(4096, 8 * ck), ((size_t)max_dyn - rest) / 12 / 4 * 4);
+    const size_t lds = rest + (size_t)stage_cap * (8 + 4);
     hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, partial_slot,
                        qtot, B, sh.G, ck, k, q_rot, d, Ds, res_c1d, Kr, RC, Br, bpv, ldesc, nlist,
                        list_res, list_corr, list_ids, out_d, out_i, topck_dbg, stage_cap,

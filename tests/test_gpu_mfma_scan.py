@@ -181,9 +181,9 @@ def test_default_choice(gpu):
         g96.set_scan_kind(0)
         assert g.scan_plan(k)[0] == "mfma_scan_kernel"
         assert g96.scan_plan(k96)[0] == "scan_skew_kernel"
-        # a short list of 600 (k = 60, alpha = 10) is beyond what one
-        # workgroup per query re-checks quickly
-        assert g.scan_plan(60)[0] != "mfma_scan_kernel"
+        # short lists longer than 1024 (k = 110, alpha = 10: 1100) keep the
+        # byte-LUT scan
+        assert g.scan_plan(110)[0] != "mfma_scan_kernel"
     finally:
         g.set_scan_kind(2)
         g96.set_scan_kind(2)
