@@ -92,9 +92,12 @@ struct DBuf {
 constexpr int kSteps = 4;
 
 // Search lanes (workspace, stream, pinned staging) that consecutive batches
-// of one call alternate between.
+// of one call rotate through.  Four: device-resident searches run as fast as
+// with two (the CUs are then the limit) and host-array searches hide more of
+// their PCIe copies (config 2: 835 k against 748 k queries/s host to host);
+// three ran slower (700 k against 883 k device-resident).
 #ifndef JHQ_LANES
-#define JHQ_LANES 2
+#define JHQ_LANES 4
 #endif
 constexpr int kLanes = JHQ_LANES;
 static_assert(kLanes >= 1, "at least one lane");
@@ -680,7 +683,7 @@ int ensure_host_staging(jhq_index* ix, int l, int Bmax, int k) {
 
 // Preallocates everything a search with k <= res_k needs (the reference's
 // alloc_workspace at the end of add(), v14/jhq_gpu_index.cu:166-206,531, and
-// realloc_ck_buffers, v14/search.cu:294-313): both lanes' workspaces, streams
+// realloc_ck_buffers, v14/search.cu:294-313): every lane's workspace, stream
 // and pinned staging, and an up-to-date skewed code copy.  Called after every
 // add / append / load and parameter change, so device searches allocate
 // nothing.
@@ -695,9 +698,9 @@ int reserve_search(jhq_index* ix) {
     return JHQ_OK;
 }
 
-// Host arrays over several batches: the batches alternate between two lanes
-// (workspace, pinned staging, stream).  While one lane's batch runs, the host
-// copies the other lane's finished results out and its next queries in.
+// Host arrays over several batches: the batches rotate through the lanes
+// (workspace, pinned staging, stream).  While the other lanes' batches run,
+// the host copies a lane's finished results out and its next queries in.
 int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, float* dists,
                           int32_t* ids) {
     const int d = ix->d;
