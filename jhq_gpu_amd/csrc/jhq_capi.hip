@@ -173,6 +173,12 @@ struct jhq_index {
     bool skew_stale = true;
     std::vector<int32_t> skew_start, skew_rows;
     DBuf<int32_t> dskew_from;
+    // row-major rows of the primary codes, kept when the pre-scan can be
+    // chosen; per list, the block start and row count they hold
+    DBuf<uint8_t> dcodes_r;
+    bool rows_stale = true;
+    std::vector<int32_t> rows_start, rows_rows;
+    DBuf<int32_t> drows_from;
     DBuf<float> dcorr;
 
     // query GEMM operand [Pi ; centroids * Pi] ((d + nlist) x d): one product
@@ -406,6 +412,8 @@ int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_
 
 bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128; }
 
+bool rows_wanted(const jhq_index* ix);
+
 // The pre-scan computes 16-query tiles over every probed list; it pays off
 // when the queries of a batch share their lists so that the tiles are mostly
 // full, and when the byte-LUT scan's work per candidate (M gathers) is large
@@ -420,6 +428,13 @@ bool skew_eligible(const jhq_index* ix) { return ix->M % 32 == 0 && ix->M <= 128
 constexpr double kMfmaMaxTileCost = 3.0;
 constexpr int kMfmaMinM = 64;
 constexpr int kMfmaMaxCk = 1024;
+
+// The row-major code copy serves the pre-scan's re-check: kept where the
+// pre-scan can run and the scan kind may choose it.
+bool rows_wanted(const jhq_index* ix) {
+    return ix->K1D == 2 && ix->Ds == 8 && ix->bpd == 1 && ix->M % 16 == 0 && ix->M <= 128 &&
+           (ix->scan_kind == 2 || (ix->scan_kind == 0 && ix->M >= kMfmaMinM));
+}
 
 // Rows computed per real (query, candidate) pair for batches of B queries
 // with P probes, measured on stored vectors taken as queries: up to 8
@@ -549,6 +564,38 @@ int refresh_skew(jhq_index* ix) {
     return JHQ_OK;
 }
 
+// Brings the row-major copy up to date: rows a list gained since the last
+// refresh (all of a list that moved).
+int refresh_rows(jhq_index* ix) {
+    if (!ix->rows_stale) return JHQ_OK;
+    const int nl = ix->nlist;
+    const size_t need = static_cast<size_t>((std::max<int64_t>(ix->pool_cap, 1) + 15) / 16 * 16) *
+                        static_cast<size_t>(ix->M);
+    if (ix->dcodes_r.n < need || static_cast<int>(ix->rows_start.size()) != nl) {
+        if (ix->dcodes_r.n < need) JHQ_TRY(ix->dcodes_r.alloc(need));
+        ix->rows_start.assign(nl, -1);
+        ix->rows_rows.assign(nl, 0);
+    }
+    std::vector<int32_t> from(nl);
+    int max_rows = 0;
+    for (int l = 0; l < nl; l++) {
+        from[l] = ix->rows_start[l] == ix->l_start[l] ? std::min(ix->rows_rows[l], ix->l_size[l]) : 0;
+        max_rows = std::max(max_rows, ix->l_size[l] - from[l]);
+    }
+    if (max_rows > 0) {
+        JHQ_TRY(ix->drows_from.ensure(nl));
+        JHQ_HIP(hipMemcpyAsync(ix->drows_from.p, from.data(), nl * sizeof(int32_t),
+                               hipMemcpyHostToDevice, ix->stream));
+        JHQ_HIP(jhq::row_codes(ix->dldesc.p, ix->drows_from.p, nl, max_rows, ix->dcodes_t.p, ix->M,
+                               ix->dcodes_r.p, ix->stream));
+        JHQ_HIP(hipStreamSynchronize(ix->stream));
+    }
+    ix->rows_start = ix->l_start;
+    ix->rows_rows = ix->l_size;
+    ix->rows_stale = false;
+    return JHQ_OK;
+}
+
 struct BatchPlan {
     int ck, P;
     jhq::ScanShape sh;
@@ -626,6 +673,7 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                ix->dcodes_t.p,
                                skew_eligible(ix) && !ix->skew_stale ? ix->dcodes_s.p : nullptr,
+                               ix->dcodes_r.p && !ix->rows_stale ? ix->dcodes_r.p : nullptr,
                                bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
                                static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
                                w.wmfma.p, w.wmfma.n, k, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
@@ -691,6 +739,7 @@ int reserve_search(jhq_index* ix) {
     if (ix->ntotal == 0 || !ix->trained) return JHQ_OK;
     JHQ_TRY(ix->quiesce());
     if (skew_eligible(ix) && ix->skew_stale) JHQ_TRY(refresh_skew(ix));
+    if (rows_wanted(ix) && ix->rows_stale) JHQ_TRY(refresh_rows(ix));
     BatchPlan bp;
     JHQ_TRY(plan_batch(ix, ix->batch_size, ix->res_k, &bp, kLanes, true));
     JHQ_TRY(ix->ensure_lanes());
@@ -1142,6 +1191,7 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     // a device search still in flight reads the lists rewritten below
     JHQ_TRY(ix->quiesce());
     ix->skew_stale = true;
+    ix->rows_stale = true;
     ix->dump_P = -1;
     const int d = ix->d, M = ix->M, bpv = ix->bpv, nlist = ix->nlist;
     hipStream_t s = ix->stream;

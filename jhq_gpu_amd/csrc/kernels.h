@@ -124,6 +124,11 @@ hipError_t scatter_plan(const unsigned long long* sorted, const int64_t* first, 
 hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
                       const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s);
 int64_t skew_bytes(int64_t pool_cap, int M);
+// Row-major copy of the primary codes (slot p's M bytes at rows[p * M],
+// pool_cap * M bytes; M a multiple of 16), rows from[l] .. size-1 of each
+// list l (from rounded down to 16).
+hipError_t row_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
+                     const uint8_t* codes_t, int M, uint8_t* rows, hipStream_t s);
 hipError_t scatter_lists(const int32_t* order, const int32_t* slist, const int32_t* sidx,
                          int64_t n, int64_t id_base, const int4* ldesc, const uint8_t* pc,
                          const uint8_t* rc, const float* co, int M, int bpv, int32_t* ids_out,
@@ -181,14 +186,16 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 // u32 per candidate slot of the batch (dump_slots, a multiple of 16, at
 // least the sum of qtot times 16) and after them one per 16 slots; ws
 // (256-byte aligned) holds mfma_scan_bytes for this num_cu.  skew: the
-// current lane-skewed copy of the codes (M % 32 == 0), or null; the re-check
-// reads members' codes from it when given.  rck = RC * Kr.
+// current lane-skewed copy of the codes (M % 32 == 0), or null; rows: the
+// current row-major copy, or null; the re-check reads members' codes from
+// rows, else skew, else codes_t.  rck = RC * Kr.
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, int rck);
 bool mfma_fuses_refine(int ck);
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
-                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew, int ck,
+                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew,
+                     const uint8_t* rows, int ck,
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,

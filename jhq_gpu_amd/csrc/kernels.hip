@@ -1238,6 +1238,41 @@ __global__ void skew_codes_kernel(const int4* __restrict__ ldesc, const int32_t*
 
 int64_t skew_bytes(int64_t pool_cap, int M) { return (pool_cap + 15) / 16 * 16 * M; }
 
+// Row-major copy of the primary codes: slot p's M bytes at rows[p * M], so
+// that one vector's codes are one contiguous run (the pre-scan's re-check
+// reads whole rows of a few candidates).  Rows from[l] .. size-1 of list l
+// (from rounded down to 16); thread (16-byte piece q, slot i % 16).
+__global__ void row_codes_kernel(const int4* __restrict__ ldesc, const int32_t* __restrict__ from,
+                                 const uint8_t* __restrict__ codes_t, int M,
+                                 uint8_t* __restrict__ rows) {
+    const int4 L = ldesc[blockIdx.x];
+    const int q = threadIdx.x >> 4;
+    if (q >= M / 16) return;
+    for (int64_t i = (int64_t)(from[blockIdx.x] & ~15) + (int64_t)blockIdx.y * 16 + (threadIdx.x & 15);
+         i < L.z; i += (int64_t)gridDim.y * 16) {
+        const uint8_t* src = codes_t + (int64_t)L.x * M + i;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            w[k] = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[k] |= (uint32_t)src[(int64_t)(16 * q + 4 * k + e) * L.y] << (8 * e);
+        }
+        *(uint4*)(rows + ((int64_t)L.x + i) * M + 16 * q) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+hipError_t row_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
+                     const uint8_t* codes_t, int M, uint8_t* rows, hipStream_t s) {
+    if (nlist <= 0 || max_rows <= 0) return hipSuccess;
+    const int64_t gy = std::min<int64_t>(((int64_t)max_rows + 15 + 15) / 16, 65535);
+    if (M % 16 != 0 || M > 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(row_codes_kernel, dim3(nlist, (unsigned)gy), dim3(M), 0, s, ldesc, from,
+                       codes_t, M, rows);
+    return hipGetLastError();
+}
+
 hipError_t skew_codes(const int4* ldesc, const int32_t* from, int nlist, int max_rows,
                       const uint8_t* codes_t, int M, uint8_t* skew, hipStream_t s) {
     if (nlist <= 0 || max_rows <= 0) return hipSuccess;
@@ -4397,7 +4432,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
                     const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                     const int32_t* __restrict__ gofs, int P, const int4* __restrict__ ldesc,
-                    const uint8_t* __restrict__ codes_t, const uint8_t* __restrict__ skew, int ck,
+                    const uint8_t* __restrict__ codes_t, const uint8_t* __restrict__ skew,
+                    const uint8_t* __restrict__ rows, int ck,
                     int k, const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
                     const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
                     const int32_t* __restrict__ list_ids, float* __restrict__ out_d,
@@ -4597,16 +4633,18 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         // member keys replace the survivors in surv.  Thread t computes
         // subspace t % M of members t / M, t / M + NT / M, ... (its query
         // values in registers); every code byte of a round is requested
-        // before the first is used, from the lane-skewed copy when there is
-        // one (a member's M bytes in M / 16 runs of 16, against M cache
-        // lines of the code-major blocks); member rows of the entries are
-        // padded to M + 1 words, so both the writes and the in-order sums
-        // of a member row are free of bank conflicts
+        // before the first is used, from the row-major copy when there is
+        // one (a member's M bytes in one run), else from the lane-skewed copy
+        // (M / 16 runs of 16), else from the code-major blocks (M cache
+        // lines); member rows of the entries are padded to M + 1 words, so
+        // both the writes and the in-order sums of a member row are free of
+        // bank conflicts
         constexpr int EPT = kRecheckCHM * 128 / NT;  // entries per thread (M <= 128)
         const int me = tid % M, mstep = NT / M;
         float qm[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) qm[k] = k < Ds ? sq[me * Ds + k] : 0.0f;
+        for (int k = 0; k < 8; k++) qm[k] = sq[me * 8 + k];  // Ds == 8
+        const float cl0 = sc1d[0], cl1 = sc1d[1];             // K1D == 2, bpd == 1
         for (int c0 = 0; c0 < nm; c0 += kRecheckCHM) {
             const int nc = min(kRecheckCHM, nm - c0);
             // every lane loads (rows past the chunk's end repeat its last
@@ -4614,7 +4652,14 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             // in flight before the first wait
             uint32_t cb[EPT];
             uint32_t wrapm = 0u;
-            if (skew) {
+            if (rows) {
+                // a member's row is one run: a wave reads 64 of its bytes
+#pragma unroll
+                for (int u = 0; u < EPT; u++) {
+                    const int jj = min(tid / M + u * mstep, nc - 1);
+                    cb[u] = rows[((int64_t)meta[4 * mp[c0 + jj]] + mc[c0 + jj]) * M + me];
+                }
+            } else if (skew) {
 #pragma unroll
                 for (int u = 0; u < EPT; u++) {
                     const int jj = min(tid / M + u * mstep, nc - 1);
@@ -4638,6 +4683,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             }
 #pragma unroll
             for (int u = 0; u < EPT; u++) cb[u] = (cb[u] - ((wrapm >> u) & 1u)) & 0xffu;
+            // one-bit digits (the pre-scan's shape): the level is a select
+            // between the two codebook values, not an LDS lookup
 #pragma unroll
             for (int u = 0; u < EPT; u++) {
                 const int jj = tid / M + u * mstep;
@@ -4645,10 +4692,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     float e = 0.0f;
 #pragma unroll
                     for (int k = 0; k < 8; k++) {
-                        if (k < Ds) {
-                            const float df = qm[k] - sc1d[(cb[u] >> (k * bpd)) & kmask];
-                            e = fmaf(df, df, e);
-                        }
+                        const float df = qm[k] - (((cb[u] >> k) & 1u) ? cl1 : cl0);
+                        e = fmaf(df, df, e);
                     }
                     ebuf[jj * (M + 1) + me] = e;
                 }
@@ -4762,7 +4807,8 @@ size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
 
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
-                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew, int ck,
+                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew,
+                     const uint8_t* rows, int ck,
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
@@ -4798,13 +4844,13 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
     if (fuse)
         hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, true>), dim3(B), dim3(kRecheckNT), lr,
                            s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
-                           gofs, P, ldesc, codes_t, skew, ck, k, res_c1d, Kr, RC, Br, bpv,
+                           gofs, P, ldesc, codes_t, skew, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
                            list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
                            partial_slot);
     else
         hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, false>), dim3(B), dim3(kRecheckNT), lr,
                            s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
-                           gofs, P, ldesc, codes_t, skew, ck, k, res_c1d, Kr, RC, Br, bpv,
+                           gofs, P, ldesc, codes_t, skew, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
                            list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
                            partial_slot);
     return hipGetLastError();
