@@ -618,6 +618,10 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
         if (!grow) return fail(JHQ_ESTATE, "the skewed code copy is out of date");
         JHQ_TRY(refresh_skew(ix));
     }
+    if (bp->sh.mfma && ix->rows_stale) {
+        if (!grow) return fail(JHQ_ESTATE, "the row-major code copy is out of date");
+        JHQ_TRY(refresh_rows(ix));
+    }
     for (int i = 0; i < nws; i++)
         JHQ_TRY(ensure_workspace(ix, ix->ws[i], bp->ck, k, bp->P, bp->sh.max_segments, grow));
     if (bp->sh.dump || bp->sh.mfma) {
@@ -672,9 +676,7 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
         JHQ_HIP(jhq::mfma_scan(w.wqrot.p, d, ix->Ds, ix->K1D, ix->bpd, ix->dc1d.p, Bq, ix->M,
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                ix->dcodes_t.p,
-                               skew_eligible(ix) && !ix->skew_stale ? ix->dcodes_s.p : nullptr,
-                               ix->dcodes_r.p && !ix->rows_stale ? ix->dcodes_r.p : nullptr,
-                               bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
+                               ix->dcodes_r.p, bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
                                static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
                                w.wmfma.p, w.wmfma.n, k, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
                                ix->bpv, ix->dres.p, ix->dcorr.p, ix->dlist_ids.p, d_out, d_ids,

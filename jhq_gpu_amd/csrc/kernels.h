@@ -185,17 +185,16 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 // and the caller runs refine_topk.  dump holds one
 // u32 per candidate slot of the batch (dump_slots, a multiple of 16, at
 // least the sum of qtot times 16) and after them one per 16 slots; ws
-// (256-byte aligned) holds mfma_scan_bytes for this num_cu.  skew: the
-// current lane-skewed copy of the codes (M % 32 == 0), or null; rows: the
-// current row-major copy, or null; the re-check reads members' codes from
-// rows, else skew, else codes_t.  rck = RC * Kr.
+// (256-byte aligned) holds mfma_scan_bytes for this num_cu.  rows: the
+// current row-major copy of the codes (row_codes), which the tiles and the
+// re-check read; codes_t: the code-major blocks (the re-check's streamed
+// fallback).  rck = RC * Kr.
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, int rck);
 bool mfma_fuses_refine(int ck);
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
-                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew,
-                     const uint8_t* rows, int ck,
+                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* rows, int ck,
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,

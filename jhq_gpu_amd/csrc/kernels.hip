@@ -4149,30 +4149,17 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
 }
 
 constexpr int kMfmaPD = 4;  // tiles in flight per wave
-// One 16-candidate tile from its LDS copy: the lane's four code dwords, the
-// bit planes, two int8 MFMA chains (hi and lo halves of the query steps),
-// and the biased integer distances of rows 4h..4h+3 (rows without a query
-// have d < 0).
+// One 16-candidate tile: the lane's code dwords cw (row j of the tile,
+// subspaces GS h .. GS h + GS - 1, four to a dword), the bit planes, two
+// int8 MFMA chains (hi and lo halves of the query steps), and the biased
+// integer distances of rows 4h..4h+3 (rows without a query have d < 0).
 template <int M>
-__device__ __forceinline__ void mfma_tile(const unsigned char* tb, int h, int j, uint32_t qsel,
+__device__ __forceinline__ void mfma_tile(const uint32_t (&cw)[M / 16], int h, int j,
                                           const mfma_v4i (&ahi)[M / 8],
                                           const mfma_v4i (&alo)[M / 8], int cand, int nl,
                                           uint32_t* dump, uint32_t* tmin, int d0, int d1, int d2,
                                           int d3) {
-    constexpr int NK = M / 8, ND = M / 16, GS = M / 4;
-    uint32_t cw[ND];
-#pragma unroll
-    for (int tt = 0; tt < ND; tt++) {
-        const int m0 = GS * h + 4 * tt;
-        const unsigned char* rp = tb + (m0 + h) * 16 + (j & 12);
-        const uint32_t r0 = *(const uint32_t*)rp;
-        const uint32_t r1 = *(const uint32_t*)(rp + 16);
-        const uint32_t r2 = *(const uint32_t*)(rp + 32);
-        const uint32_t r3 = *(const uint32_t*)(rp + 48);
-        const uint32_t x01 = __builtin_amdgcn_perm(r1, r0, qsel);
-        const uint32_t x23 = __builtin_amdgcn_perm(r3, r2, qsel);
-        cw[tt] = __builtin_amdgcn_perm(x23, x01, 0x05040100u);
-    }
+    constexpr int NK = M / 8;
     mfma_v4i ah = {0, 0, 0, 0}, alw = {0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < NK; s++) {
@@ -4224,23 +4211,42 @@ __device__ __forceinline__ void mfma_tile(const unsigned char* tb, int h, int j,
 // so the 16 addresses a read touches sit in distinct banks).  A lane's code
 // bytes for its candidate are four LDS dwords and a 4x4 byte transpose
 // (v_perm_b32); bit plane k of a code dword is (w >> k) & 0x01010101.
+// The lane's code dwords of one tile row from the row-major copy: GS = M / 4
+// bytes (ND dwords) at p, as 16-byte loads where GS is a multiple of 16.
+template <int M>
+__device__ __forceinline__ void mfma_row_load(const uint8_t* p, uint32_t (&cw)[M / 16]) {
+    constexpr int ND = M / 16;
+    if constexpr ((M / 4) % 16 == 0) {
+#pragma unroll
+        for (int t = 0; t < ND / 4; t++) {
+            const uint4 v = *(const uint4*)(p + 16 * t);
+            cw[4 * t] = v.x;
+            cw[4 * t + 1] = v.y;
+            cw[4 * t + 2] = v.z;
+            cw[4 * t + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < ND; t++) cw[t] = *(const uint32_t*)(p + 4 * t);
+    }
+}
+
+// Wave wid runs tiles [wid T / W, (wid + 1) T / W) of the batch, from the
+// group and tile wstart[wid] names.  Lane (j, h) holds row j of each tile
+// (list slot 16 t + j) for subspaces GS h .. GS h + GS - 1, read straight
+// from the row-major copy (a tile's 16 rows are one contiguous run of 16 M
+// bytes) into a ring of kMfmaPD tiles in registers.
 template <int M>
 __global__ void __launch_bounds__(256)
-mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __restrict__ dump,
+mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ rows, uint32_t* __restrict__ dump,
                  uint32_t* __restrict__ tmin) {
-    constexpr int NK = M / 8, GS = M / 4, D = 8 * M;
-    constexpr int RL = (M + 63) / 64;          // rows a lane loads per tile (1 or 2)
-    static_assert(RL <= 2, "at most 128 subspaces");
-    constexpr int TB = (M + 4) * 16;           // LDS bytes of one tile
-    __shared__ __align__(16) unsigned char ring[4][kMfmaPD * TB];
+    constexpr int NK = M / 8, ND = M / 16, GS = M / 4, D = 8 * M;
     const int lane = threadIdx.x & 63, j = lane & 15, h = lane >> 4;
-    unsigned char* my = ring[threadIdx.x >> 6];
     const int W = gridDim.x * 4, wid = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int T = w.ctl[0];
     const int a0 = (int)((int64_t)wid * T / W), a1 = (int)((int64_t)(wid + 1) * T / W);
     int left = a1 - a0;
     if (left <= 0) return;
-    const uint32_t qsel = (uint32_t)(j & 3) | ((uint32_t)(4 + (j & 3)) << 8) | 0x0c0c0000u;
     const int2 st = w.wstart[wid];
     int g = st.x, off = st.y;
     JHQ_PHASE_DECL
@@ -4250,39 +4256,25 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
         const int2 gqv = w.gq[g * 16 + j];
         const int nq = ga.w;
         const int n = min((ga.z + kGroup - 1) / kGroup - off, left);
-        // row stride: the list's capacity; slots: its size rounded up to 16
-        const int npad = ga.y, nl = ga.z;
-        const uint8_t* base = codes_t + (int64_t)ga.x * M + 16 * off;
-        // tiles past the run's last reload its last tile (kept in bounds,
-        // never used); rows past M - 1 reload row M - 1.  The ring is four
-        // named registers (no array), so it stays out of private memory.
-        const uint8_t* rowa = base + (int64_t)min(lane, M - 1) * npad;
-        const uint8_t* rowb = base + (int64_t)min(lane + 64, M - 1) * npad;
-        uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
-#define JHQ_MFMA_FETCH(U, K)                                                     \
-    do {                                                                         \
-        const int c_ = 16 * min((K), n - 1);                                     \
-        ra##U = *(const uint4*)(rowa + c_);                                      \
-        if (RL > 1) rb##U = *(const uint4*)(rowb + c_);                          \
-    } while (0)
+        const int nl = ga.z;
+        // tiles past the run's last reload its last tile (in bounds, unused)
+        const uint8_t* base = rows + ((int64_t)ga.x + 16 * off + j) * M + GS * h;
+        uint32_t c0[ND], c1[ND], c2[ND], c3[ND];
+#define JHQ_MFMA_FETCH(U, K) mfma_row_load<M>(base + (int64_t)16 * M * min((K), n - 1), c##U)
         JHQ_MFMA_FETCH(0, 0);
         JHQ_MFMA_FETCH(1, 1);
         JHQ_MFMA_FETCH(2, 2);
         JHQ_MFMA_FETCH(3, 3);
+        // query steps of row j (rows past the group's queries take query
+        // 0's: their products are never stored), requested with the rows
         mfma_v4i ahi[NK], alo[NK];
-        if (j < nq) {
-            const int b = gqv.x;
+        {
+            const int b = j < nq ? gqv.x : 0;
             const mfma_v4i* src = (const mfma_v4i*)(w.qa + (int64_t)b * 2 * D + h * NK * 16);
 #pragma unroll
             for (int s = 0; s < NK; s++) {
                 ahi[s] = src[s];
                 alo[s] = src[D / 16 + s];
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < NK; s++) {
-                ahi[s] = mfma_v4i{0, 0, 0, 0};
-                alo[s] = mfma_v4i{0, 0, 0, 0};
             }
         }
         // dump offsets of the run's first slot for query rows 4h .. 4h+3
@@ -4299,25 +4291,15 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ codes_t, uint32_t* __rest
         ph_acc[6] += 1;
         ph_acc[7] += n;
 #endif
-        // every pass issues the same loads (tiles past the last are clamped),
-        // so the wait for a ring slot leaves the later slots' loads in flight
+        // a slot's tile runs, then the slot is refilled kMfmaPD tiles ahead
 #define JHQ_MFMA_TILE(U)                                                                    \
     {                                                                                       \
         const int k = k0 + U;                                                               \
-        unsigned char* tb = my + U * TB;                                                    \
-        const bool live = k < n;                                                            \
-        if (live) {                                                                         \
-            if (lane < M) *(uint4*)(tb + (lane + lane / GS) * 16) = ra##U;                  \
-            if (RL > 1 && lane + 64 < M)                                                    \
-                *(uint4*)(tb + (lane + 64 + (lane + 64) / GS) * 16) = rb##U;                \
-        }                                                                                   \
-        JHQ_MFMA_FETCH(U, k + kMfmaPD);                                                     \
-        if (live) {                                                                         \
-            __builtin_amdgcn_s_waitcnt(0xc07f); /* this wave's LDS writes done */           \
-            mfma_tile<M>(tb, h, j, qsel, ahi, alo, cbase + 16 * k, nl, dump, tmin,          \
+        if (k < n)                                                                          \
+            mfma_tile<M>(c##U, h, j, ahi, alo, cbase + 16 * k, nl, dump, tmin,              \
                          d0 < 0 ? -1 : d0 + 16 * k, d1 < 0 ? -1 : d1 + 16 * k,              \
                          d2 < 0 ? -1 : d2 + 16 * k, d3 < 0 ? -1 : d3 + 16 * k);             \
-        }                                                                                   \
+        JHQ_MFMA_FETCH(U, k + kMfmaPD);                                                     \
     }
         for (int k0 = 0; k0 < n; k0 += kMfmaPD) {
             JHQ_MFMA_TILE(0)
@@ -4432,8 +4414,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
                     const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                     const int32_t* __restrict__ gofs, int P, const int4* __restrict__ ldesc,
-                    const uint8_t* __restrict__ codes_t, const uint8_t* __restrict__ skew,
-                    const uint8_t* __restrict__ rows, int ck,
+                    const uint8_t* __restrict__ codes_t, const uint8_t* __restrict__ rows, int ck,
                     int k, const float* __restrict__ res_c1d, int Kr, int RC, int Br, int bpv,
                     const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
                     const int32_t* __restrict__ list_ids, float* __restrict__ out_d,
@@ -4633,10 +4614,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         // member keys replace the survivors in surv.  Thread t computes
         // subspace t % M of members t / M, t / M + NT / M, ... (its query
         // values in registers); every code byte of a round is requested
-        // before the first is used, from the row-major copy when there is
-        // one (a member's M bytes in one run), else from the lane-skewed copy
-        // (M / 16 runs of 16), else from the code-major blocks (M cache
-        // lines); member rows of the entries are padded to M + 1 words, so
+        // before the first is used, from the row-major copy (a member's M
+        // bytes are one run, against M cache lines of the code-major
+        // blocks); member rows of the entries are padded to M + 1 words, so
         // both the writes and the in-order sums of a member row are free of
         // bank conflicts
         constexpr int EPT = kRecheckCHM * 128 / NT;  // entries per thread (M <= 128)
@@ -4651,38 +4631,12 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             // member) into a register of its own, so that all EPT loads are
             // in flight before the first wait
             uint32_t cb[EPT];
-            uint32_t wrapm = 0u;
-            if (rows) {
+#pragma unroll
+            for (int u = 0; u < EPT; u++) {
                 // a member's row is one run: a wave reads 64 of its bytes
-#pragma unroll
-                for (int u = 0; u < EPT; u++) {
-                    const int jj = min(tid / M + u * mstep, nc - 1);
-                    cb[u] = rows[((int64_t)meta[4 * mp[c0 + jj]] + mc[c0 + jj]) * M + me];
-                }
-            } else if (skew) {
-#pragma unroll
-                for (int u = 0; u < EPT; u++) {
-                    const int jj = min(tid / M + u * mstep, nc - 1);
-                    const int pp = mp[c0 + jj], cc = mc[c0 + jj];
-                    // subspace me of candidate cc sits at row position
-                    // me + cc % 32, wrapped positions holding code + 1
-                    int t = me + (cc & 31);
-                    const int wrap = t >= M ? 1 : 0;
-                    t -= wrap * M;
-                    wrapm |= (uint32_t)wrap << u;
-                    cb[u] = skew[skew_piece((int64_t)meta[4 * pp] + cc, t >> 4, M) + (t & 15)];
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < EPT; u++) {
-                    const int jj = min(tid / M + u * mstep, nc - 1);
-                    const int pp = mp[c0 + jj];
-                    cb[u] = codes_t[(int64_t)meta[4 * pp] * M + (int64_t)me * meta[4 * pp + 1] +
-                                    mc[c0 + jj]];
-                }
+                const int jj = min(tid / M + u * mstep, nc - 1);
+                cb[u] = rows[((int64_t)meta[4 * mp[c0 + jj]] + mc[c0 + jj]) * M + me];
             }
-#pragma unroll
-            for (int u = 0; u < EPT; u++) cb[u] = (cb[u] - ((wrapm >> u) & 1u)) & 0xffu;
             // one-bit digits (the pre-scan's shape): the level is a select
             // between the two codebook values, not an LDS lookup
 #pragma unroll
@@ -4807,8 +4761,7 @@ size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
 
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
                      int M, const int32_t* probes, const int32_t* gofs, const int32_t* qtot, int P,
-                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* skew,
-                     const uint8_t* rows, int ck,
+                     const int4* ldesc, const uint8_t* codes_t, const uint8_t* rows, int ck,
                      uint32_t* dump, int64_t dump_slots, unsigned char* ws, size_t ws_bytes,
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
@@ -4817,7 +4770,7 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
                      hipStream_t s) {
     const bool fuse = mfma_fuses_refine(ck);
     if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck, RC * Kr) || !ws || ((uintptr_t)ws & 255) ||
-        !dump || dump_slots % 16 != 0 || (skew && M % 32 != 0) || k < 1 || k > ck ||
+        !dump || !rows || dump_slots % 16 != 0 || k < 1 || k > ck ||
         (!fuse && (!partial || !partial_slot)))
         return hipErrorInvalidValue;
     // tile minima after the candidate slots
@@ -4836,7 +4789,7 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
           : M == 48 ? mfma_scan_kernel<48> : M == 64 ? mfma_scan_kernel<64>
           : M == 80 ? mfma_scan_kernel<80> : M == 96 ? mfma_scan_kernel<96>
           : M == 112 ? mfma_scan_kernel<112> : mfma_scan_kernel<128>;
-    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, codes_t, dump, tmin);
+    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, rows, dump, tmin);
     const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B, RC * Kr);
     static const int mxf = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT, true>);
     static const int mxs = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT, false>);
@@ -4844,13 +4797,13 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
     if (fuse)
         hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, true>), dim3(B), dim3(kRecheckNT), lr,
                            s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
-                           gofs, P, ldesc, codes_t, skew, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
+                           gofs, P, ldesc, codes_t, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
                            list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
                            partial_slot);
     else
         hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, false>), dim3(B), dim3(kRecheckNT), lr,
                            s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
-                           gofs, P, ldesc, codes_t, skew, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
+                           gofs, P, ldesc, codes_t, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
                            list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
                            partial_slot);
     return hipGetLastError();
