@@ -3916,7 +3916,9 @@ constexpr int kMfmaWavesPerCU = JHQ_MFMA_WPC;
 constexpr int kRecheckNT = 1024;
 constexpr int kRecheckCap = 2048;   // survivors / members held in LDS
 constexpr int kRecheckCHM = 128;    // members per exact-distance round
-constexpr int kRecheckLPT = 16;     // 16-byte row loads in flight per re-check thread
+constexpr int kRecheckLPT = 16;
+constexpr int kRecheckQCap = 2048;  // tiles listed for the tile-wise pass 2
+constexpr int kRecheckTPL = 4;      // their loads in flight per lane     // 16-byte row loads in flight per re-check thread
 constexpr int kMfmaPairsPT = 4;     // probes per work-list thread
 constexpr int kMfmaMaxBP = kMfmaPairsPT * kMfmaPlanNT;  // probes per batch
 
@@ -4479,7 +4481,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     const uint32_t* tm = tmin + qi.x / kGroup;
     const int nt = qi.z;
     uint32_t That = ~0u;
-    if (nt >= ck && nt <= 2 * kRecheckCap) {
+    const bool tiles_in_lds = nt >= ck && nt <= 2 * kRecheckCap;
+    if (tiles_in_lds) {
         uint32_t* tl = (uint32_t*)mp;  // mp and mc, free until the members
         for (int i0 = tid; i0 < nt; i0 += 4 * NT) {
             uint32_t v[4];
@@ -4542,7 +4545,60 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         __syncthreads();
         return ctl[0];
     };
-    int ns = collect(thr1);
+    // with the tile minima in LDS, only the tiles whose minimum is at or
+    // below the bound can hold a candidate at or below it: their 16 values
+    // are read (four tiles per wave, kRecheckTPL per lane in flight) instead
+    // of the whole row
+    auto collect_tiles = [&](uint32_t thr, int& ns_out) {
+        const uint32_t* tl = (const uint32_t*)mp;
+        int* qlist = (int*)ebuf;  // free until the members' entries
+        if (tid == 0) {
+            ctl[0] = 0;
+            ctl[1] = 0;
+        }
+        __syncthreads();
+        for (int t0 = 0; t0 < nt; t0 += NT) {
+            const int t = t0 + tid;
+            const bool q = t < nt && tl[t] <= thr;
+            const unsigned long long mk = __ballot(q);
+            int at = 0;
+            if (lane == 0 && mk) at = atomicAdd(&ctl[1], __popcll(mk));
+            at = __shfl(at, 0);
+            const int pos = at + __popcll(mk & lt);
+            if (q && pos < kRecheckQCap) qlist[pos] = t;
+        }
+        __syncthreads();
+        const int nqt = ctl[1];
+        if (nqt > kRecheckQCap) return false;
+        for (int i0 = wv * 4; i0 < nqt; i0 += NW * 4 * kRecheckTPL) {
+            uint32_t v[kRecheckTPL];
+            int ti[kRecheckTPL];
+#pragma unroll
+            for (int u = 0; u < kRecheckTPL; u++) {
+                const int qi2 = i0 + u * NW * 4 + (lane >> 4);
+                ti[u] = qi2 < nqt ? qlist[qi2] : -1;
+                v[u] = ti[u] >= 0 ? row[(int64_t)ti[u] * kGroup + (lane & 15)] : ~0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kRecheckTPL; u++) {
+                const bool keep = v[u] <= thr;
+                const unsigned long long mk = __ballot(keep);
+                if (!mk) continue;
+                int at = 0;
+                if (lane == 0) at = atomicAdd(&ctl[0], __popcll(mk));
+                at = __shfl(at, 0);
+                const int pos = at + __popcll(mk & lt);
+                if (keep && pos < kRecheckCap)
+                    surv[pos] = ((unsigned long long)v[u] << 32) |
+                                (uint32_t)(ti[u] * kGroup + (lane & 15));
+            }
+        }
+        __syncthreads();
+        ns_out = ctl[0];
+        return true;
+    };
+    int ns = 0;
+    if (!(tiles_in_lds && collect_tiles(thr1, ns))) ns = collect(thr1);
     uint32_t thr = thr1;
     if (ns > kRecheckCap && n >= ck) {
         // the tile minima left too many candidates: the exact ck-th smallest
