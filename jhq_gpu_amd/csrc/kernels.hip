@@ -38,7 +38,7 @@ namespace jhq {
 // workgroup accumulates wall-clock ticks (100 MHz) per phase of the scan,
 // probe-selection and refine kernels; jhq_debug_phase_ticks() reads them.
 #ifdef JHQ_PHASE_TIMING
-constexpr int kPhaseBlocks = 4096, kPhases = 10;
+constexpr int kPhaseBlocks = 4096, kPhases = 12;
 __device__ unsigned long long g_phase[4][kPhaseBlocks][kPhases];
 #define JHQ_PHASE_DECL unsigned long long ph_t = wall_clock64(), ph_acc[kPhases] = {0};
 #define JHQ_PHASE(i)                                              \
@@ -4723,6 +4723,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         JHQ_PHASE(5);
         kk = min(ck, nm);
         if (kk > 0) select_keys<NT>(surv, nm, kk, S.kout, S.kidx, S.ktmp, S.st);
+        JHQ_PHASE(11);
     } else {
         // more survivors than fit (ties at the bound): every candidate at or
         // below it, exact distances one per thread, streamed through the
@@ -4781,6 +4782,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     for (int i = tid; i < RC * Kr; i += NT) rcb[i] = res_c1d[i];
     for (int i = tid; i < d; i += NT) sqp[i + (i >> 5)] = sq[i];
     __syncthreads();
+    JHQ_PHASE(10);
     refine_short_list<NT>(S, kk, ck, k, b, kslot, cpos, cprim, fkeys, sqp, rcb, d, Ds, Kr, RC, Br,
                           bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg);
     JHQ_PHASE(0);
