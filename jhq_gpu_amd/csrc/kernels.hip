@@ -4336,6 +4336,25 @@ __device__ __forceinline__ uint32_t mfma_member_bound(const MfmaQS& Q, uint32_t 
 // The k-th smallest (1 <= k <= n) of n values get(0..n), 8 bits a round:
 // an LDS histogram of the values that match the bits found so far, and one
 // wave finds the bin that holds the k-th.  hist: 256 ints; c2: 2 ints.
+// hist[bin] += 1 for every active lane with match, wave-aggregated: the
+// lanes sharing the first pending lane's bin add their count at once (up to
+// three bins a call), the rest add one each.  The values of one query mostly
+// share their top bytes, and plain atomics on one bin ran one lane at a time.
+__device__ __forceinline__ void hist_add_wave(int* hist, uint32_t bin, bool match) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long pend = __ballot(match);
+#pragma unroll
+    for (int it = 0; it < 3; it++) {
+        if (!pend) return;
+        const int first = __ffsll((long long)pend) - 1;
+        const uint32_t b0 = (uint32_t)__shfl((int)bin, first);
+        const unsigned long long same = __ballot(match && bin == b0) & pend;
+        if (lane == first) atomicAdd(&hist[b0], __popcll(same));
+        pend &= ~same;
+    }
+    if ((pend >> lane) & 1ull) atomicAdd(&hist[bin], 1);
+}
+
 // (Inlined: as a call it saved its caller's registers to scratch memory, and
 // the re-check's tile-minimum bound took 12.5 instead of 8.8 us.)
 template <int NT, class Get>
@@ -4346,9 +4365,10 @@ __device__ __forceinline__ uint32_t block_radix_kth(Get get, int n, int k, int* 
     for (int sh = 24; sh >= 0; sh -= 8) {
         for (int i = tid; i < 256; i += NT) hist[i] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += NT) {
-            const uint32_t v = get(i);
-            if ((v & msk) == pre) atomicAdd(&hist[(v >> sh) & 255u], 1);
+        for (int i0 = 0; i0 < n; i0 += NT) {
+            const int i = i0 + tid;
+            const uint32_t v = i < n ? get(i) : 0u;
+            hist_add_wave(hist, (v >> sh) & 255u, i < n && (v & msk) == pre);
         }
         __syncthreads();
         if (wv == 0) {
@@ -4366,6 +4386,65 @@ __device__ __forceinline__ uint32_t block_radix_kth(Get get, int n, int k, int* 
             }
             int below = inc - t;
             // the lane whose bins cross kr picks the bin
+            if (below < kr && kr <= inc) {
+                int e = 0;
+                while (below + c[e] < kr) below += c[e++];
+                c2[0] = 4 * lane + e;
+                c2[1] = below;
+            }
+        }
+        __syncthreads();
+        pre |= (uint32_t)c2[0] << sh;
+        msk |= 255u << sh;
+        kr -= c2[1];
+        __syncthreads();
+    }
+    return pre;
+}
+
+// block_radix_kth over a row of n4 * 4 values in global memory: each round
+// puts kRecheckLPT 16-byte loads per thread in flight before it counts them
+// (a value at a time, each round was a chain of dependent loads: 200 us for
+// a 39 K row).
+template <int NT>
+__device__ __forceinline__ uint32_t block_radix_kth_row(const uint4* __restrict__ row4, int64_t n4,
+                                                        int k, int* hist, int* c2) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t pre = 0u, msk = 0u;
+    int kr = k;
+    for (int sh = 24; sh >= 0; sh -= 8) {
+        for (int i = tid; i < 256; i += NT) hist[i] = 0;
+        __syncthreads();
+        for (int64_t i0 = tid; i0 < n4; i0 += (int64_t)kRecheckLPT * NT) {
+            uint4 v4[kRecheckLPT];
+#pragma unroll
+            for (int u = 0; u < kRecheckLPT; u++) {
+                const int64_t i = i0 + (int64_t)u * NT;
+                v4[u] = i < n4 ? row4[i] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < kRecheckLPT; u++) {
+                const bool ok = i0 + (int64_t)u * NT < n4;
+                const uint32_t vv[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    hist_add_wave(hist, (vv[e] >> sh) & 255u, ok && (vv[e] & msk) == pre);
+            }
+        }
+        __syncthreads();
+        if (wv == 0) {
+            int c[4], t = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                c[e] = hist[4 * lane + e];
+                t += c[e];
+            }
+            int inc = t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int x = __shfl_up(inc, o);
+                if (lane >= o) inc += x;
+            }
+            int below = inc - t;
             if (below < kr && kr <= inc) {
                 int e = 0;
                 while (below + c[e] < kr) below += c[e++];
@@ -4604,9 +4683,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         // the tile minima left too many candidates: the exact ck-th smallest
         // I of the row (padding slots hold the largest value) and again
         thr = min(thr1, mfma_member_bound(
-                            Q, block_radix_kth<NT>([&](int i) { return row[i]; }, (int)n, ck,
-                                                   (int*)ebuf, ctl + 2),
-                            M));
+                            Q, block_radix_kth_row<NT>(row4, n4, ck, (int*)ebuf, ctl + 2), M));
         ns = collect(thr);
     }
     JHQ_PHASE(2);
