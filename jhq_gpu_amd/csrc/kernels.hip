@@ -38,7 +38,7 @@ namespace jhq {
 // workgroup accumulates wall-clock ticks (100 MHz) per phase of the scan,
 // probe-selection and refine kernels; jhq_debug_phase_ticks() reads them.
 #ifdef JHQ_PHASE_TIMING
-constexpr int kPhaseBlocks = 4096, kPhases = 12;
+constexpr int kPhaseBlocks = 4096, kPhases = 16;
 __device__ unsigned long long g_phase[4][kPhaseBlocks][kPhases];
 #define JHQ_PHASE_DECL unsigned long long ph_t = wall_clock64(), ph_acc[kPhases] = {0};
 #define JHQ_PHASE(i)                                              \
@@ -3918,6 +3918,9 @@ constexpr int kRecheckCap = 2048;   // survivors / members held in LDS
 constexpr int kRecheckCHM = 128;    // members per exact-distance round
 constexpr int kRecheckLPT = 16;
 constexpr int kRecheckQCap = 2048;  // tiles listed for the tile-wise pass 2
+constexpr int kRecheckQCap1 = 1536; // tiles listed for the in-register ck-th value
+constexpr int kRecheckRegV = 8;     // its values per thread
+constexpr int kRecheckTM = 16;      // tile minima per thread in flight (global)
 constexpr int kRecheckTPL = 4;      // their loads in flight per lane     // 16-byte row loads in flight per re-check thread
 constexpr int kMfmaPairsPT = 4;     // probes per work-list thread
 constexpr int kMfmaMaxBP = kMfmaPairsPT * kMfmaPlanNT;  // probes per batch
@@ -4461,6 +4464,102 @@ __device__ __forceinline__ uint32_t block_radix_kth_row(const uint4* __restrict_
     return pre;
 }
 
+// block_radix_kth over n values in global memory (any alignment), with
+// kRecheckTM loads per thread in flight per batch.
+template <int NT>
+__device__ __forceinline__ uint32_t block_radix_kth_glob(const uint32_t* __restrict__ p, int n,
+                                                         int k, int* hist, int* c2) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t pre = 0u, msk = 0u;
+    int kr = k;
+    for (int sh = 24; sh >= 0; sh -= 8) {
+        for (int i = tid; i < 256; i += NT) hist[i] = 0;
+        __syncthreads();
+        for (int i0 = 0; i0 < n; i0 += kRecheckTM * NT) {
+            uint32_t v[kRecheckTM];
+#pragma unroll
+            for (int u = 0; u < kRecheckTM; u++) {
+                const int i = i0 + u * NT + tid;
+                v[u] = i < n ? p[i] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kRecheckTM; u++)
+                hist_add_wave(hist, (v[u] >> sh) & 255u,
+                              i0 + u * NT + tid < n && (v[u] & msk) == pre);
+        }
+        __syncthreads();
+        if (wv == 0) {
+            int c[4], t = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                c[e] = hist[4 * lane + e];
+                t += c[e];
+            }
+            int inc = t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int x = __shfl_up(inc, o);
+                if (lane >= o) inc += x;
+            }
+            int below = inc - t;
+            if (below < kr && kr <= inc) {
+                int e = 0;
+                while (below + c[e] < kr) below += c[e++];
+                c2[0] = 4 * lane + e;
+                c2[1] = below;
+            }
+        }
+        __syncthreads();
+        pre |= (uint32_t)c2[0] << sh;
+        msk |= 255u << sh;
+        kr -= c2[1];
+        __syncthreads();
+    }
+    return pre;
+}
+
+// block_radix_kth over V values per thread held in registers (the padding
+// value ~0 counts as a value; k must not exceed the real ones).
+template <int NT, int V>
+__device__ __forceinline__ uint32_t block_radix_kth_regs(const uint32_t (&rv)[V], int k, int* hist,
+                                                         int* c2) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    uint32_t pre = 0u, msk = 0u;
+    int kr = k;
+    for (int sh = 24; sh >= 0; sh -= 8) {
+        for (int i = tid; i < 256; i += NT) hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < V; u++) hist_add_wave(hist, (rv[u] >> sh) & 255u, (rv[u] & msk) == pre);
+        __syncthreads();
+        if (wv == 0) {
+            int c[4], t = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                c[e] = hist[4 * lane + e];
+                t += c[e];
+            }
+            int inc = t;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int x = __shfl_up(inc, o);
+                if (lane >= o) inc += x;
+            }
+            int below = inc - t;
+            if (below < kr && kr <= inc) {
+                int e = 0;
+                while (below + c[e] < kr) below += c[e++];
+                c2[0] = 4 * lane + e;
+                c2[1] = below;
+            }
+        }
+        __syncthreads();
+        pre |= (uint32_t)c2[0] << sh;
+        msk |= 255u << sh;
+        kr -= c2[1];
+        __syncthreads();
+    }
+    return pre;
+}
+
 // Words of the re-check's entry buffer: its [kRecheckCHM][M + 1] entries, or
 // more when the refine's short-list arrays (keys, slots, positions and
 // primary distances of ck candidates), residual codebooks (rck floats) and
@@ -4554,9 +4653,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     if (tid == 0) ctl[0] = 0;
     stream_begin<NT>(S);
     // pass 1: an upper bound of the ck-th smallest I from the tile minima
-    // (each is an I value of its own tile): their exact ck-th smallest when
-    // they fit in LDS, else each wave's r-th smallest thread minimum (NW * r
-    // >= ck values are at or below the largest)
+    // (each is an I value of its own tile): their exact ck-th smallest, from
+    // an LDS copy when they fit there, else from global memory
     const uint32_t* tm = tmin + qi.x / kGroup;
     const int nt = qi.z;
     uint32_t That = ~0u;
@@ -4574,15 +4672,11 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         __syncthreads();
         That = block_radix_kth<NT>([&](int i) { return tl[i]; }, nt, ck, (int*)ebuf, ctl + 2);
     } else if (nt >= ck) {
-        uint32_t mn = ~0u;
-        for (int i = tid; i < nt; i += NT) mn = min(mn, tm[i]);
-        const int r = (ck + NW - 1) / NW;
-        const uint32_t tw = r <= 64 ? wave_kth_u32(mn, r) : ~0u;
-        if (lane == 0) wsum[wv] = (int)tw;
+        // more tile minima than LDS holds: read from global memory with the
+        // loads batched (a per-wave bound here leaves thousands of candidates
+        // with nprobe 32 over 4096 lists and ck 400)
         __syncthreads();
-        That = 0u;
-#pragma unroll
-        for (int w2 = 0; w2 < NW; w2++) That = max(That, (uint32_t)wsum[w2]);
+        That = block_radix_kth_glob<NT>(tm, nt, ck, (int*)ebuf, ctl + 2);
     } else {
         __syncthreads();
     }
@@ -4628,26 +4722,40 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     // below the bound can hold a candidate at or below it: their 16 values
     // are read (four tiles per wave, kRecheckTPL per lane in flight) instead
     // of the whole row
+    // the tiles whose minimum is at or below thr into qlist (at most cap
+    // listed; returns the count), tile minima from LDS when they fit there,
+    // else from global memory
+    auto list_tiles = [&](uint32_t thr, int* qlist, int cap) {
+        const uint32_t* tl = tiles_in_lds ? (const uint32_t*)mp : tm;
+        if (tid == 0) ctl[1] = 0;
+        __syncthreads();
+        for (int t0 = 0; t0 < nt; t0 += kRecheckTM * NT) {
+            uint32_t mv[kRecheckTM];
+#pragma unroll
+            for (int u = 0; u < kRecheckTM; u++) {
+                const int t = t0 + u * NT + tid;
+                mv[u] = t < nt ? tl[t] : ~0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kRecheckTM; u++) {
+                const int t = t0 + u * NT + tid;
+                const bool q = t < nt && mv[u] <= thr;
+                const unsigned long long mk = __ballot(q);
+                if (!mk) continue;
+                int at = 0;
+                if (lane == 0) at = atomicAdd(&ctl[1], __popcll(mk));
+                at = __shfl(at, 0);
+                const int pos = at + __popcll(mk & lt);
+                if (q && pos < cap) qlist[pos] = t;
+            }
+        }
+        __syncthreads();
+        return ctl[1];
+    };
     auto collect_tiles = [&](uint32_t thr, int& ns_out) {
-        const uint32_t* tl = (const uint32_t*)mp;
         int* qlist = (int*)ebuf;  // free until the members' entries
-        if (tid == 0) {
-            ctl[0] = 0;
-            ctl[1] = 0;
-        }
-        __syncthreads();
-        for (int t0 = 0; t0 < nt; t0 += NT) {
-            const int t = t0 + tid;
-            const bool q = t < nt && tl[t] <= thr;
-            const unsigned long long mk = __ballot(q);
-            int at = 0;
-            if (lane == 0 && mk) at = atomicAdd(&ctl[1], __popcll(mk));
-            at = __shfl(at, 0);
-            const int pos = at + __popcll(mk & lt);
-            if (q && pos < kRecheckQCap) qlist[pos] = t;
-        }
-        __syncthreads();
-        const int nqt = ctl[1];
+        if (tid == 0) ctl[0] = 0;
+        const int nqt = list_tiles(thr, qlist, kRecheckQCap);
         if (nqt > kRecheckQCap) return false;
         for (int i0 = wv * 4; i0 < nqt; i0 += NW * 4 * kRecheckTPL) {
             uint32_t v[kRecheckTPL];
@@ -4677,14 +4785,46 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         return true;
     };
     int ns = 0;
-    if (!(tiles_in_lds && collect_tiles(thr1, ns))) ns = collect(thr1);
+    if (!(nt >= ck && collect_tiles(thr1, ns))) ns = collect(thr1);
     uint32_t thr = thr1;
+    JHQ_PHASE(12);
+#ifdef JHQ_PHASE_TIMING
+    ph_acc[14] += (unsigned long long)ns;
+#endif
     if (ns > kRecheckCap && n >= ck) {
         // the tile minima left too many candidates: the exact ck-th smallest
-        // I of the row (padding slots hold the largest value) and again
-        thr = min(thr1, mfma_member_bound(
-                            Q, block_radix_kth_row<NT>(row4, n4, ck, (int*)ebuf, ctl + 2), M));
-        ns = collect(thr);
+        // I, then the pass again.  The ck-th value lies in the tiles whose
+        // minimum is at most That (the ck-th smallest minimum): their values
+        // (about 16 ck) are radix-selected in registers when they fit, else
+        // the whole row is (padding slots hold the largest value)
+        bool exact = false;
+        int n1 = -1;
+        {
+            int* qlist = (int*)ebuf + 256;  // after the radix histogram
+            n1 = list_tiles(That, qlist, kRecheckQCap1);
+            if (n1 <= kRecheckQCap1 && 16 * n1 <= kRecheckRegV * NT) {
+                uint32_t rv[kRecheckRegV];
+#pragma unroll
+                for (int u = 0; u < kRecheckRegV; u++) {
+                    const int idx = u * NT + tid;
+                    rv[u] = idx < 16 * n1 ? row[(int64_t)qlist[idx >> 4] * kGroup + (idx & 15)]
+                                          : ~0u;
+                }
+                thr = min(thr1, mfma_member_bound(
+                                    Q, block_radix_kth_regs<NT, kRecheckRegV>(rv, ck, (int*)ebuf,
+                                                                              ctl + 2),
+                                    M));
+                exact = true;
+            }
+        }
+        if (!exact)
+            thr = min(thr1, mfma_member_bound(
+                                Q, block_radix_kth_row<NT>(row4, n4, ck, (int*)ebuf, ctl + 2), M));
+        JHQ_PHASE(13);
+#ifdef JHQ_PHASE_TIMING
+        ph_acc[15] += (unsigned long long)(n1 + 1);
+#endif
+        if (!(nt >= ck && collect_tiles(thr, ns))) ns = collect(thr);
     }
     JHQ_PHASE(2);
 #ifdef JHQ_PHASE_TIMING
