@@ -3542,20 +3542,50 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
     return hipGetLastError();
 }
 
+// The refine's 8-byte-piece path: 4-bit codes, 16 | d, rows of whole pieces,
+// at most 4 pieces per lane (d <= 1024).  Its table of squared differences
+// pads each piece's 256 words by 4, so that the 16 lanes of a candidate,
+// reading pieces 16 apart, start 4 banks apart.
+constexpr int kRefineTabPiece = 16 * 16 + 4;
+__host__ __device__ inline bool refine_pieces(int d, int Br, int bpv) {
+    return Br == 4 && d % 16 == 0 && bpv % 8 == 0 && d <= 1024;
+}
+__host__ __device__ inline int refine_tab_words(int d) { return d / 16 * kRefineTabPiece; }
+
 // Residual refine and final top-k of one query's exact short list (the
 // ksel keys in S.kout, ascending, with their pool slots in kslot):
 // topck_dbg (optional) gets the short list, out_d / out_i the k best by
 // (refined dist, id), (+inf, -1) past ksel.  Called by the whole workgroup;
 // cpos, cprim and fkeys are LDS scratch of ck entries, sq the query (one pad
-// word per 32), rc the residual codebooks.
+// word per 32), rc the residual codebooks; tab (optional; refine_tab_words(d)
+// floats, used when refine_pieces holds) is LDS scratch for the table of
+// squared differences per dimension and code.
 template <int NT>
 __device__ __forceinline__ void refine_short_list(
     StreamSel& S, int ksel, int ck, int k, int b, const int* kslot, int* cpos, float* cprim,
     unsigned long long* fkeys, const float* sq, const float* rc, int d, int Ds, int Kr, int RC,
     int Br, int bpv, const uint8_t* __restrict__ list_res, const float* __restrict__ list_corr,
     const int32_t* __restrict__ list_ids, float* __restrict__ out_d, int32_t* __restrict__ out_i,
-    unsigned long long* __restrict__ topck_dbg) {
+    unsigned long long* __restrict__ topck_dbg, float* tab) {
     const int tid = threadIdx.x;
+    // codebook of dimension j: one shared codebook, or that of subspace j / Ds
+    int ds_shift = -1;
+    if (RC > 1 && (Ds & (Ds - 1)) == 0) ds_shift = __ffs(Ds) - 1;
+    auto cbo = [&](int j) -> int {
+        if (RC == 1) return 0;
+        return (ds_shift >= 0 ? (j >> ds_shift) : (j / Ds)) * Kr;
+    };
+    const bool pieces = refine_pieces(d, Br, bpv);
+    if (!pieces) tab = nullptr;
+    if (tab) {
+        // (q_j - codeword c)^2, rounded as the sum below rounds it, at
+        // tab[(j / 16) * kRefineTabPiece + (j % 16) * 16 + c]
+        for (int i = tid; i < 16 * d; i += NT) {
+            const int j = i >> 4, c = i & 15;
+            const float df = sq[j + (j >> 5)] - rc[cbo(j) + c];
+            tab[(j >> 4) * kRefineTabPiece + (j & 15) * 16 + c] = df * df;
+        }
+    }
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
             const unsigned long long kk = S.kout[r];
@@ -3568,16 +3598,9 @@ __device__ __forceinline__ void refine_short_list(
     }
     __syncthreads();
 
-    // residual refine: 16 lanes per candidate, lane l16 sums a contiguous
-    // range of dimensions, then a fixed xor tree adds the 16 partial sums.
+    // residual refine: 16 lanes per candidate, each summing its share of the
+    // dimensions, then a fixed xor tree adds the 16 partial sums.
     const int grp = tid >> 4, l16 = tid & 15;
-    // codebook of dimension j: one shared codebook, or that of subspace j / Ds
-    int ds_shift = -1;
-    if (RC > 1 && (Ds & (Ds - 1)) == 0) ds_shift = __ffs(Ds) - 1;
-    auto cbo = [&](int j) -> int {
-        if (RC == 1) return 0;
-        return (ds_shift >= 0 ? (j >> ds_shift) : (j / Ds)) * Kr;
-    };
     constexpr int NG = NT / 16;
     const int dpc = (Br == 4) ? 32 : 16;  // dimensions per 16-byte chunk
     const bool vec = (bpv % 16) == 0 && (d % dpc) == 0;
@@ -3607,7 +3630,82 @@ __device__ __forceinline__ void refine_short_list(
                 }
         }
     };
-    if (vec && chk / dpc <= 4) {
+    if (pieces) {
+        // 4-bit codes in 8-byte pieces of 16 dimensions: lane l16 sums pieces
+        // l16, l16 + 16, ... in order (a load of the 16 lanes reads 128
+        // contiguous bytes of the candidate); the next round's pieces,
+        // correction and id are loaded while this round is summed
+        const int npc = d >> 4;
+        const int np = l16 < npc ? (npc - 1 - l16) / 16 + 1 : 0;
+        uint2 wc[4], wn[4];
+        float corr_c = 0.0f, corr_n = 0.0f;
+        int id_c = 0, id_n = 0;
+        auto fetch = [&](int base, uint2 (&w)[4], float& corr, int& id) {
+            const int c = base + grp;
+            if (c < ksel) {
+                const int pos = cpos[c];
+                const uint2* rp = (const uint2*)(list_res + (int64_t)pos * bpv) + l16;
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (u < np) w[u] = rp[16 * u];
+                if (l16 == 0) {
+                    corr = list_corr[pos];
+                    id = list_ids[pos];
+                }
+            }
+        };
+        fetch(0, wc, corr_c, id_c);
+        for (int base = 0; base < ksel; base += NG) {
+            if (base + NG < ksel) fetch(base + NG, wn, corr_n, id_n);
+            const int c = base + grp;
+            const bool valid = c < ksel;
+            float sres = 0.0f;
+            // l16 opaque per round: the LDS addresses of the pieces'
+            // dimensions are formed here instead of being hoisted out of the
+            // loop (64 of them would not stay in registers)
+            int lv = l16;
+            asm volatile("" : "+v"(lv));
+            if (valid && tab) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (u < np) {
+                        const float* tp = tab + (lv + 16 * u) * kRefineTabPiece;
+                        const uint32_t ww[2] = {wc[u].x, wc[u].y};
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            sres = sres + tp[e * 16 + ((ww[e >> 3] >> (4 * (e & 7))) & 15u)];
+                    }
+                }
+            } else if (valid) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (u < np) {
+                        const int pc = lv + 16 * u;
+                        const uint32_t ww[2] = {wc[u].x, wc[u].y};
+#pragma unroll
+                        for (int e = 0; e < 16; e++) {
+                            const int jj = pc * 16 + e;
+                            const float df = sq[jj + (jj >> 5)] -
+                                             rc[cbo(jj) + ((ww[e >> 3] >> (4 * (e & 7))) & 15u)];
+                            sres = sres + df * df;
+                        }
+                    }
+                }
+            }
+            sres = sres + __shfl_xor(sres, 8);
+            sres = sres + __shfl_xor(sres, 4);
+            sres = sres + __shfl_xor(sres, 2);
+            sres = sres + __shfl_xor(sres, 1);
+            if (valid && l16 == 0) {
+                const float comp = (cprim[c] + sres) + corr_c;
+                fkeys[c] = ((unsigned long long)f2ord(comp) << 32) | (uint32_t)id_c;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) wc[u] = wn[u];
+            corr_c = corr_n;
+            id_c = id_n;
+        }
+    } else if (vec && chk / dpc <= 4) {
         // at most 4 chunks per lane: the next round's chunks, correction and
         // id are loaded while this round is summed
         const int j0 = l16 * chk, j1 = (j0 + chk) < d ? (j0 + chk) : d;
@@ -3741,7 +3839,8 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
                    const int4* __restrict__ ldesc, int nlist, const uint8_t* __restrict__ list_res,
                    const float* __restrict__ list_corr, const int32_t* __restrict__ list_ids,
                    float* __restrict__ out_d, int32_t* __restrict__ out_i,
-                   unsigned long long* __restrict__ topck_dbg, int stage_cap, int ov) {
+                   unsigned long long* __restrict__ topck_dbg, int stage_cap, int ov,
+                   int use_tab) {
     extern __shared__ __align__(16) unsigned char smem[];
     StreamSel S;
     unsigned char* p = stream_carve<NT>(smem, ck, &S);
@@ -3758,6 +3857,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     // query staged with one pad word per 32 so that lanes reading 32-dim
     // ranges at a 32-word stride hit distinct banks
     float* sq = (float*)(wsum + NT / 64);
+    float* tab = use_tab ? sq + d + d / 32 + 1 : nullptr;  // [refine_tab_words(d)]
 
     const int b = blockIdx.x, tid = threadIdx.x;
     JHQ_PHASE_DECL
@@ -3845,7 +3945,7 @@ refine_topk_kernel(const unsigned long long* __restrict__ partial,
     }
     JHQ_PHASE(1);
     refine_short_list<NT>(S, ksel, ck, k, b, kslot, cpos, cprim, fkeys, sq, rc, d, Ds, Kr, RC, Br,
-                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg);
+                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg, tab);
     JHQ_PHASE(3);
     JHQ_PHASE_FLUSH(2);
 }
@@ -3867,13 +3967,18 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
                         (NT / 64) * 4 + (size_t)(d + d / 32 + 1) * 4 + 32;
     static const int max_dyn = allow_max_lds((const void*)refine_topk_kernel<NT>);
     if ((int)rest > max_dyn) return hipErrorInvalidValue;
-    const int stage_cap =
-        (int)std::min<size_t>((size_t)std::max(4096, 8 * ck), ((size_t)max_dyn - rest) / 12 / 4 * 4);
-    const size_t lds = rest + (size_t)stage_cap * (8 + 4);
+    // the table of squared differences halves the refine's LDS reads; it is
+    // taken when a stage of 4096 keys still fits beside it
+    const size_t tab = refine_pieces(d, Br, bpv) ? (size_t)refine_tab_words(d) * 4 : 0;
+    const int use_tab = tab > 0 && rest + tab + (size_t)4096 * 12 <= (size_t)max_dyn;
+    const size_t rest_t = rest + (use_tab ? tab : 0);
+    const int stage_cap = (int)std::min<size_t>((size_t)std::max(4096, 8 * ck),
+                                                ((size_t)max_dyn - rest_t) / 12 / 4 * 4);
+    const size_t lds = rest_t + (size_t)stage_cap * (8 + 4);
     hipLaunchKernelGGL(refine_topk_kernel<NT>, dim3(B), dim3(NT), lds, s, partial, partial_slot,
                        qtot, B, sh.G, ck, k, q_rot, d, Ds, res_c1d, Kr, RC, Br, bpv, ldesc, nlist,
                        list_res, list_corr, list_ids, out_d, out_i, topck_dbg, stage_cap,
-                       sh.ov);
+                       sh.ov, use_tab);
     return hipGetLastError();
 }
 
@@ -5001,7 +5106,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     __syncthreads();
     JHQ_PHASE(10);
     refine_short_list<NT>(S, kk, ck, k, b, kslot, cpos, cprim, fkeys, sqp, rcb, d, Ds, Kr, RC, Br,
-                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg);
+                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg, nullptr);
     JHQ_PHASE(0);
     JHQ_PHASE_FLUSH(3);
 }
