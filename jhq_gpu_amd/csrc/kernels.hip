@@ -4021,12 +4021,12 @@ constexpr int kMfmaWavesPerCU = JHQ_MFMA_WPC;
 constexpr int kRecheckNT = 1024;
 constexpr int kRecheckCap = 2048;   // survivors / members held in LDS
 constexpr int kRecheckCHM = 128;    // members per exact-distance round
-constexpr int kRecheckLPT = 16;
+constexpr int kRecheckLPT = 16;     // 16-byte row loads in flight per thread (whole-row pass)
 constexpr int kRecheckQCap = 2048;  // tiles listed for the tile-wise pass 2
 constexpr int kRecheckQCap1 = 1536; // tiles listed for the in-register ck-th value
 constexpr int kRecheckRegV = 8;     // its values per thread
 constexpr int kRecheckTM = 16;      // tile minima per thread in flight (global)
-constexpr int kRecheckTPL = 4;      // their loads in flight per lane     // 16-byte row loads in flight per re-check thread
+constexpr int kRecheckTPL = 4;      // listed tiles' row loads in flight per lane
 constexpr int kMfmaPairsPT = 4;     // probes per work-list thread
 constexpr int kMfmaMaxBP = kMfmaPairsPT * kMfmaPlanNT;  // probes per batch
 
@@ -4823,10 +4823,6 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         __syncthreads();
         return ctl[0];
     };
-    // with the tile minima in LDS, only the tiles whose minimum is at or
-    // below the bound can hold a candidate at or below it: their 16 values
-    // are read (four tiles per wave, kRecheckTPL per lane in flight) instead
-    // of the whole row
     // the tiles whose minimum is at or below thr into qlist (at most cap
     // listed; returns the count), tile minima from LDS when they fit there,
     // else from global memory
@@ -4857,6 +4853,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         __syncthreads();
         return ctl[1];
     };
+    // only the tiles whose minimum is at or below the bound can hold a
+    // candidate at or below it: their 16 values are read (four tiles per
+    // wave, kRecheckTPL per lane in flight) instead of the whole row
     auto collect_tiles = [&](uint32_t thr, int& ns_out) {
         int* qlist = (int*)ebuf;  // free until the members' entries
         if (tid == 0) ctl[0] = 0;
@@ -5086,13 +5085,16 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     }
     // the refine's arrays replace the survivor and entry buffers: pool slots
     // of the short list (the probe whose canonical range holds the tag), the
-    // residual codebooks, the query with one pad word per 32
+    // residual codebooks, the query with one pad word per 32 and, when the
+    // rest of those buffers holds it, the table of squared differences
     unsigned long long* fkeys = (unsigned long long*)p0;
     int* kslot = (int*)(fkeys + ck);
     int* cpos = kslot + ck;
     float* cprim = (float*)(cpos + ck);
     float* rcb = cprim + ck;
     float* sqp = rcb + RC * Kr;
+    float* tabp = sqp + d + d / 32 + 1;
+    if (tabp + refine_tab_words(d) > sq) tabp = nullptr;
     for (int i = tid; i < kk; i += NT) {
         const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
         int32_t slot = -1;
@@ -5106,7 +5108,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     __syncthreads();
     JHQ_PHASE(10);
     refine_short_list<NT>(S, kk, ck, k, b, kslot, cpos, cprim, fkeys, sqp, rcb, d, Ds, Kr, RC, Br,
-                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg, nullptr);
+                          bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg, tabp);
     JHQ_PHASE(0);
     JHQ_PHASE_FLUSH(3);
 }
