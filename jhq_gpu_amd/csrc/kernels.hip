@@ -4026,6 +4026,7 @@ constexpr int kRecheckQCap = 2048;  // tiles listed for the tile-wise pass 2
 constexpr int kRecheckQCap1 = 1536; // tiles listed for the in-register ck-th value
 constexpr int kRecheckRegV = 8;     // its values per thread
 constexpr int kRecheckTM = 16;      // tile minima per thread in flight (global)
+constexpr int kRecheckTR = 32;      // tile minima per thread ranked in registers
 constexpr int kRecheckTPL = 4;      // listed tiles' row loads in flight per lane
 constexpr int kMfmaPairsPT = 4;     // probes per work-list thread
 constexpr int kMfmaMaxBP = kMfmaPairsPT * kMfmaPlanNT;  // probes per batch
@@ -4622,11 +4623,13 @@ __device__ __forceinline__ uint32_t block_radix_kth_glob(const uint32_t* __restr
     return pre;
 }
 
-// block_radix_kth over V values per thread held in registers (the padding
-// value ~0 counts as a value; k must not exceed the real ones).
+// block_radix_kth over V values per thread held in registers, value u of
+// thread t being entry u * NT + t of n (the padding value ~0 counts as a
+// value where entries u * NT .. u * NT + NT - 1 are partly real; k must not
+// exceed n).
 template <int NT, int V>
-__device__ __forceinline__ uint32_t block_radix_kth_regs(const uint32_t (&rv)[V], int k, int* hist,
-                                                         int* c2) {
+__device__ __forceinline__ uint32_t block_radix_kth_regs(const uint32_t (&rv)[V], int n, int k,
+                                                         int* hist, int* c2) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     uint32_t pre = 0u, msk = 0u;
     int kr = k;
@@ -4634,7 +4637,8 @@ __device__ __forceinline__ uint32_t block_radix_kth_regs(const uint32_t (&rv)[V]
         for (int i = tid; i < 256; i += NT) hist[i] = 0;
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < V; u++) hist_add_wave(hist, (rv[u] >> sh) & 255u, (rv[u] & msk) == pre);
+        for (int u = 0; u < V; u++)
+            if (u * NT < n) hist_add_wave(hist, (rv[u] >> sh) & 255u, (rv[u] & msk) == pre);
         __syncthreads();
         if (wv == 0) {
             int c[4], t = 0;
@@ -4776,10 +4780,21 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         }
         __syncthreads();
         That = block_radix_kth<NT>([&](int i) { return tl[i]; }, nt, ck, (int*)ebuf, ctl + 2);
+    } else if (nt >= ck && nt <= kRecheckTR * NT) {
+        // more tile minima than LDS holds (a per-wave bound here leaves
+        // thousands of candidates with nprobe 32 over 4096 lists and ck 400):
+        // read once into registers, all loads in flight, and ranked there
+        uint32_t rv[kRecheckTR];
+#pragma unroll
+        for (int u = 0; u < kRecheckTR; u++) {
+            const int i = u * NT + tid;
+            rv[u] = i < nt ? tm[i] : ~0u;
+        }
+        __syncthreads();
+        That = block_radix_kth_regs<NT, kRecheckTR>(rv, nt, ck, (int*)ebuf, ctl + 2);
     } else if (nt >= ck) {
-        // more tile minima than LDS holds: read from global memory with the
-        // loads batched (a per-wave bound here leaves thousands of candidates
-        // with nprobe 32 over 4096 lists and ck 400)
+        // more still: read from global memory in each round, the loads
+        // batched
         __syncthreads();
         That = block_radix_kth_glob<NT>(tm, nt, ck, (int*)ebuf, ctl + 2);
     } else {
@@ -4914,10 +4929,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     rv[u] = idx < 16 * n1 ? row[(int64_t)qlist[idx >> 4] * kGroup + (idx & 15)]
                                           : ~0u;
                 }
-                thr = min(thr1, mfma_member_bound(
-                                    Q, block_radix_kth_regs<NT, kRecheckRegV>(rv, ck, (int*)ebuf,
-                                                                              ctl + 2),
-                                    M));
+                const uint32_t t1 = block_radix_kth_regs<NT, kRecheckRegV>(rv, 16 * n1, ck,
+                                                                           (int*)ebuf, ctl + 2);
+                thr = min(thr1, mfma_member_bound(Q, t1, M));
                 exact = true;
             }
         }
