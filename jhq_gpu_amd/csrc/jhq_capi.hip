@@ -92,12 +92,12 @@ struct DBuf {
 constexpr int kSteps = 4;
 
 // Search lanes (workspace, stream, pinned staging) that consecutive batches
-// of one call rotate through.  Four: device-resident searches run as fast as
-// with two (the CUs are then the limit) and host-array searches hide more of
-// their PCIe copies (config 2: 835 k against 748 k queries/s host to host);
-// three ran slower (700 k against 883 k device-resident).
+// of one call rotate through.  Six: each lane's batch is a chain of short,
+// latency-bound kernels, and more chains in flight fill the CUs (config 2,
+// device-resident: 1.35 M queries/s with six lanes, 1.09 M with four, 1.28 M
+// with eight, 1.32 M with twelve; config 5: 695 k with six, 650 k with four).
 #ifndef JHQ_LANES
-#define JHQ_LANES 4
+#define JHQ_LANES 6
 #endif
 constexpr int kLanes = JHQ_LANES;
 static_assert(kLanes >= 1, "at least one lane");
