@@ -138,7 +138,7 @@ int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k,
 int jhq_search_device(jhq_index* idx, const float* d_q, int64_t nq, int k,
                       float* d_dists, int32_t* d_ids, void* stream);
 
-/* Preallocates the search workspace (both pipeline lanes, pinned staging)
+/* Preallocates the search workspace (every pipeline lane, pinned staging)
  * for searches with k <= k_max at the current batch_size, nprobe and alpha
  * — the reference's alloc_workspace (v14/jhq_gpu_index.cu:166-206, called at
  * the end of add(), :531) with the ck/k capacities realloc_ck_buffers
