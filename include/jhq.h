@@ -320,8 +320,11 @@ int jhq_k_final_topk(const float* d_comp_dists, const int32_t* d_topck_pos,
  * capture, serving loops, harnesses that forbid hipMalloc).  Same arguments
  * and results as jhq_k_assign, but the per-row keys live in a fixed device
  * array of 2^20 entries (8 MiB per device, held until the process ends), so
- * n is at most 1048576 (larger n fails with JHQ_EINVAL).  Calls that overlap
- * on one device share that array and race. */
+ * n is at most 1048576 (larger n fails with JHQ_EINVAL).  Calls on one device
+ * share that array, so each call's stream first waits for the previous call's
+ * kernels on that device (one event per device).  Under HIP graph capture no
+ * such wait is recorded: replays that overlap each other or other calls on
+ * one device race on the array. */
 int jhq_k_assign_noalloc(const float* d_y, int64_t n, int d, const float* d_cent,
                          const float* d_cent_norms, int nlist, int32_t* d_assign,
                          void* stream);

@@ -57,3 +57,25 @@ def test_assign_noalloc_rejects_oversize(gpu):
            _VP(i.data_ptr()), None)
     assert rc == jg.JHQ_EINVAL
     assert "at most" in jg.lib().jhq_last_error().decode()
+
+
+def test_assign_noalloc_two_streams_ordered(gpu):
+    """Calls on two streams with no host synchronisation between them: the
+    second call's stream waits for the first call's kernels on the device, so
+    neither reads keys the other wrote."""
+    import torch
+    rng = np.random.default_rng(77)
+    d, nlist = 32, 200
+    cent = rng.standard_normal((nlist, d)).astype(np.float32)
+    norms = po.cent_norms(cent)
+    tc, tn = torch.from_numpy(cent).to(gpu), torch.from_numpy(norms).to(gpu)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    ys = [rng.standard_normal((n, d)).astype(np.float32) for n in (300_000, 200_000, 250_000)]
+    ty = [torch.from_numpy(y).to(gpu) for y in ys]
+    outs = [torch.full((y.shape[0],), -7, dtype=torch.int32, device=gpu) for y in ys]
+    torch.cuda.synchronize()
+    for i, (t, o) in enumerate(zip(ty, outs)):
+        jg.k_assign_noalloc(t, tc, tn, o, stream=sa if i % 2 == 0 else sb)
+    torch.cuda.synchronize()
+    for y, o in zip(ys, outs):
+        assert np.array_equal(o.cpu().numpy(), po.assign(y, cent, norms))
