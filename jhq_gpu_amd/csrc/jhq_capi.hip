@@ -954,31 +954,45 @@ int jhq_set_nprobe(jhq_index* idx, int nprobe) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (nprobe <= 0) return fail(JHQ_EINVAL, "nprobe must be positive");
     JHQ_TRY(idx->quiesce());
+    const int prev = idx->nprobe;
     idx->nprobe = std::min(nprobe, idx->nlist);
-    return reserve_search(idx);
+    const int rc = reserve_search(idx);
+    // a failed reservation keeps the setting the workspace was reserved for
+    // (buffers only grow, so that reservation still holds)
+    if (rc != JHQ_OK) idx->nprobe = prev;
+    return rc;
 }
 
 int jhq_set_alpha(jhq_index* idx, float alpha) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (!(alpha > 0.0f)) return fail(JHQ_EINVAL, "alpha must be positive");
     JHQ_TRY(idx->quiesce());
+    const float prev = idx->alpha;
     idx->alpha = alpha;
-    return reserve_search(idx);
+    const int rc = reserve_search(idx);
+    if (rc != JHQ_OK) idx->alpha = prev;
+    return rc;
 }
 
 int jhq_reserve(jhq_index* idx, int k_max) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (k_max <= 0) return fail(JHQ_EINVAL, "k_max must be positive");
+    const int prev = idx->res_k;
     idx->res_k = std::max(idx->res_k, k_max);
-    return reserve_search(idx);
+    const int rc = reserve_search(idx);
+    if (rc != JHQ_OK) idx->res_k = prev;
+    return rc;
 }
 
 int jhq_set_scan_kind(jhq_index* idx, int kind) {
     if (!idx) return fail(JHQ_EINVAL, "null index");
     if (kind < 0 || kind > 2) return fail(JHQ_EINVAL, "scan kind must be 0, 1 or 2");
     JHQ_TRY(idx->quiesce());
+    const int prev = idx->scan_kind;
     idx->scan_kind = kind;
-    return reserve_search(idx);
+    const int rc = reserve_search(idx);
+    if (rc != JHQ_OK) idx->scan_kind = prev;
+    return rc;
 }
 
 int jhq_get_dims(const jhq_index* idx, int* Ds, int* K1D, int* bpd, int* Kr, int* bpv) {
@@ -1773,8 +1787,11 @@ int jhq_load(const char* path, jhq_index** out) {
     if (rc != JHQ_OK) return done(rc);
     ix->ntotal = n;
     ix->added = ad != 0;
-    rc = reserve_search(ix);
-    if (rc != JHQ_OK) return done(rc);
+    // The index is whole once its lists are uploaded.  If the search
+    // workspace cannot be reserved (out of memory, or a plan that does not fit
+    // in LDS), the index is still returned: host searches reserve what they
+    // need, device searches fail with JHQ_ESTATE until jhq_reserve succeeds.
+    (void)reserve_search(ix);
     *out = ix;
     return JHQ_OK;
 }
