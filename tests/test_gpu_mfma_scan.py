@@ -9,7 +9,9 @@ give the oracle's short list bit for bit, and the same results as the
 byte-LUT scans (scan kind 1) bit for bit.  Cases cover every M the kernel is
 built for up to 128, ck from 10 to 400, lists whose capacity exceeds their
 size (after appends), duplicates that overflow the re-check buffer (the
-streamed fallback), and pipelined device searches.  The cases force the
+streamed fallback), every source of the re-check's first bound (tile minima
+in LDS, in registers, from global memory) and of its exact ck-th value (in
+registers, over the whole row), and pipelined device searches.  The cases force the
 pre-scan (scan kind 2); test_default_choice checks when the default takes it."""
 import sys
 import zlib
@@ -36,8 +38,8 @@ CASES = [
     ("m112_a4", 896, 112, 8, 3, 4.0, 2500, 12, 10, 12),
     ("m128_a10", 1024, 128, 32, 6, 10.0, 3000, 20, 10, 64),
     ("m32_ck400", 256, 32, 8, 4, 4.0, 6000, 12, 100, 16),
-    # 80 K candidates per query: more tiles than the re-check holds in LDS,
-    # so its first bound comes from per-wave minima
+    # 80 K candidates per query: 5,000 tile minima, more than the re-check
+    # holds in LDS (4,096), so they are ranked from registers
     ("m32_wide", 256, 32, 2, 2, 10.0, 80000, 8, 10, 8),
 ]
 IDS = [c[0] for c in CASES]
@@ -187,3 +189,77 @@ def test_default_choice(gpu):
     finally:
         g.set_scan_kind(2)
         g96.set_scan_kind(2)
+
+
+def _from_gpu_lists(g, d):
+    cb = g.codebooks()
+    L = g.lists()
+    o = po.OracleIndex.from_state(d, g.params, cb["P"], cb["c1d"], cb["res_c1d"],
+                                  cb["centroids"], cb["cent_norms"], L["offsets"], L["ids"],
+                                  L["codes"], L["res"], L["corr"])
+    return o, L
+
+
+def test_mfma_recheck_tile_minima_from_global(gpu):
+    """One list of 600,000 vectors probed by every query: 37,500 tiles per
+    query, more tile minima than the re-check ranks in registers (32 per
+    thread x 1024 threads = 32,768), so the bound comes from the radix
+    select over global memory (block_radix_kth_glob).  The short lists must
+    equal the oracle's over the same lists and the byte-LUT scan's."""
+    d, M, n, nq, k = 128, 16, 600_000, 8, 10
+    base, q = queries_and_base(n, nq, d, 64, seed=6060)
+    p = jg.Params(M=M, B=8, Br=4, alpha=10.0, nlist=1, nprobe=1, ivf_iters=4, batch_size=8,
+                  seed=42)
+    g = jg.JHQGpuIndex(d, p)
+    g.train(base[:20_000])
+    g.add(base)
+    g.set_scan_kind(2)
+    assert g.scan_plan(k)[0] == "mfma_scan_kernel"
+    o, L = _from_gpu_lists(g, d)
+    tiles = (np.diff(L["offsets"]) + 15) // 16
+    assert tiles.sum() > 32 * 1024
+    _say("600K flat: stage-wise")
+    gr, _ = _stagewise(g, o, q, k)
+    g.set_scan_kind(1)
+    try:
+        lr = g.search_debug(q, k)
+    finally:
+        g.set_scan_kind(2)
+    _same(gr, lr)
+
+
+def test_mfma_recheck_whole_row_select(gpu):
+    """30,000 copies of the first query vector: for that query the ck
+    smallest I values all tie at the copies' I (their codes minimise the
+    ADC distance), so the ck-th smallest tile minimum is that value and
+    1,875 tiles have a minimum at or below it.  The survivors (over 30,000)
+    exceed the re-check buffer, the tiles exceed what the in-register select
+    holds (1,536 listed tiles, 8 values per thread), so the exact ck-th I
+    comes from the radix select over the whole row (block_radix_kth_row) and
+    the short list from the streamed selection; ties break by stored
+    position.  The other queries take the usual path."""
+    d, M, nlist, nprobe, k = 128, 16, 4, 2, 10
+    base, q = queries_and_base(20_000, 6, d, 8, seed=7070)
+    dup = np.repeat(q[:1], 30_000, axis=0)
+    base = np.ascontiguousarray(np.concatenate([base[:9000], dup, base[9000:]]), np.float32)
+    p = jg.Params(M=M, B=8, Br=4, alpha=4.0, nlist=nlist, nprobe=nprobe, ivf_iters=4,
+                  batch_size=8, seed=42)
+    g = jg.JHQGpuIndex(d, p)
+    g.train(base[:12_000])
+    g.add(base)
+    g.set_scan_kind(2)
+    assert g.scan_plan(k)[0] == "mfma_scan_kernel"
+    o, L = _from_gpu_lists(g, d)
+    # the copies sit in one list, next to each other
+    pos = np.empty(base.shape[0], np.int64)
+    pos[L["ids"]] = np.arange(base.shape[0])
+    dp = pos[9000:39_000]
+    assert dp.max() - dp.min() == 30_000 - 1
+    _say("30K duplicates: stage-wise")
+    gr, _ = _stagewise(g, o, q, k)
+    g.set_scan_kind(1)
+    try:
+        lr = g.search_debug(q, k)
+    finally:
+        g.set_scan_kind(2)
+    _same(gr, lr)

@@ -13,6 +13,9 @@ with exact re-check (forced with scan kind 2) or the byte-LUT scans (scan kind
   from ~256 segments (jhq_v1_plain/search.cu:126-228).
 * Config 3's shape: uint8 rows at D=128, M=16 (Ds=8, K1D=2, the wave scan),
   nlist 1024, nprobe 64, batch 64.
+* Config 4's shape: int8 heavy-tailed rows at D=100, M=25 (Ds=4, K1D=4),
+  nlist 16,384, nprobe 48, batch 32.
+* Config 2 at full size is in tests/test_gpu_fullsize.py.
 
 Each case is checked stage-wise like tests/test_gpu_parity.py: codes and lists
 bit-exact, the top-ck short list bit-exact from the GPU's rotated queries and
@@ -151,3 +154,43 @@ def test_cfg3_shape_uint8(gpu, kind, scan):
         _stagewise(g, o, qb.astype(np.float32), 10)
     finally:
         g.set_scan_kind(0)
+
+
+def test_cfg4_shape_int8(gpu):
+    """Config 4's shape: int8 rows from the heavy-tailed mixture (16 x
+    Student-t, nu = 4) at D=100, M=25 (Ds=4, K1D=4: the wave scan, 25
+    subspaces), nlist 16,384 (probe selection past 8,192 lists), nprobe 48,
+    batch 32.  The GPU-built lists are checked against the oracle's encode and
+    assignment on a sample (the oracle's k-means at this nlist would take
+    hours on the CPU); search is checked stage-wise over the GPU-built lists."""
+    seed = zlib.crc32(b"cfg4_shape") % 10000
+    d, M, nlist, nprobe, batch, k = 100, 25, 16_384, 48, 32, 10
+    xb = byte_mixture(300_000, d, 4096, seed, "int8", comp_seed=seed + 1)
+    qb = byte_mixture(64, d, 4096, seed + 100, "int8", comp_seed=seed + 1)
+    p = jg.Params(M=M, B=8, Br=4, alpha=4.0, nlist=nlist, nprobe=nprobe, ivf_iters=8,
+                  batch_size=batch, seed=42)
+    g = jg.JHQGpuIndex(d, p)
+    _say("build cfg4_shape: n=300000 nlist=16384")
+    g.train(xb)
+    g.add(xb)
+    assert g.scan_plan(k) == ("scan_wave_kernel", 40)
+    cb = g.codebooks()
+    L = g.lists()
+    o = po.OracleIndex.from_state(d, g.params, cb["P"], cb["c1d"], cb["res_c1d"],
+                                  cb["centroids"], cb["cent_norms"], L["offsets"], L["ids"],
+                                  L["codes"], L["res"], L["corr"])
+    pos = np.empty(xb.shape[0], np.int64)
+    pos[L["ids"]] = np.arange(xb.shape[0])
+    ns, na = 20_000, 2_000
+    xf = xb[:ns].astype(np.float32)
+    y = po.rotate(cb["P"], xf)
+    codes = po.primary_encode(y, M, cb["c1d"])
+    res, corr = po.residual_encode(y, codes, M, cb["c1d"], cb["res_c1d"], 4)
+    assert np.array_equal(L["codes"][pos[:ns]], codes)
+    assert np.array_equal(L["res"][pos[:ns]], res)
+    assert np.array_equal(_bits(L["corr"][pos[:ns]]), _bits(corr))
+    asg = po.assign(y[:na], cb["centroids"], cb["cent_norms"])
+    lst = np.searchsorted(L["offsets"], pos[:na], side="right") - 1
+    assert np.array_equal(lst, asg)
+    _say("cfg4_shape: stage-wise search")
+    _stagewise(g, o, qb.astype(np.float32), k)

@@ -104,17 +104,23 @@ def test_append_from_empty_and_add_guard(gpu):
         g.add(base[:10])
 
 
-def test_streaming_config5_shape(gpu):
+@pytest.mark.parametrize("kind,scan", [(2, "mfma_scan_kernel"), (1, "scan_dump_kernel")],
+                         ids=["pre_scan", "byte_lut_dump"])
+def test_streaming_config5_shape(gpu, kind, scan):
     """Config 5's shape at small N: D=768, M=96, per-subspace codebooks
     (Kr=16 each), k=100 with alpha=4 (ck=400), batch 128, inserts in batches
-    interleaved with searches."""
+    interleaved with searches.  Both scans config 5 can take: the pre-scan
+    (what bench.py --config 5 runs; ck 400 > 128, so its short lists go to
+    refine_topk_kernel) and the byte-LUT dump scan with per-query selection."""
     d, M, nlist, nprobe, k = 768, 96, 8, 4, 100
     base, q = queries_and_base(5000, 16, d, 24, seed=909)
     g, o = _pair(d, M, nlist, nprobe, 1, batch=128)
+    g.set_scan_kind(kind)
     g.train(base[:1000])
     o.train(base[:1000])
     g.add(base[:3000])
     o.add(base[:3000])
+    assert g.scan_plan(k) == (scan, 400)
     upto = 3000
     for n in (1000, 1000):
         _stagewise(g, o, q, k)
@@ -122,6 +128,7 @@ def test_streaming_config5_shape(gpu):
         upto += n
         o.add(base[:upto])
         _lists_equal(g, o)
+        assert g.scan_plan(k) == (scan, 400)
     _stagewise(g, o, q, k)
 
 
