@@ -1,25 +1,33 @@
 #!/usr/bin/env python3
 """bench.py — JHQ IVF search throughput on one MI355X.
 
-Workload ("config 2"): N=1,000,000 base and 10,000
-query vectors, D=1024 fp32, drawn from a seeded 10,000-component Gaussian
-mixture (per-component N(0, I) mean, diagonal std log-uniform in [0.1, 1],
-uniform weights) and L2-normalised.  IVF nlist=4096 trained on the first
-100,000 base vectors (the reference demo's protocol), M=128, B=8, Br=4,
-alpha=4, k=10, query batch 64.  Ground truth is exact L2 brute force.
+Default run (the driver's `python bench.py --gpus 1 --steps K --warmup W`):
 
-A "step" is one device search call over the 10,000 queries, resident in device
-memory with their results: the engine runs them in batches of 64 through the
-whole search path (query rotation and centroid scores, probe selection, byte
-LUT, ADC scan + top-ck, refine + final top-k), alternating two workspaces on
-two streams so one batch's refine overlaps the next batch's query product.
-The nprobe sweep {16, 32, 64} picks the fastest setting with recall@10 >= 0.95;
-`value` is that setting's queries/s over exactly --steps timed steps.
+* Headline, BASELINE.json configs[1] ("config 2"): N=1,000,000 base and
+  10,000 query vectors, D=1024 fp32, drawn from a seeded 10,000-component
+  Gaussian mixture (per-component N(0, I) mean, diagonal std log-uniform in
+  [0.1, 1], uniform weights) and L2-normalised.  IVF nlist=4096 trained on the
+  first 100,000 base vectors (the reference demo's protocol), M=128, B=8,
+  Br=4, k=10, query batch 64.  Ground truth is exact L2 brute force.  A
+  "step" is one device search call over the 10,000 queries, resident in HBM
+  with their results: the engine runs them in batches of 64 through the whole
+  search path, consecutive batches on six search lanes (streams forked from
+  and joined into the caller's stream).  The sweep nprobe {16, 32, 64} x
+  alpha {4, 10} picks the fastest point with recall@10 >= 0.95; when no point
+  reaches it (the codes' own recall ceiling, measured by ranking every vector
+  by its full estimate, is below 0.95 on this data) the fastest point within
+  0.001 of the best recall.  `value` is that point's queries/s over exactly
+  --steps timed steps; the host-to-host rate of the reference's protocol
+  (PCIe copies included) is reported beside it.
+* HBM-streaming leg, configs[2] ("config 3"): 100M x 128 uint8, nlist 65,536,
+  nprobe 64, M=16, batch 64 (1.6 GB of codes, streamed from HBM), under
+  `hbm_streaming_leg` with its own roofline, counters and build check.
 
-Also reported: per-kernel HIP-event times, the ADC scan's HBM roofline
-fraction, the reference's host-to-host QPS protocol, and the CPU baseline
-(the oracle's scalar search, one query at a time, on the same GPU-built
-index, timed on this host's cores).
+Each part reports per-kernel HIP-event times, the step's roofline (bytes and
+int8 ops the step must move and compute over the timed pipelined step), the
+measured HBM traffic from the committed counter run, and the CPU baseline
+(the oracle's scalar search on the same GPU-built index, one query at a time
+and over all host threads).  `--config N` runs one configuration alone.
 """
 import argparse
 import json
@@ -49,10 +57,13 @@ def parse():
                     help="timed steps, each one pass over the query set (default: 10; 3 for "
                          "configs 3-5)")
     ap.add_argument("--warmup", type=int, default=0, help="warmup steps (default: 1)")
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
-                    help="BASELINE.json workload: 2 (default, the metric's config), 1 (flat "
+    ap.add_argument("--config", type=int, default=None, choices=(1, 2, 3, 4, 5),
+                    help="BASELINE.json workload alone: 2 (the metric's config), 1 (flat "
                          "100K x 1024, one query per batch), 3 (100M uint8 D=128), 4 (100M "
-                         "int8 D=100), 5 (streaming add + search, D=768)")
+                         "int8 D=100), 5 (streaming add + search, D=768).  Default: config 2, "
+                         "then config 3 as the HBM-streaming leg of the same JSON line")
+    ap.add_argument("--no-hbm-leg", action="store_true",
+                    help="default run: skip the config-3 leg")
     ap.add_argument("--nprobe", type=str, default=None,
                     help="nprobe values swept (default: 16,32,64 for config 2, the config's own "
                          "value otherwise)")
@@ -65,6 +76,11 @@ def parse():
                     help="profiling mode: build the index, run this many search batches at the "
                          "first --nprobe/--alpha plus one 256 MiB device copy (the counter "
                          "calibration kernel), print per-step times and exit")
+    ap.add_argument("--trace-steps", type=int, default=0,
+                    help="kernel-trace mode: build the index, then run one warmup and this many "
+                         "timed device-search calls over the whole query set at the first "
+                         "--nprobe/--alpha (the pipelined step the headline times), print their "
+                         "times and exit")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--index", type=str, default=None,
                     help="configs 3/4 with --profile-batches: load the index from this file "
@@ -140,12 +156,28 @@ def main():
         print("no HIP device visible", file=sys.stderr)
         sys.exit(1)
     torch.backends.cuda.matmul.allow_tf32 = False
-    if args.config in (1, 2):
-        bench_float(args, FLOAT_CFGS[args.config])
+    if args.config is None:
+        # the headline (config 2), then the HBM-streaming workload (config 3,
+        # 1.6 GB of codes, read from HBM) reported under its own key
+        args.config = 2
+        line = bench_float(args, FLOAT_CFGS[2])
+        if not args.no_hbm_leg and args.profile_batches <= 0:
+            import gc
+            gc.collect()
+            torch.cuda.empty_cache()
+            a3 = argparse.Namespace(**vars(args))
+            a3.config, a3.nprobe, a3.alpha, a3.seed = 3, None, None, None
+            a3.cpu_seconds = min(args.cpu_seconds, 10.0)
+            log("HBM-streaming leg: config 3")
+            line["hbm_streaming_leg"] = bench_bytes(a3, LARGE[3])
+    elif args.config in (1, 2):
+        line = bench_float(args, FLOAT_CFGS[args.config])
     elif args.config in (3, 4):
-        bench_bytes(args, LARGE[args.config])
+        line = bench_bytes(args, LARGE[args.config])
     else:
-        bench_streaming(args)
+        line = bench_streaming(args)
+    if line is not None:
+        print(json.dumps(line), flush=True)
 
 
 FLOAT_CFGS = {
@@ -190,7 +222,7 @@ def bench_float(args, cf):
     hq = q.cpu().numpy()
 
     gt = None
-    if args.profile_batches <= 0:
+    if args.profile_batches <= 0 and args.trace_steps <= 0:
         t0 = time.time()
         gt = ground_truth(torch, base, q, K)
         torch.cuda.synchronize()
@@ -216,7 +248,10 @@ def bench_float(args, cf):
 
     if args.profile_batches > 0:
         profile_mode(torch, dev, ix, q, K, BATCH, nprobes[0], alphas[0], args.profile_batches)
-        return
+        return None
+    if args.trace_steps > 0:
+        trace_mode(torch, dev, ix, q, K, BATCH, nprobes[0], alphas[0], args.trace_steps)
+        return None
 
     out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
@@ -260,10 +295,14 @@ def bench_float(args, cf):
     Kst = args.steps if args.steps > 0 else 10
     run_steps(W)
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.time()
+    ev0.record()
     run_steps(Kst)
+    ev1.record()
     torch.cuda.synchronize()
     elapsed = time.time() - t0
+    ev_ms = ev0.elapsed_time(ev1) / Kst
     qps = NQ * Kst / elapsed
     ms_per_step = elapsed * 1000.0 / Kst
     rec = recall_at(out_i.cpu().numpy(), gt, K)
@@ -280,7 +319,7 @@ def bench_float(args, cf):
     step_us = {k2: v * 1000.0 / nbat for k2, v in tm.items()}
     log("per-batch us: " + " ".join(f"{k2}={v:.1f}" for k2, v in step_us.items()))
 
-    roof = scan_roofline(ix, hq, K, BATCH, step_us, cf["name"], npb, alpha,
+    roof = step_roofline(ix, hq, K, BATCH, step_us, ev_ms, cf["name"], npb, alpha,
                          use_profiles=args.scale == 1.0)
 
     # reference protocol: host arrays, warm-up + mean of 5 search() calls
@@ -302,14 +341,19 @@ def bench_float(args, cf):
         cpu = cpu_baseline(ix, npb, alpha, hq, K, out_i.cpu().numpy(), args.cpu_seconds,
                            hb[:n_train], NLIST, n_train)
 
+    metric = METRIC
+    if not gate_met:
+        metric += (" [value: queries/s with queries and results in HBM at recall@10 %.4f; the "
+                   "0.95 gate is above these codes' recall ceiling %.4f]" % (rec, ceiling))
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(qps, 1),
         "unit": "queries/s",
         "n_gpus": 1,
         "steps": Kst,
         "warmup": W,
         "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step_hip_events": round(ev_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -337,11 +381,12 @@ def bench_float(args, cf):
             "build_s": {"create": round(t_create, 2), "train": round(t_train, 2),
                         "add": round(t_add, 2)},
             "step_us_per_batch": {k2: round(v, 2) for k2, v in step_us.items()},
+            "query_product_fp32_mfma": query_product_rate(NQ, nb, D, NLIST, step_us),
         },
         "roofline": roof,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def recall_ceiling(torch, dev, ix, q, gt, k, chunk=65536):
@@ -475,8 +520,9 @@ def recall_tie_aware(dist_ret, gt_d, k=10):
 
 
 def timed_search(torch, ix, q, out_d, out_i, k, batch, warmup, steps):
-    """Queries/s and ms per step; a step is one device search over all of q
-    (the engine batches it by its batch_size)."""
+    """Queries/s, ms per step (host clock) and ms per step from HIP events on
+    the caller's stream around the timed steps; a step is one device search
+    over all of q (the engine batches it by its batch_size)."""
     nq = q.shape[0]
 
     def run(nsteps):
@@ -485,11 +531,14 @@ def timed_search(torch, ix, q, out_d, out_i, k, batch, warmup, steps):
 
     run(warmup)
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.time()
+    ev0.record()
     run(steps)
+    ev1.record()
     torch.cuda.synchronize()
     el = time.time() - t0
-    return nq * steps / el, el * 1000.0 / steps
+    return nq * steps / el, el * 1000.0 / steps, ev0.elapsed_time(ev1) / steps
 
 
 def step_times(torch, ix, q, out_d, out_i, k, batch):
@@ -500,36 +549,87 @@ def step_times(torch, ix, q, out_d, out_i, k, batch):
     return {k2: v * 1000.0 / nbat for k2, v in tm.items()}
 
 
-def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profiles=True):
-    """The scan's roofline figures at the current operating point.
+FP32_MFMA_PEAK_TFLOPS = 157.3
 
-    achieved = algorithmic code bytes per launch (sum over the batch's queries
-    of probed list sizes x M; for the pre-scan, whose re-check refines the
-    short lists in place, plus the refine's bytes) / the scan's HIP-event time
-    per launch; also the
-    scan + refine figure (codes + ck * (bpv + 4 + 4) per query over both
-    kernels' time) and, when a committed counter run matches this operating
-    point, the HBM traffic per launch and the measured limiter."""
+
+def query_product_rate(nq, nb, d, nlist, step_us):
+    """The query product (rotation and centroid scores in one fp32 MFMA
+    product, 2 * B * d * (d + nlist) flops per batch) against the fp32 MFMA
+    peak, over its HIP-event time on one stream."""
+    flops = 2.0 * (nq / nb) * d * (d + nlist)
+    us = step_us["query_gemm"]
+    tf = flops / (us * 1e-6) / 1e12
+    return {"flops_per_batch": int(flops), "us_per_batch": round(us, 2),
+            "achieved_tflops": round(tf, 2), "peak_tflops": FP32_MFMA_PEAK_TFLOPS,
+            "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "note": "HIP events around the query product on one stream (its reduce kernel "
+                    "included)"}
+
+
+def step_roofline(ix, hq, k, batch, step_us, ev_ms_per_step, workload, nprobe, alpha,
+                  use_profiles=True):
+    """The roofline of the search step at the current operating point.
+
+    Time base: one batch's share of the timed pipelined run, ev_ms_per_step /
+    batches per step (HIP events on the caller's stream bracket the timed steps;
+    the engine forks its lanes from that stream and joins them back into it).
+
+    Bytes and ops are what the dominant step's kernels must move and compute:
+    * byte-LUT scans (scan_skew / scan_wave / scan_dump): every probed code is
+      streamed once per query (sum_q sum_probed |l| * M), as the reference's
+      scan does (v14/search.cu:138-151), plus the refine's ck * (bpv + 8)
+      bytes per query;
+    * the integer-MFMA pre-scan: the batch's distinct probed lists once
+      (sum over distinct l of |l| * M), the I-value dump it writes (4 B per
+      padded (query, candidate) slot + 4 B per tile minimum) and the least of
+      it the re-check must read back (the tile minima + the 16 values of ck
+      tiles per query), plus the refine's bytes; its int8 MFMA work is
+      16 x 16 x D multiply-adds x 2 halves per 16-query x 16-candidate tile,
+      priced against 5.0 POP/s.
+    frac is the larger of bytes / time / 8 TB/s and ops / time / 5 POP/s, and
+    `bound` names that roofline.  The counter run committed under profiles/
+    for this operating point gives the measured HBM traffic per launch and
+    what limits the kernels (`limiter`)."""
     dbg = ix.search_debug(hq, k)
     L = ix.lists(include_payload=False)
     sizes = np.diff(L["offsets"]).astype(np.int64)
+    pad = (sizes + 15) // 16
     nq = hq.shape[0]
     nb = (nq + batch - 1) // batch
-    per_launch = float(sizes[dbg["probes"]].sum()) * ix.params.M / nb
-    us = step_us["scan_topck"]
+    M, D = ix.params.M, hq.shape[1]
     kernel, ck = ix.scan_plan(k)
     bpv = ix.dims()["bpv"]
-    # refine reads ck residual codes + correction + id per query
-    refine_bytes = float(nq) / nb * ck * (bpv + 4 + 4)
-    # the pre-scan's re-check refines short lists (ck <= 128) in place: its
-    # scan step then holds the refine's bytes and time (the refine step is
-    # empty)
-    fused = kernel == "mfma_scan_kernel" and ck <= 128
-    step_bytes = per_launch + (refine_bytes if fused else 0.0)
-    ach = step_bytes / (us * 1e-6) / 1e9
-    sr_us = us + (0.0 if fused else step_us["refine_topk"])
-    sr_ach = (per_launch + refine_bytes) / (sr_us * 1e-6) / 1e9
+    probes = dbg["probes"]
+    codes_per_query = float(sizes[probes].sum()) * M / nb       # per batch, counted per query
+    refine = float(nq) * ck * (bpv + 4 + 4) / nb
+    t_batch = ev_ms_per_step * 1e3 / nb                          # us per batch, pipelined
+    mfma = kernel == "mfma_scan_kernel"
+    fused = mfma and ck <= 128
+    alone_us = step_us["scan_topck"] + (0.0 if fused else step_us["refine_topk"])
+    parts = {"refine": refine}
+    ops = 0.0
+    if mfma:
+        distinct = rows = tiles = 0
+        for b in range(nb):
+            lists, cnt = np.unique(probes[b * batch:(b + 1) * batch], return_counts=True)
+            distinct += int(sizes[lists].sum()) * M
+            rows += int((((cnt + 15) // 16) * sizes[lists]).sum()) * M
+            tiles += int((((cnt + 15) // 16) * pad[lists]).sum())
+        qt = pad[probes].sum(1)                                  # tiles per query
+        dump_w = float((qt * 16 * 4 + qt * 4).sum())
+        dump_r = float((qt * 4 + np.minimum(qt, ck) * 16 * 4).sum())
+        parts.update(codes_distinct_lists=distinct / nb, dump_write=dump_w / nb,
+                     dump_read_min=dump_r / nb)
+        ops = tiles / nb * 16.0 * 16.0 * D * 2 * 2
+    else:
+        parts["codes_per_query"] = codes_per_query
+    step_bytes = sum(parts.values())
+    gbs = step_bytes / (t_batch * 1e-6) / 1e9
+    tops = ops / (t_batch * 1e-6) / 1e12
+    f_hbm, f_mfma = gbs / HBM_PEAK_GBS, tops / INT8_PEAK_TOPS
+    bound = "mfma" if f_mfma > f_hbm else "hbm"
     traffic, traffic_note, limiter = None, "no counter run at this operating point", None
+    counters = None
     pdir = os.path.join(ROOT, "profiles")
     for fn in sorted(os.listdir(pdir)) if (use_profiles and os.path.isdir(pdir)) else []:
         if not fn.endswith("_traffic.json"):
@@ -540,69 +640,60 @@ def scan_roofline(ix, hq, k, batch, step_us, workload, nprobe, alpha, use_profil
                 and float(tj.get("alpha")) == float(alpha)
                 and tj.get("workload", "").startswith(workload)):
             traffic = int(tj["traffic_bytes_per_launch"])
-            traffic_note = ("bytes per launch from %s (FETCH_SIZE x %.2f + WRITE_SIZE x %.2f)"
+            traffic_note = ("HBM bytes per launch of the step's kernels from %s (FETCH_SIZE x %.2f "
+                            "+ WRITE_SIZE x %.2f, factors from a copy kernel of known size)"
                             % (tj["source"], tj["fetch_scale"], tj["write_scale"]))
             limiter = tj.get("limiter")
+            counters = tj.get("counters")
     names = {"scan_dump_kernel": "scan_dump_kernel + select_query_kernel",
              "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel"
                                  + (" (re-check and refine)" if fused else "")}
-    extra = {}
-    if kernel == "mfma_scan_kernel":
-        # the pre-scan's integer products: per batch, each probed list's
-        # queries in 16-query tiles against its 16-row groups, two int8
-        # halves of K = d per tile (2 ops per multiply-add)
-        tiles = 0
-        row_bytes = 0
-        for b in range(nb):
-            lists, cnt = np.unique(dbg["probes"][b * batch:(b + 1) * batch], return_counts=True)
-            tiles += int((((cnt + 15) // 16) * ((sizes[lists] + 15) // 16)).sum())
-            row_bytes += int((((cnt + 15) // 16) * sizes[lists]).sum()) * ix.params.M
-        ops = tiles / nb * 16 * 16 * hq.shape[1] * 2 * 2
-        # codes are counted once per (query, probed list), as the reference's
-        # scan streams them; the pre-scan reads a list's rows once per tile of
-        # up to 16 of its queries, so the effective rate can pass the HBM peak
-        extra["achieved_note"] = (
-            "effective bandwidth: codes counted per query; the pre-scan reads each probed "
-            "list once per 16-query tile (row_reads_per_launch)")
-        extra["row_reads_per_launch"] = {
-            "bytes": int(row_bytes / nb),
-            "achieved": round(row_bytes / nb / (us * 1e-6) / 1e9, 1),
-            "frac": round(row_bytes / nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        }
-        extra["int8_mfma"] = {
-            "tiles_per_launch": round(tiles / nb, 1),
-            "ops_per_launch": int(ops),
-            "achieved_tops": round(ops / (us * 1e-6) / 1e12, 2),
-            "peak_tops": INT8_PEAK_TOPS,
-            "frac": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 5),
-            "note": "ops over the scan step's time (plan + tiles + re-check)",
-        }
-    return {
+    out = {
         "kernel": names.get(kernel, kernel),
         "dominant_step": max(step_us, key=step_us.get),
-        # the roofline the scan is measured against: it streams each probed
-        # code once per query (HBM-bound by design); the counter run, where
-        # present, names what limits it in practice
-        "bound": "hbm",
-        "achieved": round(ach, 1),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(ach / HBM_PEAK_GBS, 4),
+        "bound": bound,
+        "achieved": round(tops if bound == "mfma" else gbs, 2 if bound == "mfma" else 1),
+        "peak": INT8_PEAK_TOPS if bound == "mfma" else HBM_PEAK_GBS,
+        "unit": "TOP/s" if bound == "mfma" else "GB/s",
+        "frac": round(max(f_hbm, f_mfma), 4),
         "traffic": traffic,
+        "time_base": "us per batch in the timed pipelined run: HIP events on the caller's "
+                     "stream around the timed steps / batches per step",
+        "us_per_batch_pipelined": round(t_batch, 2),
+        "algorithmic_bytes_per_batch": int(step_bytes),
+        "bytes_breakdown": {k2: int(v) for k2, v in parts.items()},
+        "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "frac": round(f_hbm, 4)},
         "traffic_note": traffic_note,
-        "measured_limiter": limiter,
-        "algorithmic_bytes_per_launch": int(step_bytes),
-        "avg_launch_us": round(us, 2),
-        "scan_plus_refine": {
-            "bytes_per_batch": int(per_launch + refine_bytes),
-            "us_per_batch": round(sr_us, 2),
-            "achieved": round(sr_ach, 1),
-            "frac": round(sr_ach / HBM_PEAK_GBS, 4),
-            "definition": "(sum_q sum_probed |l| * M + sum_q ck * (bpv + 8)) / (scan + refine "
-                          "kernel time)",
+        "traffic_rate_over_step_gbs": (None if traffic is None
+                                       else round(traffic / (t_batch * 1e-6) / 1e9, 1)),
+        "limiter": limiter,
+        "counters": counters,
+        "kernel_alone": {
+            "us_per_launch": round(alone_us, 2),
+            "note": "the step's kernels on one stream (HIP events in a separate timing pass); "
+                    "in the pipelined run other lanes' kernels run beside them",
+            "frac_hbm": round(step_bytes / (alone_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         },
-        **extra,
     }
+    if mfma:
+        out["int8_mfma"] = {"ops_per_batch": int(ops), "achieved_tops": round(tops, 2),
+                            "peak_tops": INT8_PEAK_TOPS, "frac": round(f_mfma, 4)}
+        out["tile_row_reads_per_batch"] = int(rows / nb)
+        out["effective_per_query_codes"] = {
+            "bytes_per_batch": int(codes_per_query),
+            "gbs_over_step": round(codes_per_query / (t_batch * 1e-6) / 1e9, 1),
+            "note": "codes counted once per (query, probed list) as the reference's scan "
+                    "streams them; the pre-scan reads each list once per 16-query tile, so "
+                    "this is an effective rate, not a bandwidth",
+        }
+    else:
+        out["scan_kernel_alone"] = {
+            "us_per_launch": round(step_us["scan_topck"], 2),
+            "codes_bytes_per_launch": int(codes_per_query),
+            "frac_hbm": round(codes_per_query / (step_us["scan_topck"] * 1e-6) / 1e9
+                              / HBM_PEAK_GBS, 4),
+        }
+    return out
 
 
 def bench_bytes(args, cf):
@@ -618,7 +709,8 @@ def bench_bytes(args, cf):
     npb = int((args.nprobe or str(cf["NPROBE"])).split(",")[0])
     alpha = float((args.alpha or "4").split(",")[0])
 
-    if args.profile_batches > 0 and args.index and os.path.exists(args.index):
+    if (args.profile_batches > 0 or args.trace_steps > 0) and args.index and \
+            os.path.exists(args.index):
         # counter runs over a saved index: only the queries are generated
         _, means = gen_bytes(torch, dev, 0, D, NCOMP, seed, cf["kind"])
         qb, _ = gen_bytes(torch, dev, NQ, D, NCOMP, seed + 0x100, cf["kind"], means)
@@ -626,8 +718,11 @@ def bench_bytes(args, cf):
         ix = jg.JHQGpuIndex.load(args.index)
         ix.set_scan_kind(args.scan_kind)
         log(f"loaded {args.index} ({ix.ntotal} vectors) in {time.time() - t0:.1f}s")
-        profile_mode(torch, dev, ix, qb.float(), K, BATCH, npb, alpha, args.profile_batches)
-        return
+        if args.trace_steps > 0:
+            trace_mode(torch, dev, ix, qb.float(), K, BATCH, npb, alpha, args.trace_steps)
+        else:
+            profile_mode(torch, dev, ix, qb.float(), K, BATCH, npb, alpha, args.profile_batches)
+        return None
     t0 = time.time()
     base, means = gen_bytes(torch, dev, N, D, NCOMP, seed, cf["kind"])
     qb, _ = gen_bytes(torch, dev, NQ, D, NCOMP, seed + 0x100, cf["kind"], means)
@@ -641,7 +736,7 @@ def bench_bytes(args, cf):
     qf = qb.float()
     log(f"host copy {time.time() - t0:.1f}s")
 
-    if args.profile_batches <= 0:
+    if args.profile_batches <= 0 and args.trace_steps <= 0:
         t0 = time.time()
         gt_i, gt_d = ground_truth_int(torch, base, qf)
         torch.cuda.synchronize()
@@ -662,22 +757,25 @@ def bench_bytes(args, cf):
     log(f"add {t_add:.1f}s ({N / t_add / 1e6:.2f} M vectors/s)")
     x_sample = np.ascontiguousarray(hb[:min(N, 1_000_000)])
     del hb
-    if args.profile_batches > 0:
+    if args.profile_batches > 0 or args.trace_steps > 0:
         del base
         torch.cuda.empty_cache()
         if args.index:
             t0 = time.time()
             ix.save(args.index)
             log(f"saved {args.index} in {time.time() - t0:.1f}s")
-        profile_mode(torch, dev, ix, qf, K, BATCH, npb, alpha, args.profile_batches)
-        return
+        if args.trace_steps > 0:
+            trace_mode(torch, dev, ix, qf, K, BATCH, npb, alpha, args.trace_steps)
+        else:
+            profile_mode(torch, dev, ix, qf, K, BATCH, npb, alpha, args.profile_batches)
+        return None
 
     out_d = torch.empty((NQ, K), dtype=torch.float32, device=dev)
     out_i = torch.empty((NQ, K), dtype=torch.int32, device=dev)
     nb = (NQ + BATCH - 1) // BATCH
     W = args.warmup if args.warmup > 0 else 1
     Kst = args.steps if args.steps > 0 else 3
-    qps, ms = timed_search(torch, ix, qf, out_d, out_i, K, BATCH, W, Kst)
+    qps, ms, ev_ms = timed_search(torch, ix, qf, out_d, out_i, K, BATCH, W, Kst)
     ids = out_i.cpu().numpy()
     rec = recall_at(ids, gt_i, K)
     rec_tie = recall_tie_aware(exact_dists(torch, base, qf, ids), gt_d, K)
@@ -686,7 +784,8 @@ def bench_bytes(args, cf):
         f"tie-aware={rec_tie:.4f} 10@100={rec_ref:.4f}")
     step_us = step_times(torch, ix, qf, out_d, out_i, K, BATCH)
     log("per-batch us: " + " ".join(f"{k2}={v:.1f}" for k2, v in step_us.items()))
-    roof = scan_roofline(ix, hq.astype(np.float32), K, BATCH, step_us, cf["name"], npb, alpha)
+    roof = step_roofline(ix, hq.astype(np.float32), K, BATCH, step_us, ev_ms, cf["name"], npb,
+                         alpha, use_profiles=args.scale == 1.0)
     used, cap = ix.pool()
     cpu = None
     if not args.no_cpu_baseline:
@@ -696,7 +795,8 @@ def bench_bytes(args, cf):
         "metric": f"QPS ({N // 1_000_000}Mx{D} {cf['kind']} IVF, nprobe {npb}, batch {BATCH}); "
                   "ADC-scan HBM GB/s vs peak",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": Kst, "warmup": W,
-        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "ms_per_step": round(ms, 5), "ms_per_step_hip_events": round(ev_ms, 5),
+        "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": f"synthetic: seeded {NCOMP}-component {cf['kind']} mixture (torch Philox), "
                 f"zero fraction {zero_frac:.3f}",
@@ -711,11 +811,12 @@ def bench_bytes(args, cf):
             "build_s": {"train": round(t_train, 2), "add": round(t_add, 2)},
             "pool_slots": [used, cap],
             "step_us_per_batch": {k2: round(v, 2) for k2, v in step_us.items()},
+            "query_product_fp32_mfma": query_product_rate(NQ, nb, D, NLIST, step_us),
         },
         "roofline": roof,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 # ---------------------------------------------------------------------------
@@ -821,7 +922,7 @@ def bench_streaming(args):
 
     W = args.warmup if args.warmup > 0 else 1
     Kst = args.steps if args.steps > 0 else 3
-    qps, ms = timed_search(torch, ix, q, out_d, out_i, K, BATCH, W, Kst)
+    qps, ms, ev_ms = timed_search(torch, ix, q, out_d, out_i, K, BATCH, W, Kst)
     t0 = time.time()
     gt = ground_truth_f32(torch, base, q)
     log(f"ground truth {time.time() - t0:.1f}s")
@@ -832,13 +933,15 @@ def bench_streaming(args):
         f"recall@100={rec100:.4f}")
     step_us = step_times(torch, ix, q, out_d, out_i, K, BATCH)
     log("per-batch us: " + " ".join(f"{k2}={v:.1f}" for k2, v in step_us.items()))
-    roof = scan_roofline(ix, q.cpu().numpy(), K, BATCH, step_us, "cfg5", npb, alpha)
+    roof = step_roofline(ix, q.cpu().numpy(), K, BATCH, step_us, ev_ms, "cfg5", npb, alpha,
+                         use_profiles=sc == 1.0)
     used, cap = ix.pool()
     line = {
         "metric": "QPS after streaming add (11Mx768 IVF, nprobe 32, k=100, batch 128); "
                   "ADC-scan HBM GB/s vs peak",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": Kst, "warmup": W,
-        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "ms_per_step": round(ms, 5), "ms_per_step_hip_events": round(ev_ms, 5),
+        "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32",
         "data": "synthetic: seeded 10k-component Gaussian mixture, L2-normalised (torch Philox)",
         "config": {
@@ -860,7 +963,32 @@ def bench_streaming(args):
         "roofline": roof,
         "cpu_baseline": None,
     }
-    print(json.dumps(line), flush=True)
+    return line
+
+
+def trace_mode(torch, dev, ix, q, k, batch, nprobe, alpha, nsteps):
+    """The headline's timed step alone, for a kernel trace: one warmup and
+    `nsteps` device searches over all of q (batches pipelined on the lanes),
+    each bracketed by a host synchronisation so the trace shows whole calls."""
+    ix.set_nprobe(nprobe)
+    ix.set_alpha(alpha)
+    nq = q.shape[0]
+    out_d = torch.empty((nq, k), dtype=torch.float32, device=dev)
+    out_i = torch.empty((nq, k), dtype=torch.int32, device=dev)
+    ix.search_device(q, k, out_d, out_i)
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(nsteps):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        ix.search_device(q, k, out_d, out_i)
+        ev1.record()
+        torch.cuda.synchronize()
+        ms.append(ev0.elapsed_time(ev1))
+    print(json.dumps({"trace_steps": nsteps, "nprobe": nprobe, "alpha": alpha, "nq": nq,
+                      "batches_per_step": (nq + batch - 1) // batch,
+                      "scan_kernel": ix.scan_plan(k)[0],
+                      "ms_per_step_hip_events": [round(x, 4) for x in ms]}), flush=True)
 
 
 def profile_mode(torch, dev, ix, q, k, batch, nprobe, alpha, nbatches):
