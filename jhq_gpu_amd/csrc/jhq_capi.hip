@@ -732,6 +732,23 @@ int ensure_host_staging(jhq_index* ix, int l, int Bmax, int k) {
     return JHQ_OK;
 }
 
+// The skewed code copy serves only the byte-LUT scan of M % 32 == 0.  A
+// device search plans its batches at the index's batch size with its own k
+// (k <= res_k), so when the pre-scan is the scan for every such k no device
+// search reads the copy: it is then neither built nor refreshed at
+// reservation (appends at config 5's shape skip it), and a host search that
+// needs it refreshes it itself.
+bool skew_needed(jhq_index* ix) {
+    if (!skew_eligible(ix)) return false;
+    const int P = std::min(ix->nprobe, ix->nlist);
+    for (int k = 1; k <= ix->res_k; k++) {
+        bool mf = false;
+        if (mfma_choose(ix, ix->batch_size, P, ceil_ck(ix->alpha, k), true, &mf) != JHQ_OK || !mf)
+            return true;
+    }
+    return false;
+}
+
 // Preallocates everything a search with k <= res_k needs (the reference's
 // alloc_workspace at the end of add(), v14/jhq_gpu_index.cu:166-206,531, and
 // realloc_ck_buffers, v14/search.cu:294-313): every lane's workspace, stream
@@ -741,7 +758,7 @@ int ensure_host_staging(jhq_index* ix, int l, int Bmax, int k) {
 int reserve_search(jhq_index* ix) {
     if (ix->ntotal == 0 || !ix->trained) return JHQ_OK;
     JHQ_TRY(ix->quiesce());
-    if (skew_eligible(ix) && ix->skew_stale) JHQ_TRY(refresh_skew(ix));
+    if (ix->skew_stale && skew_needed(ix)) JHQ_TRY(refresh_skew(ix));
     if (rows_wanted(ix) && ix->rows_stale) JHQ_TRY(refresh_rows(ix));
     BatchPlan bp;
     JHQ_TRY(plan_batch(ix, ix->batch_size, ix->res_k, &bp, kLanes, true));
@@ -1455,8 +1472,9 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     if (nq == 0) return JHQ_OK;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ix->stream;
     const int Bmax = ix->batch_size;
-    // several batches: alternate two workspaces on two streams forked from s
-    // and joined back into it (step timing keeps one stream)
+    // several batches: rotate through the search lanes (workspace and stream
+    // each), forked from s and joined back into it (step timing keeps one
+    // stream)
     const bool pipe = nq > Bmax && !ix->timing;
     // enqueue-only: the reserved workspace must cover this shape (no
     // allocation, no host synchronisation)
