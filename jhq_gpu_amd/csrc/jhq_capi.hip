@@ -103,9 +103,10 @@ constexpr int kSteps = 4;
 constexpr int kLanes = JHQ_LANES;
 static_assert(kLanes >= 1, "at least one lane");
 
-// Per-batch search buffers (v14/search.cuh:24-46).  The index keeps two sets:
-// consecutive batches of one device search alternate between them on two
-// streams, so one batch's refine overlaps the next batch's query product.
+// Per-batch search buffers (v14/search.cuh:24-46).  The index keeps one set
+// per search lane (kLanes): consecutive batches of one device search take the
+// lanes in turn, each lane a stream of its own, so one batch's scan overlaps
+// the other lanes' query products, plans and re-checks.
 struct Workspace {
     DBuf<float> wq, wqrot, wscores, wout_d;
     DBuf<int32_t> wprobes, wgofs, wqtot, wout_i, wpslot;

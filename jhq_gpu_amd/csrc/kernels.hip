@@ -3543,14 +3543,20 @@ hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const
 }
 
 // The refine's 8-byte-piece path: 4-bit codes, 16 | d, rows of whole pieces,
-// at most 4 pieces per lane (d <= 1024).  Its table of squared differences
-// pads each piece's 256 words by 4, so that the 16 lanes of a candidate,
-// reading pieces 16 apart, start 4 banks apart.
-constexpr int kRefineTabPiece = 16 * 16 + 4;
+// at most 4 pieces per lane (d <= 1024).  Its table of squared differences is
+// code-major: the entry of code c and dimension 16 p + e sits at
+// c * refine_tab_row(d) + 17 p + e (one pad word per piece; a row is a
+// multiple of 64 words, so every code's row starts on bank 0).  Lane l16 of
+// candidate group g (the four groups of a wave) takes its pieces l16 + 16 u
+// in the order u = g, g + 1, ... (mod its piece count), so at every step the
+// wave's 64 reads fall on banks 17 l16 + 16 u + e (mod 64), all distinct
+// whatever the codes (reading pieces in the same order in every group put up
+// to four lanes on one bank).
 __host__ __device__ inline bool refine_pieces(int d, int Br, int bpv) {
     return Br == 4 && d % 16 == 0 && bpv % 8 == 0 && d <= 1024;
 }
-__host__ __device__ inline int refine_tab_words(int d) { return d / 16 * kRefineTabPiece; }
+__host__ __device__ inline int refine_tab_row(int d) { return (d / 16 * 17 + 63) / 64 * 64; }
+__host__ __device__ inline int refine_tab_words(int d) { return 16 * refine_tab_row(d); }
 
 // Residual refine and final top-k of one query's exact short list (the
 // ksel keys in S.kout, ascending, with their pool slots in kslot):
@@ -3577,14 +3583,49 @@ __device__ __forceinline__ void refine_short_list(
     };
     const bool pieces = refine_pieces(d, Br, bpv);
     if (!pieces) tab = nullptr;
+    const int grp = tid >> 4, l16 = tid & 15;
+    constexpr int NG = NT / 16;
+    // 4-bit codes in 8-byte pieces of 16 dimensions: lane l16 of a candidate
+    // sums its np pieces l16 + 16 up[u], u = 0 .. np-1, up[u] = (u + g) mod np
+    // with g = grp mod 4 (a load of the 16 lanes reads 128 contiguous bytes
+    // of the candidate); each round's pieces, correction and id are
+    // requested while the round before it is summed
+    const int npc = d >> 4;
+    const int np = pieces && l16 < npc ? (npc - 1 - l16) / 16 + 1 : 0;
+    // (u + g) mod np for u < np <= 4, g < 4
+    auto upiece = [&](int u) -> int {
+        int v = u + (grp & 3);
+        if (v >= np) v -= np;
+        if (v >= np) v -= np;
+        if (v >= np) v -= np;
+        return v;
+    };
+    uint2 pwc[4], pwn[4];
+    float pcorr_c = 0.0f, pcorr_n = 0.0f;
+    int pid_c = 0, pid_n = 0;
+    auto pfetch = [&](int base, uint2 (&w)[4], float& corr, int& id) {
+        const int c = base + grp;
+        if (c < ksel) {
+            const int pos = kslot[c];
+            const uint2* rp = (const uint2*)(list_res + (int64_t)pos * bpv) + l16;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (u < np) w[u] = rp[16 * upiece(u)];
+            if (l16 == 0) {
+                corr = list_corr[pos];
+                id = list_ids[pos];
+            }
+        }
+    };
+    const int trow = refine_tab_row(d);
     if (tab) {
         // (q_j - codeword c)^2, rounded as the sum below rounds it, at
-        // tab[(j / 16) * kRefineTabPiece + (j % 16) * 16 + c]
-        for (int i = tid; i < 16 * d; i += NT) {
-            const int j = i >> 4, c = i & 15;
-            const float df = sq[j + (j >> 5)] - rc[cbo(j) + c];
-            tab[(j >> 4) * kRefineTabPiece + (j & 15) * 16 + c] = df * df;
-        }
+        // tab[c * trow + (j / 16) * 17 + j % 16]
+        for (int c = 0; c < 16; c++)
+            for (int j = tid; j < d; j += NT) {
+                const float df = sq[j + (j >> 5)] - rc[cbo(j) + c];
+                tab[c * trow + (j >> 4) * 17 + (j & 15)] = df * df;
+            }
     }
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
@@ -3600,8 +3641,6 @@ __device__ __forceinline__ void refine_short_list(
 
     // residual refine: 16 lanes per candidate, each summing its share of the
     // dimensions, then a fixed xor tree adds the 16 partial sums.
-    const int grp = tid >> 4, l16 = tid & 15;
-    constexpr int NG = NT / 16;
     const int dpc = (Br == 4) ? 32 : 16;  // dimensions per 16-byte chunk
     const bool vec = (bpv % 16) == 0 && (d % dpc) == 0;
     int chk = (d + 15) / 16;
@@ -3631,32 +3670,13 @@ __device__ __forceinline__ void refine_short_list(
         }
     };
     if (pieces) {
-        // 4-bit codes in 8-byte pieces of 16 dimensions: lane l16 sums pieces
-        // l16, l16 + 16, ... in order (a load of the 16 lanes reads 128
-        // contiguous bytes of the candidate); the next round's pieces,
-        // correction and id are loaded while this round is summed
-        const int npc = d >> 4;
-        const int np = l16 < npc ? (npc - 1 - l16) / 16 + 1 : 0;
-        uint2 wc[4], wn[4];
-        float corr_c = 0.0f, corr_n = 0.0f;
-        int id_c = 0, id_n = 0;
-        auto fetch = [&](int base, uint2 (&w)[4], float& corr, int& id) {
-            const int c = base + grp;
-            if (c < ksel) {
-                const int pos = cpos[c];
-                const uint2* rp = (const uint2*)(list_res + (int64_t)pos * bpv) + l16;
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-                    if (u < np) w[u] = rp[16 * u];
-                if (l16 == 0) {
-                    corr = list_corr[pos];
-                    id = list_ids[pos];
-                }
-            }
-        };
-        fetch(0, wc, corr_c, id_c);
+        uint2(&wc)[4] = pwc;
+        uint2(&wn)[4] = pwn;
+        float &corr_c = pcorr_c, &corr_n = pcorr_n;
+        int &id_c = pid_c, &id_n = pid_n;
+        pfetch(0, wc, corr_c, id_c);
         for (int base = 0; base < ksel; base += NG) {
-            if (base + NG < ksel) fetch(base + NG, wn, corr_n, id_n);
+            if (base + NG < ksel) pfetch(base + NG, wn, corr_n, id_n);
             const int c = base + grp;
             const bool valid = c < ksel;
             float sres = 0.0f;
@@ -3666,21 +3686,27 @@ __device__ __forceinline__ void refine_short_list(
             int lv = l16;
             asm volatile("" : "+v"(lv));
             if (valid && tab) {
+                // LDS byte addresses: code c's entry is one 24-bit
+                // multiply-add from the piece's base
+                typedef __attribute__((address_space(3))) const char lds_cchar;
+                const uint32_t rowb = 4u * (uint32_t)trow;
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     if (u < np) {
-                        const float* tp = tab + (lv + 16 * u) * kRefineTabPiece;
+                        lds_cchar* tp = (lds_cchar*)(tab + (lv + 16 * upiece(u)) * 17);
                         const uint32_t ww[2] = {wc[u].x, wc[u].y};
 #pragma unroll
-                        for (int e = 0; e < 16; e++)
-                            sres = sres + tp[e * 16 + ((ww[e >> 3] >> (4 * (e & 7))) & 15u)];
+                        for (int e = 0; e < 16; e++) {
+                            const uint32_t c = (ww[e >> 3] >> (4 * (e & 7))) & 15u;
+                            sres = sres + *(__attribute__((address_space(3))) const float*)(tp + __umul24(c, rowb) + 4 * e);
+                        }
                     }
                 }
             } else if (valid) {
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     if (u < np) {
-                        const int pc = lv + 16 * u;
+                        const int pc = lv + 16 * upiece(u);
                         const uint32_t ww[2] = {wc[u].x, wc[u].y};
 #pragma unroll
                         for (int e = 0; e < 16; e++) {
@@ -4260,6 +4286,16 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
 }
 
 constexpr int kMfmaPD = 4;  // tiles in flight per wave
+// The minimum over each 16-lane row, on every lane of the row: swaps within
+// quads, then rotations by 4 and 8 inside the row (DPP operands of v_min, no
+// LDS round trips as a shuffle through ds_bpermute would take).
+__device__ __forceinline__ uint32_t row16_min_u32(uint32_t v) {
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false));   // quad [1,0,3,2]
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false));   // quad [2,3,0,1]
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false));  // row_ror:4
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));  // row_ror:8
+    return v;
+}
 // One 16-candidate tile: the lane's code dwords cw (row j of the tile,
 // subspaces GS h .. GS h + GS - 1, four to a dword), the bit planes, two
 // int8 MFMA chains (hi and lo halves of the query steps), and the biased
@@ -4295,15 +4331,10 @@ __device__ __forceinline__ void mfma_tile(const uint32_t (&cw)[M / 16], int h, i
     if (d2 >= 0) dump[d2 + j] = v2;
     if (d3 >= 0) dump[d3 + j] = v3;
     // each row's minimum over the tile's 16 candidates (the lanes of one
-    // group): the re-check bounds its ck-th smallest value from these
-    uint32_t m0 = v0, m1 = v1, m2 = v2, m3 = v3;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        m0 = min(m0, (uint32_t)__shfl_xor((int)m0, o));
-        m1 = min(m1, (uint32_t)__shfl_xor((int)m1, o));
-        m2 = min(m2, (uint32_t)__shfl_xor((int)m2, o));
-        m3 = min(m3, (uint32_t)__shfl_xor((int)m3, o));
-    }
+    // group, one DPP row): the re-check bounds its ck-th smallest value from
+    // these
+    const uint32_t m0 = row16_min_u32(v0), m1 = row16_min_u32(v1);
+    const uint32_t m2 = row16_min_u32(v2), m3 = row16_min_u32(v3);
     if (j == 0) {
         if (d0 >= 0) tmin[d0 / 16] = m0;
         if (d1 >= 0) tmin[d1 / 16] = m1;
@@ -4316,12 +4347,11 @@ __device__ __forceinline__ void mfma_tile(const uint32_t (&cw)[M / 16], int h, i
 // layout of v_mfma_i32_16x16x64_i8: A and B bytes of one lane cover the same
 // 16 dimensions; result register v of lane l is query row 4 (l / 16) + v,
 // candidate l % 16).  Each wave walks its share of the batch's tiles group by
-// group (no shared counter).  A tile of 16 candidates is M rows of 16 code
-// bytes; each row arrives with one 16-byte load, kMfmaPD tiles ahead, and is
-// written to the wave's LDS ring (rows of lane group h start one row apart,
-// so the 16 addresses a read touches sit in distinct banks).  A lane's code
-// bytes for its candidate are four LDS dwords and a 4x4 byte transpose
-// (v_perm_b32); bit plane k of a code dword is (w >> k) & 0x01010101.
+// group (no shared counter).  A tile of 16 candidates is 16 rows of M code
+// bytes in the row-major copy; lane (j, h) loads its candidate j's M / 4
+// bytes for subspaces GS h .. GS h + GS - 1 straight into registers,
+// kMfmaPD tiles ahead (no LDS); bit plane k of a code dword is
+// (w >> k) & 0x01010101.
 // The lane's code dwords of one tile row from the row-major copy: GS = M / 4
 // bytes (ND dwords) at p, as 16-byte loads where GS is a multiple of 16.
 template <int M>
@@ -4745,6 +4775,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     const float cv = tid < K1D ? c1d[tid] : 0.0f;
     const int4 Lv = tid < P ? ldesc[probes[(int64_t)b * P + tid]] : make_int4(0, 0, 0, 0);
     const int gv = tid <= P ? gofs[(int64_t)b * (P + 1) + tid] : 0;
+    // the residual codebooks for the refine, requested now as well
+    const float rcv = FUSE && tid < RC * Kr ? res_c1d[tid] : 0.0f;
     const MfmaQS Q = qs[b];
     const int64_t n = (int64_t)qi.z * kGroup;
     const uint32_t* row = dump + qi.x;
@@ -4762,24 +4794,40 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     if (tid == 0) ctl[0] = 0;
     stream_begin<NT>(S);
     // pass 1: an upper bound of the ck-th smallest I from the tile minima
-    // (each is an I value of its own tile): their exact ck-th smallest, from
-    // an LDS copy when they fit there, else from global memory
+    // (each is an I value of its own tile): with a minimum on every lane, a
+    // bound from the waves' lane minima; otherwise their exact ck-th
+    // smallest, from an LDS copy when they fit there, else from registers or
+    // global memory
     const uint32_t* tm = tmin + qi.x / kGroup;
     const int nt = qi.z;
     uint32_t That = ~0u;
     const bool tiles_in_lds = nt >= ck && nt <= 2 * kRecheckCap;
     if (tiles_in_lds) {
         uint32_t* tl = (uint32_t*)mp;  // mp and mc, free until the members
-        for (int i0 = tid; i0 < nt; i0 += 4 * NT) {
-            uint32_t v[4];
+        constexpr int TU = (2 * kRecheckCap + NT - 1) / NT;
+        uint32_t v[TU], lmin = ~0u;
 #pragma unroll
-            for (int u = 0; u < 4; u++) v[u] = i0 + u * NT < nt ? tm[i0 + u * NT] : 0u;
+        for (int u = 0; u < TU; u++) v[u] = tid + u * NT < nt ? tm[tid + u * NT] : ~0u;
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (i0 + u * NT < nt) tl[i0 + u * NT] = v[u];
+        for (int u = 0; u < TU; u++) {
+            if (tid + u * NT < nt) tl[tid + u * NT] = v[u];
+            lmin = min(lmin, v[u]);
         }
-        __syncthreads();
-        That = block_radix_kth<NT>([&](int i) { return tl[i]; }, nt, ck, (int*)ebuf, ctl + 2);
+        if (nt >= NT && ck <= 64 * NW) {
+            // every lane holds a tile minimum: each wave takes the r-th
+            // smallest of its lane minima (r = ceil(ck / waves), so r lanes,
+            // r distinct tiles, hold an I at or below it) and the largest of
+            // those bounds the ck-th smallest I: no block-wide rounds
+            const uint32_t wk = wave_kth_u32(lmin, (ck + NW - 1) / NW);
+            if (lane == 0) wsum[wv] = (int)wk;
+            __syncthreads();
+            That = 0u;
+#pragma unroll
+            for (int w = 0; w < NW; w++) That = max(That, (uint32_t)wsum[w]);
+        } else {
+            __syncthreads();
+            That = block_radix_kth<NT>([&](int i) { return tl[i]; }, nt, ck, (int*)ebuf, ctl + 2);
+        }
     } else if (nt >= ck && nt <= kRecheckTR * NT) {
         // more tile minima than LDS holds (a per-wave bound here leaves
         // thousands of candidates with nprobe 32 over 4096 lists and ck 400):
@@ -5117,7 +5165,11 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                 slot = meta[4 * q] + (tag - meta[4 * q + 3]);
         kslot[i] = slot;
     }
-    for (int i = tid; i < RC * Kr; i += NT) rcb[i] = res_c1d[i];
+    if (RC * Kr <= NT) {
+        if (tid < RC * Kr) rcb[tid] = rcv;
+    } else {
+        for (int i = tid; i < RC * Kr; i += NT) rcb[i] = res_c1d[i];
+    }
     for (int i = tid; i < d; i += NT) sqp[i + (i >> 5)] = sq[i];
     __syncthreads();
     JHQ_PHASE(10);
