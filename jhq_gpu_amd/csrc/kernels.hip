@@ -1782,6 +1782,52 @@ __device__ __forceinline__ void block_exclusive_scan(F f, int B, int* out, int* 
     __syncthreads();
 }
 
+// Two exclusive prefixes at once: out0 / out1[0..n] of f(i).x / f(i).y
+// (one pass, one pair of barriers); wsum: 2 * NT / 64 ints.
+template <int NT, class F>
+__device__ __forceinline__ void block_exclusive_scan2(F f, int n, int* out0, int* out1, int* wsum) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int per = (n + NT - 1) / NT;
+    const int s0 = min(n, tid * per), s1 = min(n, s0 + per);
+    int a = 0, c = 0;
+    for (int i = s0; i < s1; i++) {
+        const int2 v = f(i);
+        a += v.x;
+        c += v.y;
+    }
+    int ia = a, ic = c;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int ta = __shfl_up(ia, off), tc = __shfl_up(ic, off);
+        if (lane >= off) {
+            ia += ta;
+            ic += tc;
+        }
+    }
+    if (lane == 63) {
+        wsum[w] = ia;
+        wsum[NW + w] = ic;
+    }
+    __syncthreads();
+    int xa = ia - a, xc = ic - c;
+    for (int j = 0; j < w; j++) {
+        xa += wsum[j];
+        xc += wsum[NW + j];
+    }
+    for (int i = s0; i < s1; i++) {
+        const int2 v = f(i);
+        out0[i] = xa;
+        out1[i] = xc;
+        xa += v.x;
+        xc += v.y;
+    }
+    if (tid == NT - 1) {
+        out0[n] = xa;
+        out1[n] = xc;
+    }
+    __syncthreads();
+}
+
 // Each query's span starts with ov virtual groups, which stand for the cost of
 // a segment (its LUT build and merge): a workgroup whose range crosses into a
 // new query gets that many fewer real groups.  In these units query b spans
@@ -4200,9 +4246,19 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     int* hg = hc + H;           // [H + 1] group prefix
     int* htl = hg + H + 1;      // [H + 1] tile prefix
     int* qpre = htl + H + 1;    // [B + 1]
-    int* wsum = qpre + B + 1;   // [NT / 64]
-    int* hz = wsum + NT / 64;   // [H] list size of the slot
+    int* wsum = qpre + B + 1;   // [2 * NT / 64]
+    int* hz = wsum + 2 * (NT / 64);  // [H] list size of the slot
     JHQ_PHASE_DECL
+    // the pairs' lists and sizes are requested first: their two dependent
+    // loads overlap the hash clear and the query prefix
+    int pl[kMfmaPairsPT], psz[kMfmaPairsPT];
+#pragma unroll
+    for (int i = 0; i < kMfmaPairsPT; i++) {
+        const int e = tid + i * NT;
+        pl[i] = e < BP ? probes[e] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kMfmaPairsPT; i++) psz[i] = pl[i] >= 0 ? ldesc[pl[i]].z : 0;
     for (int i = tid; i < H; i += NT) {
         hk[i] = -1;
         hc[i] = 0;
@@ -4211,12 +4267,11 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     int ps[kMfmaPairsPT], pr[kMfmaPairsPT];
 #pragma unroll
     for (int i = 0; i < kMfmaPairsPT; i++) {
-        const int e = tid + i * NT;
         ps[i] = -1;
         pr[i] = 0;
-        if (e >= BP) continue;
-        const int l = probes[e];
-        const int sz = ldesc[l].z;
+        if (pl[i] < 0) continue;
+        const int l = pl[i];
+        const int sz = psz[i];
         if (sz == 0) continue;  // empty list: no slots
         int h = (int)(((uint64_t)((uint32_t)l * 2654435761u) * (uint32_t)H) >> 32);
         for (;;) {
@@ -4232,10 +4287,12 @@ mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __r
     JHQ_PHASE(0);
     // slot h holds ceil(hc / 16) groups of ceil(size / 16) tiles each
     auto ntl = [&](int h) { return (hz[h] + kGroup - 1) / kGroup; };
-    block_exclusive_scan<NT>([&](int h) { return hk[h] >= 0 ? (hc[h] + 15) / 16 : 0; }, H, hg,
-                             wsum);
-    block_exclusive_scan<NT>(
-        [&](int h) { return hk[h] >= 0 ? ((hc[h] + 15) / 16) * ntl(h) : 0; }, H, htl, wsum);
+    block_exclusive_scan2<NT>(
+        [&](int h) {
+            const int ng = hk[h] >= 0 ? (hc[h] + 15) / 16 : 0;
+            return make_int2(ng, ng > 0 ? ng * ntl(h) : 0);
+        },
+        H, hg, htl, wsum);
     const int T = htl[H];
     JHQ_PHASE(1);
     for (int h = tid; h < H; h += NT) {
@@ -4306,19 +4363,40 @@ __device__ __forceinline__ void mfma_tile(const uint32_t (&cw)[M / 16], int h, i
                                           const mfma_v4i (&alo)[M / 8], int cand, int nl,
                                           uint32_t* dump, uint32_t* tmin, int d0, int d1, int d2,
                                           int d3) {
-    constexpr int NK = M / 8;
+    constexpr int NK = M / 8, ND = M / 16;
     mfma_v4i ah = {0, 0, 0, 0}, alw = {0, 0, 0, 0};
+    // code dwords in pairs: one 64-bit shift gives bit plane k of both
+    // (bits shifted across the dword boundary land outside the byte mask)
 #pragma unroll
-    for (int s = 0; s < NK; s++) {
-        const uint32_t x = cw[s >> 1];
-        const int k0 = 4 * (s & 1);
-        mfma_v4i bv;
-        bv[0] = (int)((x >> k0) & 0x01010101u);
-        bv[1] = (int)((x >> (k0 + 1)) & 0x01010101u);
-        bv[2] = (int)((x >> (k0 + 2)) & 0x01010101u);
-        bv[3] = (int)((x >> (k0 + 3)) & 0x01010101u);
-        ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[s], bv, ah, 0, 0, 0);
-        alw = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[s], bv, alw, 0, 0, 0);
+    for (int t = 0; t < ND / 2; t++) {
+        const uint64_t X = ((uint64_t)cw[2 * t + 1] << 32) | cw[2 * t];
+        uint64_t pl[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) pl[k] = (X >> k) & 0x0101010101010101ull;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            // step 4t + q: dword 2t + q / 2, bits 4 (q % 2) .. + 3
+            const int hi = q >> 1, k0 = 4 * (q & 1);
+            mfma_v4i bv;
+#pragma unroll
+            for (int i = 0; i < 4; i++) bv[i] = (int)(uint32_t)(pl[k0 + i] >> (32 * hi));
+            ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[4 * t + q], bv, ah, 0, 0, 0);
+            alw = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[4 * t + q], bv, alw, 0, 0, 0);
+        }
+    }
+    if constexpr (ND % 2 == 1) {
+#pragma unroll
+        for (int s = NK - 2; s < NK; s++) {
+            const uint32_t x = cw[ND - 1];
+            const int k0 = 4 * (s & 1);
+            mfma_v4i bv;
+            bv[0] = (int)((x >> k0) & 0x01010101u);
+            bv[1] = (int)((x >> (k0 + 1)) & 0x01010101u);
+            bv[2] = (int)((x >> (k0 + 2)) & 0x01010101u);
+            bv[3] = (int)((x >> (k0 + 3)) & 0x01010101u);
+            ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[s], bv, ah, 0, 0, 0);
+            alw = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[s], bv, alw, 0, 0, 0);
+        }
     }
     const bool ok = cand < nl;
     const uint32_t v0 = ok ? (uint32_t)(ah[0] * 256 + alw[0]) + 0x80000000u : 0xffffffffu;
@@ -5181,7 +5259,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
 
 static size_t mfma_plan_lds(int B, int P) {
     const int H = mfma_hash_size(B * P);
-    const size_t work = (size_t)(5 * H + 4 + B + 1 + kMfmaPlanNT / 64) * 4 + 64;
+    const size_t work = (size_t)(5 * H + 4 + B + 1 + 2 * (kMfmaPlanNT / 64)) * 4 + 64;
     const size_t quant = (size_t)3 * (kMfmaPlanNT / 64) * 8 + 64;
     return std::max(work, quant);
 }
