@@ -562,8 +562,10 @@ def query_product_rate(nq, nb, d, nlist, step_us):
     return {"flops_per_batch": int(flops), "us_per_batch": round(us, 2),
             "achieved_tflops": round(tf, 2), "peak_tflops": FP32_MFMA_PEAK_TFLOPS,
             "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-            "note": "HIP events around the query product on one stream (its reduce kernel "
-                    "included)"}
+            "note": "HIP events around the query product on one stream: the product "
+                    "kernel, and the kernel that adds its split sums where the probe "
+                    "selection does not (nlist > 8192; at nlist <= 8192 the selection adds "
+                    "them)"}
 
 
 def step_roofline(ix, hq, k, batch, step_us, ev_ms_per_step, workload, nprobe, alpha,

@@ -658,11 +658,16 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
               float* d_out, int32_t* d_ids, bool want_topck, hipStream_t s) {
     const int d = ix->d;
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
+    // rotation and centroid dots in one tiled product; its split sums are
+    // added by the probe selection where the score row fits in its LDS
+    jhq::QbPlan qp{};
+    bool sel_qb = false;
     if (ix->dqmat.p) {
-        // rotation and centroid dots in one tiled product
-        const jhq::QbPlan qp = jhq::mfma_qb_plan(Bq, d + ix->nlist, d);
+        qp = jhq::mfma_qb_plan(Bq, d + ix->nlist, d);
+        sel_qb = jhq::select_adds_qb(qp, ix->nlist, d);
         JHQ_HIP(jhq::mfma_qb(qp, d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, w.wqrot.p, d,
-                             w.wscores.p, ix->nlist, ix->dnorms.p, w.wqpart.p, w.wqpart.n, s));
+                             w.wscores.p, ix->nlist, ix->dnorms.p, w.wqpart.p, w.wqpart.n, s,
+                             !sel_qb));
     } else {
         // d not a multiple of 64: the 16-row kernels
         JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, w.wqrot.p, d, s));
@@ -670,8 +675,13 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
                                    w.wscores.p, ix->nlist, s));
     }
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
-    JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
-                               w.wgofs.p, w.wqtot.p, s));
+    if (sel_qb)
+        JHQ_HIP(jhq::select_probes_qb(qp, w.wqpart.p, d, w.wqrot.p, d, ix->dnorms.p, Bq,
+                                      ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p, w.wgofs.p,
+                                      w.wqtot.p, s));
+    else
+        JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
+                                   w.wgofs.p, w.wqtot.p, s));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     if (bp.sh.mfma) {
         // the re-check refines short short lists itself

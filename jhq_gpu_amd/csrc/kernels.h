@@ -54,8 +54,10 @@ hipError_t assign_mfma_tally(const float* scratch, int64_t n, unsigned long long
 // fp32 MFMA, 64 rows x 16*C columns x K/nsplit per workgroup, the launch
 // sized to the chip.  mfma_q_ok: K % 64 == 0 and lda, ldb multiples of 4 (A
 // and Bm must also be 16-byte aligned).  With nsplit > 1 the split sums pass
-// through part (part_floats floats) and a second kernel adds them in split
-// order; launches sharing part must not overlap.
+// through part (part_floats floats, rows of split sp from sp *
+// qb_part_stride) and a second kernel adds them in split order, or, with
+// reduce false, the caller's select_probes_qb does; launches sharing part
+// must not overlap.
 bool mfma_q_ok(int K, int64_t lda, int64_t ldb);
 struct QbPlan {
     int C, NI, nsplit, ncg, R;
@@ -64,9 +66,11 @@ struct QbPlan {
 QbPlan mfma_qb_plan(int nb, int N, int K);
 // part floats that cover the plan of every nb <= nb_max
 size_t mfma_qb_space(int nb_max, int N, int K);
+int64_t qb_part_stride(const QbPlan& p, int N);
 hipError_t mfma_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm, int64_t ldb,
                    int nb, int N, int K, int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2,
-                   const float* norms, float* part, size_t part_floats, hipStream_t s);
+                   const float* norms, float* part, size_t part_floats, hipStream_t s,
+                   bool reduce = true);
 hipError_t mfma_nt_store(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
                          int K, float* C, int64_t ldc, hipStream_t s);
 hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t ldb, int nb, int N,
@@ -145,6 +149,15 @@ hipError_t relocate_lists(const int4* moves, int nmoves, int M, int bpv, const u
 // counts) and qtot[b] (= gofs[b][P]).
 hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
                          int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s);
+// The same from the split sums of mfma_qb (plan p, launched with reduce
+// false, part as given there): each query's workgroup adds its row's splits
+// in split order, stores the rotated query (the first nrot columns) to C1
+// and selects from the scores norms - 2 dot, held in LDS (no second kernel,
+// no score rows in HBM).  select_adds_qb: whether the shape allows it.
+bool select_adds_qb(const QbPlan& p, int nlist, int nrot);
+hipError_t select_probes_qb(const QbPlan& p, const float* part, int nrot, float* C1, int64_t ld1,
+                            const float* norms, int B, int nlist, int P, const int4* ldesc,
+                            int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s);
 
 // rows[i] = the stored vector at column samp[i].z of the list block (start
 // samp[i].x, row stride samp[i].y) decoded from its primary code (rotated

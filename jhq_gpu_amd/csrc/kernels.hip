@@ -708,13 +708,24 @@ bool mfma_q_ok(int K, int64_t lda, int64_t ldb) {
 // Lane (r, g) supplies row / column r of a tile and k = 16*step + 4g .. +3,
 // one k per MFMA.  The 4 wave sums meet in LDS and are added in wave order.
 // With nsplit > 1 the workgroup stores its sums to part[sp] and
-// mfma_qb_reduce_kernel adds the nsplit partial tiles in split order, so the
-// sum order is fixed.  (A last-arriving-workgroup reduction inside this
+// mfma_qb_reduce_kernel (or the probe selection, select_probes_qb) adds the
+// nsplit partial rows in split order, so the sum order is fixed.  (A last-arriving-workgroup reduction inside this
 // kernel needs device-scope fences, whose L2 write-backs cost more than the
 // second launch: 49 against 19 us per batch of 64 at D = 1024, nlist 4096;
 // the 8-wave kernel this replaces, 64 rows x 32 columns per wave with K split
 // over the waves, took 24 us on 160 workgroups.)
 // ---------------------------------------------------------------------------
+// Component q of the vector held by the quad lane that quad_perm CTRL
+// (k, k, k, k) names: one step of a 4 x 4 transpose across a quad of lanes.
+template <int CTRL>
+__device__ __forceinline__ float quad_pick(const v4f& x, int q) {
+    float b[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        b[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x[e]), CTRL, 0xf, 0xf, false));
+    return q == 0 ? b[0] : q == 1 ? b[1] : q == 2 ? b[2] : b[3];
+}
+
 template <int C, int NI>
 __global__ void __launch_bounds__(256)
 mfma_qb_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
@@ -785,12 +796,30 @@ mfma_qb_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
         }
     }
     if (nsplit > 1) {
-        // part[sp][rb][cg][tile][lane]; mfma_qb_reduce_kernel finishes
-        v4f* mine = part + ((int64_t)(sp * gridDim.z + rb) * gridDim.x + cg) * NT * 64;
+        // split sp's rows, row-major: part[sp][row][col] (64 gridDim.z rows
+        // per split); mfma_qb_reduce_kernel or the probe selection finishes.
+        // A quad of lanes (columns 4a .. 4a+3, rows 4g + e) transposes its
+        // 4 x 4 block so that lane q stores row 4g + q, four columns in one
+        // 16-byte store (N % 4 == 0; else one float at a time)
+        float* mine = reinterpret_cast<float*>(part) + (int64_t)sp * gridDim.z * 64 * N;
+        const int q = r & 3;
 #pragma unroll
         for (int j = 0; j < (NT + 3) / 4; j++) {
             const int t = wv + 4 * j;
-            if (t < NT) mine[t * 64 + lane] = sum[j];
+            if (t >= NT) continue;
+            const int c = t / RT, i = t % RT;
+            if ((N & 3) == 0) {
+                // lane kq of the quad holds column 4a + kq, rows 4g + 0..3
+                const float4 o = make_float4(quad_pick<0x00>(sum[j], q), quad_pick<0x55>(sum[j], q),
+                                             quad_pick<0xAA>(sum[j], q), quad_pick<0xFF>(sum[j], q));
+                const int col0 = n0 + 16 * c + (r & ~3);
+                if (col0 < N) *(float4*)(mine + (int64_t)(b0 + 16 * i + 4 * g + q) * N + col0) = o;
+            } else {
+                const int col = n0 + 16 * c + r;
+                if (col >= N) continue;
+#pragma unroll
+                for (int e = 0; e < 4; e++) mine[(int64_t)(b0 + 16 * i + 4 * g + e) * N + col] = sum[j][e];
+            }
         }
         return;
     }
@@ -813,36 +842,23 @@ mfma_qb_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
     }
 }
 
-// part[sp][rb][cg][tile][lane] summed over sp in order, then stored like
-// mfma_qb_kernel's epilogue; one thread per (rb, cg, tile, lane).
+// part[sp][row][col] summed over sp in order, then stored like
+// mfma_qb_kernel's epilogue; one thread per (row, col), row < nb.
 __global__ void __launch_bounds__(256)
-mfma_qb_reduce_kernel(const v4f* __restrict__ part, int nsplit, int C, int ncg, int R, int nb,
-                      int N, int nrot, float* __restrict__ C1, int64_t ld1, float* __restrict__ C2,
+mfma_qb_reduce_kernel(const float* __restrict__ part, int64_t pstride, int nsplit, int nb, int N,
+                      int nrot, float* __restrict__ C1, int64_t ld1, float* __restrict__ C2,
                       int64_t ld2, const float* __restrict__ norms) {
-    const int NT = 4 * C;
-    const int64_t per = (int64_t)R * ncg * NT * 64;
     const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (x >= per) return;
-    const int lane = (int)(x % 64);
-    const int64_t tt = x / 64;
-    const int t = (int)(tt % NT);
-    const int64_t rc = tt / NT;
-    const int cg = (int)(rc % ncg), rb = (int)(rc / ncg);
-    v4f v = part[x];
-    for (int s2 = 1; s2 < nsplit; s2++) v += part[s2 * per + x];
-    const int r = lane & 15, g = lane >> 4;
-    const int c = t / 4, i = t % 4;
-    const int col = cg * 16 * C + 16 * c + r;
-    if (col >= N) return;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int row = rb * 64 + 16 * i + 4 * g + e;
-        if (row < nb) {
-            if (col < nrot) C1[(int64_t)row * ld1 + col] = v[e];
-            else C2[(int64_t)row * ld2 + (col - nrot)] = fmaf(-2.0f, v[e], norms[col - nrot]);
-        }
-    }
+    if (x >= (int64_t)nb * N) return;
+    const int row = (int)(x / N), col = (int)(x - (int64_t)row * N);
+    float v = part[x];
+    for (int s2 = 1; s2 < nsplit; s2++) v += part[s2 * pstride + x];
+    if (col < nrot) C1[(int64_t)row * ld1 + col] = v;
+    else C2[(int64_t)row * ld2 + (col - nrot)] = fmaf(-2.0f, v, norms[col - nrot]);
 }
+
+// Floats between two splits' rows in the partial buffer of plan p.
+int64_t qb_part_stride(const QbPlan& p, int N) { return (int64_t)p.R * 64 * N; }
 
 QbPlan mfma_qb_plan(int nb, int N, int K) {
     QbPlan p{};
@@ -869,22 +885,21 @@ QbPlan mfma_qb_plan(int nb, int N, int K) {
     p.NI = m / s;
     p.ncg = (T + best - 1) / best;
     p.R = R;
-    p.part_floats = s > 1 ? (size_t)s * R * p.ncg * best * 4 * 64 * 4 : 0;
+    p.part_floats = s > 1 ? (size_t)s * R * 64 * N : 0;
     return p;
 }
 
 size_t mfma_qb_space(int nb_max, int N, int K) {
     // any plan for nb <= nb_max: ncg * C <= T + 4 column tiles, R <= R_max
     const QbPlan p = mfma_qb_plan(nb_max, N, K);
-    const size_t T = (N + 15) / 16;
-    return p.nsplit > 1 ? (size_t)p.nsplit * p.R * (T + 4) * 4 * 64 * 4 : 0;
+    return p.part_floats;
 }
 
 template <int C, int NI>
 static hipError_t launch_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm,
                             int64_t ldb, int nb, int N, int K, int nrot, float* C1, int64_t ld1,
                             float* C2, int64_t ld2, const float* norms, float* part,
-                            hipStream_t s) {
+                            bool reduce, hipStream_t s) {
     const void* fn = (const void*)mfma_qb_kernel<C, NI>;
     const int lds = 4 * C * 4 * 64 * 16;
     static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -892,18 +907,19 @@ static hipError_t launch_qb(const QbPlan& p, const float* A, int64_t lda, const 
     hipLaunchKernelGGL((mfma_qb_kernel<C, NI>), dim3(p.ncg, p.nsplit, p.R), dim3(256), lds, s, A, lda,
                        Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, p.nsplit,
                        reinterpret_cast<v4f*>(part));
-    if (p.nsplit > 1) {
-        const int64_t per = (int64_t)p.R * p.ncg * 4 * C * 64;
+    if (p.nsplit > 1 && reduce) {
+        const int64_t per = (int64_t)nb * N;
         hipLaunchKernelGGL(mfma_qb_reduce_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0,
-                           s, reinterpret_cast<const v4f*>(part), p.nsplit, C, p.ncg, p.R, nb, N,
-                           nrot, C1, ld1, C2, ld2, norms);
+                           s, part, qb_part_stride(p, N), p.nsplit, nb, N, nrot, C1, ld1, C2, ld2,
+                           norms);
     }
     return hipGetLastError();
 }
 
 hipError_t mfma_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm, int64_t ldb,
                    int nb, int N, int K, int nrot, float* C1, int64_t ld1, float* C2, int64_t ld2,
-                   const float* norms, float* part, size_t part_floats, hipStream_t s) {
+                   const float* norms, float* part, size_t part_floats, hipStream_t s,
+                   bool reduce) {
     if (nb <= 0 || N <= 0) return hipSuccess;
     if (!mfma_q_ok(K, lda, ldb) || ((uintptr_t)A & 15) || ((uintptr_t)Bm & 15) ||
         ((uintptr_t)part & 15) || p.C < 1 || p.C > 5 || p.NI < 1 || p.NI > 4 || p.R > 65535 ||
@@ -911,10 +927,10 @@ hipError_t mfma_qb(const QbPlan& p, const float* A, int64_t lda, const float* Bm
         return hipErrorInvalidValue;
 #define JHQ_QB(CC)                                                                              \
     switch (p.NI) {                                                                             \
-        case 1: return launch_qb<CC, 1>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
-        case 2: return launch_qb<CC, 2>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
-        case 3: return launch_qb<CC, 3>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
-        default: return launch_qb<CC, 4>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, s); \
+        case 1: return launch_qb<CC, 1>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, reduce, s); \
+        case 2: return launch_qb<CC, 2>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, reduce, s); \
+        case 3: return launch_qb<CC, 3>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, reduce, s); \
+        default: return launch_qb<CC, 4>(p, A, lda, Bm, ldb, nb, N, K, nrot, C1, ld1, C2, ld2, norms, part, reduce, s); \
     }
     switch (p.C) {
         case 1: JHQ_QB(1)
@@ -1608,11 +1624,24 @@ __device__ __forceinline__ uint32_t wave_kth_u32(uint32_t v, int r) {
     return res;
 }
 
-template <int NT>
+// The split sums of the query product (mfma_qb_kernel with nsplit > 1, row
+// of query b at part + sp * pstride + b * (nrot + nlist) in split sp): added
+// in split order, the rotated query stored to C1, the scores kept in LDS.
+// QB = nsplit (0: the scores are read from scores).
+struct QbPart {
+    const float* part;
+    int64_t pstride;
+    int nrot;
+    float* C1;
+    int64_t ld1;
+    const float* norms;
+};
+
+template <int NT, int QB = 0>
 __global__ void __launch_bounds__(NT)
 select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                      const int4* __restrict__ ldesc, int32_t* __restrict__ probes,
-                     int32_t* __restrict__ gofs, int32_t* __restrict__ qtot) {
+                     int32_t* __restrict__ gofs, int32_t* __restrict__ qtot, QbPart qp) {
     // Fast path (P <= kProbeFastP), two cheap passes over the row:
     //   1. every thread takes the minimum ord(score) of its share; each wave
     //      finds the ceil(P / waves)-th smallest of its 64 lane minima, and
@@ -1630,11 +1659,52 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     unsigned long long* surv = (unsigned long long*)(tail + align16((size_t)P * 4));  // [kProbeSurv]
     uint32_t* wth = (uint32_t*)(surv + kProbeSurv);  // [NW]
     int* scnt = (int*)(wth + NW);                    // [1]
+    float* srow = (float*)(scnt + 4);                // [nlist] (QB only)
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float* row = scores + (int64_t)b * nlist;
+    const float* row = QB ? srow : scores + (int64_t)b * nlist;
     JHQ_PHASE_DECL
     stream_begin<NT>(S);
     if (tid == 0) *scnt = 0;
+    if constexpr (QB > 0) {
+        // the row's split sums, every split's float4 requested before the
+        // first is added (nrot and nlist multiples of 4)
+        constexpr int U = 5;  // one round at D = 1024, nlist 4096
+        const int N4 = (qp.nrot + nlist) >> 2, R4 = qp.nrot >> 2;
+        const float4* p4 = (const float4*)(qp.part + (int64_t)b * (qp.nrot + nlist));
+        const int64_t st4 = qp.pstride >> 2;
+        for (int i0 = tid; i0 < N4; i0 += U * NT) {
+            float4 v[U][QB];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int sp = 0; sp < QB; sp++)
+                    v[u][sp] = p4[sp * st4 + min(i0 + u * NT, N4 - 1)];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * NT;
+                if (i >= N4) continue;
+                float4 a = v[u][0];
+#pragma unroll
+                for (int sp = 1; sp < QB; sp++) {
+                    a.x += v[u][sp].x;
+                    a.y += v[u][sp].y;
+                    a.z += v[u][sp].z;
+                    a.w += v[u][sp].w;
+                }
+                if (i < R4) {
+                    ((float4*)(qp.C1 + (int64_t)b * qp.ld1))[i] = a;
+                } else {
+                    const float4 nv = ((const float4*)qp.norms)[i - R4];
+                    float4 o;
+                    o.x = fmaf(-2.0f, a.x, nv.x);
+                    o.y = fmaf(-2.0f, a.y, nv.y);
+                    o.z = fmaf(-2.0f, a.z, nv.z);
+                    o.w = fmaf(-2.0f, a.w, nv.w);
+                    ((float4*)srow)[i - R4] = o;
+                }
+            }
+        }
+    }
     __syncthreads();
     JHQ_PHASE(0);
     int kk = 0;
@@ -3374,6 +3444,7 @@ constexpr int kSkewNT = JHQ_SKEW_NT;
 #endif
 constexpr int kRefineNT = JHQ_REFINE_NT;
 constexpr int kProbeNT = 512, kProbeSmallNT = 256;
+constexpr int kProbeFuseMaxList = 8192;  // score rows the selection holds in LDS
 
 
 // LDS of the wave-selection scan with wave buffers of 64 * J keys.
@@ -3489,16 +3560,17 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     return true;
 }
 
-template <int NT>
+template <int NT, int QB = 0>
 static hipError_t launch_select_probes(const float* scores, int B, int nlist, int P,
                                        const int4* ldesc, int32_t* probes, int32_t* gofs,
-                                       int32_t* qtot, hipStream_t s) {
+                                       int32_t* qtot, const QbPart& qp, hipStream_t s) {
     const size_t lds = stream_lds_bytes(NT, P) + align16((size_t)P * 4) +
-                       (size_t)kProbeSurv * 8 + (size_t)(NT / 64) * 4 + 16;
-    static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<NT>);
+                       (size_t)kProbeSurv * 8 + (size_t)(NT / 64) * 4 + 16 +
+                       (QB ? (size_t)nlist * 4 + 16 : 0);
+    static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<NT, QB>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(select_probes_kernel<NT>, dim3(B), dim3(NT), lds, s, scores, nlist, P,
-                       ldesc, probes, gofs, qtot);
+    hipLaunchKernelGGL((select_probes_kernel<NT, QB>), dim3(B), dim3(NT), lds, s, scores, nlist,
+                       P, ldesc, probes, gofs, qtot, qp);
     return hipGetLastError();
 }
 
@@ -3506,9 +3578,30 @@ hipError_t select_probes(const float* scores, int B, int nlist, int P, const int
                          int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s) {
     // short score rows: 4 waves per query (10.8 against 11.7 us per batch of
     // 64 at nlist 4096 with 8 waves; 16 waves 13.8)
+    const QbPart none{};
     if (nlist <= 8192)
-        return launch_select_probes<kProbeSmallNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot, s);
-    return launch_select_probes<kProbeNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot, s);
+        return launch_select_probes<kProbeSmallNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot,
+                                                   none, s);
+    return launch_select_probes<kProbeNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot, none, s);
+}
+
+bool select_adds_qb(const QbPlan& p, int nlist, int nrot) {
+    return p.nsplit >= 2 && p.nsplit <= 4 && nlist <= kProbeFuseMaxList && nlist % 4 == 0 &&
+           nrot % 4 == 0;
+}
+
+hipError_t select_probes_qb(const QbPlan& p, const float* part, int nrot, float* C1, int64_t ld1,
+                            const float* norms, int B, int nlist, int P, const int4* ldesc,
+                            int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s) {
+    if (!select_adds_qb(p, nlist, nrot) || ((uintptr_t)part & 15) || ((uintptr_t)C1 & 15) ||
+        ((uintptr_t)norms & 15) || ld1 % 4 != 0 || B > p.R * 64)
+        return hipErrorInvalidValue;
+    const QbPart qp{part, qb_part_stride(p, nrot + nlist), nrot, C1, ld1, norms};
+    switch (p.nsplit) {
+        case 2: return launch_select_probes<kProbeSmallNT, 2>(nullptr, B, nlist, P, ldesc, probes, gofs, qtot, qp, s);
+        case 3: return launch_select_probes<kProbeSmallNT, 3>(nullptr, B, nlist, P, ldesc, probes, gofs, qtot, qp, s);
+        default: return launch_select_probes<kProbeSmallNT, 4>(nullptr, B, nlist, P, ldesc, probes, gofs, qtot, qp, s);
+    }
 }
 
 hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d,
