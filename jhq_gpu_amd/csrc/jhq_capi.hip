@@ -113,8 +113,14 @@ struct Workspace {
     DBuf<unsigned long long> wpartial, wtopck, wdump;
     // split sums of the query product
     DBuf<float> wqpart;
-    // integer-MFMA pre-scan: quantized queries, work list, counters
+    // integer-MFMA pre-scan: quantized queries and the batch's list hash
     DBuf<unsigned char> wmfma;
+    // the hash in wmfma is clear for batches of hash_P probes at hash_ws
+    // (each batch's re-check clears it for the next; a batch that stopped
+    // between its selection and its re-check leaves it unclear)
+    bool hash_clear = false;
+    int hash_P = 0;
+    const unsigned char* hash_ws = nullptr;
 };
 
 }  // namespace
@@ -662,6 +668,18 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
     // added by the probe selection where the score row fits in its LDS
     jhq::QbPlan qp{};
     bool sel_qb = false;
+    // the pre-scan: the selection also quantizes the queries and lists the
+    // batch's (query, probe) pairs in the workspace's list hash
+    const int64_t dump_slots = static_cast<int64_t>(w.wdump.n * 2 / 17 * 16);
+    jhq::PrescanSel ps{w.wmfma.p, w.wmfma.n, dump_slots, w.wqrot.p, ix->dc1d.p, d, ix->M,
+                       ix->batch_size};
+    if (bp.sh.mfma) {
+        if (!w.hash_clear || w.hash_P != bp.P || w.hash_ws != w.wmfma.p)
+            JHQ_HIP(jhq::mfma_hash_clear(ix->batch_size, bp.P, ix->M, w.wmfma.p, w.wmfma.n, s));
+        w.hash_clear = false;
+        w.hash_P = bp.P;
+        w.hash_ws = w.wmfma.p;
+    }
     if (ix->dqmat.p) {
         qp = jhq::mfma_qb_plan(Bq, d + ix->nlist, d);
         sel_qb = jhq::select_adds_qb(qp, ix->nlist, d);
@@ -675,13 +693,14 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
                                    w.wscores.p, ix->nlist, s));
     }
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
+    const jhq::PrescanSel* psp = bp.sh.mfma ? &ps : nullptr;
     if (sel_qb)
         JHQ_HIP(jhq::select_probes_qb(qp, w.wqpart.p, d, w.wqrot.p, d, ix->dnorms.p, Bq,
                                       ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p, w.wgofs.p,
-                                      w.wqtot.p, s));
+                                      w.wqtot.p, s, psp));
     else
         JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
-                                   w.wgofs.p, w.wqtot.p, s));
+                                   w.wgofs.p, w.wqtot.p, s, psp));
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[2], s));
     if (bp.sh.mfma) {
         // the re-check refines short short lists itself
@@ -689,11 +708,12 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
                                w.wprobes.p, w.wgofs.p, w.wqtot.p, bp.P, ix->dldesc.p,
                                ix->dcodes_t.p,
                                ix->dcodes_r.p, bp.ck, reinterpret_cast<uint32_t*>(w.wdump.p),
-                               static_cast<int64_t>(w.wdump.n * 2 / 17 * 16),
-                               w.wmfma.p, w.wmfma.n, k, ix->dres_c1d.p, ix->Kr, ix->RC, ix->Br,
-                               ix->bpv, ix->dres.p, ix->dcorr.p, ix->dlist_ids.p, d_out, d_ids,
-                               want_topck ? w.wtopck.p : nullptr, w.wpartial.p, w.wpslot.p,
-                               ix->num_cu, s));
+                               dump_slots, w.wmfma.p, w.wmfma.n, k, ix->dres_c1d.p, ix->Kr,
+                               ix->RC, ix->Br, ix->bpv, ix->dres.p, ix->dcorr.p,
+                               ix->dlist_ids.p, d_out, d_ids, want_topck ? w.wtopck.p : nullptr,
+                               w.wpartial.p, w.wpslot.p, ix->num_cu, ix->batch_size, s));
+        // the re-check clears the hash for the lane's next batch
+        w.hash_clear = true;
         if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[3], s));
         if (!jhq::mfma_fuses_refine(bp.ck))
             JHQ_HIP(jhq::refine_topk(w.wpartial.p, w.wpslot.p, w.wqtot.p, Bq, bp.sh, bp.ck, k,

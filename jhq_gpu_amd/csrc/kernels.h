@@ -144,11 +144,27 @@ hipError_t relocate_lists(const int4* moves, int nmoves, int M, int bpv, const u
                           const float* corr_src, float* corr_dst, const int32_t* ids_src,
                           int32_t* ids_dst, hipStream_t s);
 
+// The integer-MFMA pre-scan's share of the probe selection (see mfma_scan):
+// its workspace (ws, ws_bytes, laid out for Bcap queries) and dump buffer
+// size (dump_slots, as given to mfma_scan), the rotated queries (q_rot
+// [B][d]; unused by select_probes_qb, which forms them) and the primary
+// codebook c1d; d = 8 M.
+struct PrescanSel {
+    unsigned char* ws;
+    size_t ws_bytes;
+    int64_t dump_slots;
+    const float* q_rot;
+    const float* c1d;
+    int d, M, Bcap;
+};
+
 // Per query: exact top-P lists by (score, list) from scores[b][nlist];
 // writes probes[b][P] (ascending), gofs[b][P+1] (prefix of padded group
-// counts) and qtot[b] (= gofs[b][P]).
+// counts) and qtot[b] (= gofs[b][P]).  With ps, also the pre-scan's query
+// steps and the batch's (query, probe) pairs in its list hash.
 hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
-                         int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s);
+                         int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s,
+                         const PrescanSel* ps = nullptr);
 // The same from the split sums of mfma_qb (plan p, launched with reduce
 // false, part as given there): each query's workgroup adds its row's splits
 // in split order, stores the rotated query (the first nrot columns) to C1
@@ -157,7 +173,8 @@ hipError_t select_probes(const float* scores, int B, int nlist, int P, const int
 bool select_adds_qb(const QbPlan& p, int nlist, int nrot);
 hipError_t select_probes_qb(const QbPlan& p, const float* part, int nrot, float* C1, int64_t ld1,
                             const float* norms, int B, int nlist, int P, const int4* ldesc,
-                            int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s);
+                            int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s,
+                            const PrescanSel* ps = nullptr);
 
 // rows[i] = the stored vector at column samp[i].z of the list block (start
 // samp[i].x, row stride samp[i].y) decoded from its primary code (rotated
@@ -196,13 +213,24 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
 // out_i [B][k] and (optional) topck_dbg [B][ck] as refine_topk writes them;
 // otherwise it goes to partial[query's segment][ck] (one segment per query)
 // and the caller runs refine_topk.  dump holds one
-// u32 per candidate slot of the batch (dump_slots, a multiple of 16, at
-// least the sum of qtot times 16) and after them one per 16 slots; ws
-// (256-byte aligned) holds mfma_scan_bytes for this num_cu.  rows: the
+// u32 per candidate slot (dump_slots, a multiple of 16, at least B times the
+// largest qtot times 16: query b's row starts at b times dump_slots / B
+// rounded down to 16) and after them one per 16 slots; ws (256-byte
+// aligned) holds mfma_scan_bytes(Bcap, P, M) and is laid out for Bcap
+// queries whatever the batch's B.  rows: the
 // current row-major copy of the codes (row_codes), which the tiles and the
 // re-check read; codes_t: the code-major blocks (the re-check's streamed
 // fallback).  rck = RC * Kr.
+// The probe selection (select_probes or select_probes_qb with a
+// PrescanSel over the same ws and dump) must run first on the same stream:
+// it quantizes the queries and lists the batch's (query, probe) pairs in a
+// hash of the probed lists in ws, which the tile kernel reads and the
+// re-check clears for the next batch.  A new ws, one last used with another
+// P, or one a batch left between its selection and its mfma_scan, is
+// cleared with mfma_hash_clear (same Bcap, P and M).
 bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, int rck);
+hipError_t mfma_hash_clear(int Bcap, int P, int M, unsigned char* ws, size_t ws_bytes,
+                           hipStream_t s);
 bool mfma_fuses_refine(int ck);
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu);
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
@@ -212,7 +240,7 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
                      int k, const float* res_c1d, int Kr, int RC, int Br, int bpv,
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
                      float* out_d, int32_t* out_i, unsigned long long* topck_dbg,
-                     unsigned long long* partial, int32_t* partial_slot, int num_cu,
+                     unsigned long long* partial, int32_t* partial_slot, int num_cu, int Bcap,
                      hipStream_t s);
 
 // IVF ADC scan + exact top-ck per segment with the byte LUT built in LDS from

@@ -1624,6 +1624,135 @@ __device__ __forceinline__ uint32_t wave_kth_u32(uint32_t v, int r) {
     return res;
 }
 
+// ---------------------------------------------------------------------------
+// Integer-MFMA pre-scan: per-query quantization and the batch's list hash
+// (written by the probe selection, read by the tile kernel and re-check).
+// ---------------------------------------------------------------------------
+struct MfmaQS {
+    double s, C, e;
+    int all, pad;  // all = 1: re-check every candidate
+};
+
+typedef int mfma_v4i __attribute__((ext_vector_type(4)));
+
+// hash slots for BP probes: load factor at most 2/3
+static int mfma_hash_size(int BP) { return (3 * BP / 2 + 127) / 64 * 64; }
+
+// A group is one probed list and up to 16 of the queries that probe it: the
+// MFMA tiles of 16 candidates over the list's slots (a probed list of nl
+// vectors fills ceil(nl / 16) 16-slot groups of each probing query's
+// candidate row).  The probe selection inserts every (query, probe) pair of
+// the batch into a hash of the probed lists (slot h: the list hk[h], its
+// size hz[h], its hc[h] pairs by rank in ql); the tile kernel numbers the
+// groups slot by slot and, in a slot, by rank (16 pairs to a group), and
+// scan wave v takes tiles [v T / W, (v + 1) T / W).  Query b's candidate row
+// starts at slot b * perq of the dump.  The re-check clears hk and hc for
+// the next batch.  Workspace pieces, 256-byte aligned, in this order.
+struct MfmaWs {
+    int8_t* qa;  // [B][2][D]: hi then lo bytes in the lanes' register order
+    MfmaQS* qs;  // [B]
+    int4* hs;    // [H] slot: (list id or -1 when free, pairs in the slot, list size, -)
+    int2* ql;    // [H][B] pair of rank r: (query, dump slot of the list's first candidate)
+    int H, B, perq;
+};
+
+static size_t mfma_carve(int B, int P, int M, unsigned char* base, MfmaWs* w) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int H = mfma_hash_size(B * P);
+    size_t off = 0;
+    const size_t o_qa = off;
+    off += al((size_t)B * 2 * 8 * M);
+    const size_t o_qs = off;
+    off += al((size_t)B * sizeof(MfmaQS));
+    const size_t o_hs = off;
+    off += al((size_t)H * sizeof(int4));
+    const size_t o_ql = off;
+    off += al((size_t)H * B * sizeof(int2));
+    if (w) {
+        w->qa = (int8_t*)(base + o_qa);
+        w->qs = (MfmaQS*)(base + o_qs);
+        w->hs = (int4*)(base + o_hs);
+        w->ql = (int2*)(base + o_ql);
+        w->H = H;
+        w->B = B;
+        w->perq = 0;
+    }
+    return off;
+}
+
+constexpr int kMfmaMaxBP = 4096;     // (query, probe) pairs per batch (hash <= 64 slots per tile-kernel thread)
+
+// The batch's pre-scan workspace in ws, carved for Bcap queries (the same
+// layout for every batch of the workspace, whose hash the previous batch
+// cleared), and the dump stride of a query's candidate row (a multiple of
+// 16: B rows fit in dump_slots).
+static bool mfma_ws(int B, int Bcap, int P, int M, unsigned char* ws, size_t ws_bytes,
+                    int64_t dump_slots, MfmaWs* w) {
+    if (!ws || ((uintptr_t)ws & 255) || B < 1 || B > Bcap ||
+        mfma_carve(Bcap, P, M, ws, w) > ws_bytes)
+        return false;
+    const int64_t perq = dump_slots / B / 16 * 16;
+    if (perq < 16 || perq > (int64_t)1 << 30) return false;
+    w->perq = (int)perq;
+    return true;
+}
+
+// Block sums / max of three doubles (every thread gets the result).
+template <int NT>
+__device__ __forceinline__ void block_reduce3(double& a, double& b, double& c, double* red) {
+    constexpr int NW = NT / 64;
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off);
+        b += __shfl_xor(b, off);
+        c = fmax(c, __shfl_xor(c, off));
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        red[3 * wv] = a;
+        red[3 * wv + 1] = b;
+        red[3 * wv + 2] = c;
+    }
+    __syncthreads();
+    a = 0.0;
+    b = 0.0;
+    c = 0.0;
+    for (int w2 = 0; w2 < NW; w2++) {
+        a += red[3 * w2];
+        b += red[3 * w2 + 1];
+        c = fmax(c, red[3 * w2 + 2]);
+    }
+}
+
+// One (query, probe) pair of the batch into the list hash: the list's slot
+// (linear probing; the first pair of a list records its size), then the
+// pair at its rank in the slot.  The hash has more slots than the batch has
+// pairs, so a free or matching slot is always found; the probe count is
+// bounded all the same.
+__device__ __forceinline__ void mfma_pair_insert(const MfmaWs& w, int l, int sz, int b, int slot0) {
+    int h = (int)(((uint64_t)((uint32_t)l * 2654435761u) * (uint32_t)w.H) >> 32);
+    bool found = false;
+    for (int tries = 0; tries < w.H && !found; tries++) {
+        const int old = atomicCAS(&w.hs[h].x, -1, l);
+        if (old == -1) w.hs[h].z = sz;
+        if (old == -1 || old == l) found = true;
+        else h = h + 1 == w.H ? 0 : h + 1;
+    }
+    if (!found) return;
+    const int r = atomicAdd(&w.hs[h].y, 1);
+    if (r < w.B) w.ql[(int64_t)h * w.B + r] = make_int2(b, slot0);
+}
+
+// What the probe selection does for the pre-scan: the workspace (with the
+// dump stride), the rotated queries (read when the selection does not add
+// the product's split sums itself) and the primary codebook.
+struct MfSel {
+    MfmaWs w;
+    const float* q_rot;
+    const float* c1d;
+    int d, M;
+};
+
 // The split sums of the query product (mfma_qb_kernel with nsplit > 1, row
 // of query b at part + sp * pstride + b * (nrot + nlist) in split sp): added
 // in split order, the rotated query stored to C1, the scores kept in LDS.
@@ -1637,11 +1766,14 @@ struct QbPart {
     const float* norms;
 };
 
-template <int NT, int QB = 0>
+// MF: for the pre-scan, also quantize the query (mf.w.qa, mf.w.qs) and
+// insert its (query, probe) pairs into the batch's list hash.
+template <int NT, int QB = 0, bool MF = false>
 __global__ void __launch_bounds__(NT)
 select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                      const int4* __restrict__ ldesc, int32_t* __restrict__ probes,
-                     int32_t* __restrict__ gofs, int32_t* __restrict__ qtot, QbPart qp) {
+                     int32_t* __restrict__ gofs, int32_t* __restrict__ qtot, QbPart qp,
+                     MfSel mf) {
     // Fast path (P <= kProbeFastP), two cheap passes over the row:
     //   1. every thread takes the minimum ord(score) of its share; each wave
     //      finds the ceil(P / waves)-th smallest of its 64 lane minima, and
@@ -1660,6 +1792,9 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     uint32_t* wth = (uint32_t*)(surv + kProbeSurv);  // [NW]
     int* scnt = (int*)(wth + NW);                    // [1]
     float* srow = (float*)(scnt + 4);                // [nlist] (QB only)
+    float* sqr = srow + (QB ? nlist : 0);             // [d] (QB and MF): the rotated query
+    int* gsz = (int*)(sqr + (QB && MF ? mf.d : 0));   // [P] (MF): the probed lists' sizes
+    double* red = (double*)(((uintptr_t)(gsz + (MF ? P : 0)) + 7) & ~(uintptr_t)7);  // [3 NW] (MF)
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* row = QB ? srow : scores + (int64_t)b * nlist;
     JHQ_PHASE_DECL
@@ -1693,6 +1828,7 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                 }
                 if (i < R4) {
                     ((float4*)(qp.C1 + (int64_t)b * qp.ld1))[i] = a;
+                    if constexpr (MF) ((float4*)sqr)[i] = a;
                 } else {
                     const float4 nv = ((const float4*)qp.norms)[i - R4];
                     float4 o;
@@ -1788,10 +1924,13 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     for (int i = tid; i < P; i += NT) {
         const int l = i < kk ? (int)(uint32_t)(S.kout[i] & 0xffffffffull) : 0;
         probes[(int64_t)b * P + i] = l;
-        gcnt[i] = i < kk ? (ldesc[l].z + kGroup - 1) / kGroup : 0;
+        const int sz = i < kk ? ldesc[l].z : 0;
+        gcnt[i] = (sz + kGroup - 1) / kGroup;
+        if constexpr (MF) gsz[i] = sz;
     }
     __syncthreads();
-    // prefix of the group counts (P is small: one wave)
+    // prefix of the group counts (P is small: one wave); for the pre-scan
+    // each probe's pair goes to the list hash with its row offset
     if (tid < 64) {
         int carry = 0;
         int32_t* g = gofs + (int64_t)b * (P + 1);
@@ -1805,11 +1944,66 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                 if (tid >= off) incl += t;
             }
             if (i < P) g[i + 1] = carry + incl;
+            if constexpr (MF) {
+                if (i < P && i < kk && gsz[i] > 0)
+                    mfma_pair_insert(mf.w, (int)(uint32_t)(S.kout[i] & 0xffffffffull), gsz[i], b,
+                                     b * mf.w.perq + (carry + incl - v) * kGroup);
+            }
             carry += __shfl(incl, 63);
         }
         if (tid == 0) qtot[b] = carry;
     }
-    JHQ_PHASE(6);
+    JHQ_PHASE(7);
+    if constexpr (MF) {
+        // the query's steps for the pre-scan: dl_k = (q_k - c1)^2 - (q_k -
+        // c0)^2 rounded to multiples of s = max |dl| / 32000 (int16 as int8
+        // hi and lo halves in the MFMA A-operand layout), C = sum (q_k - c0)^2
+        // and the bound's slack e, in double
+        const int D = mf.d, NK = mf.M / 8, GS = mf.M / 4;
+        const float* qrow = QB ? sqr : mf.q_rot + (int64_t)b * D;
+        const double c0 = mf.c1d[0], c1 = mf.c1d[1];
+        double sC = 0.0, sA = 0.0, mx = 0.0;
+        for (int i = tid; i < D; i += NT) {
+            const double q = qrow[i];
+            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
+            sC += t0 * t0;
+            sA += fabs(dl);
+            mx = fmax(mx, fabs(dl));
+        }
+        block_reduce3<NT>(sC, sA, mx, red);
+        const bool fin = isfinite(sC) && isfinite(sA) && sC + sA < 1e36;
+        const double st = fin && mx > 0.0 ? mx / 32000.0 : 1.0;
+        int8_t* qa = mf.w.qa + (int64_t)b * 2 * D;
+        for (int x = tid; x < D / 4; x += NT) {
+            // dimensions 8 m + k of subspaces m = 4 m4 .. 4 m4 + 3: lane
+            // group h = m / GS, dword mm / 4 of that group's subspaces,
+            // K-step 2 (mm / 4) + k / 4, register k % 4, byte mm % 4
+            const int m4 = x >> 3, k = x & 7, m = 4 * m4, h = m / GS, mm = m % GS;
+            uint32_t whi = 0u, wlo = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const double q = qrow[8 * (m + e) + k];
+                const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
+                const int iq = fin ? (int)rint(dl / st) : 0;
+                const int hi = (iq + 128) >> 8, lo = iq - hi * 256;
+                whi |= (uint32_t)(uint8_t)(int8_t)hi << (8 * e);
+                wlo |= (uint32_t)(uint8_t)(int8_t)lo << (8 * e);
+            }
+            const int off = h * NK * 16 + (2 * (mm >> 2) + (k >> 2)) * 16 + (k & 3) * 4;
+            *(uint32_t*)(qa + off) = whi;
+            *(uint32_t*)(qa + D + off) = wlo;
+        }
+        if (tid == 0) {
+            MfmaQS Q;
+            Q.s = st;
+            Q.C = sC;
+            Q.e = 0.5000001 * st * D + 1e-12 * (sC + sA);
+            Q.all = fin ? 0 : 1;
+            Q.pad = 0;
+            mf.w.qs[b] = Q;
+        }
+    }
+    JHQ_PHASE(8);
     JHQ_PHASE_FLUSH(1);
 }
 
@@ -3459,7 +3653,6 @@ static size_t scan_wave_lds(int NT, int M, int d, int P, int ck, int K1D, int B,
            (size_t)K1D * 4 + NW * 4 + 64;
 }
 
-static size_t mfma_plan_lds(int B, int P);
 static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B, int rck);
 bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanShape* out,
                bool skew, bool mfma, int rck) {
@@ -3476,7 +3669,7 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
         out->mfma = 1;
         out->nt = 1024;
         out->lds = (int)mfma_recheck_lds(M, d, P, ck, K1D, B, rck);
-        out->region = (int)mfma_plan_lds(B, P);
+        out->region = 0;
         return true;
     }
     out->G = target_wg;
@@ -3560,29 +3753,57 @@ bool scan_plan(int M, int d, int P, int ck, int K1D, int B, int target_wg, ScanS
     return true;
 }
 
-template <int NT, int QB = 0>
+template <int NT, int QB = 0, bool MF = false>
 static hipError_t launch_select_probes(const float* scores, int B, int nlist, int P,
                                        const int4* ldesc, int32_t* probes, int32_t* gofs,
-                                       int32_t* qtot, const QbPart& qp, hipStream_t s) {
+                                       int32_t* qtot, const QbPart& qp, const MfSel& mf,
+                                       hipStream_t s) {
     const size_t lds = stream_lds_bytes(NT, P) + align16((size_t)P * 4) +
                        (size_t)kProbeSurv * 8 + (size_t)(NT / 64) * 4 + 16 +
-                       (QB ? (size_t)nlist * 4 + 16 : 0);
-    static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<NT, QB>);
+                       (QB ? (size_t)nlist * 4 + 16 : 0) +
+                       (MF ? (size_t)(QB ? mf.d : 0) * 4 + (size_t)P * 4 + 8 +
+                                 (size_t)3 * (NT / 64) * 8
+                           : 0);
+    static const int max_dyn = allow_max_lds((const void*)select_probes_kernel<NT, QB, MF>);
     if ((int)lds > max_dyn) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((select_probes_kernel<NT, QB>), dim3(B), dim3(NT), lds, s, scores, nlist,
-                       P, ldesc, probes, gofs, qtot, qp);
+    hipLaunchKernelGGL((select_probes_kernel<NT, QB, MF>), dim3(B), dim3(NT), lds, s, scores,
+                       nlist, P, ldesc, probes, gofs, qtot, qp, mf);
     return hipGetLastError();
 }
 
+// The pre-scan's part of the selection (ps set): its workspace, with the
+// dump stride, and the checks the quantization needs.
+static hipError_t prescan_sel(const PrescanSel* ps, int B, int P, MfSel* mf) {
+    if (!ps) return hipSuccess;
+    if (!ps->c1d || ps->d != 8 * ps->M || (int64_t)ps->Bcap * P > kMfmaMaxBP ||
+        !mfma_ws(B, ps->Bcap, P, ps->M, ps->ws, ps->ws_bytes, ps->dump_slots, &mf->w))
+        return hipErrorInvalidValue;
+    mf->q_rot = ps->q_rot;
+    mf->c1d = ps->c1d;
+    mf->d = ps->d;
+    mf->M = ps->M;
+    return hipSuccess;
+}
+
 hipError_t select_probes(const float* scores, int B, int nlist, int P, const int4* ldesc,
-                         int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s) {
+                         int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s,
+                         const PrescanSel* ps) {
     // short score rows: 4 waves per query (10.8 against 11.7 us per batch of
     // 64 at nlist 4096 with 8 waves; 16 waves 13.8)
     const QbPart none{};
+    MfSel mf{};
+    const hipError_t e = prescan_sel(ps, B, P, &mf);
+    if (e != hipSuccess) return e;
+    if (ps && !ps->q_rot) return hipErrorInvalidValue;
     if (nlist <= 8192)
-        return launch_select_probes<kProbeSmallNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot,
-                                                   none, s);
-    return launch_select_probes<kProbeNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot, none, s);
+        return ps ? launch_select_probes<kProbeSmallNT, 0, true>(scores, B, nlist, P, ldesc, probes,
+                                                                 gofs, qtot, none, mf, s)
+                  : launch_select_probes<kProbeSmallNT>(scores, B, nlist, P, ldesc, probes, gofs,
+                                                        qtot, none, mf, s);
+    return ps ? launch_select_probes<kProbeNT, 0, true>(scores, B, nlist, P, ldesc, probes, gofs,
+                                                        qtot, none, mf, s)
+              : launch_select_probes<kProbeNT>(scores, B, nlist, P, ldesc, probes, gofs, qtot, none,
+                                               mf, s);
 }
 
 bool select_adds_qb(const QbPlan& p, int nlist, int nrot) {
@@ -3592,16 +3813,27 @@ bool select_adds_qb(const QbPlan& p, int nlist, int nrot) {
 
 hipError_t select_probes_qb(const QbPlan& p, const float* part, int nrot, float* C1, int64_t ld1,
                             const float* norms, int B, int nlist, int P, const int4* ldesc,
-                            int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s) {
+                            int32_t* probes, int32_t* gofs, int32_t* qtot, hipStream_t s,
+                            const PrescanSel* ps) {
     if (!select_adds_qb(p, nlist, nrot) || ((uintptr_t)part & 15) || ((uintptr_t)C1 & 15) ||
         ((uintptr_t)norms & 15) || ld1 % 4 != 0 || B > p.R * 64)
         return hipErrorInvalidValue;
     const QbPart qp{part, qb_part_stride(p, nrot + nlist), nrot, C1, ld1, norms};
+    MfSel mf{};
+    const hipError_t e = prescan_sel(ps, B, P, &mf);
+    if (e != hipSuccess) return e;
+    if (ps && ps->d != nrot) return hipErrorInvalidValue;
+#define JHQ_SELQB(NS)                                                                          \
+    return ps ? launch_select_probes<kProbeSmallNT, NS, true>(nullptr, B, nlist, P, ldesc, probes, \
+                                                              gofs, qtot, qp, mf, s)           \
+              : launch_select_probes<kProbeSmallNT, NS>(nullptr, B, nlist, P, ldesc, probes, gofs, \
+                                                        qtot, qp, mf, s);
     switch (p.nsplit) {
-        case 2: return launch_select_probes<kProbeSmallNT, 2>(nullptr, B, nlist, P, ldesc, probes, gofs, qtot, qp, s);
-        case 3: return launch_select_probes<kProbeSmallNT, 3>(nullptr, B, nlist, P, ldesc, probes, gofs, qtot, qp, s);
-        default: return launch_select_probes<kProbeSmallNT, 4>(nullptr, B, nlist, P, ldesc, probes, gofs, qtot, qp, s);
+        case 2: JHQ_SELQB(2)
+        case 3: JHQ_SELQB(3)
+        default: JHQ_SELQB(4)
     }
+#undef JHQ_SELQB
 }
 
 hipError_t scan_topck(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d,
@@ -4173,7 +4405,6 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
 // selected from them, so the result does not depend on the MFMA values.
 // Queries with non-finite or huge values re-check every candidate.
 // ---------------------------------------------------------------------------
-constexpr int kMfmaPlanNT = 1024;
 // Tile-kernel waves per CU: one 4-wave workgroup.  The waves are bound by
 // issue and by their start-up load chain, and with the CU's other slots free
 // the other pipeline lane's kernels run beside them (config 2: 886 k queries/s
@@ -4193,247 +4424,6 @@ constexpr int kRecheckRegV = 8;     // its values per thread
 constexpr int kRecheckTM = 16;      // tile minima per thread in flight (global)
 constexpr int kRecheckTR = 32;      // tile minima per thread ranked in registers
 constexpr int kRecheckTPL = 4;      // listed tiles' row loads in flight per lane
-constexpr int kMfmaPairsPT = 4;     // probes per work-list thread
-constexpr int kMfmaMaxBP = kMfmaPairsPT * kMfmaPlanNT;  // probes per batch
-
-struct MfmaQS {
-    double s, C, e;
-    int all, pad;  // all = 1: re-check every candidate
-};
-
-typedef int mfma_v4i __attribute__((ext_vector_type(4)));
-
-// hash slots for BP probes: load factor at most 2/3
-static int mfma_hash_size(int BP) { return (3 * BP / 2 + 127) / 64 * 64; }
-
-// A group is one probed list and up to 16 of the queries that probe it: the
-// MFMA tiles of 16 candidates over the list's slots (a probed list of nl
-// vectors fills ceil(nl / 16) 16-slot groups of each probing query's
-// candidate row).  The batch's tiles are numbered group by group, and scan
-// wave v takes tiles [v T / W, (v + 1) T / W).  Workspace pieces, 256-byte
-// aligned, in this order.
-struct MfmaWs {
-    int8_t* qa;      // [B][2][D]: hi then lo bytes in the lanes' register order
-    MfmaQS* qs;      // [B]
-    int2* gq;        // [B*P][16]: a group's queries (query, dump offset of the
-                     //            list's first slot); entries past its count unused
-    int4* grp;       // [B*P]: (block start, row stride, size, queries)
-    int2* wstart;    // [waves]: (group, tile in the group) where a wave starts
-    int4* qinfo;     // [B]: (first slot of the query's row, its segment, tiles, 0)
-    int* ctl;        // [16]: tiles of the batch, groups
-};
-
-static size_t mfma_carve(int B, int P, int M, int nwaves, unsigned char* base, MfmaWs* w) {
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    size_t off = 0;
-    const size_t o_qa = off;
-    off += al((size_t)B * 2 * 8 * M);
-    const size_t o_qs = off;
-    off += al((size_t)B * sizeof(MfmaQS));
-    const size_t o_gq = off;
-    off += al((size_t)B * P * 16 * sizeof(int2));
-    const size_t o_g = off;
-    off += al((size_t)B * P * sizeof(int4));
-    const size_t o_ws = off;
-    off += al((size_t)nwaves * sizeof(int2));
-    const size_t o_qi = off;
-    off += al((size_t)B * sizeof(int4));
-    const size_t o_ctl = off;
-    off += al(16 * sizeof(int));
-    if (w) {
-        w->qa = (int8_t*)(base + o_qa);
-        w->qs = (MfmaQS*)(base + o_qs);
-        w->gq = (int2*)(base + o_gq);
-        w->grp = (int4*)(base + o_g);
-        w->wstart = (int2*)(base + o_ws);
-        w->qinfo = (int4*)(base + o_qi);
-        w->ctl = (int*)(base + o_ctl);
-    }
-    return off;
-}
-
-// Block sums / max of three doubles (every thread gets the result).
-template <int NT>
-__device__ __forceinline__ void block_reduce3(double& a, double& b, double& c, double* red) {
-    constexpr int NW = NT / 64;
-    for (int off = 32; off > 0; off >>= 1) {
-        a += __shfl_xor(a, off);
-        b += __shfl_xor(b, off);
-        c = fmax(c, __shfl_xor(c, off));
-    }
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) {
-        red[3 * wv] = a;
-        red[3 * wv + 1] = b;
-        red[3 * wv + 2] = c;
-    }
-    __syncthreads();
-    a = 0.0;
-    b = 0.0;
-    c = 0.0;
-    for (int w2 = 0; w2 < NW; w2++) {
-        a += red[3 * w2];
-        b += red[3 * w2 + 1];
-        c = fmax(c, red[3 * w2 + 2]);
-    }
-}
-
-// Workgroups 0..B-1 quantize one query each; workgroup B builds the batch's
-// work list: the distinct probed lists (a hash in LDS), the queries of each
-// (in arrival order; the order does not change any result), the groups and
-// where each of the nwaves scan waves starts.
-template <int NT>
-__global__ void __launch_bounds__(NT)
-mfma_plan_kernel(const float* __restrict__ q_rot, int d, int M, const float* __restrict__ c1d,
-                 const int32_t* __restrict__ probes, const int32_t* __restrict__ gofs,
-                 const int32_t* __restrict__ qtot, int B, int P, const int4* __restrict__ ldesc,
-                 MfmaWs w, int H, int nwaves) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int tid = threadIdx.x;
-    if ((int)blockIdx.x < B) {
-        const int b = blockIdx.x, D = d, NK = M / 8, GS = M / 4;
-        double* red = (double*)smem;
-        const double c0 = c1d[0], c1 = c1d[1];
-        double sC = 0.0, sA = 0.0, mx = 0.0;
-        for (int i = tid; i < D; i += NT) {
-            const double q = q_rot[(int64_t)b * d + i];
-            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
-            sC += t0 * t0;
-            sA += fabs(dl);
-            mx = fmax(mx, fabs(dl));
-        }
-        block_reduce3<NT>(sC, sA, mx, red);
-        const bool fin = isfinite(sC) && isfinite(sA) && sC + sA < 1e36;
-        const double s = fin && mx > 0.0 ? mx / 32000.0 : 1.0;
-        int8_t* qa = w.qa + (int64_t)b * 2 * D;
-        for (int i = tid; i < D; i += NT) {
-            const double q = q_rot[(int64_t)b * d + i];
-            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
-            const int iq = fin ? (int)rint(dl / s) : 0;
-            const int hi = (iq + 128) >> 8, lo = iq - hi * 256;
-            // dimension i = 8 m + k: lane group h = m / GS, dword t and byte
-            // e of that group's subspaces, K-step 2t + k / 4, register k % 4
-            const int m = i >> 3, k = i & 7, h = m / GS, mm = m % GS;
-            const int off = h * NK * 16 + (2 * (mm >> 2) + (k >> 2)) * 16 + (k & 3) * 4 + (mm & 3);
-            qa[off] = (int8_t)hi;
-            qa[D + off] = (int8_t)lo;
-        }
-        if (tid == 0) {
-            MfmaQS Q;
-            Q.s = s;
-            Q.C = sC;
-            Q.e = 0.5000001 * s * D + 1e-12 * (sC + sA);
-            Q.all = fin ? 0 : 1;
-            Q.pad = 0;
-            w.qs[b] = Q;
-        }
-        return;
-    }
-    // ---- work list ----
-    // a pair e = (query b, probe p) of the batch is taken by thread e % NT;
-    // its hash slot and rank stay in that thread's registers
-    const int BP = B * P;
-    int* hk = (int*)smem;       // [H] list id or -1
-    int* hc = hk + H;           // [H] queries of the slot
-    int* hg = hc + H;           // [H + 1] group prefix
-    int* htl = hg + H + 1;      // [H + 1] tile prefix
-    int* qpre = htl + H + 1;    // [B + 1]
-    int* wsum = qpre + B + 1;   // [2 * NT / 64]
-    int* hz = wsum + 2 * (NT / 64);  // [H] list size of the slot
-    JHQ_PHASE_DECL
-    // the pairs' lists and sizes are requested first: their two dependent
-    // loads overlap the hash clear and the query prefix
-    int pl[kMfmaPairsPT], psz[kMfmaPairsPT];
-#pragma unroll
-    for (int i = 0; i < kMfmaPairsPT; i++) {
-        const int e = tid + i * NT;
-        pl[i] = e < BP ? probes[e] : -1;
-    }
-#pragma unroll
-    for (int i = 0; i < kMfmaPairsPT; i++) psz[i] = pl[i] >= 0 ? ldesc[pl[i]].z : 0;
-    for (int i = tid; i < H; i += NT) {
-        hk[i] = -1;
-        hc[i] = 0;
-    }
-    block_exclusive_scan<NT>([&](int b) { return (int)qtot[b]; }, B, qpre, wsum);
-    int ps[kMfmaPairsPT], pr[kMfmaPairsPT];
-#pragma unroll
-    for (int i = 0; i < kMfmaPairsPT; i++) {
-        ps[i] = -1;
-        pr[i] = 0;
-        if (pl[i] < 0) continue;
-        const int l = pl[i];
-        const int sz = psz[i];
-        if (sz == 0) continue;  // empty list: no slots
-        int h = (int)(((uint64_t)((uint32_t)l * 2654435761u) * (uint32_t)H) >> 32);
-        for (;;) {
-            const int old = atomicCAS(&hk[h], -1, l);
-            if (old == -1) hz[h] = sz;  // the slot's first pair records the size
-            if (old == -1 || old == l) break;
-            h = h + 1 == H ? 0 : h + 1;
-        }
-        pr[i] = atomicAdd(&hc[h], 1);
-        ps[i] = h;
-    }
-    __syncthreads();
-    JHQ_PHASE(0);
-    // slot h holds ceil(hc / 16) groups of ceil(size / 16) tiles each
-    auto ntl = [&](int h) { return (hz[h] + kGroup - 1) / kGroup; };
-    block_exclusive_scan2<NT>(
-        [&](int h) {
-            const int ng = hk[h] >= 0 ? (hc[h] + 15) / 16 : 0;
-            return make_int2(ng, ng > 0 ? ng * ntl(h) : 0);
-        },
-        H, hg, htl, wsum);
-    const int T = htl[H];
-    JHQ_PHASE(1);
-    for (int h = tid; h < H; h += NT) {
-        if (hk[h] < 0) continue;
-        const int4 L = ldesc[hk[h]];
-        for (int t = 0; t < (hc[h] + 15) / 16; t++)
-            w.grp[hg[h] + t] = make_int4(L.x, L.y, L.z, min(16, hc[h] - 16 * t));
-    }
-    // the query of rank r in slot h is entry r % 16 of the slot's group r / 16
-#pragma unroll
-    for (int i = 0; i < kMfmaPairsPT; i++) {
-        if (ps[i] < 0) continue;
-        const int e = tid + i * NT, b = e / P, p = e - b * P;
-        w.gq[(hg[ps[i]] + pr[i] / 16) * 16 + (pr[i] & 15)] =
-            make_int2(b, (qpre[b] + gofs[(int64_t)b * (P + 1) + p]) * kGroup);
-    }
-    JHQ_PHASE(2);
-    // wave v starts at tile a = v T / W: in slot h with htl[h] <= a <
-    // htl[h + 1] (the largest h with htl[h] <= a is occupied when a < T)
-    for (int v = tid; v < nwaves; v += NT) {
-        const int a = (int)((int64_t)v * T / nwaves);
-        int2 st = make_int2(0, 0);
-        if (a < T) {
-            int lo = 0, hi = H - 1;
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (htl[mid] <= a) lo = mid;
-                else hi = mid - 1;
-            }
-            const int nt = ntl(lo), r = a - htl[lo];
-            st = make_int2(hg[lo] + r / nt, r - (r / nt) * nt);
-        }
-        w.wstart[v] = st;
-    }
-    JHQ_PHASE(3);
-    // segment of query b: the queries before it that have candidates (a
-    // prefix into hc, whose counts are no longer read)
-    if (tid == 0) {
-        w.ctl[0] = T;
-        w.ctl[1] = hg[H];
-    }
-    __syncthreads();
-    block_exclusive_scan<NT>([&](int b) { return qpre[b + 1] > qpre[b] ? 1 : 0; }, B, hc, wsum);
-    for (int b = tid; b < B; b += NT)
-        w.qinfo[b] = make_int4(qpre[b] * kGroup, hc[b], qpre[b + 1] - qpre[b], 0);
-    JHQ_PHASE(4);
-    JHQ_PHASE_FLUSH(2);
-}
 
 constexpr int kMfmaPD = 4;  // tiles in flight per wave
 // The minimum over each 16-lane row, on every lane of the row: swaps within
@@ -4543,32 +4533,96 @@ __device__ __forceinline__ void mfma_row_load(const uint8_t* p, uint32_t (&cw)[M
     }
 }
 
-// Wave wid runs tiles [wid T / W, (wid + 1) T / W) of the batch, from the
-// group and tile wstart[wid] names.  Lane (j, h) holds row j of each tile
+// Wave wid runs tiles [wid T / W, (wid + 1) T / W) of the batch; each
+// workgroup finds where its waves start from the hash of the batch's lists
+// (a scan of per-thread slot chunks).  Lane (j, h) holds row j of each tile
 // (list slot 16 t + j) for subspaces GS h .. GS h + GS - 1, read straight
 // from the row-major copy (a tile's 16 rows are one contiguous run of 16 M
 // bytes) into a ring of kMfmaPD tiles in registers.
 template <int M>
 __global__ void __launch_bounds__(256)
-mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ rows, uint32_t* __restrict__ dump,
-                 uint32_t* __restrict__ tmin) {
-    constexpr int NK = M / 8, ND = M / 16, GS = M / 4, D = 8 * M;
-    const int lane = threadIdx.x & 63, j = lane & 15, h = lane >> 4;
-    const int W = gridDim.x * 4, wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int T = w.ctl[0];
+mfma_scan_kernel(MfmaWs w, const int4* __restrict__ ldesc, const uint8_t* __restrict__ rows,
+                 uint32_t* __restrict__ dump, uint32_t* __restrict__ tmin) {
+    constexpr int NK = M / 8, ND = M / 16, GS = M / 4, D = 8 * M, NT = 256;
+    __shared__ int csum[NT + 1], wsm[NT / 64];
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, h = lane >> 4;
+    const int W = gridDim.x * 4, wid = blockIdx.x * 4 + (tid >> 6);
+    const int H = w.H;
+    JHQ_PHASE_DECL
+    // the batch's tiles: thread t sums the slots of its chunk (per slots;
+    // per <= 64 since H <= 64 NT), and an exclusive scan of the chunk sums
+    // gives csum (csum[NT] = T)
+    const int per = (H + NT - 1) / NT;
+    const int cs0 = min(H, tid * per), cs1 = min(H, cs0 + per);
+    int mine = 0;
+    for (int sb = cs0; sb < cs1; sb += 8) {
+        int4 rec[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) rec[u] = sb + u < cs1 ? w.hs[sb + u] : make_int4(-1, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (rec[u].x >= 0) mine += ((rec[u].y + 15) >> 4) * ((rec[u].z + kGroup - 1) / kGroup);
+    }
+    int inc = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) wsm[tid >> 6] = inc;
+    __syncthreads();
+    int wbase = 0;
+    for (int w2 = 0; w2 < (tid >> 6); w2++) wbase += wsm[w2];
+    csum[tid] = wbase + inc - mine;
+    if (tid == NT - 1) csum[NT] = wbase + inc;
+    __syncthreads();
+    const int T = csum[NT];
+    JHQ_PHASE(2);
     const int a0 = (int)((int64_t)wid * T / W), a1 = (int)((int64_t)(wid + 1) * T / W);
     int left = a1 - a0;
     if (left <= 0) return;
-    const int2 st = w.wstart[wid];
-    int g = st.x, off = st.y;
-    JHQ_PHASE_DECL
+    // the chunk holding tile a0 (the last with csum <= a0), then its slot:
+    // lane l takes slot s0 + l
+    int lo = 0, hi = NT - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (csum[mid] <= a0) lo = mid;
+        else hi = mid - 1;
+    }
+    const int s0 = min(H, lo * per), s1 = min(H, s0 + per);
+    int tl = 0, nzl = 1;
+    if (s0 + lane < s1) {
+        const int4 rec = w.hs[s0 + lane];
+        if (rec.x >= 0) {
+            nzl = (rec.z + kGroup - 1) / kGroup;
+            tl = ((rec.y + 15) >> 4) * nzl;
+        }
+    }
+    int tinc = tl;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(tinc, o);
+        if (lane >= o) tinc += t;
+    }
+    const int rel = a0 - csum[lo];
+    const unsigned long long fm = __ballot(s0 + lane < s1 && tinc > rel);
+    if (fm == 0ull) return;  // not reached: tile a0 lies in chunk lo
+    const int fl = __ffsll((long long)fm) - 1;
+    int hs = s0 + fl;
+    const int rr = rel - __shfl(tinc - tl, fl), nz0 = __shfl(nzl, fl);
+    int gt = rr / nz0, off = rr - gt * nz0;
+    int4 srec = w.hs[hs];
+    JHQ_PHASE(3);
     while (left > 0) {
-        // the group record and its 16 query entries are loaded side by side
-        const int4 ga = w.grp[g];
-        const int2 gqv = w.gq[g * 16 + j];
-        const int nq = ga.w;
-        const int n = min((ga.z + kGroup - 1) / kGroup - off, left);
-        const int nl = ga.z;
+        // the slot's list and the group's 16 pair entries
+        const int cnt = srec.y;
+        const int r = 16 * gt + j;
+        const int2 gqv = r < w.B ? w.ql[(int64_t)hs * w.B + r] : make_int2(0, 0);
+        const int4 L = ldesc[srec.x];
+        const int nq = min(16, cnt - 16 * gt);
+        const int n = min((L.z + kGroup - 1) / kGroup - off, left);
+        const int nl = L.z;
+        const int4 ga = make_int4(L.x, L.y, L.z, nq);
         // tiles past the run's last reload its last tile (in bounds, unused)
         const uint8_t* base = rows + ((int64_t)ga.x + 16 * off + j) * M + GS * h;
         uint32_t c0[ND], c1[ND], c2[ND], c3[ND];
@@ -4622,8 +4676,24 @@ mfma_scan_kernel(MfmaWs w, const uint8_t* __restrict__ rows, uint32_t* __restric
 #undef JHQ_MFMA_TILE
 #undef JHQ_MFMA_FETCH
         left -= n;
-        g++;
         off = 0;
+        // the next group: the slot's next 16 pairs, else the next occupied
+        // slot (64 slots looked at a time, one per lane)
+        if (++gt >= (cnt + 15) >> 4 && left > 0) {
+            gt = 0;
+            int found = -1;
+            for (int sb = hs + 1; sb < H && found < 0; sb += 64) {
+                const int4 rec = sb + lane < H ? w.hs[sb + lane] : make_int4(-1, 0, 0, 0);
+                const unsigned long long oc = __ballot(rec.x >= 0);
+                if (oc) {
+                    const int fl2 = __ffsll((long long)oc) - 1;
+                    found = sb + fl2;
+                    srec = make_int4(__shfl(rec.x, fl2), __shfl(rec.y, fl2), __shfl(rec.z, fl2), 0);
+                }
+            }
+            if (found < 0) break;
+            hs = found;
+        }
         JHQ_PHASE(1);
     }
     JHQ_PHASE_FLUSH(0);
@@ -4900,7 +4970,7 @@ bool mfma_fuses_refine(int ck) { return ck <= kMfmaFuseMaxCk; }
 template <int NT, bool FUSE>
 __global__ void __launch_bounds__(NT)
 mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restrict__ tmin,
-                    const MfmaQS* __restrict__ qs, const int4* __restrict__ qinfo,
+                    MfmaWs w, const int32_t* __restrict__ qtot,
                     const float* __restrict__ q_rot, int d, int Ds, int K1D, int bpd,
                     const float* __restrict__ c1d, int M, const int32_t* __restrict__ probes,
                     const int32_t* __restrict__ gofs, int P, const int4* __restrict__ ldesc,
@@ -4928,8 +4998,19 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const unsigned long long lt = (1ull << lane) - 1ull;
     JHQ_PHASE_DECL
-    const int4 qi = qinfo[b];
+    // the query's row: first dump slot and tiles (x, z); y, its segment
+    // among the queries with candidates, is counted where it is needed.  The
+    // workgroups clear the batch's list hash for the next batch on their way
+    // out (the tile kernel, its only reader, has finished)
+    const int4 qi = make_int4(b * w.perq, 0, qtot[b], 0);
+    auto clear_hash = [&]() {
+        const int B = gridDim.x, h0 = (int)((int64_t)b * w.H / B);
+        const int h1 = (int)((int64_t)(b + 1) * w.H / B);
+        for (int h = h0 + tid; h < h1; h += NT) w.hs[h] = make_int4(-1, 0, 0, 0);
+    };
+    const MfmaQS* qs = w.qs;
     if (qi.z == 0) {
+        clear_hash();
         // no candidates: no neighbours (without FUSE, refine sees no segment)
         if (!FUSE) return;
         for (int r = tid; r < k; r += NT) {
@@ -4994,7 +5075,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             __syncthreads();
             That = 0u;
 #pragma unroll
-            for (int w = 0; w < NW; w++) That = max(That, (uint32_t)wsum[w]);
+            for (int w2 = 0; w2 < NW; w2++) That = max(That, (uint32_t)wsum[w2]);
         } else {
             __syncthreads();
             That = block_radix_kth<NT>([&](int i) { return tl[i]; }, nt, ck, (int*)ebuf, ctl + 2);
@@ -5299,8 +5380,13 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     }
     __syncthreads();
     if (!FUSE) {
+        clear_hash();
         // the short list and its pool slots (the probe whose canonical
-        // range holds the tag) as the query's one segment
+        // range holds the tag) as the query's one segment: the number of
+        // earlier queries with candidates
+        int seg = 0;
+        for (int i = lane; i < b; i += 64) seg += qtot[i] > 0 ? 1 : 0;
+        for (int o = 32; o > 0; o >>= 1) seg += __shfl_xor(seg, o);
         for (int i = tid; i < ck; i += NT) {
             int32_t slot = -1;
             if (i < kk) {
@@ -5309,8 +5395,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
                     if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
                         slot = meta[4 * q] + (tag - meta[4 * q + 3]);
             }
-            partial[(int64_t)qi.y * ck + i] = i < kk ? S.kout[i] : ~0ull;
-            partial_slot[(int64_t)qi.y * ck + i] = slot;
+            partial[(int64_t)seg * ck + i] = i < kk ? S.kout[i] : ~0ull;
+            partial_slot[(int64_t)seg * ck + i] = slot;
         }
         JHQ_PHASE(0);
         JHQ_PHASE_FLUSH(3);
@@ -5346,15 +5432,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     JHQ_PHASE(10);
     refine_short_list<NT>(S, kk, ck, k, b, kslot, cpos, cprim, fkeys, sqp, rcb, d, Ds, Kr, RC, Br,
                           bpv, list_res, list_corr, list_ids, out_d, out_i, topck_dbg, tabp);
+    clear_hash();
     JHQ_PHASE(0);
     JHQ_PHASE_FLUSH(3);
-}
-
-static size_t mfma_plan_lds(int B, int P) {
-    const int H = mfma_hash_size(B * P);
-    const size_t work = (size_t)(5 * H + 4 + B + 1 + 2 * (kMfmaPlanNT / 64)) * 4 + 64;
-    const size_t quant = (size_t)3 * (kMfmaPlanNT / 64) * 8 + 64;
-    return std::max(work, quant);
 }
 
 static size_t mfma_recheck_lds(int M, int d, int P, int ck, int K1D, int B, int rck) {
@@ -5368,14 +5448,23 @@ bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, 
     if (K1D != 2 || bpd != 1 || Ds != 8 || d != 8 * M) return false;
     if (M % 16 != 0 || M < 16 || M > 128 || d > kRecheckNT || P >= kRecheckNT) return false;
     if (B < 1 || P < 1 || (int64_t)B * P > kMfmaMaxBP || ck < 1 || ck > kRecheckCap) return false;
-    return mfma_plan_lds(B, P) <= (size_t)kLdsBytes - 1024 &&
-           mfma_recheck_lds(M, d, P, ck, K1D, B, rck) <= (size_t)kLdsBytes - 1024;
+    return mfma_recheck_lds(M, d, P, ck, K1D, B, rck) <= (size_t)kLdsBytes - 1024;
 }
 
 static int mfma_scan_waves(int num_cu) { return std::max(1, num_cu) * kMfmaWavesPerCU; }
 
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
-    return mfma_carve(B, P, M, mfma_scan_waves(num_cu), nullptr, nullptr);
+    (void)num_cu;
+    return mfma_carve(B, P, M, nullptr, nullptr);
+}
+
+hipError_t mfma_hash_clear(int Bcap, int P, int M, unsigned char* ws, size_t ws_bytes,
+                           hipStream_t s) {
+    MfmaWs w;
+    if (!ws || ((uintptr_t)ws & 255) || mfma_carve(Bcap, P, M, ws, &w) > ws_bytes)
+        return hipErrorInvalidValue;
+    // every slot (-1, 0, -1, 0): free, no pairs (its size is set on use)
+    return fill_u64((unsigned long long*)w.hs, (int64_t)w.H * 2, 0x00000000ffffffffull, s);
 }
 
 hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const float* c1d, int B,
@@ -5386,42 +5475,36 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
                      const uint8_t* list_res, const float* list_corr, const int32_t* list_ids,
                      float* out_d, int32_t* out_i, unsigned long long* topck_dbg,
                      unsigned long long* partial, int32_t* partial_slot, int num_cu,
-                     hipStream_t s) {
+                     int Bcap, hipStream_t s) {
     const bool fuse = mfma_fuses_refine(ck);
-    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck, RC * Kr) || !ws || ((uintptr_t)ws & 255) ||
-        !dump || !rows || dump_slots % 16 != 0 || k < 1 || k > ck ||
-        (!fuse && (!partial || !partial_slot)))
+    if (!mfma_scan_ok(M, d, Ds, K1D, bpd, B, P, ck, RC * Kr) || !dump || !rows ||
+        dump_slots % 16 != 0 || k < 1 || k > ck || (!fuse && (!partial || !partial_slot)))
         return hipErrorInvalidValue;
     // tile minima after the candidate slots
     uint32_t* tmin = dump + dump_slots;
     MfmaWs w;
+    if ((int64_t)Bcap * P > kMfmaMaxBP || !mfma_ws(B, Bcap, P, M, ws, ws_bytes, dump_slots, &w))
+        return hipErrorInvalidValue;
     const int nwaves = mfma_scan_waves(num_cu);
-    if (mfma_carve(B, P, M, nwaves, ws, &w) > ws_bytes) return hipErrorInvalidValue;
-    const int H = mfma_hash_size(B * P);
-    const size_t lp = mfma_plan_lds(B, P);
-    static const int mxp = allow_max_lds((const void*)mfma_plan_kernel<kMfmaPlanNT>);
-    if ((int)lp > mxp) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mfma_plan_kernel<kMfmaPlanNT>, dim3(B + 1), dim3(kMfmaPlanNT), lp, s, q_rot,
-                       d, M, c1d, probes, gofs, qtot, B, P, ldesc, w, H, nwaves);
-    using SFn = void (*)(MfmaWs, const uint8_t*, uint32_t*, uint32_t*);
+    using SFn = void (*)(MfmaWs, const int4*, const uint8_t*, uint32_t*, uint32_t*);
     SFn f = M == 16 ? mfma_scan_kernel<16> : M == 32 ? mfma_scan_kernel<32>
           : M == 48 ? mfma_scan_kernel<48> : M == 64 ? mfma_scan_kernel<64>
           : M == 80 ? mfma_scan_kernel<80> : M == 96 ? mfma_scan_kernel<96>
           : M == 112 ? mfma_scan_kernel<112> : mfma_scan_kernel<128>;
-    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, rows, dump, tmin);
+    hipLaunchKernelGGL(f, dim3(nwaves / 4), dim3(256), 0, s, w, ldesc, rows, dump, tmin);
     const size_t lr = mfma_recheck_lds(M, d, P, ck, K1D, B, RC * Kr);
     static const int mxf = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT, true>);
     static const int mxs = allow_max_lds((const void*)mfma_recheck_kernel<kRecheckNT, false>);
     if ((int)lr > (fuse ? mxf : mxs)) return hipErrorInvalidValue;
     if (fuse)
         hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, true>), dim3(B), dim3(kRecheckNT), lr,
-                           s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
+                           s, dump, tmin, w, qtot, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
                            gofs, P, ldesc, codes_t, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
                            list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
                            partial_slot);
     else
         hipLaunchKernelGGL((mfma_recheck_kernel<kRecheckNT, false>), dim3(B), dim3(kRecheckNT), lr,
-                           s, dump, tmin, w.qs, w.qinfo, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
+                           s, dump, tmin, w, qtot, q_rot, d, Ds, K1D, bpd, c1d, M, probes,
                            gofs, P, ldesc, codes_t, rows, ck, k, res_c1d, Kr, RC, Br, bpv,
                            list_res, list_corr, list_ids, out_d, out_i, topck_dbg, partial,
                            partial_slot);
