@@ -648,7 +648,7 @@ def step_roofline(ix, hq, k, batch, step_us, ev_ms_per_step, workload, nprobe, a
             limiter = tj.get("limiter")
             counters = tj.get("counters")
     names = {"scan_dump_kernel": "scan_dump_kernel + select_query_kernel",
-             "mfma_scan_kernel": "mfma_plan_kernel + mfma_scan_kernel + mfma_recheck_kernel"
+             "mfma_scan_kernel": "mfma_scan_kernel + mfma_recheck_kernel"
                                  + (" (re-check and refine)" if fused else "")}
     out = {
         "kernel": names.get(kernel, kernel),
