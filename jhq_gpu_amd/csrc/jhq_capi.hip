@@ -87,6 +87,42 @@ struct DBuf {
         JHQ_HIP(hipMemcpy(p, h, count * sizeof(T), hipMemcpyHostToDevice));
         return JHQ_OK;
     }
+    // the same into the buffer it already has when that is large enough (n
+    // stays its capacity)
+    int upload_keep(const T* h, size_t count) {
+        JHQ_TRY(ensure(count));
+        JHQ_HIP(hipMemcpy(p, h, count * sizeof(T), hipMemcpyHostToDevice));
+        return JHQ_OK;
+    }
+    size_t bytes() const { return p ? n * sizeof(T) : 0; }
+};
+
+// Device scratch of an insert (codes, residual codes and corrections of the
+// new vectors, their lists, input and rotated batches, sort and scatter
+// buffers), kept between inserts so that streaming appends allocate nothing
+// once warm; released after an insert whose buffers exceed kInsertKeepBytes.
+constexpr size_t kInsertKeepBytes = size_t(256) << 20;
+struct InsertScratch {
+    DBuf<uint8_t> pc, rc;
+    DBuf<float> co;
+    DBuf<int32_t> asg;
+    DBuf<float> xb[2], yb;
+    DBuf<uint8_t> raw[2];
+    DBuf<unsigned long long> keys;
+    DBuf<unsigned char> oscr;
+    DBuf<int32_t> order, slist, sidx;
+    DBuf<int4> moves;
+    size_t bytes() const {
+        return pc.bytes() + rc.bytes() + co.bytes() + asg.bytes() + xb[0].bytes() +
+               xb[1].bytes() + yb.bytes() + raw[0].bytes() + raw[1].bytes() + keys.bytes() +
+               oscr.bytes() + order.bytes() + slist.bytes() + sidx.bytes() + moves.bytes();
+    }
+    void release() {
+        pc.release(); rc.release(); co.release(); asg.release();
+        xb[0].release(); xb[1].release(); yb.release(); raw[0].release(); raw[1].release();
+        keys.release(); oscr.release(); order.release(); slist.release(); sidx.release();
+        moves.release();
+    }
 };
 
 constexpr int kSteps = 4;
@@ -196,6 +232,8 @@ struct jhq_index {
     // rows it re-checked since the insert began (device)
     DBuf<float> dascr;
     DBuf<unsigned long long> drecheck;
+    // an insert's scratch, kept between inserts (appends) up to kInsertKeepBytes
+    InsertScratch ins;
 
     // search workspaces; ws[1] and the lane streams serve pipelined batches
     Workspace ws[kLanes];
@@ -1153,7 +1191,7 @@ int upload_ldesc(jhq_index* ix) {
         h[l] = make_int4(ix->l_start[l], ix->l_cap[l], ix->l_size[l], static_cast<int>(cb));
         cb += ix->l_size[l];
     }
-    return ix->dldesc.upload(h.data(), h.size());
+    return ix->dldesc.upload_keep(h.data(), h.size());
 }
 
 // The skew scan's copy of the codes (M a multiple of 32, at most 128).
@@ -1266,23 +1304,33 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         JHQ_HIP(jhq::fill_u64(ix->drecheck.p, 1, 0ull, s));
     }
 
-    DBuf<uint8_t> dpc, drc;
-    DBuf<float> dco;
-    DBuf<int32_t> dasg;
-    JHQ_TRY(dpc.alloc(static_cast<size_t>(n) * M));
-    JHQ_TRY(drc.alloc(static_cast<size_t>(n) * bpv));
-    JHQ_TRY(dco.alloc(static_cast<size_t>(n)));
-    JHQ_TRY(dasg.alloc(static_cast<size_t>(n)));
+    InsertScratch& sc = ix->ins;
+    // the scratch goes back to the device after an insert too large to keep
+    struct Trim {
+        InsertScratch& sc;
+        ~Trim() {
+            if (sc.bytes() > kInsertKeepBytes) sc.release();
+        }
+    } trim{sc};
+    DBuf<uint8_t>& dpc = sc.pc;
+    DBuf<uint8_t>& drc = sc.rc;
+    DBuf<float>& dco = sc.co;
+    DBuf<int32_t>& dasg = sc.asg;
+    JHQ_TRY(dpc.ensure(static_cast<size_t>(n) * M));
+    JHQ_TRY(drc.ensure(static_cast<size_t>(n) * bpv));
+    JHQ_TRY(dco.ensure(static_cast<size_t>(n)));
+    JHQ_TRY(dasg.ensure(static_cast<size_t>(n)));
     {
         const int64_t AB = std::min<int64_t>(ix->add_batch, n);
-        DBuf<float> dxb[2], dyb;
-        DBuf<uint8_t> draw[2];
-        DBuf<unsigned long long> keys;
+        DBuf<float>* dxb = sc.xb;
+        DBuf<float>& dyb = sc.yb;
+        DBuf<uint8_t>* draw = sc.raw;
+        DBuf<unsigned long long>& keys = sc.keys;
         for (int i = 0; i < 2 && i * AB < n; i++) {
-            JHQ_TRY(dxb[i].alloc(static_cast<size_t>(AB) * d));
-            if (dtype != JHQ_F32) JHQ_TRY(draw[i].alloc(static_cast<size_t>(AB) * d));
+            JHQ_TRY(dxb[i].ensure(static_cast<size_t>(AB) * d));
+            if (dtype != JHQ_F32) JHQ_TRY(draw[i].ensure(static_cast<size_t>(AB) * d));
         }
-        JHQ_TRY(dyb.alloc(static_cast<size_t>(AB) * d));
+        JHQ_TRY(dyb.ensure(static_cast<size_t>(AB) * d));
         // the copies run on their own stream a batch ahead of the kernels; an
         // input buffer is refilled once the kernels that read it (two batches
         // back) are done
@@ -1339,8 +1387,8 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     // stable order by (list, id) of the new vectors (the reference's
     // thrust::sort_by_key, v14/jhq_gpu_index.cu:468-486): keys (list << 32 |
     // vector) radix-sorted on the device; the host reads the list counts only
-    DBuf<unsigned char> oscr;
-    JHQ_TRY(oscr.alloc(jhq::kmeans_scratch_bytes(n, nlist)));
+    DBuf<unsigned char>& oscr = sc.oscr;
+    JHQ_TRY(oscr.ensure(jhq::kmeans_scratch_bytes(n, nlist)));
     const unsigned long long* sorted = nullptr;
     const int64_t* first = nullptr;
     JHQ_HIP(jhq::list_order(dasg.p, n, nlist, oscr.p, oscr.n, &sorted, &first, s));
@@ -1400,8 +1448,8 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         if (used > INT32_MAX) return fail(JHQ_EINVAL, "list pool exceeds int32 slots");
         JHQ_TRY(grow_pool(ix, used));  // only an empty pool grows here
         if (!moves.empty()) {
-            DBuf<int4> dmoves;
-            JHQ_TRY(dmoves.upload(moves.data(), moves.size()));
+            DBuf<int4>& dmoves = sc.moves;
+            JHQ_TRY(dmoves.upload_keep(moves.data(), moves.size()));
             JHQ_HIP(jhq::relocate_lists(dmoves.p, static_cast<int>(moves.size() / 2), M, bpv,
                                         ix->dcodes_t.p, ix->dcodes_t.p, ix->dres.p, ix->dres.p,
                                         ix->dcorr.p, ix->dcorr.p, ix->dlist_ids.p, ix->dlist_ids.p,
@@ -1416,10 +1464,12 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     // descriptors still hold the sizes before the insert)
     {
         JHQ_TRY(upload_ldesc(ix));
-        DBuf<int32_t> dorder, dslist, dsidx;
-        JHQ_TRY(dorder.alloc(static_cast<size_t>(n)));
-        JHQ_TRY(dslist.alloc(static_cast<size_t>(n)));
-        JHQ_TRY(dsidx.alloc(static_cast<size_t>(n)));
+        DBuf<int32_t>& dorder = sc.order;
+        DBuf<int32_t>& dslist = sc.slist;
+        DBuf<int32_t>& dsidx = sc.sidx;
+        JHQ_TRY(dorder.ensure(static_cast<size_t>(n)));
+        JHQ_TRY(dslist.ensure(static_cast<size_t>(n)));
+        JHQ_TRY(dsidx.ensure(static_cast<size_t>(n)));
         JHQ_HIP(jhq::scatter_plan(sorted, first, ix->dldesc.p, n, dorder.p, dslist.p, dsidx.p, s));
         JHQ_HIP(jhq::scatter_lists(dorder.p, dslist.p, dsidx.p, n, id_base, ix->dldesc.p, dpc.p,
                                    drc.p, dco.p, M, bpv, ix->dlist_ids.p, ix->dcodes_t.p, ix->dres.p,

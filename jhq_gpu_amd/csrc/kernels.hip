@@ -1096,6 +1096,15 @@ encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int 
     const int kmask = K1D - 1;
     float dot = 0.0f;
     uint32_t code = 0u, rbyte = 0u;
+    // whole 32-dimension chunks of 4-bit residuals (16 bytes) and of one-byte
+    // 8-dimension codes (4 bytes) are gathered in registers and stored with
+    // one 16-byte and one 4-byte store (a vector's rows are bpv and M bytes
+    // apart, so byte stores would each be a transaction of their own)
+    const bool wide_res = (mode & 2) && Br == 4 && bpv % 16 == 0 && d % 32 == 0 &&
+                          ((uintptr_t)res & 15) == 0;
+    const bool wide_code = (mode & 1) && Ds == 8 && M % 4 == 0 && d % 32 == 0 &&
+                           ((uintptr_t)codes & 3) == 0;
+    uint32_t rw[4] = {0u, 0u, 0u, 0u}, cwd = 0u;
     for (int c0 = 0; c0 < d; c0 += 32) {
         const int cw = (d - c0) < 32 ? (d - c0) : 32;
         for (int i = 0; i < 32; i++) {
@@ -1114,7 +1123,8 @@ encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int 
                     dig = (K1D == 1) ? 0 : nearest_mid(cmid, K1D, val);
                     code |= (uint32_t)dig << (k * bpd);
                     if (k == Ds - 1) {
-                        codes[vid * M + m] = (uint8_t)code;
+                        if (wide_code) cwd |= (code & 0xFFu) << (8 * (m & 3));
+                        else codes[vid * M + m] = (uint8_t)code;
                         code = 0u;
                     }
                 } else {
@@ -1126,7 +1136,10 @@ encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int 
                     const float r = val - yhat;
                     const int ri = (Kr == 1) ? 0 : nearest_mid(rmid + cb * Kr, Kr, r);
                     const float rhat = rval[cb * Kr + ri];
-                    if (Br == 4) {
+                    if (wide_res) {
+                        // nibble jj of the chunk: word jj / 8, bits 4 (jj % 8)
+                        rw[jj >> 3] |= (uint32_t)(ri & 0x0F) << (4 * (jj & 7));
+                    } else if (Br == 4) {
                         if ((j & 1) == 0) {
                             rbyte = (uint32_t)(ri & 0x0F);
                         } else {
@@ -1138,6 +1151,14 @@ encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int 
                     }
                     dot = fmaf(yhat, rhat, dot);
                 }
+            }
+            if (wide_res) {
+                *(uint4*)(res + vid * bpv + (c0 >> 1)) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+                rw[0] = rw[1] = rw[2] = rw[3] = 0u;
+            }
+            if (wide_code) {
+                *(uint32_t*)(codes + vid * M + (c0 >> 3)) = cwd;
+                cwd = 0u;
             }
         }
         __syncthreads();
