@@ -207,6 +207,23 @@ struct jhq_index {
     // re-reservations and host searches wait on it
     hipEvent_t done_ev = nullptr;
     bool done_pending = false;
+    // inserts and row refreshes end without a host wait: their last work on
+    // `stream` is tail_ev; device searches wait for it on the device, and
+    // everything that reads or rewrites the lists from the host waits first
+    hipEvent_t tail_ev = nullptr;
+    bool tail_pending = false;
+    // pinned staging of the asynchronous descriptor uploads (two, taken in
+    // turn; one is written again once its copy's event has passed) and of
+    // the row refresh's first rows
+    int4* h_ldesc[2] = {};
+    size_t h_ldesc_n[2] = {};
+    hipEvent_t ldesc_ev[2] = {};
+    bool ldesc_pending[2] = {};
+    int ldesc_turn = 0;
+    int32_t* h_from = nullptr;
+    size_t h_from_n = 0;
+    hipEvent_t from_ev = nullptr;
+    bool from_pending = false;
     DBuf<float> dP, dc1d, dres_c1d, dcent, dnorms;
     DBuf<int4> dldesc;
     DBuf<int32_t> dlist_ids;
@@ -260,6 +277,14 @@ struct jhq_index {
             if (h_d[l]) (void)hipHostFree(h_d[l]);
             if (h_i[l]) (void)hipHostFree(h_i[l]);
         }
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (int t = 0; t < 2; t++) {
+            if (h_ldesc[t]) (void)hipHostFree(h_ldesc[t]);
+            if (ldesc_ev[t]) (void)hipEventDestroy(ldesc_ev[t]);
+        }
+        if (h_from) (void)hipHostFree(h_from);
+        if (from_ev) (void)hipEventDestroy(from_ev);
+        if (tail_ev) (void)hipEventDestroy(tail_ev);
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
         for (auto& e : lane_ev)
@@ -298,15 +323,36 @@ struct jhq_index {
         num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
         JHQ_HIP(hipStreamCreate(&stream));
         JHQ_HIP(hipEventCreateWithFlags(&done_ev, hipEventDisableTiming));
+        JHQ_HIP(hipEventCreateWithFlags(&tail_ev, hipEventDisableTiming));
+        JHQ_HIP(hipEventCreateWithFlags(&from_ev, hipEventDisableTiming));
+        for (auto& e : ldesc_ev) JHQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
         return JHQ_OK;
     }
 
     // Blocks until the last device search has finished with the lists and
     // workspaces.
-    int quiesce() {
+    int quiesce_searches() {
         if (!done_pending) return JHQ_OK;
         JHQ_HIP(hipEventSynchronize(done_ev));
         done_pending = false;
+        return JHQ_OK;
+    }
+
+    // Blocks until the last device search and the last insert's (or row
+    // refresh's) enqueued work have finished.
+    int quiesce() {
+        JHQ_TRY(quiesce_searches());
+        if (!tail_pending) return JHQ_OK;
+        JHQ_HIP(hipEventSynchronize(tail_ev));
+        tail_pending = false;
+        return JHQ_OK;
+    }
+
+    // Marks the work enqueued on `stream` so far as the tail device searches
+    // and host accesses wait for.
+    int mark_tail() {
+        JHQ_HIP(hipEventRecord(tail_ev, stream));
+        tail_pending = true;
         return JHQ_OK;
     }
 };
@@ -618,7 +664,11 @@ int refresh_rows(jhq_index* ix) {
     const size_t need = static_cast<size_t>((std::max<int64_t>(ix->pool_cap, 1) + 15) / 16 * 16) *
                         static_cast<size_t>(ix->M);
     if (ix->dcodes_r.n < need || static_cast<int>(ix->rows_start.size()) != nl) {
-        if (ix->dcodes_r.n < need) JHQ_TRY(ix->dcodes_r.alloc(need));
+        // (the old copy may still be read by enqueued work)
+        if (ix->dcodes_r.n < need) {
+            JHQ_TRY(ix->quiesce());
+            JHQ_TRY(ix->dcodes_r.alloc(need));
+        }
         ix->rows_start.assign(nl, -1);
         ix->rows_rows.assign(nl, 0);
     }
@@ -629,12 +679,21 @@ int refresh_rows(jhq_index* ix) {
         max_rows = std::max(max_rows, ix->l_size[l] - from[l]);
     }
     if (max_rows > 0) {
+        // enqueued only (from pinned staging): device searches wait for the
+        // tail event, host searches run on the same stream or lanes forked
+        // from it
+        if (ix->from_pending) JHQ_HIP(hipEventSynchronize(ix->from_ev));
+        ix->from_pending = false;
+        JHQ_TRY(ensure_pinned(ix->h_from, ix->h_from_n, static_cast<size_t>(nl)));
+        std::memcpy(ix->h_from, from.data(), nl * sizeof(int32_t));
         JHQ_TRY(ix->drows_from.ensure(nl));
-        JHQ_HIP(hipMemcpyAsync(ix->drows_from.p, from.data(), nl * sizeof(int32_t),
+        JHQ_HIP(hipMemcpyAsync(ix->drows_from.p, ix->h_from, nl * sizeof(int32_t),
                                hipMemcpyHostToDevice, ix->stream));
+        JHQ_HIP(hipEventRecord(ix->from_ev, ix->stream));
+        ix->from_pending = true;
         JHQ_HIP(jhq::row_codes(ix->dldesc.p, ix->drows_from.p, nl, max_rows, ix->dcodes_t.p, ix->M,
                                ix->dcodes_r.p, ix->stream));
-        JHQ_HIP(hipStreamSynchronize(ix->stream));
+        JHQ_TRY(ix->mark_tail());
     }
     ix->rows_start = ix->l_start;
     ix->rows_rows = ix->l_size;
@@ -684,10 +743,13 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
         }
         // keys (dump scan) or biased integer distances (MFMA pre-scan)
         // (the pre-scan: u32 slots and one tile minimum per 16 after them)
+        // (grown with an eighth to spare: appends lengthen the lists a little
+        // at a time, and each reallocation here is one per lane)
         const size_t slots = static_cast<size_t>(Bq) * std::max<int64_t>(ix->dump_perq, 1);
+        const size_t words = bp->sh.mfma ? (slots + slots / 16 + 40) / 2 : slots;
         for (int i = 0; i < nws; i++)
-            JHQ_TRY(need(ix->ws[i].wdump, bp->sh.mfma ? (slots + slots / 16 + 40) / 2 : slots,
-                         grow));
+            if (!ix->ws[i].wdump.has(words))
+                JHQ_TRY(need(ix->ws[i].wdump, grow ? words + words / 8 : words, grow));
         if (bp->sh.mfma)
             for (int i = 0; i < nws; i++)
                 JHQ_TRY(need(ix->ws[i].wmfma, jhq::mfma_scan_bytes(Bq, bp->P, ix->M, ix->num_cu),
@@ -826,7 +888,10 @@ bool skew_needed(jhq_index* ix) {
 // nothing.
 int reserve_search(jhq_index* ix) {
     if (ix->ntotal == 0 || !ix->trained) return JHQ_OK;
-    JHQ_TRY(ix->quiesce());
+    // workspaces may be regrown: no device search may be using them (an
+    // insert's enqueued tail does not read them; the refreshes below are
+    // enqueued behind it)
+    JHQ_TRY(ix->quiesce_searches());
     if (ix->skew_stale && skew_needed(ix)) JHQ_TRY(refresh_skew(ix));
     if (rows_wanted(ix) && ix->rows_stale) JHQ_TRY(refresh_rows(ix));
     BatchPlan bp;
@@ -1183,15 +1248,34 @@ int train_impl(jhq_index* ix, const float* x, int64_t n_train) {
     return JHQ_OK;
 }
 
-// Uploads the ListDesc array {start, cap, size, cbase} from the host mirror.
-int upload_ldesc(jhq_index* ix) {
-    std::vector<int4> h(static_cast<size_t>(ix->nlist));
-    int64_t cb = 0;
-    for (int l = 0; l < ix->nlist; l++) {
-        h[l] = make_int4(ix->l_start[l], ix->l_cap[l], ix->l_size[l], static_cast<int>(cb));
-        cb += ix->l_size[l];
+// Uploads the ListDesc array {start, cap, size, cbase} from the host mirror:
+// synchronously, or (s given) enqueued on s from pinned staging.
+int upload_ldesc(jhq_index* ix, hipStream_t s = nullptr) {
+    const size_t nl = static_cast<size_t>(ix->nlist);
+    auto fill = [&](int4* h) {
+        int64_t cb = 0;
+        for (int l = 0; l < ix->nlist; l++) {
+            h[l] = make_int4(ix->l_start[l], ix->l_cap[l], ix->l_size[l], static_cast<int>(cb));
+            cb += ix->l_size[l];
+        }
+    };
+    if (!s) {
+        std::vector<int4> h(nl);
+        fill(h.data());
+        return ix->dldesc.upload_keep(h.data(), h.size());
     }
-    return ix->dldesc.upload_keep(h.data(), h.size());
+    const int t = ix->ldesc_turn;
+    ix->ldesc_turn ^= 1;
+    if (ix->ldesc_pending[t]) JHQ_HIP(hipEventSynchronize(ix->ldesc_ev[t]));
+    ix->ldesc_pending[t] = false;
+    JHQ_TRY(ensure_pinned(ix->h_ldesc[t], ix->h_ldesc_n[t], nl));
+    fill(ix->h_ldesc[t]);
+    JHQ_TRY(ix->dldesc.ensure(nl));
+    JHQ_HIP(hipMemcpyAsync(ix->dldesc.p, ix->h_ldesc[t], nl * sizeof(int4), hipMemcpyHostToDevice,
+                           s));
+    JHQ_HIP(hipEventRecord(ix->ldesc_ev[t], s));
+    ix->ldesc_pending[t] = true;
+    return JHQ_OK;
 }
 
 // The skew scan's copy of the codes (M a multiple of 32, at most 128).
@@ -1306,12 +1390,17 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
 
     InsertScratch& sc = ix->ins;
     // the scratch goes back to the device after an insert too large to keep
+    // (once the enqueued work that reads it is done)
     struct Trim {
         InsertScratch& sc;
+        hipStream_t s;
         ~Trim() {
-            if (sc.bytes() > kInsertKeepBytes) sc.release();
+            if (sc.bytes() > kInsertKeepBytes) {
+                (void)hipStreamSynchronize(s);
+                sc.release();
+            }
         }
-    } trim{sc};
+    } trim{sc, s};
     DBuf<uint8_t>& dpc = sc.pc;
     DBuf<uint8_t>& drc = sc.rc;
     DBuf<float>& dco = sc.co;
@@ -1376,9 +1465,9 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
                 std::fprintf(stderr, "[jhq] add: %lld / %lld vectors enqueued\n",
                              static_cast<long long>(start + nb), static_cast<long long>(n));
         }
-        JHQ_HIP(hipStreamSynchronize(s));
     }
     if (verbose() && ix->drecheck.p) {
+        JHQ_HIP(hipStreamSynchronize(s));
         unsigned long long rc = 0;
         JHQ_HIP(hipMemcpy(&rc, ix->drecheck.p, sizeof(rc), hipMemcpyDeviceToHost));
         std::fprintf(stderr, "[jhq] add: %llu of %lld rows re-checked by the fixed-order argmin\n",
@@ -1463,7 +1552,7 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
     // scatter the new vectors behind each list's current candidates (the
     // descriptors still hold the sizes before the insert)
     {
-        JHQ_TRY(upload_ldesc(ix));
+        JHQ_TRY(upload_ldesc(ix, s));
         DBuf<int32_t>& dorder = sc.order;
         DBuf<int32_t>& dslist = sc.slist;
         DBuf<int32_t>& dsidx = sc.sidx;
@@ -1474,10 +1563,12 @@ int insert_impl(jhq_index* ix, const void* x, int dtype, int64_t n, bool exact_f
         JHQ_HIP(jhq::scatter_lists(dorder.p, dslist.p, dsidx.p, n, id_base, ix->dldesc.p, dpc.p,
                                    drc.p, dco.p, M, bpv, ix->dlist_ids.p, ix->dcodes_t.p, ix->dres.p,
                                    ix->dcorr.p, s));
-        JHQ_HIP(hipStreamSynchronize(s));
         for (int l = 0; l < nlist; l++) ix->l_size[l] += static_cast<int32_t>(add[l + 1]);
     }
-    JHQ_TRY(upload_ldesc(ix));
+    // the descriptors with the new sizes follow the scatter on s; the host
+    // does not wait (device searches wait for the tail event)
+    JHQ_TRY(upload_ldesc(ix, s));
+    JHQ_TRY(ix->mark_tail());
     ix->ntotal += n;
     ix->broken = false;
     return JHQ_OK;
@@ -1566,6 +1657,8 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     // ordered after the previous device search (it shares the workspaces),
     // whatever stream that one ran on
     if (ix->done_pending) JHQ_HIP(hipStreamWaitEvent(s, ix->done_ev, 0));
+    // and after the last insert's or row refresh's enqueued work
+    if (ix->tail_pending) JHQ_HIP(hipStreamWaitEvent(s, ix->tail_ev, 0));
     if (!pipe) {
         for (int64_t q0 = 0; q0 < nq; q0 += Bmax) {
             const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));

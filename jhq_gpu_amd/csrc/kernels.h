@@ -26,7 +26,7 @@ hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t 
                           int64_t n, int m, int d, const float* norms,
                           unsigned long long* keys, hipStream_t s);
 // EPI argmin over the rows rowidx[0 .. min(n_max, *ndev)) of A (ndev read on
-// the device); keys[i] belongs to row rowidx[i].  n_max <= 65535 * 128.
+// the device); keys[i] belongs to row rowidx[i].
 hipError_t gemm_nt_argmin_rows(const float* A, int64_t lda, const int32_t* rowidx,
                                const int32_t* ndev, int64_t n_max, const float* Bm, int64_t ldb,
                                int m, int d, const float* norms, unsigned long long* keys,

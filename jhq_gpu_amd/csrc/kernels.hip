@@ -315,119 +315,121 @@ gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
     __shared__ __align__(16) float Bs[2][BK][BN + 4];
     const int tid = threadIdx.x;
     const int tx = tid % TX, ty = tid / TX;
-    const int64_t row0 = (int64_t)blockIdx.y * BM;
+    int64_t row0 = (int64_t)blockIdx.y * BM;
     const int col0 = blockIdx.x * BN;
     if constexpr (EPI == EPI_ARGMIN_IDX) {
         const int64_t c = *ndev;
         if (c < n) n = c;
-        if (row0 >= n) return;
     }
+    // one row tile; EPI_ARGMIN_IDX: row tiles blockIdx.y, + gridDim.y, ... below n
+    for (; row0 < n; row0 += (int64_t)gridDim.y * BM) {
+        float ra[AL], rb[BL];
+        auto gload = [&](int k0) {
+#pragma unroll
+            for (int i = 0; i < AL; i++) {
+                const int e = tid + i * NT, r = e / BK, kk = e % BK;
+                const int64_t gr = row0 + r;
+                const int gk = k0 + kk;
+                if constexpr (EPI == EPI_ARGMIN_IDX)
+                    ra[i] = (gr < n && gk < d) ? A[(int64_t)rowidx[gr] * lda + gk] : 0.0f;
+                else
+                    ra[i] = (gr < n && gk < d) ? A[gr * lda + gk] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < BL; i++) {
+                const int e = tid + i * NT, r = e / BK, kk = e % BK;
+                const int gc = col0 + r, gk = k0 + kk;
+                rb[i] = (gc < m && gk < d) ? Bm[(int64_t)gc * ldb + gk] : 0.0f;
+            }
+        };
+        auto sstore = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < AL; i++) {
+                const int e = tid + i * NT;
+                As[buf][e % BK][e / BK] = ra[i];
+            }
+#pragma unroll
+            for (int i = 0; i < BL; i++) {
+                const int e = tid + i * NT;
+                Bs[buf][e % BK][e / BK] = rb[i];
+            }
+        };
+        // thread's rows / cols: groups of 4 interleaved across the tile when
+        // TM (TN) is a multiple of 4, contiguous otherwise.
+        auto row_of = [&](int i) {
+            return (TM % 4 == 0) ? (i / 4) * (TY * 4) + ty * 4 + (i % 4) : ty * TM + i;
+        };
+        auto col_of = [&](int j) {
+            return (TN % 4 == 0) ? (j / 4) * (TX * 4) + tx * 4 + (j % 4) : tx * TN + j;
+        };
 
-    float ra[AL], rb[BL];
-    auto gload = [&](int k0) {
+        float acc[TM][TN];
 #pragma unroll
-        for (int i = 0; i < AL; i++) {
-            const int e = tid + i * NT, r = e / BK, kk = e % BK;
-            const int64_t gr = row0 + r;
-            const int gk = k0 + kk;
-            if constexpr (EPI == EPI_ARGMIN_IDX)
-                ra[i] = (gr < n && gk < d) ? A[(int64_t)rowidx[gr] * lda + gk] : 0.0f;
-            else
-                ra[i] = (gr < n && gk < d) ? A[gr * lda + gk] : 0.0f;
-        }
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int i = 0; i < BL; i++) {
-            const int e = tid + i * NT, r = e / BK, kk = e % BK;
-            const int gc = col0 + r, gk = k0 + kk;
-            rb[i] = (gc < m && gk < d) ? Bm[(int64_t)gc * ldb + gk] : 0.0f;
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < AL; i++) {
-            const int e = tid + i * NT;
-            As[buf][e % BK][e / BK] = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < BL; i++) {
-            const int e = tid + i * NT;
-            Bs[buf][e % BK][e / BK] = rb[i];
-        }
-    };
-    // thread's rows / cols: groups of 4 interleaved across the tile when
-    // TM (TN) is a multiple of 4, contiguous otherwise.
-    auto row_of = [&](int i) {
-        return (TM % 4 == 0) ? (i / 4) * (TY * 4) + ty * 4 + (i % 4) : ty * TM + i;
-    };
-    auto col_of = [&](int j) {
-        return (TN % 4 == 0) ? (j / 4) * (TX * 4) + tx * 4 + (j % 4) : tx * TN + j;
-    };
+            for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
 
-    float acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
-
-    const int nk = (d + BK - 1) / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int t = 0; t < nk; t++) {
-        const int buf = t & 1;
-        if (t + 1 < nk) gload((t + 1) * BK);
-#pragma unroll
-        for (int kk = 0; kk < BK; kk++) {
-            float a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++) a[i] = As[buf][kk][row_of(i)];
-#pragma unroll
-            for (int j = 0; j < TN; j++) b[j] = Bs[buf][kk][col_of(j)];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-        }
-        if (t + 1 < nk) sstore(buf ^ 1);
+        const int nk = (d + BK - 1) / BK;
+        gload(0);
+        sstore(0);
         __syncthreads();
-    }
+        for (int t = 0; t < nk; t++) {
+            const int buf = t & 1;
+            if (t + 1 < nk) gload((t + 1) * BK);
+#pragma unroll
+            for (int kk = 0; kk < BK; kk++) {
+                float a[TM], b[TN];
+#pragma unroll
+                for (int i = 0; i < TM; i++) a[i] = As[buf][kk][row_of(i)];
+#pragma unroll
+                for (int j = 0; j < TN; j++) b[j] = Bs[buf][kk][col_of(j)];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+            }
+            if (t + 1 < nk) sstore(buf ^ 1);
+            __syncthreads();
+        }
 
-    if constexpr (EPI == EPI_ARGMIN || EPI == EPI_ARGMIN_IDX) {
+        if constexpr (EPI == EPI_ARGMIN || EPI == EPI_ARGMIN_IDX) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int64_t gr = row0 + row_of(i);
-            unsigned long long best = ~0ull;
+            for (int i = 0; i < TM; i++) {
+                const int64_t gr = row0 + row_of(i);
+                unsigned long long best = ~0ull;
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int gc = col0 + col_of(j);
-                if (gc < m) {
-                    const float sc = fmaf(-2.0f, acc[i][j], norms[gc]);
-                    const unsigned long long key =
-                        ((unsigned long long)f2ord(sc) << 32) | (unsigned long long)(uint32_t)gc;
-                    best = key < best ? key : best;
+                for (int j = 0; j < TN; j++) {
+                    const int gc = col0 + col_of(j);
+                    if (gc < m) {
+                        const float sc = fmaf(-2.0f, acc[i][j], norms[gc]);
+                        const unsigned long long key =
+                            ((unsigned long long)f2ord(sc) << 32) | (unsigned long long)(uint32_t)gc;
+                        best = key < best ? key : best;
+                    }
+                }
+#pragma unroll
+                for (int off = TX / 2; off > 0; off >>= 1) {
+                    const unsigned long long o = __shfl_xor(best, off);
+                    best = o < best ? o : best;
+                }
+                if (tx == 0 && gr < n && best != ~0ull) atomicMin(&amin[gr], best);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int64_t gr = row0 + row_of(i);
+                if (gr >= n) continue;
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int gc = col0 + col_of(j);
+                    if (gc >= m) continue;
+                    float v = acc[i][j];
+                    if constexpr (EPI == EPI_SCORE) v = fmaf(-2.0f, v, norms[gc]);
+                    C[gr * ldc + gc] = v;
                 }
             }
-#pragma unroll
-            for (int off = TX / 2; off > 0; off >>= 1) {
-                const unsigned long long o = __shfl_xor(best, off);
-                best = o < best ? o : best;
-            }
-            if (tx == 0 && gr < n && best != ~0ull) atomicMin(&amin[gr], best);
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int64_t gr = row0 + row_of(i);
-            if (gr >= n) continue;
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int gc = col0 + col_of(j);
-                if (gc >= m) continue;
-                float v = acc[i][j];
-                if constexpr (EPI == EPI_SCORE) v = fmaf(-2.0f, v, norms[gc]);
-                C[gr * ldc + gc] = v;
-            }
-        }
+        if constexpr (EPI != EPI_ARGMIN_IDX) break;
     }
 }
 
@@ -579,9 +581,13 @@ hipError_t gemm_nt_argmin_rows(const float* A, int64_t lda, const int32_t* rowid
                                int m, int d, const float* norms, unsigned long long* keys,
                                hipStream_t s) {
     if (n_max <= 0 || m <= 0) return hipSuccess;
-    if ((n_max + 127) / 128 > 65535) return hipErrorInvalidValue;
-    dim3 grid((m + 127) / 128, (unsigned)((n_max + 127) / 128));
-    hipLaunchKernelGGL((gemm_nt_kernel<128, 128, 16, 8, 8, EPI_ARGMIN_IDX>), grid, dim3(256), 0, s,
+    // the listed rows are few (near ties of an assignment, typically a few
+    // in 10 000): 16-row tiles of 32 lists, k in steps of 64 (the time is the
+    // chain of k steps), and at most 16 workgroup rows that step over the
+    // row tiles below the count read on the device
+    const int64_t tiles = (n_max + 15) / 16;
+    dim3 grid((m + 31) / 32, (unsigned)(tiles < 16 ? tiles : 16));
+    hipLaunchKernelGGL((gemm_nt_kernel<16, 32, 64, 2, 2, EPI_ARGMIN_IDX>), grid, dim3(128), 0, s,
                        A, lda, Bm, ldb, n_max, m, d, nullptr, 0, norms, keys, rowidx, ndev);
     return hipGetLastError();
 }
@@ -1054,9 +1060,12 @@ hipError_t keys_to_assign(const unsigned long long* keys, int64_t n, int32_t* as
 }
 
 // ---------------------------------------------------------------------------
-// Encode: one thread per vector, rows staged through LDS in 32-dim chunks so
-// the global reads are coalesced while each thread walks its own vector in
-// dimension order (the residual correction is a sequential fmaf chain).
+// Encode: a workgroup takes kEncV vectors and walks their dimensions in
+// chunks of kEncC.  Every thread quantizes dimensions of the chunk (reads of
+// consecutive floats of one vector), the digits and residual indices are
+// packed into code and residual bytes from LDS, and one lane per vector
+// carries that vector's residual correction: a sequential fmaf chain in
+// dimension order over the quantized values the chunk left in LDS.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int nearest_mid(const float* mids, int n, float v) {
     int lo = 0, hi = n - 1;
@@ -1068,112 +1077,112 @@ __device__ __forceinline__ int nearest_mid(const float* mids, int n, float v) {
     return lo;
 }
 
-__global__ void __launch_bounds__(256)
+constexpr int kEncV = 16, kEncC = 128, kEncT = 256;
+constexpr int kEncPer = kEncV * kEncC / kEncT;  // dimensions a thread quantizes per chunk
+
+__global__ void __launch_bounds__(kEncT)
 encode_kernel(const float* __restrict__ y, int64_t n, int d, int M, int Ds, int K1D, int bpd,
               const float* __restrict__ c1d, int Kr, int RC, int Br, int bpv,
               const float* __restrict__ res_c1d, uint8_t* __restrict__ codes,
               uint8_t* __restrict__ res, float* __restrict__ corr, int mode) {
     // RC residual codebooks of Kr words: one shared by every dimension (the
     // reference, v14/jhq_gpu_index.cu:302-330) or one per subspace (RC = M)
-    __shared__ float tile[256][33];
     __shared__ float cval[256], cmid[256];
+    // the chunk's quantized values (yhat, rhat) per vector; the odd row
+    // stride puts the chain lanes' reads of one column in distinct banks
+    __shared__ float yh[kEncV][kEncC + 1], rh[kEncV][kEncC + 1];
+    __shared__ uint8_t dg[kEncV][kEncC], rq[kEncV][kEncC];
     extern __shared__ float rsh[];  // rval[RC*Kr], rmid[RC*Kr]
     float* rval = rsh;
     float* rmid = rsh + RC * Kr;
     const int tid = threadIdx.x;
-    const int64_t v0 = (int64_t)blockIdx.x * 256;
-    const int64_t vid = v0 + tid;
+    const int64_t v0 = (int64_t)blockIdx.x * kEncV;
+    const int nv = (n - v0) < kEncV ? (int)(n - v0) : kEncV;
     if (tid < K1D) cval[tid] = c1d[tid];
     if (mode & 2)
-        for (int i = tid; i < RC * Kr; i += 256) rval[i] = res_c1d[i];
+        for (int i = tid; i < RC * Kr; i += kEncT) rval[i] = res_c1d[i];
     __syncthreads();
     if (tid + 1 < K1D) cmid[tid] = 0.5f * (cval[tid] + cval[tid + 1]);
     if (mode & 2)
-        for (int i = tid; i < RC * Kr; i += 256)
+        for (int i = tid; i < RC * Kr; i += kEncT)
             if ((i % Kr) + 1 < Kr) rmid[i] = 0.5f * (rval[i] + rval[i + 1]);
     __syncthreads();
-    const bool live = vid < n;
     const int kmask = K1D - 1;
-    float dot = 0.0f;
-    uint32_t code = 0u, rbyte = 0u;
-    // whole 32-dimension chunks of 4-bit residuals (16 bytes) and of one-byte
-    // 8-dimension codes (4 bytes) are gathered in registers and stored with
-    // one 16-byte and one 4-byte store (a vector's rows are bpv and M bytes
-    // apart, so byte stores would each be a transaction of their own)
-    const bool wide_res = (mode & 2) && Br == 4 && bpv % 16 == 0 && d % 32 == 0 &&
-                          ((uintptr_t)res & 15) == 0;
-    const bool wide_code = (mode & 1) && Ds == 8 && M % 4 == 0 && d % 32 == 0 &&
-                           ((uintptr_t)codes & 3) == 0;
-    uint32_t rw[4] = {0u, 0u, 0u, 0u}, cwd = 0u;
-    for (int c0 = 0; c0 < d; c0 += 32) {
-        const int cw = (d - c0) < 32 ? (d - c0) : 32;
-        for (int i = 0; i < 32; i++) {
-            const int e = tid + i * 256, row = e >> 5, col = e & 31;
-            const int64_t gv = v0 + row;
-            tile[row][col] = (gv < n && col < cw) ? y[gv * d + c0 + col] : 0.0f;
+    float dot = 0.0f;  // lane v < nv: vector v0 + v's chain
+    for (int c0 = 0; c0 < d; c0 += kEncC) {
+        const int cw = (d - c0) < kEncC ? (d - c0) : kEncC;
+        float val[kEncPer];
+#pragma unroll
+        for (int i = 0; i < kEncPer; i++) {
+            const int e = tid + i * kEncT, v = e / kEncC, jj = e % kEncC;
+            val[i] = (v < nv && jj < cw) ? y[(v0 + v) * d + c0 + jj] : 0.0f;
         }
-        __syncthreads();
-        if (live) {
-            for (int jj = 0; jj < cw; jj++) {
-                const int j = c0 + jj;
-                const float val = tile[tid][jj];
-                const int m = j / Ds, k = j - m * Ds;
-                int dig;
-                if (mode & 1) {
-                    dig = (K1D == 1) ? 0 : nearest_mid(cmid, K1D, val);
-                    code |= (uint32_t)dig << (k * bpd);
-                    if (k == Ds - 1) {
-                        if (wide_code) cwd |= (code & 0xFFu) << (8 * (m & 3));
-                        else codes[vid * M + m] = (uint8_t)code;
-                        code = 0u;
-                    }
-                } else {
-                    dig = (codes[vid * M + m] >> (k * bpd)) & kmask;
-                }
-                if (mode & 2) {
-                    const int cb = (RC == 1) ? 0 : m;
-                    const float yhat = cval[dig];
-                    const float r = val - yhat;
-                    const int ri = (Kr == 1) ? 0 : nearest_mid(rmid + cb * Kr, Kr, r);
-                    const float rhat = rval[cb * Kr + ri];
-                    if (wide_res) {
-                        // nibble jj of the chunk: word jj / 8, bits 4 (jj % 8)
-                        rw[jj >> 3] |= (uint32_t)(ri & 0x0F) << (4 * (jj & 7));
-                    } else if (Br == 4) {
-                        if ((j & 1) == 0) {
-                            rbyte = (uint32_t)(ri & 0x0F);
-                        } else {
-                            rbyte |= (uint32_t)(ri & 0x0F) << 4;
-                            res[vid * bpv + (j >> 1)] = (uint8_t)rbyte;
-                        }
-                    } else {
-                        res[vid * bpv + j] = (uint8_t)ri;
-                    }
-                    dot = fmaf(yhat, rhat, dot);
-                }
-            }
-            if (wide_res) {
-                *(uint4*)(res + vid * bpv + (c0 >> 1)) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
-                rw[0] = rw[1] = rw[2] = rw[3] = 0u;
-            }
-            if (wide_code) {
-                *(uint32_t*)(codes + vid * M + (c0 >> 3)) = cwd;
-                cwd = 0u;
+#pragma unroll
+        for (int i = 0; i < kEncPer; i++) {
+            const int e = tid + i * kEncT, v = e / kEncC, jj = e % kEncC;
+            if (v >= nv || jj >= cw) continue;
+            const int j = c0 + jj;
+            const int m = j / Ds, k = j - m * Ds;
+            int dig;
+            if (mode & 1) dig = (K1D == 1) ? 0 : nearest_mid(cmid, K1D, val[i]);
+            else dig = (codes[(v0 + v) * M + m] >> (k * bpd)) & kmask;
+            dg[v][jj] = (uint8_t)dig;
+            if (mode & 2) {
+                const int cb = (RC == 1) ? 0 : m;
+                const float yhat = cval[dig];
+                const float r = val[i] - yhat;
+                const int ri = (Kr == 1) ? 0 : nearest_mid(rmid + cb * Kr, Kr, r);
+                rq[v][jj] = (uint8_t)ri;
+                yh[v][jj] = yhat;
+                rh[v][jj] = rval[cb * Kr + ri];
             }
         }
         __syncthreads();
+        if (mode & 1) {
+            // whole subspaces of the chunk (c0 is a multiple of Ds, which divides 32)
+            const int ms = cw / Ds;
+            for (int e = tid; e < kEncV * ms; e += kEncT) {
+                const int v = e / ms, mm = e - v * ms;
+                if (v >= nv) continue;
+                uint32_t code = 0u;
+                for (int k = 0; k < Ds; k++) code |= (uint32_t)dg[v][mm * Ds + k] << (k * bpd);
+                codes[(v0 + v) * M + c0 / Ds + mm] = (uint8_t)code;
+            }
+        }
+        if (mode & 2) {
+            if (Br == 4) {
+                // two dimensions a byte, the even one in the low nibble; an odd
+                // last dimension alone in the low nibble of the last byte
+                const int nb = (cw + 1) >> 1;
+                for (int e = tid; e < kEncV * nb; e += kEncT) {
+                    const int v = e / nb, b = e - v * nb;
+                    if (v >= nv) continue;
+                    const uint32_t lo = rq[v][2 * b] & 0x0Fu;
+                    const uint32_t hi = (2 * b + 1 < cw) ? (rq[v][2 * b + 1] & 0x0Fu) : 0u;
+                    res[(v0 + v) * bpv + (c0 >> 1) + b] = (uint8_t)(lo | (hi << 4));
+                }
+            } else {
+                for (int e = tid; e < kEncV * cw; e += kEncT) {
+                    const int v = e / cw, jj = e - v * cw;
+                    if (v >= nv) continue;
+                    res[(v0 + v) * bpv + c0 + jj] = rq[v][jj];
+                }
+            }
+            if (tid < nv)
+                for (int jj = 0; jj < cw; jj++) dot = fmaf(yh[tid][jj], rh[tid][jj], dot);
+        }
+        __syncthreads();
     }
-    if (live && (mode & 2)) {
-        if (Br == 4 && (d & 1)) res[vid * bpv + (d >> 1)] = (uint8_t)rbyte;
-        corr[vid] = 2.0f * dot;
-    }
+    if ((mode & 2) && tid < nv) corr[v0 + tid] = 2.0f * dot;
 }
 
 hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int bpd,
                   const float* c1d, int Kr, int RC, int Br, int bpv, const float* res_c1d,
                   uint8_t* codes, uint8_t* res, float* corr, int mode, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    if (K1D > 256 || Kr > 256 || (32 % Ds) != 0 || (RC != 1 && RC != M)) return hipErrorInvalidValue;
+    if (K1D > 256 || Kr > 256 || (32 % Ds) != 0 || (RC != 1 && RC != M) || Ds * M != d ||
+        ((mode & 2) && Br != 4 && Br != 8))
+        return hipErrorInvalidValue;
     const size_t lds = (size_t)2 * RC * Kr * sizeof(float);
     if (lds > 96 * 1024) return hipErrorInvalidValue;
     if (lds > 48 * 1024) {
@@ -1182,8 +1191,9 @@ hipError_t encode(const float* y, int64_t n, int d, int M, int Ds, int K1D, int 
                                                          96 * 1024);
         if (e != hipSuccess) return e;
     }
-    const int64_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(encode_kernel, dim3((unsigned)blocks), dim3(256), lds, s, y, n, d, M, Ds,
+    const int64_t blocks = (n + kEncV - 1) / kEncV;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(encode_kernel, dim3((unsigned)blocks), dim3(kEncT), lds, s, y, n, d, M, Ds,
                        K1D, bpd, c1d, Kr, RC, Br, bpv, res_c1d, codes, res, corr, mode);
     return hipGetLastError();
 }
