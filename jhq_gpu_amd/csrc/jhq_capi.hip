@@ -384,7 +384,7 @@ int assign_rows(jhq_index* ix, const float* d_y, int64_t n, int32_t* d_assign,
                 DBuf<unsigned long long>& keys) {
     JHQ_TRY(keys.ensure(static_cast<size_t>(n)));
     if (jhq::assign_mfma_ok(ix->d, d_y, ix->dcent.p) && (n + 127) / 128 <= 65535) {
-        JHQ_TRY(ix->dascr.ensure(jhq::assign_mfma_scratch_floats(n)));
+        JHQ_TRY(ix->dascr.ensure(jhq::assign_mfma_scratch_floats(n, ix->d, ix->nlist)));
         JHQ_HIP(jhq::assign_mfma(d_y, n, ix->d, ix->dcent.p, ix->nlist, ix->dnorms.p, d_assign,
                                  ix->dascr.p, ix->dascr.n, keys.p, ix->stream));
         if (verbose() && ix->drecheck.p)
@@ -2078,7 +2078,7 @@ int jhq_k_assign(const float* d_y, int64_t n, int d, const float* d_cent, const 
     hipError_t e = hipSuccess;
     if (jhq::assign_mfma_ok(d, d_y, d_cent) && (n + 127) / 128 <= 65535) {
         // MFMA scores, fixed-order re-check of near ties: the same lists
-        const size_t sf = jhq::assign_mfma_scratch_floats(std::max<int64_t>(n, 1));
+        const size_t sf = jhq::assign_mfma_scratch_floats(std::max<int64_t>(n, 1), d, nlist);
         float* scr = nullptr;
         e = hipMallocAsync(reinterpret_cast<void**>(&scr), sf * sizeof(float), s);
         if (e == hipSuccess) {

@@ -31,12 +31,14 @@ hipError_t gemm_nt_argmin_rows(const float* A, int64_t lda, const int32_t* rowid
                                const int32_t* ndev, int64_t n_max, const float* Bm, int64_t ldb,
                                int m, int d, const float* norms, unsigned long long* keys,
                                hipStream_t s);
-// IVF assignment on fp32 MFMA with the fixed-order argmin re-checking every
-// row whose two best approximate scores are closer than the error bound
+// IVF assignment on bf16 MFMA (each float split into two bf16, three
+// products per pair) with the fixed-order argmin re-checking every row whose
+// two best approximate scores are closer than the error bound
 // (assign_mfma.hip); the result equals gemm_nt_argmin's bit for bit.
-// scratch: assign_mfma_scratch_floats(n) floats; keys: n u64.  Enqueue only.
+// scratch: assign_mfma_scratch_floats(n, d, nlist) floats; keys: n u64.
+// Enqueue only.
 bool assign_mfma_ok(int d, const float* Y, const float* Cm);
-size_t assign_mfma_scratch_floats(int64_t n);
+size_t assign_mfma_scratch_floats(int64_t n, int d, int nlist);
 hipError_t assign_mfma(const float* Y, int64_t n, int d, const float* Cm, int nlist,
                        const float* norms, int32_t* assign, float* scratch,
                        size_t scratch_floats, unsigned long long* keys, hipStream_t s);

@@ -297,16 +297,13 @@ __device__ __forceinline__ int block_topk(GetV getv, GetT gett, int n, int k, in
 // ---------------------------------------------------------------------------
 // Fixed-order SIMT GEMM  C = A * Bm^T  (both operands k-contiguous rows)
 // ---------------------------------------------------------------------------
-// EPI_ARGMIN_IDX: EPI_ARGMIN over the rows rowidx[0 .. min(n, *ndev)) of A
-// (row i of the product is A's row rowidx[i]; keys indexed by i)
-enum { EPI_STORE = 0, EPI_SCORE = 1, EPI_ARGMIN = 2, EPI_ARGMIN_IDX = 3 };
+enum { EPI_STORE = 0, EPI_SCORE = 1, EPI_ARGMIN = 2 };
 
 template <int BM, int BN, int BK, int TM, int TN, int EPI>
 __global__ void __launch_bounds__((BM / TM) * (BN / TN))
 gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict__ Bm,
                int64_t ldb, int64_t n, int m, int d, float* __restrict__ C, int64_t ldc,
-               const float* __restrict__ norms, unsigned long long* __restrict__ amin,
-               const int32_t* __restrict__ rowidx, const int32_t* __restrict__ ndev) {
+               const float* __restrict__ norms, unsigned long long* __restrict__ amin) {
     constexpr int TX = BN / TN, TY = BM / TM, NT = TX * TY;
     constexpr int AL = BM * BK / NT, BL = BN * BK / NT;
     static_assert((BM * BK) % NT == 0 && (BN * BK) % NT == 0, "tile/threads mismatch");
@@ -315,121 +312,111 @@ gemm_nt_kernel(const float* __restrict__ A, int64_t lda, const float* __restrict
     __shared__ __align__(16) float Bs[2][BK][BN + 4];
     const int tid = threadIdx.x;
     const int tx = tid % TX, ty = tid / TX;
-    int64_t row0 = (int64_t)blockIdx.y * BM;
+    const int64_t row0 = (int64_t)blockIdx.y * BM;
     const int col0 = blockIdx.x * BN;
-    if constexpr (EPI == EPI_ARGMIN_IDX) {
-        const int64_t c = *ndev;
-        if (c < n) n = c;
-    }
-    // one row tile; EPI_ARGMIN_IDX: row tiles blockIdx.y, + gridDim.y, ... below n
-    for (; row0 < n; row0 += (int64_t)gridDim.y * BM) {
-        float ra[AL], rb[BL];
-        auto gload = [&](int k0) {
-#pragma unroll
-            for (int i = 0; i < AL; i++) {
-                const int e = tid + i * NT, r = e / BK, kk = e % BK;
-                const int64_t gr = row0 + r;
-                const int gk = k0 + kk;
-                if constexpr (EPI == EPI_ARGMIN_IDX)
-                    ra[i] = (gr < n && gk < d) ? A[(int64_t)rowidx[gr] * lda + gk] : 0.0f;
-                else
-                    ra[i] = (gr < n && gk < d) ? A[gr * lda + gk] : 0.0f;
-            }
-#pragma unroll
-            for (int i = 0; i < BL; i++) {
-                const int e = tid + i * NT, r = e / BK, kk = e % BK;
-                const int gc = col0 + r, gk = k0 + kk;
-                rb[i] = (gc < m && gk < d) ? Bm[(int64_t)gc * ldb + gk] : 0.0f;
-            }
-        };
-        auto sstore = [&](int buf) {
-#pragma unroll
-            for (int i = 0; i < AL; i++) {
-                const int e = tid + i * NT;
-                As[buf][e % BK][e / BK] = ra[i];
-            }
-#pragma unroll
-            for (int i = 0; i < BL; i++) {
-                const int e = tid + i * NT;
-                Bs[buf][e % BK][e / BK] = rb[i];
-            }
-        };
-        // thread's rows / cols: groups of 4 interleaved across the tile when
-        // TM (TN) is a multiple of 4, contiguous otherwise.
-        auto row_of = [&](int i) {
-            return (TM % 4 == 0) ? (i / 4) * (TY * 4) + ty * 4 + (i % 4) : ty * TM + i;
-        };
-        auto col_of = [&](int j) {
-            return (TN % 4 == 0) ? (j / 4) * (TX * 4) + tx * 4 + (j % 4) : tx * TN + j;
-        };
 
-        float acc[TM][TN];
+    float ra[AL], rb[BL];
+    auto gload = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int i = 0; i < AL; i++) {
+            const int e = tid + i * NT, r = e / BK, kk = e % BK;
+            const int64_t gr = row0 + r;
+            const int gk = k0 + kk;
+            ra[i] = (gr < n && gk < d) ? A[gr * lda + gk] : 0.0f;
+        }
 #pragma unroll
-            for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
+        for (int i = 0; i < BL; i++) {
+            const int e = tid + i * NT, r = e / BK, kk = e % BK;
+            const int gc = col0 + r, gk = k0 + kk;
+            rb[i] = (gc < m && gk < d) ? Bm[(int64_t)gc * ldb + gk] : 0.0f;
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < AL; i++) {
+            const int e = tid + i * NT;
+            As[buf][e % BK][e / BK] = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BL; i++) {
+            const int e = tid + i * NT;
+            Bs[buf][e % BK][e / BK] = rb[i];
+        }
+    };
+    // thread's rows / cols: groups of 4 interleaved across the tile when
+    // TM (TN) is a multiple of 4, contiguous otherwise.
+    auto row_of = [&](int i) {
+        return (TM % 4 == 0) ? (i / 4) * (TY * 4) + ty * 4 + (i % 4) : ty * TM + i;
+    };
+    auto col_of = [&](int j) {
+        return (TN % 4 == 0) ? (j / 4) * (TX * 4) + tx * 4 + (j % 4) : tx * TN + j;
+    };
 
-        const int nk = (d + BK - 1) / BK;
-        gload(0);
-        sstore(0);
+    float acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
+
+    const int nk = (d + BK - 1) / BK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int t = 0; t < nk; t++) {
+        const int buf = t & 1;
+        if (t + 1 < nk) gload((t + 1) * BK);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk++) {
+            float a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = As[buf][kk][row_of(i)];
+#pragma unroll
+            for (int j = 0; j < TN; j++) b[j] = Bs[buf][kk][col_of(j)];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        if (t + 1 < nk) sstore(buf ^ 1);
         __syncthreads();
-        for (int t = 0; t < nk; t++) {
-            const int buf = t & 1;
-            if (t + 1 < nk) gload((t + 1) * BK);
-#pragma unroll
-            for (int kk = 0; kk < BK; kk++) {
-                float a[TM], b[TN];
-#pragma unroll
-                for (int i = 0; i < TM; i++) a[i] = As[buf][kk][row_of(i)];
-#pragma unroll
-                for (int j = 0; j < TN; j++) b[j] = Bs[buf][kk][col_of(j)];
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-            }
-            if (t + 1 < nk) sstore(buf ^ 1);
-            __syncthreads();
-        }
+    }
 
-        if constexpr (EPI == EPI_ARGMIN || EPI == EPI_ARGMIN_IDX) {
+    if constexpr (EPI == EPI_ARGMIN) {
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int64_t gr = row0 + row_of(i);
-                unsigned long long best = ~0ull;
+        for (int i = 0; i < TM; i++) {
+            const int64_t gr = row0 + row_of(i);
+            unsigned long long best = ~0ull;
 #pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int gc = col0 + col_of(j);
-                    if (gc < m) {
-                        const float sc = fmaf(-2.0f, acc[i][j], norms[gc]);
-                        const unsigned long long key =
-                            ((unsigned long long)f2ord(sc) << 32) | (unsigned long long)(uint32_t)gc;
-                        best = key < best ? key : best;
-                    }
+            for (int j = 0; j < TN; j++) {
+                const int gc = col0 + col_of(j);
+                if (gc < m) {
+                    const float sc = fmaf(-2.0f, acc[i][j], norms[gc]);
+                    const unsigned long long key =
+                        ((unsigned long long)f2ord(sc) << 32) | (unsigned long long)(uint32_t)gc;
+                    best = key < best ? key : best;
                 }
-#pragma unroll
-                for (int off = TX / 2; off > 0; off >>= 1) {
-                    const unsigned long long o = __shfl_xor(best, off);
-                    best = o < best ? o : best;
-                }
-                if (tx == 0 && gr < n && best != ~0ull) atomicMin(&amin[gr], best);
             }
-        } else {
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int64_t gr = row0 + row_of(i);
-                if (gr >= n) continue;
+            for (int off = TX / 2; off > 0; off >>= 1) {
+                const unsigned long long o = __shfl_xor(best, off);
+                best = o < best ? o : best;
+            }
+            if (tx == 0 && gr < n && best != ~0ull) atomicMin(&amin[gr], best);
+        }
+    } else {
 #pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int gc = col0 + col_of(j);
-                    if (gc >= m) continue;
-                    float v = acc[i][j];
-                    if constexpr (EPI == EPI_SCORE) v = fmaf(-2.0f, v, norms[gc]);
-                    C[gr * ldc + gc] = v;
-                }
+        for (int i = 0; i < TM; i++) {
+            const int64_t gr = row0 + row_of(i);
+            if (gr >= n) continue;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int gc = col0 + col_of(j);
+                if (gc >= m) continue;
+                float v = acc[i][j];
+                if constexpr (EPI == EPI_SCORE) v = fmaf(-2.0f, v, norms[gc]);
+                C[gr * ldc + gc] = v;
             }
         }
-        if constexpr (EPI != EPI_ARGMIN_IDX) break;
     }
 }
 
@@ -446,8 +433,7 @@ static hipError_t launch_gemm(const float* A, int64_t lda, const float* Bm, int6
         dim3 grid((m + BN - 1) / BN, (unsigned)((nr + BM - 1) / BM));
         hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, TM, TN, EPI>), grid, dim3(NT), 0, s,
                            A + r0 * lda, lda, Bm, ldb, nr, m, d,
-                           C ? C + r0 * ldc : nullptr, ldc, norms, amin ? amin + r0 : nullptr,
-                           nullptr, nullptr);
+                           C ? C + r0 * ldc : nullptr, ldc, norms, amin ? amin + r0 : nullptr);
     }
     return hipGetLastError();
 }
@@ -576,19 +562,124 @@ hipError_t gemm_nt_argmin(const float* A, int64_t lda, const float* Bm, int64_t 
                                                         norms, keys, s);
 }
 
+// EPI_ARGMIN over listed rows: keys[i] = the smallest
+// (f2ord(fmaf(-2, dot, norms[c])) << 32 | c) over the lists c, for the row
+// A[rowidx[i]], i < min(n_max, *ndev); each dot the fmaf chain in k order,
+// as in gemm_nt_kernel.  The listed rows are few (the near ties of an
+// assignment): a workgroup takes 128 lists, one per thread, and steps over
+// groups of 8 rows staged in LDS; each list value read feeds the group's 8
+// chains, and each row's minimum goes out as one atomic per wave.
+constexpr int kArgRows = 8, kArgCols = 128, kArgK = 512, kArgKB = 64;
+
+__global__ void __launch_bounds__(kArgCols)
+argmin_rows_kernel(const float* __restrict__ A, int64_t lda, const int32_t* __restrict__ rowidx,
+                   const int32_t* __restrict__ ndev, int64_t n_max, const float* __restrict__ Bm,
+                   int64_t ldb, int m, int d, const float* __restrict__ norms,
+                   unsigned long long* __restrict__ keys) {
+    __shared__ __align__(16) float ys[kArgRows][kArgK];
+    const int tid = threadIdx.x;
+    const int col = blockIdx.x * kArgCols + tid;
+    int64_t cnt = *ndev;
+    if (cnt > n_max) cnt = n_max;
+    const float* brow = Bm + (int64_t)(col < m ? col : 0) * ldb;
+    const bool vec = (ldb % 4) == 0 && ((uintptr_t)Bm & 15) == 0;
+    for (int64_t g0 = (int64_t)blockIdx.y * kArgRows; g0 < cnt;
+         g0 += (int64_t)gridDim.y * kArgRows) {
+        const int nr = (cnt - g0) < kArgRows ? (int)(cnt - g0) : kArgRows;
+        int64_t rbase[kArgRows];
+#pragma unroll
+        for (int i = 0; i < kArgRows; i++) rbase[i] = (int64_t)rowidx[g0 + (i < nr ? i : nr - 1)] * lda;
+        float acc[kArgRows];
+#pragma unroll
+        for (int i = 0; i < kArgRows; i++) acc[i] = 0.0f;
+        for (int k0 = 0; k0 < d; k0 += kArgK) {
+            const int kw = (d - k0) < kArgK ? (d - k0) : kArgK;
+            // all of the chunk's loads in flight at once (rows past nr and
+            // k past kw read a valid element and store zero)
+            constexpr int kPer = kArgRows * kArgK / kArgCols;
+            static_assert(kArgK % kArgCols == 0, "a thread's elements stay in one row per k block");
+            float v[kPer];
+#pragma unroll
+            for (int t = 0; t < kPer; t++) {
+                const int e = tid + t * kArgCols, i = e / kArgK, kk = e % kArgK;
+                const int kc = kk < kw ? kk : kw - 1;
+                v[t] = A[rbase[i] + k0 + kc];
+            }
+            __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+            for (int t = 0; t < kPer; t++) {
+                const int e = tid + t * kArgCols, i = e / kArgK, kk = e % kArgK;
+                ys[i][kk] = (i < nr && kk < kw) ? v[t] : 0.0f;
+            }
+            __syncthreads();
+            if (col < m) {
+                int kk = 0;
+                if (vec && kw >= kArgKB) {
+                    // the list's values kArgKB at a time, the next kArgKB
+                    // loading while these feed the chains
+                    constexpr int J = kArgKB / 4;
+                    const int kend = kw / kArgKB * kArgKB;
+                    float4 cur[J], nxt[J];
+#pragma unroll
+                    for (int j = 0; j < J; j++) cur[j] = *(const float4*)(brow + k0 + 4 * j);
+                    for (; kk < kend; kk += kArgKB) {
+                        if (kk + kArgKB < kend) {
+#pragma unroll
+                            for (int j = 0; j < J; j++)
+                                nxt[j] = *(const float4*)(brow + k0 + kk + kArgKB + 4 * j);
+                        }
+#pragma unroll
+                        for (int j = 0; j < J; j++) {
+                            const float4 b = cur[j];
+#pragma unroll
+                            for (int i = 0; i < kArgRows; i++) {
+                                const float4 a = *(const float4*)&ys[i][kk + 4 * j];
+                                acc[i] = fmaf(a.x, b.x, acc[i]);
+                                acc[i] = fmaf(a.y, b.y, acc[i]);
+                                acc[i] = fmaf(a.z, b.z, acc[i]);
+                                acc[i] = fmaf(a.w, b.w, acc[i]);
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < J; j++) cur[j] = nxt[j];
+                    }
+                }
+                for (; kk < kw; kk++) {
+                    const float b = brow[k0 + kk];
+#pragma unroll
+                    for (int i = 0; i < kArgRows; i++) acc[i] = fmaf(ys[i][kk], b, acc[i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kArgRows; i++) {
+            if (i >= nr) break;
+            unsigned long long key = ~0ull;
+            if (col < m) {
+                const float sc = fmaf(-2.0f, acc[i], norms[col]);
+                key = ((unsigned long long)f2ord(sc) << 32) | (unsigned long long)(uint32_t)col;
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const unsigned long long o = __shfl_xor(key, off);
+                key = o < key ? o : key;
+            }
+            if ((tid & 63) == 0 && key != ~0ull) atomicMin(&keys[g0 + i], key);
+        }
+    }
+}
+
 hipError_t gemm_nt_argmin_rows(const float* A, int64_t lda, const int32_t* rowidx,
                                const int32_t* ndev, int64_t n_max, const float* Bm, int64_t ldb,
                                int m, int d, const float* norms, unsigned long long* keys,
                                hipStream_t s) {
     if (n_max <= 0 || m <= 0) return hipSuccess;
-    // the listed rows are few (near ties of an assignment, typically a few
-    // in 10 000): 16-row tiles of 32 lists, k in steps of 64 (the time is the
-    // chain of k steps), and at most 16 workgroup rows that step over the
-    // row tiles below the count read on the device
-    const int64_t tiles = (n_max + 15) / 16;
-    dim3 grid((m + 31) / 32, (unsigned)(tiles < 16 ? tiles : 16));
-    hipLaunchKernelGGL((gemm_nt_kernel<16, 32, 64, 2, 2, EPI_ARGMIN_IDX>), grid, dim3(128), 0, s,
-                       A, lda, Bm, ldb, n_max, m, d, nullptr, 0, norms, keys, rowidx, ndev);
+    // up to 32 workgroup rows step over the groups of rows below the count
+    // read on the device
+    const int64_t groups = (n_max + kArgRows - 1) / kArgRows;
+    dim3 grid((m + kArgCols - 1) / kArgCols, (unsigned)(groups < 32 ? groups : 32));
+    hipLaunchKernelGGL(argmin_rows_kernel, grid, dim3(kArgCols), 0, s, A, lda, rowidx, ndev, n_max,
+                       Bm, ldb, m, d, norms, keys);
     return hipGetLastError();
 }
 
