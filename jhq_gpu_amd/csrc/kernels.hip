@@ -1916,7 +1916,9 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     float* srow = (float*)(scnt + 4);                // [nlist] (QB only)
     float* sqr = srow + (QB ? nlist : 0);             // [d] (QB and MF): the rotated query
     int* gsz = (int*)(sqr + (QB && MF ? mf.d : 0));   // [P] (MF): the probed lists' sizes
-    double* red = (double*)(((uintptr_t)(gsz + (MF ? P : 0)) + 7) & ~(uintptr_t)7);  // [3 NW] (MF)
+    // [3 NW] (MF); aligned by offset from smem, not through an integer
+    // address, so its loads stay LDS loads
+    double* red = (double*)(smem + ((((unsigned char*)(gsz + (MF ? P : 0)) - smem) + 7) & ~(ptrdiff_t)7));
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* row = QB ? srow : scores + (int64_t)b * nlist;
     JHQ_PHASE_DECL
@@ -5263,16 +5265,28 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     // the tiles whose minimum is at or below thr into qlist (at most cap
     // listed; returns the count), tile minima from LDS when they fit there,
     // else from global memory
-    auto list_tiles = [&](uint32_t thr, int* qlist, int cap) {
-        const uint32_t* tl = tiles_in_lds ? (const uint32_t*)mp : tm;
+    auto list_tiles = [&](uint32_t thr, int* qlist, int cap) __attribute__((always_inline)) {
+        // (two loops, not one pointer that may point to either memory: a
+        // load through such a pointer is a flat load, which every LDS wait
+        // then also waits for)
+        using lds_u32 = const __attribute__((address_space(3))) uint32_t;
+        lds_u32* tl = (lds_u32*)mp;
         if (tid == 0) ctl[1] = 0;
         __syncthreads();
         for (int t0 = 0; t0 < nt; t0 += kRecheckTM * NT) {
             uint32_t mv[kRecheckTM];
+            if (tiles_in_lds) {
 #pragma unroll
-            for (int u = 0; u < kRecheckTM; u++) {
-                const int t = t0 + u * NT + tid;
-                mv[u] = t < nt ? tl[t] : ~0u;
+                for (int u = 0; u < kRecheckTM; u++) {
+                    const int t = t0 + u * NT + tid;
+                    mv[u] = t < nt ? tl[t] : ~0u;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < kRecheckTM; u++) {
+                    const int t = t0 + u * NT + tid;
+                    mv[u] = t < nt ? tm[t] : ~0u;
+                }
             }
 #pragma unroll
             for (int u = 0; u < kRecheckTM; u++) {
