@@ -2928,7 +2928,7 @@ scan_wave_kernel(const float* __restrict__ q_rot, int d, int Ds, int K1D, int bp
         for (;;) {
             int t = 0, take = 1;
             if (lane == 0) {
-                const int done = *(volatile int*)&ctl[2];
+                const int done = *(volatile __attribute__((address_space(3))) int*)&ctl[2];
                 take = nunit - done > 4 * NW ? 2 : 1;
                 t = atomicAdd(&ctl[2], take);
             }
