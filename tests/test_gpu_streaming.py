@@ -40,7 +40,7 @@ def _pair(d, M, nlist, nprobe, per_sub, alpha=4.0, Br=4, batch=32):
 @pytest.mark.parametrize("per_sub", [0, 1], ids=["shared_books", "per_subspace_books"])
 def test_streaming_append_equals_one_shot(gpu, per_sub):
     d, M, nlist, nprobe, k = 64, 16, 16, 5, 10
-    base, q = queries_and_base(7000, 30, d, 40, seed=501 + per_sub)
+    base, q = queries_and_base(12800, 30, d, 40, seed=501 + per_sub)
     g, o = _pair(d, M, nlist, nprobe, per_sub)
     g.train(base[:2000])
     o.train(base[:2000])
@@ -48,8 +48,9 @@ def test_streaming_append_equals_one_shot(gpu, per_sub):
     assert np.array_equal(_bits(cb["res_c1d"]), _bits(o.res_c1d))
     g.add(base[:1200])
     upto = 1200
-    # ragged appends, one that fits in the existing blocks, some that move lists
-    for n in (5, 1, 700, 2300, 40, 2754):
+    # ragged appends, one that fits in the existing blocks, some that move
+    # lists, and a larger one (several encode workgroups' worth, as config 5)
+    for n in (5, 1, 700, 2300, 40, 2754, 5800):
         g.append(base[upto:upto + n])
         upto += n
         o.add(base[:upto])
@@ -139,7 +140,7 @@ def test_byte_ingestion(gpu, dtype):
     d, M, nlist, nprobe, k = 100, 25, 8, 3, 10
     rng = np.random.default_rng(31 if dtype == "uint8" else 32)
     cent = rng.normal(0, 30, (12, d))
-    x = cent[rng.integers(0, 12, 4000)] + rng.normal(0, 20, (4000, d))
+    x = cent[rng.integers(0, 12, 9000)] + rng.normal(0, 20, (9000, d))
     if dtype == "uint8":
         xb = np.clip(np.rint(x + 128), 0, 255).astype(np.uint8)
     else:
