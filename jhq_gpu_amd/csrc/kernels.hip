@@ -5145,15 +5145,30 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             for (int r = tid; r < ck; r += NT) topck_dbg[(int64_t)b * ck + r] = ~0ull;
         return;
     }
-    // the query, codebook and probe table are requested now and stored in
-    // LDS after pass 1, whose loads do not wait for them (d <= NT, P < NT)
+    // the probed lists' ids are requested first (their descriptors depend on
+    // them), then pass 1's tile minima (when they go through LDS), then the
+    // query, codebook and probe table (d <= NT, P < NT): a load waits only
+    // for those issued before it, so the descriptors and the LDS stores do
+    // not wait for the tile minima
+    // (list ids are non-negative: an unsigned index, whose widening does not
+    // wait for the load)
+    const int prb = tid < P ? probes[(int64_t)b * P + tid] : 0;
+    const uint32_t* tm = tmin + qi.x / kGroup;
+    const int nt = qi.z;
+    const bool tiles_in_lds = nt >= ck && nt <= 2 * kRecheckCap;
+    constexpr int TU = (2 * kRecheckCap + NT - 1) / NT;
+    uint32_t tv[TU];
+    if (tiles_in_lds) {
+#pragma unroll
+        for (int u = 0; u < TU; u++) tv[u] = tid + u * NT < nt ? tm[tid + u * NT] : ~0u;
+    }
     const float qv = tid < d ? q_rot[(int64_t)b * d + tid] : 0.0f;
     const float cv = tid < K1D ? c1d[tid] : 0.0f;
-    const int4 Lv = tid < P ? ldesc[probes[(int64_t)b * P + tid]] : make_int4(0, 0, 0, 0);
     const int gv = tid <= P ? gofs[(int64_t)b * (P + 1) + tid] : 0;
     // the residual codebooks for the refine, requested now as well
     const float rcv = FUSE && tid < RC * Kr ? res_c1d[tid] : 0.0f;
     const MfmaQS Q = qs[b];
+    const int4 Lv = tid < P ? ldesc[(uint32_t)prb] : make_int4(0, 0, 0, 0);
     const int64_t n = (int64_t)qi.z * kGroup;
     const uint32_t* row = dump + qi.x;
     const uint4* row4 = (const uint4*)row;
@@ -5174,20 +5189,14 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     // bound from the waves' lane minima; otherwise their exact ck-th
     // smallest, from an LDS copy when they fit there, else from registers or
     // global memory
-    const uint32_t* tm = tmin + qi.x / kGroup;
-    const int nt = qi.z;
     uint32_t That = ~0u;
-    const bool tiles_in_lds = nt >= ck && nt <= 2 * kRecheckCap;
     if (tiles_in_lds) {
         uint32_t* tl = (uint32_t*)mp;  // mp and mc, free until the members
-        constexpr int TU = (2 * kRecheckCap + NT - 1) / NT;
-        uint32_t v[TU], lmin = ~0u;
-#pragma unroll
-        for (int u = 0; u < TU; u++) v[u] = tid + u * NT < nt ? tm[tid + u * NT] : ~0u;
+        uint32_t lmin = ~0u;
 #pragma unroll
         for (int u = 0; u < TU; u++) {
-            if (tid + u * NT < nt) tl[tid + u * NT] = v[u];
-            lmin = min(lmin, v[u]);
+            if (tid + u * NT < nt) tl[tid + u * NT] = tv[u];
+            lmin = min(lmin, tv[u]);
         }
         if (nt >= NT && ck <= 64 * NW) {
             // every lane holds a tile minimum: each wave takes the r-th
