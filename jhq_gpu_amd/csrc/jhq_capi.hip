@@ -256,6 +256,10 @@ struct jhq_index {
     Workspace ws[kLanes];
     hipStream_t lane[kLanes] = {};
     hipEvent_t lane_ev[kLanes + 1] = {};  // fork, then each lane's last batch done
+    // the lanes pipelined batches take, in turn: one per hardware queue the
+    // lanes landed on (calibrate_lanes)
+    int lane_use[kLanes] = {};
+    int nlanes = 0;
     // inserts: the two input buffers' copied / consumed events (the copies run
     // on the last lane's stream, idle while an insert runs: a stream of its
     // own would share one of the process's 4 hardware queues with a lane and
@@ -308,7 +312,69 @@ struct jhq_index {
         if (lane[kLanes - 1]) return JHQ_OK;
         for (auto& l : lane) JHQ_HIP(hipStreamCreate(&l));
         for (auto& e : lane_ev) JHQ_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        calibrate_lanes();
         return JHQ_OK;
+    }
+
+    // Which lanes run side by side.  HIP gives each stream one of the
+    // process's hardware queues (GPU_MAX_HW_QUEUES, 4 by default) and shares
+    // a queue between streams beyond those; a queue runs one kernel at a
+    // time, so two lanes on one queue run their batches one after the other
+    // (with six lanes, two queues carried two lanes each and the other two
+    // sat idle half of a search).  A one-wave kernel of fixed length runs on
+    // the lanes taken so far and on the next lane at once: if they finish
+    // within 1.5 times one kernel's time, the next lane has a queue of its
+    // own and is taken.  Any failure leaves every lane in use.
+    void calibrate_lanes() {
+        nlanes = kLanes;
+        for (int l = 0; l < kLanes; l++) lane_use[l] = l;
+        if (kLanes < 2) return;
+        float* buf = nullptr;
+        hipEvent_t e0 = nullptr, e1[kLanes] = {};
+        int use[kLanes], n = 1;
+        use[0] = 0;
+        bool ok = hipMalloc(reinterpret_cast<void**>(&buf), kLanes * sizeof(float)) == hipSuccess &&
+                  hipEventCreate(&e0) == hipSuccess;
+        for (int l = 0; ok && l < kLanes; l++) ok = hipEventCreate(&e1[l]) == hipSuccess;
+        // the span from the first lane's start to the last lane's end
+        auto span = [&](const int* ls, int m, float* ms) {
+            constexpr int kIters = 200000;  // a few hundred us
+            if (hipEventRecord(e0, lane[ls[0]]) != hipSuccess) return false;
+            for (int i = 1; i < m; i++)
+                if (hipStreamWaitEvent(lane[ls[i]], e0, 0) != hipSuccess) return false;
+            for (int i = 0; i < m; i++)
+                if (jhq::lane_probe(buf + ls[i], kIters, lane[ls[i]]) != hipSuccess ||
+                    hipEventRecord(e1[i], lane[ls[i]]) != hipSuccess)
+                    return false;
+            *ms = 0.f;
+            for (int i = 0; i < m; i++) {
+                float t = 0.f;
+                if (hipEventSynchronize(e1[i]) != hipSuccess ||
+                    hipEventElapsedTime(&t, e0, e1[i]) != hipSuccess)
+                    return false;
+                *ms = std::max(*ms, t);
+            }
+            return true;
+        };
+        float t1 = 0.f, t = 0.f;
+        ok = ok && span(use, 1, &t1) && span(use, 1, &t1) && t1 > 0.f;  // the first run loads the kernel
+        for (int j = 1; ok && j < kLanes; j++) {
+            use[n] = j;
+            ok = span(use, n + 1, &t);
+            if (ok && t < 1.5f * t1) n++;
+        }
+        if (ok && n >= 1) {
+            nlanes = n;
+            for (int i = 0; i < n; i++) lane_use[i] = use[i];
+        }
+        if (e0) (void)hipEventDestroy(e0);
+        for (auto& e : e1)
+            if (e) (void)hipEventDestroy(e);
+        if (buf) (void)hipFree(buf);
+        (void)hipGetLastError();
+        if (verbose())
+            std::fprintf(stderr, "[jhq] search lanes: %d of %d on queues of their own\n", nlanes,
+                         kLanes);
     }
 
     int ensure_stream() {
@@ -912,8 +978,10 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
     JHQ_TRY(plan_batch(ix, Bmax, k, &bp, kLanes, true));
     JHQ_TRY(ix->ensure_lanes());
     for (int l = 0; l < kLanes; l++) JHQ_TRY(ensure_host_staging(ix, l, Bmax, k));
+    const int nl = ix->nlanes;
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], ix->stream));
-    for (int l = 0; l < kLanes; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
+    for (int i = 0; i < nl; i++)
+        JHQ_HIP(hipStreamWaitEvent(ix->lane[ix->lane_use[i]], ix->lane_ev[0], 0));
     int64_t pend_q0[kLanes];
     int pend_b[kLanes];
     for (int l = 0; l < kLanes; l++) {
@@ -931,7 +999,7 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
     int64_t bi = 0;
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
         const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
-        const int l = static_cast<int>(bi % kLanes);
+        const int l = ix->lane_use[bi % nl];
         Workspace& w = ix->ws[l];
         hipStream_t st = ix->lane[l];
         JHQ_TRY(collect(l));  // the lane's previous batch is done: its buffers are free
@@ -948,9 +1016,9 @@ int search_host_pipelined(jhq_index* ix, const float* q, int64_t nq, int k, floa
         pend_b[l] = Bq;
     }
     // the pending batches, oldest first
-    for (int j = 0; j < kLanes; j++) JHQ_TRY(collect(static_cast<int>((bi + j) % kLanes)));
-    for (int l = 0; l < kLanes; l++)
-        JHQ_HIP(hipStreamWaitEvent(ix->stream, ix->lane_ev[1 + l], 0));
+    for (int j = 0; j < nl; j++) JHQ_TRY(collect(ix->lane_use[(bi + j) % nl]));
+    for (int i = 0; i < nl; i++)
+        JHQ_HIP(hipStreamWaitEvent(ix->stream, ix->lane_ev[1 + ix->lane_use[i]], 0));
     return JHQ_OK;
 }
 
@@ -1669,16 +1737,19 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
         ix->done_pending = true;
         return JHQ_OK;
     }
+    const int nl = ix->nlanes;
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], s));
-    for (int l = 0; l < kLanes; l++) JHQ_HIP(hipStreamWaitEvent(ix->lane[l], ix->lane_ev[0], 0));
+    for (int i = 0; i < nl; i++)
+        JHQ_HIP(hipStreamWaitEvent(ix->lane[ix->lane_use[i]], ix->lane_ev[0], 0));
     int64_t bi = 0;
     for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
         const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
-        const int l = static_cast<int>(bi % kLanes);
+        const int l = ix->lane_use[bi % nl];
         JHQ_TRY(run_batch(ix, ix->ws[l], d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k,
                           d_ids + q0 * k, false, ix->lane[l]));
     }
-    for (int l = 0; l < kLanes; l++) {
+    for (int i = 0; i < nl; i++) {
+        const int l = ix->lane_use[i];
         JHQ_HIP(hipEventRecord(ix->lane_ev[1 + l], ix->lane[l]));
         JHQ_HIP(hipStreamWaitEvent(s, ix->lane_ev[1 + l], 0));
     }

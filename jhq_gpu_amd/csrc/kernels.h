@@ -80,6 +80,8 @@ hipError_t mfma_nt_score(const float* A, int64_t lda, const float* Bm, int64_t l
 // uint8 (dtype 1) / int8 (dtype 2) elements to float32.
 hipError_t convert_to_f32(const void* src, int dtype, int64_t n, float* dst, hipStream_t s);
 hipError_t fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
+// One wave spending a fixed time (iters dependent fmaf steps); *out = the chain's value.
+hipError_t lane_probe(float* out, int iters, hipStream_t s);
 hipError_t keys_to_assign(const unsigned long long* keys, int64_t n, int32_t* assign,
                           hipStream_t s);
 

@@ -1135,6 +1135,20 @@ hipError_t fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipS
     return hipGetLastError();
 }
 
+// One wave of a fixed-length dependent fmaf chain (the search lanes' queue
+// probe): its time is set by the chain, not by the GPU's load.
+__global__ void __launch_bounds__(64) lane_probe_kernel(float* out, int iters) {
+    float x = (float)threadIdx.x;
+    for (int i = 0; i < iters; i++) x = fmaf(x, 0.999999f, 1.0f);
+    if (threadIdx.x == 0) *out = x;
+}
+
+hipError_t lane_probe(float* out, int iters, hipStream_t s) {
+    if (!out || iters < 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(lane_probe_kernel, dim3(1), dim3(64), 0, s, out, iters);
+    return hipGetLastError();
+}
+
 __global__ void keys_to_assign_kernel(const unsigned long long* keys, int64_t n, int32_t* a) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
