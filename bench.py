@@ -11,8 +11,9 @@ Default run (the driver's `python bench.py --gpus 1 --steps K --warmup W`):
   Br=4, k=10, query batch 64.  Ground truth is exact L2 brute force.  A
   "step" is one device search call over the 10,000 queries, resident in HBM
   with their results: the engine runs them in batches of 64 through the whole
-  search path, consecutive batches on six search lanes (streams forked from
-  and joined into the caller's stream).  The sweep nprobe {16, 32, 64} x
+  search path, consecutive batches on the search lanes that have hardware
+  queues of their own (four of six streams; forked from and joined into the
+  caller's stream).  The sweep nprobe {16, 32, 64} x
   alpha {4, 10} picks the fastest point with recall@10 >= 0.95; when no point
   reaches it (the codes' own recall ceiling, measured by ranking every vector
   by its full estimate, is below 0.95 on this data) the fastest point within

@@ -130,8 +130,9 @@ int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k,
  * the workspace reserved for k <= k_max (jhq_reserve; add(), append(),
  * load() and the setters reserve k_max = 10 at the index's batch_size,
  * nprobe and alpha) and fails with JHQ_ESTATE for a larger k.
- * More than batch_size queries: consecutive batches rotate through six
- * internal search lanes (a workspace and a stream each) forked from `stream`
+ * More than batch_size queries: consecutive batches rotate through the
+ * internal search lanes (a workspace and a stream each; of six created, the
+ * ones on hardware queues of their own) forked from `stream`
  * and joined back into it, so the call is stream-ordered on `stream` like a
  * single launch.  Consecutive device
  * searches are ordered after each other whatever their streams; add,

@@ -128,11 +128,13 @@ struct InsertScratch {
 constexpr int kSteps = 4;
 
 // Search lanes (workspace, stream, pinned staging) that consecutive batches
-// of one call rotate through.  Six: each lane's batch is a chain of short,
-// latency-bound kernels, and more chains in flight fill the CUs (config 2,
-// device-resident: 1.35 M queries/s with six lanes, 1.09 M with four, 1.24 M
-// with five, 1.15 M with seven, 1.28 M with eight, 1.32 M with twelve; config
-// 5: 695 k with six, 650 k with four, 662 k with five, 627 k with seven).
+// of one call rotate through.  Six are created and the ones on hardware
+// queues of their own are used (calibrate_lanes: four with HIP's default
+// four queues): each lane's batch is a chain of short, latency-bound
+// kernels, and more chains in flight fill the CUs, but two lanes on one
+// queue run one after the other (config 2, device-resident: 1.75 M queries/s
+// on the four lanes with queues of their own, 1.50 M rotating through all
+// six; four lanes created alone landed on two queues, 1.19 M).
 #ifndef JHQ_LANES
 #define JHQ_LANES 6
 #endif

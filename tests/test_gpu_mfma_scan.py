@@ -153,7 +153,7 @@ def test_mfma_after_appends(gpu):
 
 
 def test_mfma_device_search_pipelined(gpu):
-    """Many batches of a device search (six lanes, one workspace each) return
+    """Many batches of a device search (the search lanes, one workspace each) return
     what the host search returns."""
     import torch
     g, o, q, k = _build(CASES[IDS.index("m32_a4")])

@@ -211,7 +211,7 @@ def test_search_device_matches_host(gpu, case):
 
 @pytest.mark.parametrize("name", ["ds8_k1d2", "m64_ds4_ck100", "k100_ck400"])
 def test_search_device_pipelined_batches(gpu, name):
-    """A device search over many batches (six lanes, each a workspace and a stream,
+    """A device search over many batches (the search lanes, each a workspace and a stream,
     joined into the caller's stream) returns what one call per batch and the
     host search return, including a ragged last batch."""
     import torch
