@@ -4543,15 +4543,16 @@ hipError_t refine_topk(const unsigned long long* partial, const int32_t* partial
 // selected from them, so the result does not depend on the MFMA values.
 // Queries with non-finite or huge values re-check every candidate.
 // ---------------------------------------------------------------------------
-// Tile-kernel waves per CU: one 4-wave workgroup.  The waves are bound by
-// issue and by their start-up load chain, and with the CU's other slots free
-// the other pipeline lane's kernels run beside them (config 2: 886 k queries/s
-// against 847 k with two workgroups per CU, 859 k with three waves, 790 k
-// with two).
-#ifndef JHQ_MFMA_WPC
-#define JHQ_MFMA_WPC 4
-#endif
-constexpr int kMfmaWavesPerCU = JHQ_MFMA_WPC;
+// Tile-kernel waves per CU (on average), by the batch's (query, probe)
+// pairs: two (one 4-wave workgroup on every other CU) for at most
+// kMfmaFewPairs, else four.  The waves are bound by issue and by their
+// start-up load chain, and the CUs left free run the other search lanes'
+// kernels beside them.  With the lanes on hardware queues of their own,
+// config 2 (1024 pairs) runs at 1.81 M queries/s against 1.75 M with one
+// workgroup per CU, 1.77 M with three waves per CU, 1.56 M with one, 1.64 M
+// with six, 1.54 M with eight; config 5 (4096 pairs, more tiles per batch)
+// at 728 k with four waves per CU against 713 k with two.
+constexpr int kMfmaWpcFew = 2, kMfmaWpcMany = 4, kMfmaFewPairs = 2048;
 constexpr int kRecheckNT = 1024;
 constexpr int kRecheckCap = 2048;   // survivors / members held in LDS
 constexpr int kRecheckCHM = 128;    // members per exact-distance round
@@ -5610,7 +5611,14 @@ bool mfma_scan_ok(int M, int d, int Ds, int K1D, int bpd, int B, int P, int ck, 
     return mfma_recheck_lds(M, d, P, ck, K1D, B, rck) <= (size_t)kLdsBytes - 1024;
 }
 
-static int mfma_scan_waves(int num_cu) { return std::max(1, num_cu) * kMfmaWavesPerCU; }
+static int mfma_scan_waves(int num_cu, int B, int P) {
+#ifdef JHQ_MFMA_WPC
+    const int wpc = JHQ_MFMA_WPC;  // a fixed count, for measurements
+#else
+    const int wpc = (int64_t)B * P <= kMfmaFewPairs ? kMfmaWpcFew : kMfmaWpcMany;
+#endif
+    return std::max(1, num_cu) * wpc;
+}
 
 size_t mfma_scan_bytes(int B, int P, int M, int num_cu) {
     (void)num_cu;
@@ -5644,7 +5652,7 @@ hipError_t mfma_scan(const float* q_rot, int d, int Ds, int K1D, int bpd, const 
     MfmaWs w;
     if ((int64_t)Bcap * P > kMfmaMaxBP || !mfma_ws(B, Bcap, P, M, ws, ws_bytes, dump_slots, &w))
         return hipErrorInvalidValue;
-    const int nwaves = mfma_scan_waves(num_cu);
+    const int nwaves = mfma_scan_waves(num_cu, B, P);
     using SFn = void (*)(MfmaWs, const int4*, const uint8_t*, uint32_t*, uint32_t*);
     SFn f = M == 16 ? mfma_scan_kernel<16> : M == 32 ? mfma_scan_kernel<32>
           : M == 48 ? mfma_scan_kernel<48> : M == 64 ? mfma_scan_kernel<64>
