@@ -4127,14 +4127,26 @@ __device__ __forceinline__ void refine_short_list(
         }
     };
     const int trow = refine_tab_row(d);
+    // the first round's pieces, correction and id are requested before the
+    // table is built (kslot is complete on entry)
+    if (pieces) pfetch(0, pwc, pcorr_c, pid_c);
     if (tab) {
         // (q_j - codeword c)^2, rounded as the sum below rounds it, at
-        // tab[c * trow + (j / 16) * 17 + j % 16]
-        for (int c = 0; c < 16; c++)
-            for (int j = tid; j < d; j += NT) {
-                const float df = sq[j + (j >> 5)] - rc[cbo(j) + c];
-                tab[c * trow + (j >> 4) * 17 + (j & 15)] = df * df;
+        // tab[c * trow + (j / 16) * 17 + j % 16]; the query value and the 16
+        // codewords of dimension j are read before its 16 stores
+        for (int j = tid; j < d; j += NT) {
+            const float qj = sq[j + (j >> 5)];
+            const float* rj = rc + cbo(j);
+            float cv[16];
+#pragma unroll
+            for (int c = 0; c < 16; c++) cv[c] = rj[c];
+            float* tj = tab + (j >> 4) * 17 + (j & 15);
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                const float df = qj - cv[c];
+                tj[c * trow] = df * df;
             }
+        }
     }
     for (int r = tid; r < ck; r += NT) {
         if (r < ksel) {
@@ -4183,7 +4195,6 @@ __device__ __forceinline__ void refine_short_list(
         uint2(&wn)[4] = pwn;
         float &corr_c = pcorr_c, &corr_n = pcorr_n;
         int &id_c = pid_c, &id_n = pid_n;
-        pfetch(0, wc, corr_c, id_c);
         for (int base = 0; base < ksel; base += NG) {
             if (base + NG < ksel) pfetch(base + NG, wn, corr_n, id_n);
             const int c = base + grp;
