@@ -141,6 +141,16 @@ constexpr int kSteps = 4;
 constexpr int kLanes = JHQ_LANES;
 static_assert(kLanes >= 1, "at least one lane");
 
+// Consecutive batches of a device search that one lane takes together: their
+// query product runs once over all their rows (each split sum is that of the
+// batch's own product, the same bits), so the [Pi ; C Pi] operand is read
+// once per pair of batches.
+#ifndef JHQ_QB_SHARE
+#define JHQ_QB_SHARE 2
+#endif
+constexpr int kQbShare = JHQ_QB_SHARE;
+static_assert(kQbShare >= 1, "at least one batch per product");
+
 // Per-batch search buffers (v14/search.cuh:24-46).  The index keeps one set
 // per search lane (kLanes): consecutive batches of one device search take the
 // lanes in turn, each lane a stream of its own, so one batch's scan overlaps
@@ -564,7 +574,10 @@ int ensure_workspace(jhq_index* ix, Workspace& w, int ck, int k, int P, int max_
     JHQ_TRY(need(w.wout_d, B * k, grow));
     JHQ_TRY(need(w.wout_i, B * k, grow));
     if (ix->dqmat.p) {
-        const size_t pf = jhq::mfma_qb_space(ix->batch_size, ix->d + ix->nlist, ix->d);
+        // split sums for kQbShare batches (a device search's lanes run the
+        // product once for consecutive batches)
+        const size_t pf =
+            jhq::mfma_qb_space(ix->batch_size * kQbShare, ix->d + ix->nlist, ix->d);
         if (pf) JHQ_TRY(need(w.wqpart, pf, grow));
     }
     return JHQ_OK;
@@ -827,15 +840,23 @@ int plan_batch(jhq_index* ix, int Bq, int k, BatchPlan* bp, int nws, bool grow) 
 }
 
 // One batch of Bq queries at d_q (device) through the whole pipeline
-// (the graph body of v14/search.cu:315-386).
+// (the graph body of v14/search.cu:315-386).  share: the query product of
+// share.rows consecutive queries (this batch's first, share.row0 = 0) runs
+// once, and the later batches of the group (share.row0 = their first row)
+// take their split sums from it; share.rows = 0: the batch's own product.
+struct QbShare {
+    int rows = 0, row0 = 0;
+};
 int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, const BatchPlan& bp,
-              float* d_out, int32_t* d_ids, bool want_topck, hipStream_t s) {
+              float* d_out, int32_t* d_ids, bool want_topck, hipStream_t s,
+              QbShare share = QbShare{}) {
     const int d = ix->d;
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[0], s));
     // rotation and centroid dots in one tiled product; its split sums are
     // added by the probe selection where the score row fits in its LDS
     jhq::QbPlan qp{};
     bool sel_qb = false;
+    const int qrows = share.rows > 0 ? share.rows : Bq;
     // the pre-scan: the selection also quantizes the queries and lists the
     // batch's (query, probe) pairs in the workspace's list hash
     const int64_t dump_slots = static_cast<int64_t>(w.wdump.n * 2 / 17 * 16);
@@ -849,11 +870,15 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
         w.hash_ws = w.wmfma.p;
     }
     if (ix->dqmat.p) {
-        qp = jhq::mfma_qb_plan(Bq, d + ix->nlist, d);
+        qp = jhq::mfma_qb_plan(qrows, d + ix->nlist, d);
         sel_qb = jhq::select_adds_qb(qp, ix->nlist, d);
-        JHQ_HIP(jhq::mfma_qb(qp, d_q, d, ix->dqmat.p, d, Bq, d + ix->nlist, d, d, w.wqrot.p, d,
-                             w.wscores.p, ix->nlist, ix->dnorms.p, w.wqpart.p, w.wqpart.n, s,
-                             !sel_qb));
+        // a shared product leaves its sums split (the selection adds them)
+        if (share.rows > 0 && (!sel_qb || share.row0 + Bq > qrows))
+            return fail(JHQ_EINVAL, "query product shared where the selection does not add it");
+        if (share.row0 == 0)
+            JHQ_HIP(jhq::mfma_qb(qp, d_q, d, ix->dqmat.p, d, qrows, d + ix->nlist, d, d,
+                                 w.wqrot.p, d, w.wscores.p, ix->nlist, ix->dnorms.p, w.wqpart.p,
+                                 w.wqpart.n, s, !sel_qb));
     } else {
         // d not a multiple of 64: the 16-row kernels
         JHQ_HIP(jhq::mfma_nt_store(d_q, d, ix->dP.p, d, Bq, d, d, w.wqrot.p, d, s));
@@ -863,9 +888,10 @@ int run_batch(jhq_index* ix, Workspace& w, const float* d_q, int Bq, int k, cons
     if (ix->timing) JHQ_HIP(hipEventRecord(ix->ev[1], s));
     const jhq::PrescanSel* psp = bp.sh.mfma ? &ps : nullptr;
     if (sel_qb)
-        JHQ_HIP(jhq::select_probes_qb(qp, w.wqpart.p, d, w.wqrot.p, d, ix->dnorms.p, Bq,
-                                      ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p, w.wgofs.p,
-                                      w.wqtot.p, s, psp));
+        JHQ_HIP(jhq::select_probes_qb(qp, w.wqpart.p + static_cast<size_t>(share.row0) *
+                                                           (d + ix->nlist),
+                                      d, w.wqrot.p, d, ix->dnorms.p, Bq, ix->nlist, bp.P,
+                                      ix->dldesc.p, w.wprobes.p, w.wgofs.p, w.wqtot.p, s, psp));
     else
         JHQ_HIP(jhq::select_probes(w.wscores.p, Bq, ix->nlist, bp.P, ix->dldesc.p, w.wprobes.p,
                                    w.wgofs.p, w.wqtot.p, s, psp));
@@ -1743,12 +1769,25 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
     JHQ_HIP(hipEventRecord(ix->lane_ev[0], s));
     for (int i = 0; i < nl; i++)
         JHQ_HIP(hipStreamWaitEvent(ix->lane[ix->lane_use[i]], ix->lane_ev[0], 0));
+    // consecutive batches share their lane's query product where the
+    // selection adds its split sums
+    const int d = ix->d;
+    const bool share = kQbShare > 1 && ix->dqmat.p &&
+                       jhq::select_adds_qb(jhq::mfma_qb_plan(Bmax * kQbShare, d + ix->nlist, d),
+                                           ix->nlist, d);
     int64_t bi = 0;
-    for (int64_t q0 = 0; q0 < nq; q0 += Bmax, bi++) {
-        const int Bq = static_cast<int>(std::min<int64_t>(Bmax, nq - q0));
+    for (int64_t q0 = 0; q0 < nq; bi++) {
         const int l = ix->lane_use[bi % nl];
-        JHQ_TRY(run_batch(ix, ix->ws[l], d_q + q0 * ix->d, Bq, k, bp, d_dists + q0 * k,
-                          d_ids + q0 * k, false, ix->lane[l]));
+        const int64_t rows = std::min<int64_t>(static_cast<int64_t>(Bmax) * (share ? kQbShare : 1),
+                                               nq - q0);
+        const QbShare sh{rows > Bmax ? static_cast<int>(rows) : 0, 0};
+        for (int64_t r0 = 0; r0 < rows; r0 += Bmax) {
+            const int Bq = static_cast<int>(std::min<int64_t>(Bmax, rows - r0));
+            JHQ_TRY(run_batch(ix, ix->ws[l], d_q + (q0 + r0) * d, Bq, k, bp,
+                              d_dists + (q0 + r0) * k, d_ids + (q0 + r0) * k, false, ix->lane[l],
+                              QbShare{sh.rows, sh.rows ? static_cast<int>(r0) : 0}));
+        }
+        q0 += rows;
     }
     for (int i = 0; i < nl; i++) {
         const int l = ix->lane_use[i];
