@@ -142,8 +142,9 @@ def test_cfg2_full_stagewise(gpu, nprobe):
 
 @pytest.mark.parametrize("nprobe", [16, 64])
 def test_cfg2_full_device_search_lanes(gpu, nprobe):
-    """Seven batches through the pipelined device search (the search lanes) equal
-    the debug search of the same queries, batch by batch on one stream."""
+    """Seven batches through the pipelined device search (the search lanes; three
+    pairs that each share one query product, then one batch alone) equal the
+    debug search of the same queries, batch by batch on one stream."""
     import torch
     g, o, hb, hq, cb, L = _cfg2(gpu)
     g.set_nprobe(nprobe)

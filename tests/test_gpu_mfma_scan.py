@@ -153,8 +153,9 @@ def test_mfma_after_appends(gpu):
 
 
 def test_mfma_device_search_pipelined(gpu):
-    """Many batches of a device search (the search lanes, one workspace each) return
-    what the host search returns."""
+    """Many batches of a device search (the search lanes, one workspace each;
+    consecutive batch pairs of a lane share one query product, the last pair
+    ragged) return what the host search returns."""
     import torch
     g, o, q, k = _build(CASES[IDS.index("m32_a4")])
     batch = CASES[IDS.index("m32_a4")][-1]

@@ -209,11 +209,13 @@ def test_search_device_matches_host(gpu, case):
     assert np.array_equal(_bits(od.cpu().numpy()), _bits(d1))
 
 
-@pytest.mark.parametrize("name", ["ds8_k1d2", "m64_ds4_ck100", "k100_ck400"])
+@pytest.mark.parametrize("name", ["ds8_k1d2", "m64_ds4_ck100", "k100_ck400", "d1024_m128"])
 def test_search_device_pipelined_batches(gpu, name):
     """A device search over many batches (the search lanes, each a workspace and a stream,
-    joined into the caller's stream) returns what one call per batch and the
-    host search return, including a ragged last batch."""
+    joined into the caller's stream; consecutive batch pairs of a lane share one
+    query product where the probe selection adds its split sums, as at d = 1024) returns what
+    one call per batch and the host search return, including a ragged last
+    batch (the second of the last pair)."""
     import torch
     case = CASES[IDS.index(name)]
     g, o, base, q, k = _build(case)
