@@ -1939,19 +1939,23 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     stream_begin<NT>(S);
     if (tid == 0) *scnt = 0;
     if constexpr (QB > 0) {
-        // the row's split sums, every split's float4 requested before the
-        // first is added (nrot and nlist multiples of 4)
+        // the row's split sums and the centroid norms, every float4 requested
+        // before the first is added (nrot and nlist multiples of 4)
         constexpr int U = 5;  // one round at D = 1024, nlist 4096
         const int N4 = (qp.nrot + nlist) >> 2, R4 = qp.nrot >> 2;
         const float4* p4 = (const float4*)(qp.part + (int64_t)b * (qp.nrot + nlist));
+        const float4* n4 = (const float4*)qp.norms;
         const int64_t st4 = qp.pstride >> 2;
         for (int i0 = tid; i0 < N4; i0 += U * NT) {
-            float4 v[U][QB];
+            float4 v[U][QB], nw[U];
 #pragma unroll
-            for (int u = 0; u < U; u++)
+            for (int u = 0; u < U; u++) {
 #pragma unroll
                 for (int sp = 0; sp < QB; sp++)
                     v[u][sp] = p4[sp * st4 + min(i0 + u * NT, N4 - 1)];
+                // (a clamped index where the float4 is the rotated query's)
+                nw[u] = n4[min(max(i0 + u * NT - R4, 0), N4 - R4 - 1)];
+            }
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int i = i0 + u * NT;
@@ -1968,7 +1972,7 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
                     ((float4*)(qp.C1 + (int64_t)b * qp.ld1))[i] = a;
                     if constexpr (MF) ((float4*)sqr)[i] = a;
                 } else {
-                    const float4 nv = ((const float4*)qp.norms)[i - R4];
+                    const float4 nv = nw[u];
                     float4 o;
                     o.x = fmaf(-2.0f, a.x, nv.x);
                     o.y = fmaf(-2.0f, a.y, nv.y);
