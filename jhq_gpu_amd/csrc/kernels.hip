@@ -1985,6 +1985,22 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
     }
     __syncthreads();
     JHQ_PHASE(0);
+    // the pre-scan's sums over the rotated query (C, the sum and the largest
+    // of |dl|), before the selection: after it the query's steps are stored
+    // beside the pair inserts
+    double qC = 0.0, qA = 0.0, qmx = 0.0;
+    if constexpr (MF) {
+        const float* qrow = QB ? sqr : mf.q_rot + (int64_t)b * mf.d;
+        const double c0 = mf.c1d[0], c1 = mf.c1d[1];
+        for (int i = tid; i < mf.d; i += NT) {
+            const double q = qrow[i];
+            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
+            qC += t0 * t0;
+            qA += fabs(dl);
+            qmx = fmax(qmx, fabs(dl));
+        }
+        block_reduce3<NT>(qC, qA, qmx, red);
+    }
     int kk = 0;
     bool exact = false;
     if (P <= kProbeFastP) {
@@ -2104,19 +2120,13 @@ select_probes_kernel(const float* __restrict__ scores, int nlist, int P,
         const int D = mf.d, NK = mf.M / 8, GS = mf.M / 4;
         const float* qrow = QB ? sqr : mf.q_rot + (int64_t)b * D;
         const double c0 = mf.c1d[0], c1 = mf.c1d[1];
-        double sC = 0.0, sA = 0.0, mx = 0.0;
-        for (int i = tid; i < D; i += NT) {
-            const double q = qrow[i];
-            const double t0 = q - c0, t1 = q - c1, dl = t1 * t1 - t0 * t0;
-            sC += t0 * t0;
-            sA += fabs(dl);
-            mx = fmax(mx, fabs(dl));
-        }
-        block_reduce3<NT>(sC, sA, mx, red);
+        const double sC = qC, sA = qA, mx = qmx;
         const bool fin = isfinite(sC) && isfinite(sA) && sC + sA < 1e36;
         const double st = fin && mx > 0.0 ? mx / 32000.0 : 1.0;
         int8_t* qa = mf.w.qa + (int64_t)b * 2 * D;
-        for (int x = tid; x < D / 4; x += NT) {
+        // waves 1 .. NW-1 (all of them when NW = 1), while wave 0 inserts
+        const int x0 = NW > 1 ? tid - 64 : tid, xs = NW > 1 ? NT - 64 : NT;
+        for (int x = x0 < 0 ? D / 4 : x0; x < D / 4; x += xs) {
             // dimensions 8 m + k of subspaces m = 4 m4 .. 4 m4 + 3: lane
             // group h = m / GS, dword mm / 4 of that group's subspaces,
             // K-step 2 (mm / 4) + k / 4, register k % 4, byte mm % 4
