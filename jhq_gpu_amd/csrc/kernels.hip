@@ -4755,12 +4755,12 @@ mfma_scan_kernel(MfmaWs w, const int4* __restrict__ ldesc, const uint8_t* __rest
     }
     const int s0 = min(H, lo * per), s1 = min(H, s0 + per);
     int tl = 0, nzl = 1;
-    if (s0 + lane < s1) {
-        const int4 rec = w.hs[s0 + lane];
-        if (rec.x >= 0) {
-            nzl = (rec.z + kGroup - 1) / kGroup;
-            tl = ((rec.y + 15) >> 4) * nzl;
-        }
+    // (a clamped load, then the select: no load through a selected pointer)
+    int4 rec0 = w.hs[min(s0 + lane, H - 1)];
+    if (s0 + lane >= s1) rec0.x = -1;
+    if (rec0.x >= 0) {
+        nzl = (rec0.z + kGroup - 1) / kGroup;
+        tl = ((rec0.y + 15) >> 4) * nzl;
     }
     int tinc = tl;
 #pragma unroll
@@ -4775,7 +4775,8 @@ mfma_scan_kernel(MfmaWs w, const int4* __restrict__ ldesc, const uint8_t* __rest
     int hs = s0 + fl;
     const int rr = rel - __shfl(tinc - tl, fl), nz0 = __shfl(nzl, fl);
     int gt = rr / nz0, off = rr - gt * nz0;
-    int4 srec = w.hs[hs];
+    // the first slot's record is lane fl's (no second load)
+    int4 srec = make_int4(__shfl(rec0.x, fl), __shfl(rec0.y, fl), __shfl(rec0.z, fl), 0);
     JHQ_PHASE(3);
     while (left > 0) {
         // the slot's list and the group's 16 pair entries
