@@ -1508,7 +1508,7 @@ hipError_t relocate_lists(const int4* moves, int nmoves, int M, int bpv, const u
 // ---------------------------------------------------------------------------
 template <int NT>
 __device__ __forceinline__ void rank_select(const unsigned long long* in, int n, int k,
-                                            unsigned long long* out) {
+                                            unsigned long long* out, int* src = nullptr) {
     // Key i's rank = number of keys smaller than it; keys are distinct except
     // for the ~0 padding, which ranks after every key that is written
     // (k <= number of real keys).  tpk lanes share one key, each counting over
@@ -1524,23 +1524,30 @@ __device__ __forceinline__ void rank_select(const unsigned long long* in, int n,
 #pragma unroll 8
         for (int j = j0; j < j1; j++) r += (in[j] < ki) ? 1 : 0;
         for (int off = tpk >> 1; off > 0; off >>= 1) r += __shfl_xor(r, off);
-        if (part == 0 && i < n && r < k) out[r] = ki;
+        if (part == 0 && i < n && r < k) {
+            out[r] = ki;
+            if (src) src[r] = i;
+        }
     }
     __syncthreads();
 }
 
 // Exact top-k of n keys in LDS (n >= k, the first k are real) into out[0..k).
+// Returns whether src (optional, k ints; may be idx) holds each output key's
+// index in `in` (the ranking path, for short inputs).
 template <int NT>
-__device__ __forceinline__ void select_keys(const unsigned long long* in, int n, int k,
+__device__ __forceinline__ bool select_keys(const unsigned long long* in, int n, int k,
                                             unsigned long long* out, int* idx,
-                                            unsigned long long* tmp, SelState* st) {
+                                            unsigned long long* tmp, SelState* st,
+                                            int* src = nullptr) {
     if ((int64_t)n * n <= (int64_t)NT * 512) {
-        rank_select<NT>(in, n, k, out);
-    } else {
-        block_topk<NT>([&](int i) { return (uint32_t)(in[i] >> 32); },
-                       [&](int i) { return (uint32_t)(in[i] & 0xffffffffull); }, n, k, idx, tmp,
-                       out, st);
+        rank_select<NT>(in, n, k, out, src);
+        return src != nullptr;
     }
+    block_topk<NT>([&](int i) { return (uint32_t)(in[i] >> 32); },
+                   [&](int i) { return (uint32_t)(in[i] & 0xffffffffull); }, n, k, idx, tmp,
+                   out, st);
+    return false;
 }
 
 // Values each wave contributes to the first-round bound.
@@ -5457,6 +5464,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         return e;
     };
     int kk = 0;
+    bool by_member = false;
     if (ns <= kRecheckCap) {
         // the ck-th smallest I among the survivors, then the members
         uint32_t thr2 = thr;
@@ -5543,7 +5551,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
         }
         JHQ_PHASE(5);
         kk = min(ck, nm);
-        if (kk > 0) select_keys<NT>(surv, nm, kk, S.kout, S.kidx, S.ktmp, S.st);
+        // (S.kidx: each selected member's index, when the ranking path ran)
+        if (kk > 0) by_member = select_keys<NT>(surv, nm, kk, S.kout, S.kidx, S.ktmp, S.st, S.kidx);
         JHQ_PHASE(11);
     } else {
         // more survivors than fit (ties at the bound): every candidate at or
@@ -5601,11 +5610,18 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     float* tabp = sqp + d + d / 32 + 1;
     if (tabp + refine_tab_words(d) > sq) tabp = nullptr;
     for (int i = tid; i < kk; i += NT) {
-        const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
         int32_t slot = -1;
-        for (int q = 0; q < P; q++)
-            if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
-                slot = meta[4 * q] + (tag - meta[4 * q + 3]);
+        if (by_member) {
+            // the member's probe and column (mp, mc are intact until the
+            // refine's table)
+            const int mi = S.kidx[i];
+            slot = meta[4 * mp[mi]] + mc[mi];
+        } else {
+            const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
+            for (int q = 0; q < P; q++)
+                if (tag >= meta[4 * q + 3] && tag - meta[4 * q + 3] < meta[4 * q + 2])
+                    slot = meta[4 * q] + (tag - meta[4 * q + 3]);
+        }
         kslot[i] = slot;
     }
     if (RC * Kr <= NT) {
