@@ -134,7 +134,9 @@ int jhq_search_ex(jhq_index* idx, const void* q, int dtype, int64_t nq, int k,
  * internal search lanes (a workspace and a stream each; of six created, the
  * ones on hardware queues of their own) forked from `stream`
  * and joined back into it, so the call is stream-ordered on `stream` like a
- * single launch.  Consecutive device
+ * single launch; a lane takes two consecutive batches at a time and runs
+ * their query product as one launch (each batch's results are those of
+ * its own product).  Consecutive device
  * searches are ordered after each other whatever their streams; add,
  * append, host searches, setters and destroy wait for the last one. */
 int jhq_search_device(jhq_index* idx, const float* d_q, int64_t nq, int k,
