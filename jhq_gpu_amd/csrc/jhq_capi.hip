@@ -1780,12 +1780,13 @@ int jhq_search_device(jhq_index* ix, const float* d_q, int64_t nq, int k, float*
         const int l = ix->lane_use[bi % nl];
         const int64_t rows = std::min<int64_t>(static_cast<int64_t>(Bmax) * (share ? kQbShare : 1),
                                                nq - q0);
-        const QbShare sh{rows > Bmax ? static_cast<int>(rows) : 0, 0};
+        // one batch alone keeps its own product
+        const int srows = rows > Bmax ? static_cast<int>(rows) : 0;
         for (int64_t r0 = 0; r0 < rows; r0 += Bmax) {
             const int Bq = static_cast<int>(std::min<int64_t>(Bmax, rows - r0));
             JHQ_TRY(run_batch(ix, ix->ws[l], d_q + (q0 + r0) * d, Bq, k, bp,
                               d_dists + (q0 + r0) * k, d_ids + (q0 + r0) * k, false, ix->lane[l],
-                              QbShare{sh.rows, sh.rows ? static_cast<int>(r0) : 0}));
+                              QbShare{srows, srows ? static_cast<int>(r0) : 0}));
         }
         q0 += rows;
     }
