@@ -4596,7 +4596,7 @@ constexpr int kRecheckTM = 16;      // tile minima per thread in flight (global)
 constexpr int kRecheckTR = 32;      // tile minima per thread ranked in registers
 constexpr int kRecheckTPL = 4;      // listed tiles' row loads in flight per lane
 
-constexpr int kMfmaPD = 4;  // tiles in flight per wave
+constexpr int kMfmaPD = 6;  // tiles in flight per wave
 // The minimum over each 16-lane row, on every lane of the row: swaps within
 // quads, then rotations by 4 and 8 inside the row (DPP operands of v_min, no
 // LDS round trips as a shuffle through ds_bpermute would take).
@@ -4797,12 +4797,14 @@ mfma_scan_kernel(MfmaWs w, const int4* __restrict__ ldesc, const uint8_t* __rest
         const int4 ga = make_int4(L.x, L.y, L.z, nq);
         // tiles past the run's last reload its last tile (in bounds, unused)
         const uint8_t* base = rows + ((int64_t)ga.x + 16 * off + j) * M + GS * h;
-        uint32_t c0[ND], c1[ND], c2[ND], c3[ND];
+        uint32_t c0[ND], c1[ND], c2[ND], c3[ND], c4[ND], c5[ND];
 #define JHQ_MFMA_FETCH(U, K) mfma_row_load<M>(base + (int64_t)16 * M * min((K), n - 1), c##U)
         JHQ_MFMA_FETCH(0, 0);
         JHQ_MFMA_FETCH(1, 1);
         JHQ_MFMA_FETCH(2, 2);
         JHQ_MFMA_FETCH(3, 3);
+        JHQ_MFMA_FETCH(4, 4);
+        JHQ_MFMA_FETCH(5, 5);
         // query steps of row j (rows past the group's queries take query
         // 0's: their products are never stored), requested with the rows
         mfma_v4i ahi[NK], alo[NK];
@@ -4844,6 +4846,8 @@ mfma_scan_kernel(MfmaWs w, const int4* __restrict__ ldesc, const uint8_t* __rest
             JHQ_MFMA_TILE(1)
             JHQ_MFMA_TILE(2)
             JHQ_MFMA_TILE(3)
+            JHQ_MFMA_TILE(4)
+            JHQ_MFMA_TILE(5)
         }
 #undef JHQ_MFMA_TILE
 #undef JHQ_MFMA_FETCH
