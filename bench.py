@@ -13,7 +13,8 @@ Default run (the driver's `python bench.py --gpus 1 --steps K --warmup W`):
   with their results: the engine runs them in batches of 64 through the whole
   search path, consecutive batches on the search lanes that have hardware
   queues of their own (four of six streams; forked from and joined into the
-  caller's stream).  The sweep nprobe {16, 32, 64} x
+  caller's stream; a lane takes two consecutive batches at a time, with one
+  query-product launch for both).  The sweep nprobe {16, 32, 64} x
   alpha {4, 10} picks the fastest point with recall@10 >= 0.95; when no point
   reaches it (the codes' own recall ceiling, measured by ranking every vector
   by its full estimate, is below 0.95 on this data) the fastest point within
