@@ -5162,8 +5162,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     StreamSel S;
     unsigned char* p0 = stream_carve<NT>(smem, ck, &S);
     unsigned long long* surv = (unsigned long long*)p0;        // [kRecheckCap]
-    int* mp = (int*)(surv + kRecheckCap);                      // [kRecheckCap] member probe
-    int* mc = mp + kRecheckCap;                                // [kRecheckCap] member column
+    int* mp = (int*)(surv + kRecheckCap);                      // [kRecheckCap] member pool slot
+    int* mc = mp + kRecheckCap;                                // [kRecheckCap] member tag
     float* ebuf = (float*)(mc + kRecheckCap);                  // [CHM][M + 1] (or more)
     float* sq = ebuf + recheck_ebuf_words(M, ck, RC * Kr, d, FUSE);  // [d]
     float* sc1d = sq + d;                                      // [K1D]
@@ -5490,8 +5490,9 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             if (keep) {
                 int pp, cc;
                 locate((int)(uint32_t)surv[i], pp, cc);
-                mp[at + __popcll(mk & lt)] = pp;
-                mc[at + __popcll(mk & lt)] = cc;
+                // the member's pool slot and its tag (canonical position)
+                mp[at + __popcll(mk & lt)] = meta[4 * pp] + cc;
+                mc[at + __popcll(mk & lt)] = meta[4 * pp + 3] + cc;
             }
         }
         __syncthreads();
@@ -5524,7 +5525,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             for (int u = 0; u < EPT; u++) {
                 // a member's row is one run: a wave reads 64 of its bytes
                 const int jj = min(tid / M + u * mstep, nc - 1);
-                cb[u] = rows[((int64_t)meta[4 * mp[c0 + jj]] + mc[c0 + jj]) * M + me];
+                cb[u] = rows[(int64_t)mp[c0 + jj] * M + me];
             }
             // one-bit digits (the pre-scan's shape): the level is a select
             // between the two codebook values, not an LDS lookup
@@ -5547,9 +5548,7 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
             if (tid < nc) {
                 float acc = 0.0f;
                 for (int m = 0; m < M; m++) acc += ebuf[tid * (M + 1) + m];
-                const int pp = mp[c0 + tid], cc = mc[c0 + tid];
-                surv[c0 + tid] = ((unsigned long long)f2ord(acc) << 32) |
-                                 (uint32_t)(meta[4 * pp + 3] + cc);
+                surv[c0 + tid] = ((unsigned long long)f2ord(acc) << 32) | (uint32_t)mc[c0 + tid];
             }
             __syncthreads();
         }
@@ -5616,10 +5615,8 @@ mfma_recheck_kernel(const uint32_t* __restrict__ dump, const uint32_t* __restric
     for (int i = tid; i < kk; i += NT) {
         int32_t slot = -1;
         if (by_member) {
-            // the member's probe and column (mp, mc are intact until the
-            // refine's table)
-            const int mi = S.kidx[i];
-            slot = meta[4 * mp[mi]] + mc[mi];
+            // the member's pool slot (mp is intact until the refine's table)
+            slot = mp[S.kidx[i]];
         } else {
             const int tag = (int)(uint32_t)(S.kout[i] & 0xffffffffull);
             for (int q = 0; q < P; q++)
